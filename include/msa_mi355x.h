@@ -1,0 +1,116 @@
+/*
+ * C ABI of the MI355X (gfx950) MiniMax-M3 sparse-attention kernels.
+ *
+ * Every entry point takes raw device pointers, int64 sizes, scalars and a
+ * hipStream_t passed as void*. Kernels are enqueued on that stream and the call
+ * returns without synchronising. No entry point allocates device memory: all
+ * outputs and workspaces are owned by the caller (sizes from the *_bytes /
+ * *_elems queries). Return value: 0 on success, 1 invalid argument,
+ * 2 unsupported configuration, 3 HIP launch failure.
+ *
+ * Layouts are the reference's TND layout: q [T,Hq,D], k/v [T,G,D],
+ * index_q [T,G,Di], index_k [T,1,Di], scores [T,G,NB] fp32, indices [T,G,K]
+ * int32, cu_seqlens [num_seqs+1] int32, all contiguous. Query heads
+ * [g*Hq/G, (g+1)*Hq/G) belong to KV group g. Block ids are sequence-local.
+ * dtype codes: 0 = fp32, 1 = fp16, 2 = bf16.
+ */
+#ifndef MSA_MI355X_H_
+#define MSA_MI355X_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Stage 2: causal top-k with forced local blocks.
+ * Replaces triton/topk.py:11-47 (m3_topk; eager twin eager/ops.py:94-129).
+ * indices [T,G,topk_blocks] int32, left-aligned, -1 padded; ties in
+ * descending-value order are emitted by ascending block id. */
+int msa_topk(const float* scores, const int32_t* cu_seqlens, int64_t num_seqs,
+             int64_t total_tokens, int64_t groups, int64_t num_blocks, int64_t block_size,
+             int64_t topk_blocks, int64_t local_blocks, int32_t* indices, void* stream);
+
+/* k2q CSR workspace: number of int32 tile counters, G * sum_s nb_s (nb_s + 1) / 2,
+ * from the host copy of cu_block_lens. Host-only helper (no device access). */
+int64_t msa_k2q_counter_elems(int64_t num_seqs, const int32_t* host_cu_block_lens, int64_t groups);
+
+/* Block->query CSR. Replaces triton/k2q.py:39-128 (build_k2q_csr; K2QCSR :20-36).
+ * cu_block_lens [num_seqs+1] int32 and tri_prefix [num_seqs+1] int64
+ * (tri_prefix[s] = G * sum_{s'<s} nb(nb+1)/2) are device copies of host metadata.
+ * workspace: int32 [counter_elems + total_blocks*groups].
+ * Outputs: row_ptr [total_blocks*groups+1], query_indices/slot_indices
+ * [T*G*K] (tail = -1), edges ordered by (query, slot) inside each row. */
+int msa_k2q_build(const int32_t* indices, const int32_t* cu_seqlens, const int32_t* cu_block_lens,
+                  const int64_t* tri_prefix, int64_t num_seqs, int64_t total_tokens, int64_t groups,
+                  int64_t topk_slots, int64_t block_size, int64_t total_blocks,
+                  int64_t counter_elems, int32_t* row_ptr, int32_t* query_indices,
+                  int32_t* slot_indices, int32_t* workspace, void* stream);
+
+/* Stage 1 forward: per-group causal block maxima of scale * (index_q . index_k).
+ * Replaces triton/index_score.py:93-136 (_index_score_forward) and the launch at
+ * :237-265. scores = fl32(scale * exact winning dot); -inf for blocks with no
+ * causal key. tie_info (nullable, int32 [T,G,NB]): winner offset + 1 for a
+ * unique exact maximum, -count for exact ties, 0 for invalid blocks
+ * (same encoding as index_score.py:128-136). */
+int msa_score_fwd(const void* index_q, const void* index_k, int32_t dtype,
+                  const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
+                  int64_t groups, int64_t index_dim, int64_t num_blocks, int64_t block_size,
+                  double scale, float* scores, int32_t* tie_info, void* stream);
+
+/* Score backward workspace in bytes (transposed tie/grad staging). */
+int64_t msa_score_bwd_workspace_bytes(int64_t total_tokens, int64_t groups, int64_t num_blocks,
+                                      int64_t index_dim);
+
+/* Stage 1 backward (amax subgradient: unique winner gets ds*scale, exact ties
+ * split it evenly). Replaces index_score.py:139-232 (_index_score_backward_q,
+ * _index_score_backward_k_group, _index_score_reduce_k; launches :268-295).
+ * grad_q [T,G,Di] / grad_k [T,1,Di] in the input dtype, either nullable.
+ * Deterministic: no floating-point atomics. */
+int msa_score_bwd(const void* index_q, const void* index_k, int32_t dtype,
+                  const int32_t* cu_seqlens, const int32_t* cu_block_lens, const int32_t* tie_info,
+                  const float* grad_scores, int64_t num_seqs, int64_t total_tokens, int64_t groups,
+                  int64_t index_dim, int64_t num_blocks, int64_t block_size, int64_t total_blocks,
+                  double scale, void* grad_q, void* grad_k, void* workspace, void* stream);
+
+/* Stage 3 forward: online-softmax sparse GQA attention over the selected blocks.
+ * Replaces triton/sparse_attention.py:35-84 (_forward_kernel; launch :336-359).
+ * out [T,Hq,D] in the input dtype; lse [T,Hq] fp32 (natural log, -inf for rows
+ * without keys, whose output is 0). Slots with id < 0 or id > qb(t) are ignored;
+ * keys after the query inside its own block are masked. */
+int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t dtype, const int32_t* indices,
+                 const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
+                 int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
+                 int64_t block_size, double scale, void* out, float* lse, void* stream);
+
+/* Stage 3 backward, query pass: dQ (nullable) and per-(t,h) statistics
+ * stats [T,Hq,3] fp32 = (probability mass, center, centered delta) consumed by
+ * the KV pass. Replaces sparse_attention.py:87-198 (_backward_kernel with
+ * ACCUMULATE_KV=False; launch :376-385). */
+int msa_attn_bwd_dq(const void* q, const void* k, const void* v, int32_t dtype, const void* out,
+                    const void* grad_out, const float* lse, const int32_t* indices,
+                    const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
+                    int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
+                    int64_t block_size, double scale, void* grad_q, float* stats, void* stream);
+
+/* Stage 3 backward workspace in bytes for msa_attn_bwd_dkdv. */
+int64_t msa_attn_bwd_workspace_bytes(int64_t total_tokens, int64_t q_heads, int64_t kv_groups,
+                                     int64_t head_dim, int64_t topk_slots, int64_t total_blocks,
+                                     int64_t block_size);
+
+/* Stage 3 backward, KV pass: dK/dV (either nullable) owned per (key block, group)
+ * row of the k2q CSR, no floating-point atomics. Replaces
+ * sparse_attention.py:223-295 (_backward_kv_kernel; launch :386-393). */
+int msa_attn_bwd_dkdv(const void* q, const void* k, const void* v, int32_t dtype,
+                      const void* grad_out, const float* lse, const float* stats,
+                      const int32_t* cu_seqlens, const int32_t* cu_block_lens,
+                      const int32_t* row_ptr, const int32_t* query_indices, int64_t num_seqs,
+                      int64_t total_tokens, int64_t q_heads, int64_t kv_groups, int64_t head_dim,
+                      int64_t total_blocks, int64_t block_size, double scale, void* grad_k,
+                      void* grad_v, void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSA_MI355X_H_ */

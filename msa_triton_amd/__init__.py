@@ -1,0 +1,42 @@
+"""MI355X-native MiniMax-M3 three-stage sparse attention (drop-in for ``msa_triton.triton``).
+
+The public operators keep the reference facade (triton/__init__.py:4-29): the
+implementation module is imported on first call, so importing the package does
+not load the native library.
+
+    m3_index_score(index_q, index_k, cu_seqlens, max_seqlen, *, block_size=128, scale=1.0)
+    m3_topk(scores, cu_seqlens, *, block_size=128, topk_blocks=16, local_blocks=1)
+    m3_sparse_attention(q, k, v, indices, cu_seqlens, max_seqlen, *, block_size=128,
+                        scale=None, return_lse=False)
+
+All three run as hand-written gfx950 HIP kernels behind the C ABI declared in
+``include/msa_mi355x.h``; there is no CPU or eager fallback.
+"""
+
+
+def m3_index_score(index_q, index_k, cu_seqlens, max_seqlen, *, block_size=128, scale=1.0):
+    from .index_score import m3_index_score as implementation
+
+    return implementation(index_q, index_k, cu_seqlens, max_seqlen, block_size=block_size, scale=scale)
+
+
+def m3_topk(scores, cu_seqlens, *, block_size=128, topk_blocks=16, local_blocks=1):
+    from .topk import m3_topk as implementation
+
+    return implementation(
+        scores, cu_seqlens, block_size=block_size, topk_blocks=topk_blocks, local_blocks=local_blocks
+    )
+
+
+def m3_sparse_attention(
+    q, k, v, indices, cu_seqlens, max_seqlen, *, block_size=128, scale=None, return_lse=False
+):
+    from .sparse_attention import m3_sparse_attention as implementation
+
+    return implementation(
+        q, k, v, indices, cu_seqlens, max_seqlen,
+        block_size=block_size, scale=scale, return_lse=return_lse,
+    )
+
+
+__all__ = ["m3_index_score", "m3_topk", "m3_sparse_attention"]

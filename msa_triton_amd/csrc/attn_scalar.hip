@@ -1,0 +1,335 @@
+// Stage 3, VALU path: sparse GQA attention forward, query-pass backward and
+// CSR-driven KV-pass backward for every input dtype. Logits, dP and the
+// softmax are evaluated in FP64: bf16/fp16/fp32 products are exact in FP64, so
+// the query pass and the KV pass see identical logits/dP values and the
+// softmax-gradient cancellation (dp - delta) is consistent between them. The bf16 hot path uses the MFMA kernels
+// (attn_mfma.hip); this file serves fp16/fp32 inputs and shapes outside the
+// MFMA templates.
+//
+// Semantics (triton/sparse_attention.py):
+//   forward  :35-84  slots with 0 <= id <= qb(t) are visited in slot order,
+//                    keys after the query in its own block are masked, online
+//                    softmax, out = 0 and lse = -inf for rows without keys;
+//   query bwd:87-198 p = exp(s - lse), mass = sum p, center c = O . dO,
+//                    delta = sum p (dp - c) / mass,
+//                    dS = p/mass * ((dp - c) - delta) * scale, dQ = sum dS k;
+//   KV bwd   :223-295 per key, walk its (block, group) CSR row and accumulate
+//                    dK += dS q, dV += p/mass dO over the R heads of each edge.
+// The query pass forms dQ = scale/mass * (sum p (dp-c) k - delta * sum p k),
+// which needs one pass over the keys instead of two.
+#include "common.hpp"
+
+namespace msa {
+
+struct RowCtx {
+  int64_t start;  // sequence start token
+  int64_t qb;     // query block of t
+};
+
+__device__ __forceinline__ RowCtx row_ctx(const int32_t* __restrict__ cu, int nseq, int64_t t, int B) {
+  const int s = find_seq(cu, nseq, t);
+  RowCtx c;
+  c.start = cu[s];
+  c.qb = (t - c.start) / B;
+  return c;
+}
+
+// Forward: one wavefront per (t, h). Keys are processed 64 at a time: each lane
+// evaluates one key's logit, lanes then own head dims for the P.V update.
+template <int DT, int DPL>
+__global__ __launch_bounds__(256) void attn_fwd_valu(const void* __restrict__ q, const void* __restrict__ k,
+                                                     const void* __restrict__ v,
+                                                     const int32_t* __restrict__ indices,
+                                                     const int32_t* __restrict__ cu, int nseq, int64_t T,
+                                                     int Hq, int G, int D, int K, int B, double scale,
+                                                     void* __restrict__ out, float* __restrict__ lse) {
+  extern __shared__ float smem[];
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t th = static_cast<int64_t>(blockIdx.x) * 4 + wid;
+  const bool active = th < T * Hq;
+  float* qs = smem + wid * D;
+  if (active)
+    for (int d = lane; d < D; d += kWave) qs[d] = load_as_f32<DT>(q, th * D + d);
+  __syncthreads();
+  if (!active) return;
+  const int64_t t = th / Hq;
+  const int h = static_cast<int>(th % Hq);
+  const int g = h / (Hq / G);
+  const RowCtx rc = row_ctx(cu, nseq, t, B);
+  double m = -__builtin_inf(), l = 0.0;
+  double o[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) o[j] = 0.0;
+  const int32_t* sel = indices + (t * G + g) * K;
+  for (int slot = 0; slot < K; ++slot) {
+    const int blk = sel[slot];
+    if (blk < 0 || blk > rc.qb) continue;
+    const int64_t kb0 = rc.start + static_cast<int64_t>(blk) * B;
+    const int64_t kend = (kb0 + B < t + 1) ? kb0 + B : t + 1;
+    for (int64_t base = kb0; base < kend; base += kWave) {
+      const int64_t key = base + lane;
+      double sv = -__builtin_inf();
+      if (key < kend) {
+        const int64_t off = (key * G + g) * D;
+        double acc = 0.0;
+        for (int d = 0; d < D; ++d) acc = fma(static_cast<double>(qs[d]), static_cast<double>(load_as_f32<DT>(k, off + d)), acc);
+        sv = acc * scale;
+      }
+      const double mt = wave_max_f64(sv);
+      const double mn = fmax(m, mt);
+      const double alpha = (m == -__builtin_inf()) ? 0.0 : exp(m - mn);
+      const double p = (key < kend) ? exp(sv - mn) : 0.0;
+      l = l * alpha + wave_sum_f64(p);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) o[j] *= alpha;
+      const int n = kend - base < kWave ? static_cast<int>(kend - base) : kWave;
+      for (int i = 0; i < n; ++i) {
+        const double pi = __shfl(p, i, kWave);
+        const int64_t off = ((base + i) * G + g) * D;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          const int d = lane + j * kWave;
+          if (d < D) o[j] = fma(pi, static_cast<double>(load_as_f32<DT>(v, off + d)), o[j]);
+        }
+      }
+      m = mn;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) {
+    const int d = lane + j * kWave;
+    if (d < D) store_from_f32<DT>(out, th * D + d, l > 0.0 ? static_cast<float>(o[j] / l) : 0.f);
+  }
+  if (lane == 0) lse[th] = l > 0.0 ? static_cast<float>(m + log(l)) : -__builtin_inff();
+}
+
+// Query-pass backward: one wavefront per (t, h).
+template <int DT, int DPL>
+__global__ __launch_bounds__(256) void attn_bwd_dq_valu(
+    const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
+    const void* __restrict__ out, const void* __restrict__ dout, const float* __restrict__ lse,
+    const int32_t* __restrict__ indices, const int32_t* __restrict__ cu, int nseq, int64_t T, int Hq, int G,
+    int D, int K, int B, double scale, void* __restrict__ dq, float* __restrict__ stats) {
+  extern __shared__ float smem[];
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t th = static_cast<int64_t>(blockIdx.x) * 4 + wid;
+  const bool active = th < T * Hq;
+  float* qs = smem + wid * 2 * D;
+  float* gs = qs + D;
+  double cpart = 0.0;
+  if (active) {
+    for (int d = lane; d < D; d += kWave) {
+      qs[d] = load_as_f32<DT>(q, th * D + d);
+      const float gd = load_as_f32<DT>(dout, th * D + d);
+      gs[d] = gd;
+      cpart = fma(static_cast<double>(load_as_f32<DT>(out, th * D + d)), static_cast<double>(gd), cpart);
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  const int64_t t = th / Hq;
+  const int h = static_cast<int>(th % Hq);
+  const int g = h / (Hq / G);
+  const RowCtx rc = row_ctx(cu, nseq, t, B);
+  const double c = wave_sum_f64(cpart);
+  const double row_lse = lse[th];
+  double mass = 0.0, delta = 0.0;
+  double a[DPL], bsum[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) a[j] = bsum[j] = 0.0;
+  const int32_t* sel = indices + (t * G + g) * K;
+  if (row_lse != -__builtin_inf()) {
+    for (int slot = 0; slot < K; ++slot) {
+      const int blk = sel[slot];
+      if (blk < 0 || blk > rc.qb) continue;
+      const int64_t kb0 = rc.start + static_cast<int64_t>(blk) * B;
+      const int64_t kend = (kb0 + B < t + 1) ? kb0 + B : t + 1;
+      for (int64_t base = kb0; base < kend; base += kWave) {
+        const int64_t key = base + lane;
+        double p = 0.0, u = 0.0;
+        if (key < kend) {
+          const int64_t off = (key * G + g) * D;
+          double sacc = 0.0, dacc = 0.0;
+          for (int d = 0; d < D; ++d) {
+            sacc = fma(static_cast<double>(qs[d]), static_cast<double>(load_as_f32<DT>(k, off + d)), sacc);
+            dacc = fma(static_cast<double>(gs[d]), static_cast<double>(load_as_f32<DT>(v, off + d)), dacc);
+          }
+          p = exp(sacc * scale - row_lse);
+          u = p * (dacc - c);
+          mass += p;
+          delta += u;
+        }
+        const int n = kend - base < kWave ? static_cast<int>(kend - base) : kWave;
+        for (int i = 0; i < n; ++i) {
+          const double pi = __shfl(p, i, kWave);
+          const double ui = __shfl(u, i, kWave);
+          const int64_t off = ((base + i) * G + g) * D;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) {
+            const int d = lane + j * kWave;
+            if (d < D) {
+              const double kv = load_as_f32<DT>(k, off + d);
+              a[j] = fma(ui, kv, a[j]);
+              bsum[j] = fma(pi, kv, bsum[j]);
+            }
+          }
+        }
+      }
+    }
+  }
+  const double msum = wave_sum_f64(mass);
+  const double dsum = wave_sum_f64(delta);
+  const bool has = msum > 0.0;
+  const double dhat = has ? dsum / msum : 0.0;
+  if (dq) {
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const int d = lane + j * kWave;
+      if (d < D) {
+        const double val = has ? static_cast<double>(scale) * (a[j] - dhat * bsum[j]) / msum : 0.0;
+        store_from_f32<DT>(dq, th * D + d, static_cast<float>(val));
+      }
+    }
+  }
+  if (lane == 0 && stats) {
+    stats[th * 3 + 0] = has ? static_cast<float>(msum) : 1.f;
+    stats[th * 3 + 1] = static_cast<float>(c);
+    stats[th * 3 + 2] = static_cast<float>(dhat);
+  }
+}
+
+// KV-pass backward: one wavefront per (key token, group); walks the key's
+// (block, group) CSR row in order, all R heads of each edge.
+template <int DT, int DPL>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_valu(
+    const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
+    const void* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ stats,
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ row_ptr,
+    const int32_t* __restrict__ qidx, int nseq, int64_t T, int Hq, int G, int D, int B, double scale,
+    void* __restrict__ dk, void* __restrict__ dv) {
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t jg = static_cast<int64_t>(blockIdx.x) * 4 + wid;
+  if (jg >= T * G) return;
+  const int64_t j = jg / G;
+  const int g = static_cast<int>(jg % G);
+  const int s = find_seq(cu, nseq, j);
+  const int64_t blk = (j - cu[s]) / B;
+  const int64_t row = (static_cast<int64_t>(cu_blocks[s]) + blk) * G + g;
+  const int64_t e0 = row_ptr[row], e1 = row_ptr[row + 1];
+  const int R = Hq / G;
+  float kr[DPL], vr[DPL];
+  double gk[DPL], gv[DPL];
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) {
+    const int d = lane + i * kWave;
+    kr[i] = d < D ? load_as_f32<DT>(k, jg * D + d) : 0.f;
+    vr[i] = d < D ? load_as_f32<DT>(v, jg * D + d) : 0.f;
+    gk[i] = gv[i] = 0.0;
+  }
+  for (int64_t e = e0; e < e1; ++e) {
+    const int64_t t = qidx[e];
+    if (t < j) continue;
+    for (int r = 0; r < R; ++r) {
+      const int64_t th = t * Hq + static_cast<int64_t>(g) * R + r;
+      float qv[DPL], gdv[DPL];
+      double sp = 0.0, dp = 0.0;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) {
+        const int d = lane + i * kWave;
+        qv[i] = d < D ? load_as_f32<DT>(q, th * D + d) : 0.f;
+        gdv[i] = d < D ? load_as_f32<DT>(dout, th * D + d) : 0.f;
+        sp = fma(static_cast<double>(qv[i]), static_cast<double>(kr[i]), sp);
+        dp = fma(static_cast<double>(gdv[i]), static_cast<double>(vr[i]), dp);
+      }
+      sp = wave_sum_f64(sp);
+      dp = wave_sum_f64(dp);
+      const double mass = stats[th * 3 + 0], c = stats[th * 3 + 1], dhat = stats[th * 3 + 2];
+      const double p = exp(sp * scale - static_cast<double>(lse[th])) / mass;
+      const double dsv = p * ((dp - c) - dhat) * scale;
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) {
+        gk[i] = fma(dsv, static_cast<double>(qv[i]), gk[i]);
+        gv[i] = fma(p, static_cast<double>(gdv[i]), gv[i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) {
+    const int d = lane + i * kWave;
+    if (d < D) {
+      if (dk) store_from_f32<DT>(dk, jg * D + d, static_cast<float>(gk[i]));
+      if (dv) store_from_f32<DT>(dv, jg * D + d, static_cast<float>(gv[i]));
+    }
+  }
+}
+
+template <int DT, int DPL>
+int attn_valu_launch_fwd(const void* q, const void* k, const void* v, const int32_t* idx, const int32_t* cu,
+                         int nseq, int64_t T, int Hq, int G, int D, int K, int B, double scale, void* out,
+                         float* lse, hipStream_t st) {
+  hipLaunchKernelGGL((attn_fwd_valu<DT, DPL>), dim3(grid_1d(T * Hq, 4)), dim3(256), 4 * D * sizeof(float), st, q,
+                     k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse);
+  return status_from(hipGetLastError());
+}
+
+template <int DT, int DPL>
+int attn_valu_launch_dq(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                        const float* lse, const int32_t* idx, const int32_t* cu, int nseq, int64_t T, int Hq,
+                        int G, int D, int K, int B, double scale, void* dq, float* stats, hipStream_t st) {
+  hipLaunchKernelGGL((attn_bwd_dq_valu<DT, DPL>), dim3(grid_1d(T * Hq, 4)), dim3(256), 8 * D * sizeof(float),
+                     st, q, k, v, out, dout, lse, idx, cu, nseq, T, Hq, G, D, K, B, scale, dq, stats);
+  return status_from(hipGetLastError());
+}
+
+template <int DT, int DPL>
+int attn_valu_launch_dkdv(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                          const float* stats, const int32_t* cu, const int32_t* cu_blocks, const int32_t* row_ptr,
+                          const int32_t* qidx, int nseq, int64_t T, int Hq, int G, int D, int B, double scale,
+                          void* dk, void* dv, hipStream_t st) {
+  hipLaunchKernelGGL((attn_bwd_dkdv_valu<DT, DPL>), dim3(grid_1d(T * G, 4)), dim3(256), 0, st, q, k, v, dout,
+                     lse, stats, cu, cu_blocks, row_ptr, qidx, nseq, T, Hq, G, D, B, scale, dk, dv);
+  return status_from(hipGetLastError());
+}
+
+#define MSA_DPL_DISPATCH(D, FN, ...)                     \
+  ((D) <= 64    ? FN<DT, 1>(__VA_ARGS__)                 \
+   : (D) <= 128 ? FN<DT, 2>(__VA_ARGS__)                 \
+   : (D) <= 256 ? FN<DT, 4>(__VA_ARGS__)                 \
+                : FN<DT, 8>(__VA_ARGS__))
+
+template <int DT>
+int attn_fwd_valu_dispatch(const void* q, const void* k, const void* v, const int32_t* idx, const int32_t* cu,
+                           int nseq, int64_t T, int Hq, int G, int D, int K, int B, double scale, void* out,
+                           float* lse, hipStream_t st) {
+  return MSA_DPL_DISPATCH(D, attn_valu_launch_fwd, q, k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse, st);
+}
+
+template <int DT>
+int attn_dq_valu_dispatch(const void* q, const void* k, const void* v, const void* out, const void* dout,
+                          const float* lse, const int32_t* idx, const int32_t* cu, int nseq, int64_t T, int Hq,
+                          int G, int D, int K, int B, double scale, void* dq, float* stats, hipStream_t st) {
+  return MSA_DPL_DISPATCH(D, attn_valu_launch_dq, q, k, v, out, dout, lse, idx, cu, nseq, T, Hq, G, D, K, B, scale,
+                          dq, stats, st);
+}
+
+template <int DT>
+int attn_dkdv_valu_dispatch(const void* q, const void* k, const void* v, const void* dout, const float* lse,
+                            const float* stats, const int32_t* cu, const int32_t* cu_blocks,
+                            const int32_t* row_ptr, const int32_t* qidx, int nseq, int64_t T, int Hq, int G, int D,
+                            int B, double scale, void* dk, void* dv, hipStream_t st) {
+  return MSA_DPL_DISPATCH(D, attn_valu_launch_dkdv, q, k, v, dout, lse, stats, cu, cu_blocks, row_ptr, qidx, nseq,
+                          T, Hq, G, D, B, scale, dk, dv, st);
+}
+
+// Explicit instantiations used by attn_api.hip.
+template int attn_fwd_valu_dispatch<kF32>(const void*, const void*, const void*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
+template int attn_fwd_valu_dispatch<kF16>(const void*, const void*, const void*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
+template int attn_fwd_valu_dispatch<kBF16>(const void*, const void*, const void*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
+template int attn_dq_valu_dispatch<kF32>(const void*, const void*, const void*, const void*, const void*, const float*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
+template int attn_dq_valu_dispatch<kF16>(const void*, const void*, const void*, const void*, const void*, const float*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
+template int attn_dq_valu_dispatch<kBF16>(const void*, const void*, const void*, const void*, const void*, const float*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
+template int attn_dkdv_valu_dispatch<kF32>(const void*, const void*, const void*, const void*, const float*, const float*, const int32_t*, const int32_t*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, double, void*, void*, hipStream_t);
+template int attn_dkdv_valu_dispatch<kF16>(const void*, const void*, const void*, const void*, const float*, const float*, const int32_t*, const int32_t*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, double, void*, void*, hipStream_t);
+template int attn_dkdv_valu_dispatch<kBF16>(const void*, const void*, const void*, const void*, const float*, const float*, const int32_t*, const int32_t*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, double, void*, void*, hipStream_t);
+
+}  // namespace msa

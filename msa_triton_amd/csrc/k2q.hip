@@ -1,0 +1,266 @@
+// Deterministic block->query CSR ("k2q") for the KV-owned backward.
+//
+// Semantics follow triton/k2q.py:94-128 (K2QCSR at :20-36):
+//   edge (t, g, s) with id = indices[t,g,s] is valid iff 0 <= id < nb(seq) and
+//   id <= qb(t); its row is (cu_block_lens[seq] + id) * G + g; row_ptr is the
+//   exclusive prefix of the row counts; inside a row edges are ordered by
+//   (query token, slot) ascending; unused tail entries are -1.
+//
+// Instead of the reference's argsort over int64 keys this is a stable counting
+// sort whose tiles are the query blocks themselves: every token of query block
+// qb can only reach rows with block id <= qb, so tile (seq, qb) owns a compact
+// counter range of (qb+1)*G entries.
+//   1. k2q_count   : per-tile histogram of its edges (integer atomics -> exact).
+//   2. k2q_rowscan : per row, exclusive prefix of the counts over the tiles
+//                    qb >= b (in qb order), giving the tile's start inside the row.
+//   3. k2q_ptrscan : exclusive scan of row totals -> row_ptr (one workgroup).
+//   4. k2q_scatter : each tile walks its tokens in order and places edges at
+//                    row_ptr[row] + tile offset + running count + duplicate rank.
+//   5. k2q_tail    : entries at or beyond row_ptr[rows] become -1.
+// The scatter is sequential over the B tokens of a tile but parallel over the
+// G*K edges of a token and over all tiles.
+#include "common.hpp"
+
+namespace msa {
+
+struct TileInfo {
+  int seq;
+  int qb;
+  int64_t tok_begin;
+  int64_t tok_end;
+  int64_t counter_base;  // offset of this tile's (qb+1)*G counters
+};
+
+// tri_prefix[s] = G * sum_{s'<s} nb(s') * (nb(s') + 1) / 2, computed on the host.
+__device__ __forceinline__ TileInfo tile_info(int64_t tile, const int32_t* __restrict__ cu,
+                                              const int32_t* __restrict__ cu_blocks,
+                                              const int64_t* __restrict__ tri_prefix, int nseq, int G,
+                                              int B) {
+  TileInfo ti;
+  ti.seq = upper_index(cu_blocks, nseq + 1, tile);
+  // Skip empty sequences that share the same block boundary.
+  while (ti.seq < nseq && cu_blocks[ti.seq + 1] <= tile) ++ti.seq;
+  ti.qb = static_cast<int>(tile - cu_blocks[ti.seq]);
+  const int64_t start = cu[ti.seq];
+  const int64_t end = cu[ti.seq + 1];
+  ti.tok_begin = start + static_cast<int64_t>(ti.qb) * B;
+  ti.tok_end = ti.tok_begin + B < end ? ti.tok_begin + B : end;
+  ti.counter_base = tri_prefix[ti.seq] + static_cast<int64_t>(G) * ti.qb * (ti.qb + 1) / 2;
+  return ti;
+}
+
+__global__ __launch_bounds__(256) void k2q_count(const int32_t* __restrict__ indices,
+                                                 const int32_t* __restrict__ cu,
+                                                 const int32_t* __restrict__ cu_blocks,
+                                                 const int64_t* __restrict__ tri_prefix, int nseq,
+                                                 int G, int K, int B, int32_t* __restrict__ counters) {
+  const TileInfo ti = tile_info(blockIdx.x, cu, cu_blocks, tri_prefix, nseq, G, B);
+  const int64_t ncnt = static_cast<int64_t>(ti.qb + 1) * G;
+  int32_t* cnt = counters + ti.counter_base;
+  for (int64_t i = threadIdx.x; i < ncnt; i += blockDim.x) cnt[i] = 0;
+  __syncthreads();
+  const int nb = cu_blocks[ti.seq + 1] - cu_blocks[ti.seq];
+  const int64_t edges = (ti.tok_end - ti.tok_begin) * G * K;
+  const int32_t* src = indices + ti.tok_begin * G * K;
+  for (int64_t e = threadIdx.x; e < edges; e += blockDim.x) {
+    const int id = src[e];
+    const int g = static_cast<int>((e / K) % G);
+    if (id >= 0 && id < nb && id <= ti.qb) atomicAdd(&cnt[static_cast<int64_t>(id) * G + g], 1);
+  }
+}
+
+// One thread per row: rewrite the row's per-tile counts into exclusive
+// offsets (in tile order) and emit the row total.
+__global__ __launch_bounds__(256) void k2q_rowscan(const int32_t* __restrict__ cu_blocks,
+                                                   const int64_t* __restrict__ tri_prefix, int nseq,
+                                                   int G, int64_t rows, int32_t* __restrict__ counters,
+                                                   int32_t* __restrict__ totals) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  const int64_t gb = r / G;
+  const int g = static_cast<int>(r % G);
+  int s = upper_index(cu_blocks, nseq + 1, gb);
+  while (s < nseq && cu_blocks[s + 1] <= gb) ++s;
+  const int b = static_cast<int>(gb - cu_blocks[s]);
+  const int nb = cu_blocks[s + 1] - cu_blocks[s];
+  int32_t running = 0;
+  for (int qb = b; qb < nb; ++qb) {
+    const int64_t idx = tri_prefix[s] + static_cast<int64_t>(G) * qb * (qb + 1) / 2 +
+                        static_cast<int64_t>(b) * G + g;
+    const int32_t c = counters[idx];
+    counters[idx] = running;
+    running += c;
+  }
+  totals[r] = running;
+}
+
+// Exclusive scan of totals[0..rows) into row_ptr[0..rows], one workgroup of 1024.
+__global__ __launch_bounds__(1024) void k2q_ptrscan(const int32_t* __restrict__ totals, int64_t rows,
+                                                    int32_t* __restrict__ row_ptr) {
+  __shared__ int32_t warp_sums[16];
+  __shared__ int32_t carry_s;
+  if (threadIdx.x == 0) carry_s = 0;
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  for (int64_t base = 0; base < rows; base += 1024) {
+    const int64_t i = base + threadIdx.x;
+    const int32_t v = i < rows ? totals[i] : 0;
+    // inclusive wave scan
+    int32_t x = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int32_t y = __shfl_up(x, o, kWave);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) warp_sums[wid] = x;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      int32_t w = warp_sums[threadIdx.x];
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const int32_t y = __shfl_up(w, o, 16);
+        if (static_cast<int>(threadIdx.x) >= o) w += y;
+      }
+      warp_sums[threadIdx.x] = w;  // inclusive over waves
+    }
+    __syncthreads();
+    const int32_t carry = carry_s;
+    const int32_t wave_off = wid > 0 ? warp_sums[wid - 1] : 0;
+    if (i < rows) row_ptr[i] = carry + wave_off + x - v;
+    __syncthreads();
+    if (threadIdx.x == 0) carry_s = carry + warp_sums[15];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) row_ptr[rows] = carry_s;
+}
+
+// One workgroup per tile; tokens processed in order, edges of a token in parallel.
+__global__ __launch_bounds__(1024) void k2q_scatter(const int32_t* __restrict__ indices,
+                                                    const int32_t* __restrict__ cu,
+                                                    const int32_t* __restrict__ cu_blocks,
+                                                    const int64_t* __restrict__ tri_prefix, int nseq,
+                                                    int G, int K, int B,
+                                                    const int32_t* __restrict__ row_ptr,
+                                                    int32_t* __restrict__ counters,
+                                                    int32_t* __restrict__ query_idx,
+                                                    int32_t* __restrict__ slot_idx) {
+  extern __shared__ int32_t ids[];  // G*K ids of the current token
+  const TileInfo ti = tile_info(blockIdx.x, cu, cu_blocks, tri_prefix, nseq, G, B);
+  int32_t* cnt = counters + ti.counter_base;
+  const int nb = cu_blocks[ti.seq + 1] - cu_blocks[ti.seq];
+  const int64_t row_base = static_cast<int64_t>(cu_blocks[ti.seq]) * G;
+  const int GK = G * K;
+  for (int64_t t = ti.tok_begin; t < ti.tok_end; ++t) {
+    const int32_t* src = indices + t * GK;
+    for (int e = threadIdx.x; e < GK; e += blockDim.x) {
+      const int id = src[e];
+      ids[e] = (id >= 0 && id < nb && id <= ti.qb) ? id : -1;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < GK; e += blockDim.x) {
+      const int id = ids[e];
+      if (id >= 0) {
+        const int g = e / K, slot = e % K;
+        const int32_t* mine = ids + g * K;
+        int rank = 0;
+        for (int s2 = 0; s2 < slot; ++s2) rank += (mine[s2] == id);
+        const int64_t lr = static_cast<int64_t>(id) * G + g;
+        const int64_t pos = static_cast<int64_t>(row_ptr[row_base + lr]) + cnt[lr] + rank;
+        query_idx[pos] = static_cast<int32_t>(t);
+        slot_idx[pos] = slot;
+      }
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < GK; e += blockDim.x) {
+      const int id = ids[e];
+      if (id >= 0) {
+        const int g = e / K, slot = e % K;
+        const int32_t* mine = ids + g * K;
+        bool first = true;
+        int dup = 0;
+        for (int s2 = 0; s2 < K; ++s2) {
+          if (mine[s2] == id) {
+            if (s2 < slot) first = false;
+            ++dup;
+          }
+        }
+        if (first) cnt[static_cast<int64_t>(id) * G + g] += dup;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(256) void k2q_tail(const int32_t* __restrict__ row_ptr, int64_t rows,
+                                                int64_t capacity, int32_t* __restrict__ query_idx,
+                                                int32_t* __restrict__ slot_idx) {
+  const int64_t used = row_ptr[rows];
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x + used; i < capacity;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    query_idx[i] = -1;
+    slot_idx[i] = -1;
+  }
+}
+
+__global__ __launch_bounds__(256) void fill_i32(int32_t* __restrict__ dst, int64_t n, int32_t value) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    dst[i] = value;
+}
+
+inline unsigned capped_grid(int64_t n) {
+  unsigned g = grid_1d(n, 256);
+  return g > 65535u * 16u ? 65535u * 16u : g;
+}
+
+}  // namespace msa
+
+using namespace msa;
+
+// Number of int32 counters the tile histogram needs: G * sum_s nb_s (nb_s + 1) / 2.
+extern "C" int64_t msa_k2q_counter_elems(int64_t num_seqs, const int32_t* host_cu_block_lens,
+                                         int64_t groups) {
+  int64_t counters = 0;
+  for (int64_t s = 0; s < num_seqs; ++s) {
+    const int64_t nb = host_cu_block_lens[s + 1] - host_cu_block_lens[s];
+    counters += groups * nb * (nb + 1) / 2;
+  }
+  return counters;
+}
+
+// workspace: int32 [counter_elems + total_blocks * groups].
+// tri_prefix: int64 [num_seqs + 1], tri_prefix[s] = G * sum_{s'<s} nb(nb+1)/2.
+extern "C" int msa_k2q_build(const int32_t* indices, const int32_t* cu_seqlens,
+                             const int32_t* cu_block_lens, const int64_t* tri_prefix,
+                             int64_t num_seqs, int64_t total_tokens, int64_t groups, int64_t topk_slots,
+                             int64_t block_size, int64_t total_blocks, int64_t counter_elems,
+                             int32_t* row_ptr, int32_t* query_indices, int32_t* slot_indices,
+                             int32_t* workspace, void* stream) {
+  if (num_seqs <= 0 || total_tokens < 0 || groups <= 0 || topk_slots < 0 || block_size <= 0 ||
+      total_blocks < 0 || counter_elems < 0)
+    return kErrInvalidArgument;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t rows = total_blocks * groups;
+  const int64_t capacity = total_tokens * groups * topk_slots;
+  if (capacity == 0 || rows == 0) {
+    hipLaunchKernelGGL(fill_i32, dim3(capped_grid(rows + 1)), dim3(256), 0, st, row_ptr, rows + 1, 0);
+    return status_from(hipGetLastError());
+  }
+  int32_t* counters = workspace;
+  int32_t* totals = workspace + counter_elems;
+  const int nseq = static_cast<int>(num_seqs), G = static_cast<int>(groups);
+  const int K = static_cast<int>(topk_slots), B = static_cast<int>(block_size);
+  hipLaunchKernelGGL(k2q_count, dim3(static_cast<unsigned>(total_blocks)), dim3(256), 0, st, indices,
+                     cu_seqlens, cu_block_lens, tri_prefix, nseq, G, K, B, counters);
+  hipLaunchKernelGGL(k2q_rowscan, dim3(grid_1d(rows, 256)), dim3(256), 0, st, cu_block_lens, tri_prefix,
+                     nseq, G, rows, counters, totals);
+  hipLaunchKernelGGL(k2q_ptrscan, dim3(1), dim3(1024), 0, st, totals, rows, row_ptr);
+  const int GK = G * K;
+  const int threads = GK <= 64 ? 64 : (GK >= 1024 ? 1024 : ((GK + 63) / 64) * 64);
+  hipLaunchKernelGGL(k2q_scatter, dim3(static_cast<unsigned>(total_blocks)), dim3(threads),
+                     static_cast<size_t>(GK) * 4, st, indices, cu_seqlens, cu_block_lens, tri_prefix, nseq,
+                     G, K, B, row_ptr, counters, query_indices, slot_indices);
+  hipLaunchKernelGGL(k2q_tail, dim3(capped_grid(capacity)), dim3(256), 0, st, row_ptr, rows, capacity,
+                     query_indices, slot_indices);
+  return status_from(hipGetLastError());
+}

@@ -1,0 +1,83 @@
+// Exact FP64 evaluation helpers for the indexer score, shared by the exact
+// kernel, the MFMA kernel's certification step and the backward tie paths.
+//
+// All exact dots use ONE summation order (sequential FMA over the index dim in
+// one lane), so every kernel that re-evaluates a (query, key) dot reproduces
+// the same FP64 bits and tie membership is consistent between forward and
+// backward.
+#pragma once
+#include "common.hpp"
+
+namespace msa {
+
+struct BlockMax {
+  double best;  // directed exact max (sign(scale) * dot), 0 when scale == 0
+  int count;    // number of keys attaining it
+  int first;    // smallest key offset (from the block start) attaining it
+};
+
+__device__ __forceinline__ double directed(double dot, double scale) {
+  return scale > 0.0 ? dot : (scale < 0.0 ? -dot : 0.0);
+}
+
+template <int DT>
+__device__ __forceinline__ double exact_dot(const void* __restrict__ a, int64_t ia,
+                                            const void* __restrict__ b, int64_t ib, int n) {
+  double acc = 0.0;
+  for (int d = 0; d < n; ++d)
+    acc = fma(static_cast<double>(load_as_f32<DT>(a, ia + d)), static_cast<double>(load_as_f32<DT>(b, ib + d)), acc);
+  return acc;
+}
+
+// Wave-cooperative exact block max over keys [k0, k1) for query row offset qoff.
+template <int DT>
+__device__ BlockMax block_max_exact(const void* __restrict__ iq, int64_t qoff, const void* __restrict__ ik,
+                                    int64_t k0, int64_t k1, int Di, double scale, int lane) {
+  double best = -__builtin_inf();
+  int count = 0, first = 0x7fffffff;
+  for (int64_t kk = k0 + lane; kk < k1; kk += kWave) {
+    const double v = directed(exact_dot<DT>(iq, qoff, ik, kk * Di, Di), scale);
+    if (v > best) {
+      best = v;
+      count = 1;
+      first = static_cast<int>(kk - k0);
+    } else if (v == best) {
+      ++count;
+    }
+  }
+  const double wbest = wave_max_f64(best);
+  const bool on = (best == wbest) && count > 0;
+  BlockMax r;
+  r.best = wbest;
+  r.count = wave_sum_i32(on ? count : 0);
+  int f = on ? first : 0x7fffffff;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) f = min(f, __shfl_xor(f, o, kWave));
+  r.first = f;
+  return r;
+}
+
+// Calls fn(key) for each key in [k0, k1) whose directed exact dot equals best,
+// in ascending key order (uniform control flow across the wave).
+template <int DT, typename Fn>
+__device__ void for_each_winner(const void* __restrict__ iq, int64_t qoff, const void* __restrict__ ik,
+                                int64_t k0, int64_t k1, int Di, double scale, double best, int lane, Fn fn) {
+  for (int64_t base = k0; base < k1; base += kWave) {
+    const int64_t kk = base + lane;
+    bool win = false;
+    if (kk < k1) win = directed(exact_dot<DT>(iq, qoff, ik, kk * Di, Di), scale) == best;
+    uint64_t mask = __ballot(win);
+    while (mask) {
+      const int i = __builtin_ctzll(mask);
+      mask &= mask - 1;
+      fn(base + i);
+    }
+  }
+}
+
+// MFMA score path (bf16). Declared here, defined in score_mfma.hip.
+bool score_mfma_supported(int Di, int B);
+int score_fwd_mfma_launch(const void* iq, const void* ik, const int32_t* cu, int nseq, int64_t rows, int G,
+                          int Di, int NB, int B, double scale, float* scores, int32_t* tie, hipStream_t st);
+
+}  // namespace msa

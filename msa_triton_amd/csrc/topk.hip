@@ -1,0 +1,108 @@
+// Causal top-k block selection with forced local blocks.
+//
+// Semantics follow triton/topk.py:31-46 (eager twin eager/ops.py:94-129):
+//   * blocks b > qb(t) are masked to -inf,
+//   * blocks in (qb-L, qb] are forced to +inf,
+//   * the min(K, NB) largest are returned in descending order, -inf picks
+//     become -1, and the row is right-padded with -1 up to K slots.
+// Ties (equal values, e.g. several +inf local blocks) are emitted in
+// ascending block order; this is the canonical order documented for the
+// drop-in (torch.topk leaves it unspecified).
+//
+// One wavefront owns one (token, group) row and holds the row's causal prefix
+// in registers (VPL values per lane). Selection is an iterated wave argmax on a
+// 64-bit key (ordered float bits << 32 | ~block) so that the comparison
+// itself implements "larger value, then smaller block id".
+#include "common.hpp"
+
+namespace msa {
+
+// Monotone map of float bits onto uint32 (+0 and -0 collapse to the same key).
+__device__ __forceinline__ uint32_t ordered_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if (u == 0x80000000u) u = 0u;
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+constexpr uint32_t kKeyNegInf = 0x007fffffu;  // ordered_key(-inf)
+constexpr uint32_t kKeyPosInf = 0xff800000u;  // ordered_key(+inf)
+
+template <int VPL>
+__global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ scores,
+                                                   const int32_t* __restrict__ cu, int nseq,
+                                                   int64_t rows, int G, int NB, int B, int K, int L,
+                                                   int32_t* __restrict__ out) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t t = row / G;
+  const int s = find_seq(cu, nseq, t);
+  const int64_t qb = (t - cu[s]) / B;
+  const int n = static_cast<int>(qb + 1 < NB ? qb + 1 : NB);
+  const int count = K < NB ? K : NB;
+  const int sel = count < n ? count : n;
+  const float* src = scores + row * NB;
+  int32_t* dst = out + row * K;
+
+  uint64_t key[VPL];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int b = v * kWave + lane;
+    uint32_t k = 0u;  // below every real key: never selected
+    if (b < n) {
+      k = (L > 0 && b > qb - L) ? kKeyPosInf : ordered_key(src[b]);
+    }
+    key[v] = (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(b));
+  }
+  uint64_t best = 0;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) best = key[v] > best ? key[v] : best;
+
+  for (int it = 0; it < sel; ++it) {
+    const uint64_t win = wave_max_u64(best);
+    const int b = static_cast<int>(~static_cast<uint32_t>(win));
+    const uint32_t k = static_cast<uint32_t>(win >> 32);
+    if (lane == 0) dst[it] = (k == kKeyNegInf) ? -1 : b;
+    if ((b & 63) == lane) {
+      best = 0;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        if (key[v] == win) key[v] = 0;
+        best = key[v] > best ? key[v] : best;
+      }
+    }
+  }
+  for (int it = sel + lane; it < K; it += kWave) dst[it] = -1;
+}
+
+}  // namespace msa
+
+using namespace msa;
+
+extern "C" int msa_topk(const float* scores, const int32_t* cu_seqlens, int64_t num_seqs,
+                        int64_t total_tokens, int64_t groups, int64_t num_blocks, int64_t block_size,
+                        int64_t topk_blocks, int64_t local_blocks, int32_t* indices, void* stream) {
+  if (total_tokens < 0 || groups <= 0 || num_blocks <= 0 || block_size <= 0 || topk_blocks < 0 ||
+      local_blocks < 0 || local_blocks > topk_blocks || num_seqs <= 0)
+    return kErrInvalidArgument;
+  if (num_blocks > 64 * 64) return kErrUnsupported;
+  const int64_t rows = total_tokens * groups;
+  if (rows == 0 || topk_blocks == 0) return kOk;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(grid_1d(rows, 4)), block(256);
+  const int nseq = static_cast<int>(num_seqs);
+  const int G = static_cast<int>(groups), NB = static_cast<int>(num_blocks);
+  const int B = static_cast<int>(block_size), K = static_cast<int>(topk_blocks);
+  const int L = static_cast<int>(local_blocks);
+#define MSA_TOPK_LAUNCH(V) \
+  hipLaunchKernelGGL(topk_kernel<V>, grid, block, 0, st, scores, cu_seqlens, nseq, rows, G, NB, B, K, L, indices)
+  if (NB <= 64) MSA_TOPK_LAUNCH(1);
+  else if (NB <= 128) MSA_TOPK_LAUNCH(2);
+  else if (NB <= 256) MSA_TOPK_LAUNCH(4);
+  else if (NB <= 512) MSA_TOPK_LAUNCH(8);
+  else if (NB <= 1024) MSA_TOPK_LAUNCH(16);
+  else if (NB <= 2048) MSA_TOPK_LAUNCH(32);
+  else MSA_TOPK_LAUNCH(64);
+#undef MSA_TOPK_LAUNCH
+  return status_from(hipGetLastError());
+}

@@ -1,0 +1,150 @@
+"""Stage 3: TND sparse GQA attention over selected KV blocks, with autograd.
+
+Mirrors triton/sparse_attention.py:429-485 of the reference (signature,
+defaults, validation order, messages and exception types) and the
+``_SparseAttention`` autograd contract (:334-395): per-input
+``needs_input_grad``; the query pass always runs when any grad is needed
+(it produces the per-row statistics the KV pass consumes); the k2q CSR is
+built only when dK or dV is needed; lse is non-differentiable.
+
+Execution: ``msa_attn_fwd`` (online softmax, saves lse), ``msa_attn_bwd_dq``
+(dQ and per-row statistics: probability mass, center, centered delta),
+``build_k2q_csr`` and ``msa_attn_bwd_dkdv`` (dK/dV owned per key block and
+group, no floating-point atomics). Saved state is q, k, v, out and lse in the
+input dtype / fp32; no fp32 staging copies of q/k/v/out are made.
+"""
+
+from __future__ import annotations
+
+import math
+
+import torch
+
+from . import _lib
+from . import k2q as _k2q
+from .layout import sequence_lengths, sequence_meta
+
+
+class _SparseAttention(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, q, k, v, indices, cu_seqlens, block_size, scale, meta):
+        q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+        indices = indices.contiguous()
+        cu = cu_seqlens.contiguous()
+        total, heads, dim = q.shape
+        groups = k.shape[1]
+        out = torch.empty_like(q)
+        lse = torch.empty((total, heads), device=q.device, dtype=torch.float32)
+        if total:
+            with torch.cuda.device(q.device):
+                status = _lib.lib().msa_attn_fwd(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[q.dtype], indices.data_ptr(),
+                    cu.data_ptr(), meta.num_seqs, total, heads, groups, dim, indices.shape[2], block_size,
+                    scale, out.data_ptr(), lse.data_ptr(), _lib.stream_of(q.device),
+                )
+            _lib.check(status, "msa_attn_fwd")
+        ctx.save_for_backward(q, k, v, indices, cu, out, lse)
+        ctx.meta = meta
+        ctx.scale = scale
+        ctx.block_size = block_size
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    def backward(ctx, grad_output, grad_lse):
+        q, k, v, indices, cu, out, lse = ctx.saved_tensors
+        meta = ctx.meta
+        need_q, need_k, need_v = ctx.needs_input_grad[:3]
+        need_kv = need_k or need_v
+        dq = torch.empty_like(q) if need_q else None
+        dk = torch.empty_like(k) if need_k else None
+        dv = torch.empty_like(v) if need_v else None
+        total, heads, dim = q.shape
+        groups = k.shape[1]
+        if total and (need_q or need_kv):
+            lib = _lib.lib()
+            device = q.device
+            stream = _lib.stream_of(device)
+            if grad_output is None:
+                grad_output = torch.zeros_like(out)
+            dout = grad_output.to(q.dtype).contiguous()
+            stats = torch.empty((total, heads, 3), device=device, dtype=torch.float32) if need_kv else None
+            with torch.cuda.device(device):
+                status = lib.msa_attn_bwd_dq(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[q.dtype], out.data_ptr(),
+                    dout.data_ptr(), lse.data_ptr(), indices.data_ptr(), cu.data_ptr(), meta.num_seqs, total,
+                    heads, groups, dim, indices.shape[2], ctx.block_size, ctx.scale, _lib.ptr(dq),
+                    _lib.ptr(stats), stream,
+                )
+            _lib.check(status, "msa_attn_bwd_dq")
+            if need_kv:
+                # Looked up through the module so the CSR build stays observable.
+                csr = _k2q.build_k2q_csr(indices, cu, block_size=ctx.block_size)
+                ws_bytes = lib.msa_attn_bwd_workspace_bytes(
+                    total, heads, groups, dim, indices.shape[2], meta.total_blocks, ctx.block_size
+                )
+                workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+                with torch.cuda.device(device):
+                    status = lib.msa_attn_bwd_dkdv(
+                        q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[q.dtype], dout.data_ptr(),
+                        lse.data_ptr(), stats.data_ptr(), cu.data_ptr(), csr.cu_block_lens.data_ptr(),
+                        csr.row_ptr.data_ptr(), csr.query_indices.data_ptr(), meta.num_seqs, total, heads,
+                        groups, dim, meta.total_blocks, ctx.block_size, ctx.scale, _lib.ptr(dk), _lib.ptr(dv),
+                        workspace.data_ptr(), ws_bytes, stream,
+                    )
+                _lib.check(status, "msa_attn_bwd_dkdv")
+        return dq, dk, dv, None, None, None, None, None
+
+
+def m3_sparse_attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    indices: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    max_seqlen: int,
+    *,
+    block_size: int = 128,
+    scale: float | None = None,
+    return_lse: bool = False,
+):
+    """Apply causal block-sparse attention to packed TND tensors.
+
+    ``indices[T, G, K]`` holds distinct sequence-local block ids with ``-1``
+    padding. Each contiguous group of ``Hq / G`` query heads shares a
+    selection. Empty selections produce zero output and zero input gradients.
+    The optional natural-log LSE is FP32 and non-differentiable.
+    """
+    if q.ndim != 3 or k.ndim != 3 or v.shape != k.shape:
+        raise ValueError("Expected q[T,Hq,D] and matching k/v[T,G,D].")
+    if q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError("q/k/v must have matching token and head dimensions.")
+    if k.shape[1] <= 0 or q.shape[1] <= 0 or q.shape[1] % k.shape[1]:
+        raise ValueError("Hq must be a positive multiple of G.")
+    if q.shape[2] <= 0:
+        raise ValueError("Head dimension must be positive.")
+    if q.dtype not in (torch.bfloat16, torch.float16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise TypeError("q/k/v must share a BF16, FP16, or FP32 dtype.")
+    if indices.ndim != 3 or indices.shape[:2] != (q.shape[0], k.shape[1]) or indices.dtype != torch.int32:
+        raise ValueError("indices must be int32 [T,G,K].")
+    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2 or cu_seqlens.dtype != torch.int32:
+        raise ValueError("cu_seqlens must be int32 [num_sequences + 1].")
+    if any(x.device != q.device for x in (k, v, indices, cu_seqlens)):
+        raise ValueError("All inputs must reside on the same device.")
+    if not isinstance(block_size, int) or block_size <= 0:
+        raise ValueError("block_size must be a positive integer.")
+    if not isinstance(max_seqlen, int) or max_seqlen <= 0:
+        raise ValueError("max_seqlen must be a positive integer.")
+    lengths = sequence_lengths(cu_seqlens, q.shape[0])
+    if max(lengths) > max_seqlen:
+        raise ValueError("max_seqlen is smaller than an actual sequence.")
+    effective_scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
+    if not math.isfinite(effective_scale):
+        raise ValueError("scale must be finite.")
+    _lib.require_gpu(q, "m3_sparse_attention")
+    bounds = [0]
+    for length in lengths:
+        bounds.append(bounds[-1] + length)
+    meta = sequence_meta(bounds, block_size)
+    output, lse = _SparseAttention.apply(q, k, v, indices, cu_seqlens, block_size, effective_scale, meta)
+    return (output, lse) if return_lse else output

@@ -1,0 +1,344 @@
+"""CPU oracle for the MiniMax-M3 sparse-attention path -- TEST INFRASTRUCTURE ONLY.
+
+This module restates the reference algorithm in numpy (float64 / int64) so that
+the HIP kernels can be checked against it. It is imported only by ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py``; the
+product path (``msa_triton_amd``) never calls it.
+
+Functions and the reference code they restate:
+  index_score          triton/index_score.py:93-136, tests/reference_fp64.py:16-45
+  index_score_backward triton/index_score.py:139-232 (amax subgradient,
+                       ties split evenly as torch.amax, eager/ops.py:81-82)
+  topk                 triton/topk.py:31-46 (eager/ops.py:94-129)
+  k2q_csr              triton/k2q.py:94-128
+  sparse_attention     tests/reference_fp64.py:48-85 (dense per sequence/group)
+  sparse_attention_backward   gradient of the above (softmax backward)
+  attention_rows / attention_kv_rows   the same math restricted to sampled
+                       query rows / key rows, gathering only selected blocks,
+                       for parity at sizes where the dense form does not fit.
+
+Pinning (see tests/test_oracle_*.py): every function is checked against the
+reference's known-answer cases (tests/test_eager.py:143-170,
+tests/test_topk.py:20-66, tests/test_k2q.py:101-135,
+tests/test_triton_score.py:133-182, docs/code_review_response.md:33-41 and
+:246-250), against independent brute force (exact rational dots, pure-Python
+ranking and inversion loops) and against torch float64 autograd of an
+independently written dense formulation.
+
+Order conventions: ``topk`` emits descending values with ties in ascending
+block order (the drop-in's documented canonical order; torch.topk leaves tie
+order unspecified, so the reference's order among equal values is unpinned).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+
+def bounds_of(cu) -> list[int]:
+    return [int(x) for x in np.asarray(cu).reshape(-1)]
+
+
+def _token_positions(bounds):
+    """(seq id, sequence start) for every packed token."""
+    total = bounds[-1]
+    seq = np.zeros(total, dtype=np.int64)
+    start = np.zeros(total, dtype=np.int64)
+    for s, (a, b) in enumerate(zip(bounds[:-1], bounds[1:])):
+        seq[a:b] = s
+        start[a:b] = a
+    return seq, start
+
+
+# --------------------------------------------------------------------------- stage 1
+
+
+def index_score(iq, ik, cu, max_seqlen, *, block_size=128, scale=1.0):
+    """Exact block maxima.
+
+    Returns (scores_f64, scores_f32, tie) where scores_f64[t,g,b] is
+    max over causal keys j of block b of scale * (iq[t,g] . ik[j]) evaluated in
+    float64 (-inf if none), scores_f32 its float32 rounding (the public score),
+    and tie the winner code: offset+1 for a unique maximum, -count for ties,
+    0 for blocks without causal keys. Winners compare the directed dot
+    sign(scale) * dot, as the reference's compensated comparison does.
+    """
+    q = np.asarray(iq, dtype=np.float64)
+    k = np.asarray(ik, dtype=np.float64)[:, 0, :]
+    bounds = bounds_of(cu)
+    total, groups, _ = q.shape
+    nb = (max_seqlen + block_size - 1) // block_size
+    out = np.full((total, groups, nb), -np.inf)
+    tie = np.zeros((total, groups, nb), dtype=np.int32)
+    sign = 1.0 if scale > 0 else (-1.0 if scale < 0 else 0.0)
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        length = b - a
+        for blk in range(nb):
+            lo, hi = blk * block_size, min((blk + 1) * block_size, length)
+            if lo >= hi:
+                continue
+            dots = np.einsum("tgd,kd->tgk", q[a:b], k[a + lo : a + hi])  # [S,G,n]
+            pos = np.arange(length)[:, None]
+            allowed = np.arange(lo, hi)[None, :] <= pos  # [S, n]
+            directed = np.where(allowed[:, None, :], sign * dots, -np.inf)
+            best = directed.max(-1)
+            valid = allowed.any(-1)
+            winners = (directed == best[..., None]) & allowed[:, None, :]
+            count = winners.sum(-1)
+            first = winners.argmax(-1)
+            code = np.where(count == 1, first + 1, -count).astype(np.int32)
+            with np.errstate(invalid="ignore"):
+                scores = np.abs(scale) * best
+            out[a:b, :, blk] = np.where(valid[:, None], scores, -np.inf)
+            tie[a:b, :, blk] = np.where(valid[:, None], code, 0)
+    return out, out.astype(np.float32), tie
+
+
+def index_score_backward(iq, ik, cu, max_seqlen, ds, *, block_size=128, scale=1.0):
+    """Exact amax subgradient: returns (dq [T,G,Di], dk [T,1,Di]) in float64."""
+    q = np.asarray(iq, dtype=np.float64)
+    k = np.asarray(ik, dtype=np.float64)[:, 0, :]
+    ds = np.asarray(ds, dtype=np.float64)
+    bounds = bounds_of(cu)
+    total, groups, dim = q.shape
+    nb = (max_seqlen + block_size - 1) // block_size
+    dq = np.zeros_like(q)
+    dk = np.zeros((total, dim))
+    sign = 1.0 if scale > 0 else (-1.0 if scale < 0 else 0.0)
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        length = b - a
+        for blk in range(nb):
+            lo, hi = blk * block_size, min((blk + 1) * block_size, length)
+            if lo >= hi:
+                continue
+            dots = np.einsum("tgd,kd->tgk", q[a:b], k[a + lo : a + hi])
+            pos = np.arange(length)[:, None]
+            allowed = np.arange(lo, hi)[None, :] <= pos
+            directed = np.where(allowed[:, None, :], sign * dots, -np.inf)
+            best = directed.max(-1, keepdims=True)
+            winners = (directed == best) & allowed[:, None, :]
+            count = np.maximum(winners.sum(-1, keepdims=True), 1)
+            weight = winners * (ds[a:b, :, blk][..., None] * scale / count)  # [S,G,n]
+            weight = np.where(allowed.any(-1)[:, None, None], weight, 0.0)
+            dq[a:b] += np.einsum("tgk,kd->tgd", weight, k[a + lo : a + hi])
+            dk[a + lo : a + hi] += np.einsum("tgk,tgd->kd", weight, q[a:b])
+    return dq, dk[:, None, :]
+
+
+# --------------------------------------------------------------------------- stage 2
+
+
+def topk(scores, cu, *, block_size=128, topk_blocks=16, local_blocks=1):
+    """Causal mask, +inf local boost, top-min(K, NB) in canonical order, -1 padding."""
+    scores = np.asarray(scores, dtype=np.float32)
+    bounds = bounds_of(cu)
+    total, groups, nb = scores.shape
+    result = np.full((total, groups, topk_blocks), -1, dtype=np.int32)
+    if total == 0 or topk_blocks == 0:
+        return result
+    _, start = _token_positions(bounds)
+    qb = (np.arange(total) - start) // block_size
+    blocks = np.arange(nb)
+    valid = blocks[None, :] <= qb[:, None]
+    ranked = np.where(valid[:, None, :], scores.astype(np.float64), -np.inf)
+    if local_blocks:
+        local = valid & (blocks[None, :] > qb[:, None] - local_blocks)
+        ranked = np.where(local[:, None, :], np.inf, ranked)
+    count = min(topk_blocks, nb)
+    order = np.argsort(-ranked, axis=-1, kind="stable")[..., :count]
+    values = np.take_along_axis(ranked, order, axis=-1)
+    result[..., :count] = np.where(values == -np.inf, -1, order).astype(np.int32)
+    return result
+
+
+# --------------------------------------------------------------------------- k2q CSR
+
+
+def k2q_csr(indices, cu, *, block_size):
+    """(row_ptr, query_indices, slot_indices, cu_block_lens) as int32 arrays."""
+    ids = np.asarray(indices, dtype=np.int64)
+    total, groups, slots = ids.shape
+    bounds = bounds_of(cu)
+    lengths = [b - a for a, b in zip(bounds[:-1], bounds[1:])]
+    counts = [(n + block_size - 1) // block_size for n in lengths]
+    cu_blocks = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    num_rows = int(cu_blocks[-1]) * groups
+    capacity = total * groups * slots
+    row_ptr = np.zeros(num_rows + 1, dtype=np.int32)
+    query = np.full(capacity, -1, dtype=np.int32)
+    slot = np.full(capacity, -1, dtype=np.int32)
+    if capacity == 0:
+        return row_ptr, query, slot, cu_blocks.astype(np.int32)
+    seq, start = _token_positions(bounds)
+    seq_blocks = np.asarray(counts, dtype=np.int64)[seq]
+    qb = (np.arange(total) - start) // block_size
+    valid = (ids >= 0) & (ids < seq_blocks[:, None, None]) & (ids <= qb[:, None, None])
+    rows = (cu_blocks[seq][:, None, None] + ids) * groups + np.arange(groups)[None, :, None]
+    flat_valid = valid.reshape(-1)
+    flat_rows = rows.reshape(-1)[flat_valid]
+    edges = np.nonzero(flat_valid)[0]
+    order = np.argsort(flat_rows, kind="stable")
+    edges = edges[order]
+    n = edges.size
+    query[:n] = edges // (groups * slots)
+    slot[:n] = edges % slots
+    row_ptr[1:] = np.cumsum(np.bincount(flat_rows, minlength=num_rows))
+    return row_ptr, query, slot, cu_blocks.astype(np.int32)
+
+
+# --------------------------------------------------------------------------- stage 3
+
+
+def _selected_mask(ids_seq, length, block_size):
+    """[S, S] bool: key j visible to query t (selected block and j <= t)."""
+    pos = np.arange(length)
+    key_block = pos // block_size
+    sel = (key_block[None, :, None] == ids_seq[:, None, :]).any(-1)  # [S(t), S(j)]
+    return sel & (pos[None, :] <= pos[:, None])
+
+
+def sparse_attention(q, k, v, indices, cu, *, block_size=128, scale=None, dout=None):
+    """Dense per-(sequence, group) FP64 attention.
+
+    Returns (out, lse) and, when ``dout`` is given, also (dq, dk, dv).
+    A key is visible when its block id appears among the query's selected ids
+    and it is not after the query; rows without visible keys give out = 0,
+    lse = -inf and zero gradients.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    ids = np.asarray(indices, dtype=np.int64)
+    total, heads, dim = q.shape
+    groups = k.shape[1]
+    ratio = heads // groups
+    scale = dim ** -0.5 if scale is None else float(scale)
+    bounds = bounds_of(cu)
+    out = np.zeros_like(q)
+    lse = np.full((total, heads), -np.inf)
+    grads = dout is not None
+    if grads:
+        do = np.asarray(dout, dtype=np.float64)
+        dq, dk, dv = np.zeros_like(q), np.zeros_like(k), np.zeros_like(v)
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        length = b - a
+        if length == 0:
+            continue
+        for g in range(groups):
+            hs = slice(g * ratio, (g + 1) * ratio)
+            allowed = _selected_mask(ids[a:b, g], length, block_size)  # [S, S]
+            has = allowed.any(-1)
+            logits = np.einsum("trd,kd->trk", q[a:b, hs], k[a:b, g]) * scale
+            masked = np.where(allowed[:, None, :], logits, -np.inf)
+            m = np.where(has[:, None], masked.max(-1), 0.0)
+            e = np.where(allowed[:, None, :], np.exp(masked - m[..., None]), 0.0)
+            denom = e.sum(-1)
+            safe = np.where(has[:, None], denom, 1.0)
+            p = e / safe[..., None]
+            out[a:b, hs] = np.einsum("trk,kd->trd", p, v[a:b, g])
+            lse[a:b, hs] = np.where(has[:, None], m + np.log(safe), -np.inf)
+            if grads:
+                dov = do[a:b, hs]
+                dp = np.einsum("trd,kd->trk", dov, v[a:b, g])
+                delta = (p * dp).sum(-1, keepdims=True)
+                dlogit = p * (dp - delta)
+                dq[a:b, hs] = scale * np.einsum("trk,kd->trd", dlogit, k[a:b, g])
+                dk[a:b, g] = scale * np.einsum("trk,trd->kd", dlogit, q[a:b, hs])
+                dv[a:b, g] = np.einsum("trk,trd->kd", p, dov)
+    if grads:
+        return out, lse, dq, dk, dv
+    return out, lse
+
+
+def _row_keys(t, g, ids, start, block_size):
+    """Sorted visible key tokens for query token t in group g (duplicates removed)."""
+    pos = t - start
+    qb = pos // block_size
+    keys = []
+    for blk in sorted(set(int(x) for x in ids[t, g] if 0 <= x <= qb)):
+        lo = start + blk * block_size
+        hi = min(lo + block_size, t + 1)
+        keys.extend(range(lo, hi))
+    return np.asarray(keys, dtype=np.int64)
+
+
+def attention_rows(q, k, v, indices, cu, tokens, *, block_size=128, scale=None, dout=None):
+    """Sparse FP64 attention for selected query tokens only.
+
+    Returns dict with out [n,H,D], lse [n,H] and, with ``dout``, dq [n,H,D] and
+    the per-row softmax-gradient center delta [n,H] = sum_j p_j dp_j.
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    ids = np.asarray(indices)
+    total, heads, dim = q.shape
+    groups = k.shape[1]
+    ratio = heads // groups
+    scale = dim ** -0.5 if scale is None else float(scale)
+    _, start = _token_positions(bounds_of(cu))
+    tokens = np.asarray(tokens, dtype=np.int64)
+    res = {"out": np.zeros((len(tokens), heads, dim)), "lse": np.full((len(tokens), heads), -np.inf)}
+    if dout is not None:
+        do = np.asarray(dout, dtype=np.float64)
+        res["dq"] = np.zeros((len(tokens), heads, dim))
+        res["delta"] = np.zeros((len(tokens), heads))
+    for i, t in enumerate(tokens):
+        for g in range(groups):
+            keys = _row_keys(int(t), g, ids, int(start[t]), block_size)
+            if keys.size == 0:
+                continue
+            hs = slice(g * ratio, (g + 1) * ratio)
+            kk, vv = k[keys, g], v[keys, g]
+            logits = q[t, hs] @ kk.T * scale  # [R, n]
+            m = logits.max(-1, keepdims=True)
+            e = np.exp(logits - m)
+            den = e.sum(-1, keepdims=True)
+            p = e / den
+            res["out"][i, hs] = p @ vv
+            res["lse"][i, hs] = (m + np.log(den))[:, 0]
+            if dout is not None:
+                dp = do[t, hs] @ vv.T
+                delta = (p * dp).sum(-1, keepdims=True)
+                res["dq"][i, hs] = scale * (p * (dp - delta)) @ kk
+                res["delta"][i, hs] = delta[:, 0]
+    return res
+
+
+def attention_kv_rows(q, k, v, indices, cu, dout, keys, *, block_size=128, scale=None):
+    """Sparse FP64 dK/dV for selected key tokens (all groups): returns (dk, dv) [n,G,D]."""
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    do = np.asarray(dout, dtype=np.float64)
+    ids = np.asarray(indices)
+    total, heads, dim = q.shape
+    groups = k.shape[1]
+    ratio = heads // groups
+    scale = dim ** -0.5 if scale is None else float(scale)
+    bounds = bounds_of(cu)
+    seq, start = _token_positions(bounds)
+    keys = np.asarray(keys, dtype=np.int64)
+    dk = np.zeros((len(keys), groups, dim))
+    dv = np.zeros((len(keys), groups, dim))
+    cache = {}
+    for i, j in enumerate(keys):
+        j = int(j)
+        s = int(seq[j])
+        a, b = bounds[s], bounds[s + 1]
+        blk = (j - a) // block_size
+        for g in range(groups):
+            for t in range(j, b):
+                if not np.any(ids[t, g] == blk):
+                    continue
+                if (t, g) not in cache:
+                    row = attention_rows(q, k, v, ids, cu, [t], block_size=block_size, scale=scale, dout=do)
+                    cache[(t, g)] = (row["lse"][0], row["delta"][0])
+                lse_t, delta_t = cache[(t, g)]
+                hs = slice(g * ratio, (g + 1) * ratio)
+                logit = q[t, hs] @ k[j, g] * scale  # [R]
+                p = np.exp(logit - lse_t[hs])
+                dp = do[t, hs] @ v[j, g]
+                dk[i, g] += scale * (p * (dp - delta_t[hs])) @ q[t, hs]
+                dv[i, g] += p @ do[t, hs]
+    return dk, dv

@@ -1,0 +1,251 @@
+"""GPU parity of stage 3 (m3_sparse_attention forward + backward) against the FP64 oracle.
+
+Gate: the reference's own, atol=rtol=1e-4 after rounding the FP64 oracle to the
+public dtype (tests/test_triton_attention.py:58-97). Cases mirror
+tests/test_triton_attention.py: the 8 shape cases, empty selection,
+non-contiguous inputs, future-only selections, empty packing, scale/metadata
+errors, the 257-token rounding regression, hot KV rows, slot-order invariance,
+the 7 needs-grad combinations with the CSR spy, fp16/fp32 and GQA=16.
+"""
+
+from __future__ import annotations
+
+import importlib
+
+import numpy as np
+import pytest
+import torch
+
+import msa_triton_amd as msa
+from oracle import msa_oracle as O
+from tests.helpers import attention_inputs, np64
+
+pytestmark = pytest.mark.gpu
+
+
+def _to(device, tensors, indices, cu):
+    return tuple(x.to(device).detach().requires_grad_() for x in tensors), indices.to(device), cu.to(device)
+
+
+def _oracle(tensors, indices, cu, block_size, scale=None, dout=None):
+    return O.sparse_attention(*(np64(x) for x in tensors), indices.cpu().numpy(), cu.cpu().numpy(),
+                              block_size=block_size, scale=scale,
+                              dout=None if dout is None else np64(dout))
+
+
+def _close(actual, expected_np, dtype=torch.bfloat16):
+    torch.testing.assert_close(actual.detach().cpu(), torch.from_numpy(expected_np).to(dtype), atol=1e-4, rtol=1e-4)
+
+
+def _assert_lse(actual, expected):
+    actual = actual.detach().cpu()
+    expected = torch.from_numpy(expected).float()
+    assert torch.equal(torch.isneginf(actual), torch.isneginf(expected))
+    finite = torch.isfinite(expected)
+    torch.testing.assert_close(actual[finite], expected[finite], atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("lengths,groups,ratio,dimension,block_size,topk,scale", [
+    ([1], 1, 1, 5, 128, 1, None),
+    ([7, 3], 2, 2, 8, 3, 3, None),
+    ([17, 5], 3, 1, 16, 8, 2, 0.2),
+    ([129, 1], 1, 2, 8, 128, 3, None),
+    ([127, 128, 257], 1, 1, 8, 128, 3, None),
+    ([5, 1, 9], 2, 4, 32, 4, 4, None),
+    ([5, 3], 2, 2, 128, 4, 2, None),
+    ([0, 3, 0, 2, 0], 2, 2, 8, 2, 2, None),
+])
+def test_forward_backward_against_fp64(lengths, groups, ratio, dimension, block_size, topk, scale, device):
+    cpu, indices, cu = attention_inputs(lengths, groups, ratio, dimension, block_size, topk)
+    tensors, indices_d, cu_d = _to(device, cpu, indices, cu)
+    grad = torch.randn(cpu[0].shape, generator=torch.Generator().manual_seed(5678)).bfloat16()
+    out, lse, dq, dk, dv = _oracle(cpu, indices, cu, block_size, scale, grad)
+    actual, actual_lse = msa.m3_sparse_attention(*tensors, indices_d, cu_d, max(lengths), block_size=block_size,
+                                                 scale=scale, return_lse=True)
+    assert actual.dtype == torch.bfloat16 and actual_lse.dtype == torch.float32 and not actual_lse.requires_grad
+    _close(actual, out)
+    _assert_lse(actual_lse, lse)
+    actual.backward(grad.to(device))
+    for tensor, ref in zip(tensors, (dq, dk, dv)):
+        _close(tensor.grad, ref)
+
+
+@pytest.mark.parametrize("topk", [0, 3])
+def test_empty_selection_has_zero_output_and_gradients(topk, device):
+    cpu, indices, cu = attention_inputs([3, 2], 2, 2, 7, 2, topk)
+    tensors, indices, cu = _to(device, cpu, indices, cu)
+    indices.fill_(-1)
+    output, lse = msa.m3_sparse_attention(*tensors, indices, cu, 3, block_size=2, return_lse=True)
+    assert torch.count_nonzero(output) == 0 and torch.isneginf(lse).all()
+    output.sum().backward()
+    for tensor in tensors:
+        assert tensor.grad is not None and torch.count_nonzero(tensor.grad) == 0
+
+
+def test_noncontiguous_inputs_and_masked_queries(device):
+    cpu, indices, cu = attention_inputs([5, 2], 2, 2, 5, 3, 2)
+    indices[1] = -1
+    tensors, indices_d, cu_d = _to(device, cpu, indices, cu)
+    tensors = tuple(x.detach().transpose(1, 2).contiguous().transpose(1, 2).requires_grad_() for x in tensors)
+    assert not tensors[0].is_contiguous()
+    grad = torch.randn(cpu[0].shape, generator=torch.Generator().manual_seed(73)).bfloat16()
+    out, lse, dq, dk, dv = _oracle(cpu, indices, cu, 3, None, grad)
+    actual, actual_lse = msa.m3_sparse_attention(*tensors, indices_d, cu_d, 5, block_size=3, return_lse=True)
+    _close(actual, out)
+    _assert_lse(actual_lse, lse)
+    actual.backward(grad.to(device))
+    for tensor, ref in zip(tensors, (dq, dk, dv)):
+        _close(tensor.grad, ref)
+    assert torch.count_nonzero(tensors[0].grad[1]) == 0
+
+
+def test_default_return_is_output_tensor(device):
+    cpu, indices, cu = attention_inputs([2], 1, 1, 4, 2, 1)
+    tensors, indices, cu = _to(device, cpu, indices, cu)
+    output = msa.m3_sparse_attention(*tensors, indices, cu, 2, block_size=2)
+    assert isinstance(output, torch.Tensor) and output.shape == tensors[0].shape
+
+
+def test_future_only_selected_blocks_are_safely_masked(device):
+    cpu, indices, cu = attention_inputs([5, 2], 1, 2, 8, 3, 1)
+    indices.fill_(1)
+    tensors, indices_d, cu_d = _to(device, cpu, indices, cu)
+    ones = torch.ones(cpu[0].shape, dtype=torch.bfloat16)
+    out, lse, dq, dk, dv = _oracle(cpu, indices, cu, 3, None, ones)
+    actual, actual_lse = msa.m3_sparse_attention(*tensors, indices_d, cu_d, 5, block_size=3, return_lse=True)
+    _close(actual, out)
+    _assert_lse(actual_lse, lse)
+    actual.sum().backward()
+    for tensor, ref in zip(tensors, (dq, dk, dv)):
+        _close(tensor.grad, ref)
+
+
+def test_empty_packed_input(device):
+    cpu, indices, cu = attention_inputs([0, 0], 1, 2, 8, 4, 1)
+    tensors, indices, cu = _to(device, cpu, indices, cu)
+    output, lse = msa.m3_sparse_attention(*tensors, indices, cu, 4, block_size=4, return_lse=True)
+    assert output.shape == (0, 2, 8) and lse.shape == (0, 2)
+    output.sum().backward()
+    for tensor in tensors:
+        assert tensor.grad is not None and tensor.grad.shape == tensor.shape
+
+
+def test_rejects_invalid_sequence_metadata_on_device(device):
+    cpu, indices, cu = attention_inputs([2], 1, 1, 4, 2, 1)
+    tensors, indices, cu = _to(device, cpu, indices, cu)
+    with pytest.raises(ValueError, match="scale must be finite"):
+        msa.m3_sparse_attention(*tensors, indices, cu, 2, block_size=2, scale=float("nan"))
+    with pytest.raises(ValueError, match="smaller"):
+        msa.m3_sparse_attention(*tensors, indices, cu, 1, block_size=2)
+    cu[-1] = 1
+    with pytest.raises(ValueError, match="end at total_tokens"):
+        msa.m3_sparse_attention(*tensors, indices, cu, 2, block_size=2)
+
+
+def test_long_key_accumulation_bf16_rounding_regression(device):
+    rng = np.random.default_rng(1234)
+    cpu = tuple(torch.from_numpy(rng.standard_normal((512, 1, 8))).float().bfloat16()[255:] for _ in range(3))
+    grad = torch.from_numpy(rng.standard_normal((512, 1, 8))).float().bfloat16()[255:]
+    indices = torch.full((257, 1, 3), -1, dtype=torch.int32)
+    for token in range(257):
+        current = token // 128
+        chosen = [current] + [b for b in range(current) if b % 2 == 0]
+        indices[token, 0, : len(chosen)] = torch.tensor(chosen, dtype=torch.int32)
+    cu = torch.tensor([0, 257], dtype=torch.int32)
+    tensors, indices_d, cu_d = _to(device, cpu, indices, cu)
+    out, _, dq, dk, dv = _oracle(cpu, indices, cu, 128, None, grad)
+    actual = msa.m3_sparse_attention(*tensors, indices_d, cu_d, 257)
+    _close(actual, out)
+    actual.backward(grad.to(device))
+    for tensor, ref in zip(tensors, (dq, dk, dv)):
+        _close(tensor.grad, ref)
+
+
+def test_hot_kv_rows_match_fp64(device):
+    lengths, groups, ratio, dim, block_size = [41, 5], 2, 4, 16, 8
+    cpu, _, cu = attention_inputs(lengths, groups, ratio, dim, block_size, 2)
+    selected = torch.full((sum(lengths), groups, 2), -1, dtype=torch.int32)
+    start = 0
+    for length in lengths:
+        for position in range(length):
+            selected[start + position, 0, 0] = 0
+            selected[start + position, 1, 0] = position // block_size
+        start += length
+    tensors, indices_d, cu_d = _to(device, cpu, selected, cu)
+    grad = torch.randn(cpu[0].shape, generator=torch.Generator().manual_seed(819)).bfloat16()
+    out, _, dq, dk, dv = _oracle(cpu, selected, cu, block_size, None, grad)
+    actual = msa.m3_sparse_attention(*tensors, indices_d, cu_d, max(lengths), block_size=block_size)
+    _close(actual, out)
+    actual.backward(grad.to(device))
+    for tensor, ref in zip(tensors, (dq, dk, dv)):
+        _close(tensor.grad, ref)
+
+
+def test_selected_block_order_preserves_output_and_gradients(device):
+    cpu, indices, cu = attention_inputs([9, 3], 2, 2, 7, 3, 3)
+    reordered = torch.full(indices.shape, -1, dtype=torch.int32)
+    for token in range(indices.shape[0]):
+        for group in range(indices.shape[1]):
+            valid = indices[token, group]
+            valid = valid[valid >= 0].flip(0)
+            reordered[token, group, : valid.numel()] = valid
+    grad = torch.randn(cpu[0].shape, generator=torch.Generator().manual_seed(127)).bfloat16()
+    out, _, dq, dk, dv = _oracle(cpu, indices, cu, 3, None, grad)
+    for selected in (indices, reordered):
+        tensors, sel_d, cu_d = _to(device, cpu, selected, cu)
+        actual = msa.m3_sparse_attention(*tensors, sel_d, cu_d, 9, block_size=3)
+        _close(actual, out)
+        actual.backward(grad.to(device))
+        for tensor, ref in zip(tensors, (dq, dk, dv)):
+            _close(tensor.grad, ref)
+
+
+@pytest.mark.parametrize("needs_grad", [
+    (True, False, False), (False, True, False), (False, False, True),
+    (True, True, False), (True, False, True), (False, True, True), (True, True, True),
+])
+def test_independent_input_gradients_and_q_only_skips_csr(needs_grad, device, monkeypatch):
+    cpu, indices, cu = attention_inputs([0, 5, 0, 3, 0], 2, 2, 8, 3, 2)
+    indices[2] = -1
+    tensors = tuple(x.to(device).detach().requires_grad_(need) for x, need in zip(cpu, needs_grad))
+    saved_inputs = tuple(x.detach().clone() for x in tensors)
+    k2q_module = importlib.import_module("msa_triton_amd.k2q")
+    original_build = k2q_module.build_k2q_csr
+    csr_calls = []
+
+    def checked_build(*args, **kwargs):
+        assert needs_grad[1] or needs_grad[2], "Q-only backward must not build CSR"
+        csr_calls.append(True)
+        return original_build(*args, **kwargs)
+
+    monkeypatch.setattr(k2q_module, "build_k2q_csr", checked_build)
+    grad = torch.randn(cpu[0].shape, generator=torch.Generator().manual_seed(190)).bfloat16()
+    out, _, dq, dk, dv = _oracle(cpu, indices, cu, 3, None, grad)
+    actual = msa.m3_sparse_attention(*tensors, indices.to(device), cu.to(device), 5, block_size=3)
+    _close(actual, out)
+    actual.backward(grad.to(device))
+    assert len(csr_calls) == int(needs_grad[1] or needs_grad[2])
+    for tensor, saved in zip(tensors, saved_inputs):
+        torch.testing.assert_close(tensor.detach(), saved, atol=0, rtol=0)
+    for tensor, ref, need in zip(tensors, (dq, dk, dv), needs_grad):
+        if need:
+            _close(tensor.grad, ref)
+        else:
+            assert tensor.grad is None
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_dtype_and_gqa16_forward_backward_against_fp64(dtype, device):
+    _, indices, cu = attention_inputs([5, 3], 1, 16, 8, 3, 2)
+    generator = torch.Generator().manual_seed(320)
+    shapes = ((8, 16, 8), (8, 1, 8), (8, 1, 8))
+    cpu = tuple(torch.randn(s, generator=generator).to(dtype) for s in shapes)
+    grad = torch.randn(cpu[0].shape, generator=generator).to(dtype)
+    out, lse, dq, dk, dv = _oracle(cpu, indices, cu, 3, None, grad)
+    tensors, indices_d, cu_d = _to(device, cpu, indices, cu)
+    actual, actual_lse = msa.m3_sparse_attention(*tensors, indices_d, cu_d, 5, block_size=3, return_lse=True)
+    _close(actual, out, dtype)
+    _assert_lse(actual_lse, lse)
+    actual.backward(grad.to(device))
+    for tensor, ref in zip(tensors, (dq, dk, dv)):
+        _close(tensor.grad, ref, dtype)

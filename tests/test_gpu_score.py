@@ -1,0 +1,137 @@
+"""GPU parity of stage 1 (m3_index_score) against the CPU oracle.
+
+Forward: scores bit-exact to fl32(scale * exact winning dot), -inf pattern
+exact. Backward: within the reference gate (atol=rtol=1e-4 after rounding the
+FP64 oracle to the input dtype, tests/test_triton_score.py:32-77). Cases
+mirror tests/test_triton_score.py, including the low-bit winner known answers.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import msa_triton_amd as msa
+from oracle import msa_oracle as O
+from tests.helpers import cu_list, cu_tensor
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(q_cpu, k_cpu, lengths, max_seqlen, block_size, scale, upstream, device):
+    q = q_cpu.to(device).clone().requires_grad_()
+    k = k_cpu.to(device).clone().requires_grad_()
+    cu = cu_tensor(lengths, device)
+    actual = msa.m3_index_score(q, k, cu, max_seqlen, block_size=block_size, scale=scale)
+    _, exp32, _ = O.index_score(q_cpu.double().numpy(), k_cpu.double().numpy(), cu_list(lengths), max_seqlen,
+                                block_size=block_size, scale=scale)
+    got = actual.detach().cpu().numpy()
+    assert got.dtype == np.float32
+    np.testing.assert_array_equal(got, exp32)
+    actual.backward(upstream.to(device))
+    dq, dk = O.index_score_backward(q_cpu.double().numpy(), k_cpu.double().numpy(), cu_list(lengths), max_seqlen,
+                                    upstream.double().numpy(), block_size=block_size, scale=scale)
+    dtype = q_cpu.dtype
+    torch.testing.assert_close(q.grad.cpu(), torch.from_numpy(dq).to(dtype), atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(k.grad.cpu(), torch.from_numpy(dk).to(dtype), atol=1e-4, rtol=1e-4)
+    return actual
+
+
+@pytest.mark.parametrize("lengths,groups,dim,block_size,scale", [
+    ([1], 1, 1, 4, 1.0), ([0, 0], 2, 7, 4, 1.0), ([0, 3, 0, 2, 0], 2, 7, 4, 1.0), ([3, 7], 2, 7, 4, 1.0),
+    ([7, 11], 4, 16, 8, 0.5), ([9], 2, 64, 4, 1.0), ([5], 4, 128, 128, 1.0),
+])
+def test_score_forward_backward_fp64(lengths, groups, dim, block_size, scale, device):
+    generator = torch.Generator().manual_seed(731)
+    q_cpu = torch.randn(sum(lengths), groups, dim, generator=generator).to(torch.bfloat16)
+    k_cpu = torch.randn(sum(lengths), 1, dim, generator=generator).to(torch.bfloat16)
+    max_seqlen = max(lengths) + block_size
+    nb = (max_seqlen + block_size - 1) // block_size
+    upstream = torch.randn((sum(lengths), groups, nb), generator=generator).to(torch.bfloat16).float()
+    _run(q_cpu, k_cpu, lengths, max_seqlen, block_size, scale, upstream, device)
+
+
+@pytest.mark.parametrize("lengths", [[127], [128], [129], [1, 129, 257]])
+def test_score_causal_block_and_packing_boundaries(lengths, device):
+    generator = torch.Generator().manual_seed(97)
+    q = torch.randn(sum(lengths), 2, 4, generator=generator).to(torch.bfloat16)
+    k = torch.randn(sum(lengths), 1, 4, generator=generator).to(torch.bfloat16)
+    actual = msa.m3_index_score(q.to(device), k.to(device), cu_tensor(lengths, device), max(lengths), block_size=128)
+    _, exp32, _ = O.index_score(q.double().numpy(), k.double().numpy(), cu_list(lengths), max(lengths), block_size=128)
+    np.testing.assert_array_equal(actual.cpu().numpy(), exp32)
+
+
+@pytest.mark.parametrize("scale", [1.0, 0.0, -1.0])
+def test_score_ties_split_backward_and_invalid_blocks_have_zero_gradient(scale, device):
+    q_cpu = torch.ones(5, 2, 3, dtype=torch.bfloat16)
+    k_cpu = torch.ones(5, 1, 3, dtype=torch.bfloat16)
+    _run(q_cpu, k_cpu, [2, 3], 8, 4, scale, torch.ones(5, 2, 2), device)
+
+
+def test_score_groups_remain_independent(device):
+    q = torch.tensor([[[1., 0.], [0., 1.]]] * 4, dtype=torch.bfloat16, device=device)
+    k = torch.tensor([[[9., 1.]], [[1., 8.]], [[0., 0.]], [[0., 0.]]], dtype=torch.bfloat16, device=device)
+    scores = msa.m3_index_score(q, k, cu_tensor([4], device), 4, block_size=1)
+    assert scores.shape == (4, 2, 4)
+    assert scores[-1, 0].argmax().item() == 0 and scores[-1, 1].argmax().item() == 1
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("scale", [1.0, -1.0, 0.0])
+@pytest.mark.parametrize("case", ["cancellation_unique", "cancellation_tie", "rounded_score_tie"])
+def test_score_winners_retain_low_bits(case, scale, dtype, device):
+    small = 2**-12
+    if case.startswith("cancellation"):
+        query, key0 = [1.0, small, 1.0], [1.0, small, -1.0]
+        key1 = [0.0, small if case.endswith("tie") else 0.0, 0.0]
+    else:
+        query, key0, key1 = [1.0, 1.0], [1.0, 2**-24], [1.0, 0.0]
+    q_cpu = torch.tensor([[query], [query]], dtype=dtype)
+    k_cpu = torch.tensor([[key0], [key1]], dtype=dtype)
+    grad = torch.zeros(2, 1, 1)
+    grad[1] = 1
+    _run(q_cpu, k_cpu, [2], 2, 2, scale, grad, device)
+
+
+@pytest.mark.parametrize("exact_tie", [False, True])
+def test_fp32_product_residual_changes_winner(exact_tie, device):
+    query = [1 + 2**-12, 1.0]
+    q_cpu = torch.tensor([[query], [query]], dtype=torch.float32)
+    k_cpu = torch.tensor([[[1 + 2**-12, -1 - 2**-11]], [[0.0, 2**-24 if exact_tie else 0.0]]], dtype=torch.float32)
+    grad = torch.zeros(2, 1, 1)
+    grad[1] = 1
+    _run(q_cpu, k_cpu, [2], 2, 2, 1.0, grad, device)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_score_dtype_and_packed_backward(dtype, device):
+    generator = torch.Generator().manual_seed(928)
+    q_cpu = torch.randn(6, 2, 7, generator=generator).to(dtype)
+    k_cpu = torch.randn(6, 1, 7, generator=generator).to(dtype)
+    grad = torch.randn((6, 2, 2), generator=generator)
+    _run(q_cpu, k_cpu, [2, 0, 4], 8, 4, 0.3, grad, device)
+
+
+def test_no_grad_with_trainable_inputs_preserves_score_values(device):
+    q = torch.tensor([[[1.0, 2**-12, 1.0]]] * 2, dtype=torch.bfloat16, device=device, requires_grad=True)
+    k = torch.tensor([[[1.0, 2**-12, -1.0]], [[0.0, 0.0, 0.0]]], dtype=torch.bfloat16, device=device,
+                     requires_grad=True)
+    cu = cu_tensor([2], device)
+    trainable = msa.m3_index_score(q, k, cu, 4, block_size=2)
+    with torch.no_grad():
+        inference = msa.m3_index_score(q, k, cu, 4, block_size=2)
+    assert trainable.requires_grad and not inference.requires_grad
+    torch.testing.assert_close(trainable, inference, atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("lengths,groups,dim,block,seed", [
+    ([1280 - 512, 512], 2, 64, 128, 71), ([2048], 4, 128, 128, 3), ([300, 1, 777], 3, 96, 64, 4),
+])
+def test_score_medium_sizes_bit_exact(lengths, groups, dim, block, seed, device):
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(sum(lengths), groups, dim, generator=gen).bfloat16()
+    k = torch.randn(sum(lengths), 1, dim, generator=gen).bfloat16()
+    got = msa.m3_index_score(q.to(device), k.to(device), cu_tensor(lengths, device), max(lengths), block_size=block)
+    _, exp32, _ = O.index_score(q.double().numpy(), k.double().numpy(), cu_list(lengths), max(lengths), block_size=block)
+    np.testing.assert_array_equal(got.cpu().numpy(), exp32)

@@ -1,0 +1,134 @@
+"""GPU parity of stage 2 (m3_topk) and the k2q CSR against the CPU oracle: bit-exact.
+
+Cases mirror tests/test_topk.py and tests/test_k2q.py of the reference, plus
+adversarial ties/-inf rows and BASELINE-sized rows (T=8192..65536 rows).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import msa_triton_amd as msa
+from msa_triton_amd.k2q import build_k2q_csr
+from oracle import msa_oracle as O
+from tests.helpers import cu_list, cu_tensor
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("lengths,block,k,local", [
+    ([1, 7, 3], 2, 3, 1), ([127, 128, 129], 128, 16, 1), ([17, 0, 9], 4, 2, 0), ([8, 5], 2, 3, 3), ([2], 1, 0, 0),
+])
+def test_topk_matches_oracle(lengths, block, k, local, device):
+    groups, blocks = 3, (max(lengths) + block - 1) // block
+    scores_cpu = torch.randn(sum(lengths), groups, blocks, generator=torch.Generator().manual_seed(82))
+    scores = scores_cpu.to(device)
+    saved = scores.clone()
+    cu = cu_tensor(lengths, device)
+    selected = msa.m3_topk(scores, cu, block_size=block, topk_blocks=k, local_blocks=local)
+    assert selected.dtype == torch.int32 and selected.shape == (sum(lengths), groups, k)
+    assert not selected.requires_grad
+    torch.testing.assert_close(scores, saved, atol=0, rtol=0)
+    expected = O.topk(scores_cpu.numpy(), cu_list(lengths), block_size=block, topk_blocks=k, local_blocks=local)
+    np.testing.assert_array_equal(selected.cpu().numpy(), expected)
+
+
+def test_topk_equal_scores_local_and_no_gradient(device):
+    scores = torch.zeros(7, 2, 4, requires_grad=True, device=device)
+    cu = cu_tensor([7], device)
+    out = msa.m3_topk(scores, cu, block_size=2, topk_blocks=2, local_blocks=1)
+    assert not out.requires_grad
+    expected = O.topk(np.zeros((7, 2, 4), np.float32), [0, 7], block_size=2, topk_blocks=2, local_blocks=1)
+    np.testing.assert_array_equal(out.cpu().numpy(), expected)
+
+
+def test_topk_adversarial_ties_infinities_and_wide_rows(device):
+    gen = torch.Generator().manual_seed(5)
+    lengths, block, groups, k = [700, 300], 4, 2, 9
+    nb = (max(lengths) + block - 1) // block
+    scores = torch.randint(-3, 3, (sum(lengths), groups, nb), generator=gen).float()
+    scores[::7] = float("-inf")
+    scores[::11, :, ::3] = float("inf")
+    scores[5::13] = -0.0
+    cu = cu_tensor(lengths, device)
+    for local in (0, 2, 9):
+        got = msa.m3_topk(scores.to(device), cu, block_size=block, topk_blocks=k, local_blocks=local)
+        ref = O.topk(scores.numpy(), cu_list(lengths), block_size=block, topk_blocks=k, local_blocks=local)
+        np.testing.assert_array_equal(got.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("total,groups,nb,k,local", [(8192, 4, 64, 16, 1), (32768, 4, 256, 16, 1), (4096, 8, 512, 32, 2)])
+def test_topk_baseline_sized_rows(total, groups, nb, k, local, device):
+    gen = torch.Generator().manual_seed(total)
+    block = 128 if nb * 128 >= total else 64
+    lengths = [total]
+    scores = torch.randn(total, groups, nb, generator=gen)
+    got = msa.m3_topk(scores.to(device), cu_tensor(lengths, device), block_size=block, topk_blocks=k, local_blocks=local)
+    ref = O.topk(scores.numpy(), cu_list(lengths), block_size=block, topk_blocks=k, local_blocks=local)
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
+
+
+def _check_csr(ids_cpu, lengths, block_size, device):
+    ids = ids_cpu.to(device)
+    original = ids.clone()
+    result = build_k2q_csr(ids, cu_tensor(lengths, device), block_size=block_size)
+    expected = O.k2q_csr(ids_cpu.contiguous().numpy(), cu_list(lengths), block_size=block_size)
+    for actual, exp in zip((result.row_ptr, result.query_indices, result.slot_indices, result.cu_block_lens), expected):
+        assert actual.dtype == torch.int32 and actual.device == ids.device and not actual.requires_grad
+        np.testing.assert_array_equal(actual.cpu().numpy(), exp)
+    torch.testing.assert_close(ids, original, atol=0, rtol=0)
+    return result
+
+
+@pytest.mark.parametrize("lengths,groups,slots,block_size", [
+    ([1], 1, 4, 128), ([3, 5], 3, 5, 2), ([0, 3, 0, 2, 0], 2, 4, 2),
+    ([127, 128, 129], 4, 5, 128), ([0, 0], 3, 5, 128), ([4, 2], 3, 0, 2),
+])
+def test_k2q_matches_oracle(lengths, groups, slots, block_size, device):
+    generator = torch.Generator().manual_seed(951)
+    max_blocks = (max(lengths) + block_size - 1) // block_size
+    ids = torch.randint(-2, max_blocks + 4, (sum(lengths), groups, slots), generator=generator, dtype=torch.int32)
+    _check_csr(ids, lengths, block_size, device)
+
+
+def test_k2q_duplicates_and_block_reset(device):
+    ids = torch.tensor(
+        [[[0, 0, 1], [1, 0, -1]], [[0, -1, 8], [0, 0, 1]], [[1, 0, 1], [0, 1, -2]], [[0, 0, 1], [0, -1, 9]],
+         [[0, 0, -1], [0, 0, -1]]], dtype=torch.int32)
+    result = _check_csr(ids, [3, 2], 2, device)
+    assert result.cu_block_lens.cpu().tolist() == [0, 2, 3]
+    ptr = result.row_ptr.cpu().tolist()
+    assert set(result.query_indices[ptr[4]:ptr[5]].cpu().tolist()) == {3, 4}
+
+
+def test_k2q_hotspots_tail_block_noncontiguous_and_all_invalid(device):
+    lengths, groups, slots, block_size = [9, 5], 4, 3, 4
+    ids = torch.full((sum(lengths), groups, slots), -1, dtype=torch.int32)
+    start = 0
+    for length in lengths:
+        for local in range(length):
+            ids[start + local, :, 0] = local // block_size
+            ids[start + local, :, 1] = 0
+            if local // block_size > 0:
+                ids[start + local, :, 2] = local // block_size - 1
+        start += length
+    _check_csr(ids, lengths, block_size, device)
+    base = torch.tensor([[[0, 1, 2, -1], [0, -1, 9, 0]]] * 5, dtype=torch.int32)
+    _check_csr(base.transpose(1, 2), [2, 3], 2, device)
+    bad = torch.full((7, 2, 4), 99, dtype=torch.int32)
+    bad[:, :, 0] = -1
+    result = _check_csr(bad, [3, 4], 2, device)
+    assert result.row_ptr.count_nonzero().item() == 0
+
+
+@pytest.mark.parametrize("lengths,groups,k,block", [
+    ([8192], 4, 16, 128), ([2048, 3072, 5120, 6144], 4, 16, 128), ([32768], 4, 16, 128),
+])
+def test_k2q_baseline_sized(lengths, groups, k, block, device):
+    gen = torch.Generator().manual_seed(len(lengths))
+    total = sum(lengths)
+    scores = torch.randn(total, groups, (max(lengths) + block - 1) // block, generator=gen)
+    ids = msa.m3_topk(scores.to(device), cu_tensor(lengths, device), block_size=block, topk_blocks=k, local_blocks=1)
+    _check_csr(ids.cpu(), lengths, block, device)

@@ -1,0 +1,160 @@
+"""Pin the stage-1 oracle (oracle.msa_oracle.index_score / index_score_backward).
+
+Checks: the reference's known answers (tests/test_eager.py:143-152,
+tests/test_triton_score.py:111-182, docs/code_review_response.md:33-41), exact
+rational brute force for the public fp32 rounding, and torch float64 autograd
+of an independently written amax formulation for the subgradient.
+"""
+
+from __future__ import annotations
+
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import msa_oracle as O
+from tests.helpers import cu_list
+
+
+def _grads(q, k, cu, max_seqlen, block_size, scale, upstream):
+    dq, dk = O.index_score_backward(q, k, cu, max_seqlen, upstream, block_size=block_size, scale=scale)
+    return dq, dk
+
+
+def test_ties_split_gradient_and_future_mask_is_zero():
+    # tests/test_eager.py:143-152
+    q = np.ones((3, 1, 1))
+    k = np.ones((3, 1, 1))
+    cu = [0, 3]
+    s64, s32, tie = O.index_score(q, k, cu, 4, block_size=4)
+    assert s32.shape == (3, 1, 1)
+    ds = np.zeros((3, 1, 1))
+    ds[-1] = 1.0
+    dq, dk = _grads(q, k, cu, 4, 4, 1.0, ds)
+    np.testing.assert_array_equal(dq[:, 0, 0], [0.0, 0.0, 1.0])
+    np.testing.assert_allclose(dk[:, 0, 0], [1 / 3] * 3, rtol=0, atol=1e-15)
+    assert tie[-1, 0, 0] == -3 and tie[0, 0, 0] == 1
+    ds = np.zeros((3, 1, 1))
+    ds[0] = 1.0
+    _, dk = _grads(q, k, cu, 4, 4, 1.0, ds)
+    np.testing.assert_array_equal(dk[:, 0, 0], [1.0, 0.0, 0.0])
+
+
+@pytest.mark.parametrize("exact_tie", [False, True])
+def test_cancellation_known_answers(exact_tie):
+    # docs/code_review_response.md:26-41: score[1] = 2^-24 with a unique winner,
+    # dQ[1] = [1, 2^-12, -1], dK[0] = [1, 2^-12, 1]; with k1 = [0, 2^-12, 0] an exact tie.
+    small = 2.0**-12
+    q = np.array([[[1.0, small, 1.0]], [[1.0, small, 1.0]]])
+    k1 = [0.0, small, 0.0] if exact_tie else [0.0, 0.0, 0.0]
+    k = np.array([[[1.0, small, -1.0]], [k1]])
+    s64, s32, tie = O.index_score(q, k, [0, 2], 2, block_size=2)
+    if exact_tie:
+        assert s32[1, 0, 0] == np.float32(2.0**-24) and tie[1, 0, 0] == -2
+    else:
+        assert s32[1, 0, 0] == np.float32(5.960464477539063e-08) and tie[1, 0, 0] == 1
+    ds = np.zeros((2, 1, 1))
+    ds[1] = 1.0
+    dq, dk = _grads(q, k, [0, 2], 2, 2, 1.0, ds)
+    if exact_tie:
+        np.testing.assert_array_equal(dq[1, 0], [0.5, 0.5 * small + 0.5 * small, -0.5])
+        np.testing.assert_array_equal(dk[:, 0], [[0.5, 0.5 * small, 0.5], [0.5, 0.5 * small, 0.5]])
+    else:
+        np.testing.assert_array_equal(dq[1, 0], [1.0, small, -1.0])
+        np.testing.assert_array_equal(dk[:, 0], [[1.0, small, 1.0], [0.0, 0.0, 0.0]])
+
+
+def test_rounded_score_tie_has_unique_exact_winner():
+    # tests/test_triton_score.py:145-146: both public scores round to 1.0 in fp32,
+    # the exact winner is unique (key0).
+    q = np.array([[[1.0, 1.0]], [[1.0, 1.0]]])
+    k = np.array([[[1.0, 2.0**-24]], [[1.0, 0.0]]])
+    _, s32, tie = O.index_score(q, k, [0, 2], 2, block_size=2)
+    assert s32[1, 0, 0] == np.float32(1.0) and tie[1, 0, 0] == 1
+
+
+def test_groups_remain_independent():
+    # tests/test_triton_score.py:111-120
+    q = np.array([[[1.0, 0.0], [0.0, 1.0]]] * 4)
+    k = np.array([[[9.0, 1.0]], [[1.0, 8.0]], [[0.0, 0.0]], [[0.0, 0.0]]])
+    _, s32, _ = O.index_score(q, k, [0, 4], 4, block_size=1)
+    assert s32.shape == (4, 2, 4)
+    assert s32[-1, 0].argmax() == 0 and s32[-1, 1].argmax() == 1
+
+
+@pytest.mark.parametrize("scale", [1.0, -1.0, 0.0, 0.3])
+def test_public_score_is_correctly_rounded_exact_max(scale):
+    """Brute force with exact rationals: fl32(max_j scale * dot) for random bf16 data."""
+    gen = torch.Generator().manual_seed(7)
+    lengths, groups, dim, block = [5, 7], 2, 9, 3
+    q = torch.randn(sum(lengths), groups, dim, generator=gen).bfloat16().double().numpy()
+    k = torch.randn(sum(lengths), 1, dim, generator=gen).bfloat16().double().numpy()
+    cu = cu_list(lengths)
+    _, s32, tie = O.index_score(q, k, cu, 8, block_size=block, scale=scale)
+    sc = Fraction(scale)
+    for a, b in zip(cu[:-1], cu[1:]):
+        for t in range(a, b):
+            for g in range(groups):
+                for blk in range(s32.shape[2]):
+                    keys = [j for j in range(a + blk * block, min(a + (blk + 1) * block, b)) if j <= t]
+                    if not keys:
+                        assert s32[t, g, blk] == -np.inf and tie[t, g, blk] == 0
+                        continue
+                    exact = [sc * sum(Fraction(x) * Fraction(y) for x, y in zip(q[t, g], k[j, 0])) for j in keys]
+                    best = max(exact)
+                    expected = _round_f32(best)
+                    assert s32[t, g, blk] == expected
+                    winners = [i for i, e in enumerate(exact) if e == best]
+                    code = winners[0] + 1 if len(winners) == 1 else -len(winners)
+                    assert tie[t, g, blk] == code
+
+
+def _round_f32(x: Fraction) -> np.float32:
+    """Correctly rounded fp32 of an exact rational (ties to even)."""
+    guess = np.float32(float(x))
+    candidates = [np.nextafter(guess, np.float32(-np.inf)), guess, np.nextafter(guess, np.float32(np.inf))]
+    best = min(candidates, key=lambda c: (abs(Fraction(float(c)) - x), int(np.float32(c).view(np.int32)) & 1))
+    return np.float32(best)
+
+
+def _torch_amax_reference(q, k, cu, max_seqlen, block_size, scale):
+    """Independent dense formulation differentiated by torch float64 autograd."""
+    total, groups, dim = q.shape
+    nb = (max_seqlen + block_size - 1) // block_size
+    cols = []
+    for a, b in zip(cu[:-1], cu[1:]):
+        n = b - a
+        logits = torch.einsum("tgd,kd->tgk", q[a:b], k[a:b, 0]) * scale  # [n, G, n]
+        pos = torch.arange(n)
+        causal = pos[None, :] <= pos[:, None]
+        masked = logits.masked_fill(~causal[:, None, :], float("-inf"))
+        pad = nb * block_size - n
+        masked = torch.nn.functional.pad(masked, (0, pad), value=float("-inf"))
+        cols.append(masked.reshape(n, groups, nb, block_size).amax(-1))
+    return torch.cat(cols)
+
+
+@pytest.mark.parametrize("lengths,groups,dim,block_size,scale", [
+    ([3, 7], 2, 7, 4, 1.0), ([7, 11], 4, 16, 8, 0.5), ([9], 2, 64, 4, 1.0), ([0, 3, 0, 2, 0], 2, 7, 4, 1.0),
+    ([6, 5], 2, 5, 4, -1.0),
+])
+def test_backward_matches_torch_amax_autograd(lengths, groups, dim, block_size, scale):
+    gen = torch.Generator().manual_seed(731)
+    total = sum(lengths)
+    q = torch.randn(total, groups, dim, generator=gen).bfloat16().double().requires_grad_()
+    k = torch.randn(total, 1, dim, generator=gen).bfloat16().double().requires_grad_()
+    cu = cu_list(lengths)
+    max_seqlen = max(lengths) + block_size
+    ref = _torch_amax_reference(q, k, cu, max_seqlen, block_size, scale)
+    s64, _, _ = O.index_score(q.detach().numpy(), k.detach().numpy(), cu, max_seqlen, block_size=block_size, scale=scale)
+    finite = torch.isfinite(ref)
+    np.testing.assert_array_equal(np.isfinite(s64), finite.numpy())
+    np.testing.assert_allclose(s64[np.isfinite(s64)], ref[finite].detach().numpy(), rtol=1e-13, atol=1e-13)
+    upstream = torch.randn(ref.shape, generator=gen).double()
+    ref.backward(upstream.masked_fill(~finite, 0))
+    dq, dk = O.index_score_backward(q.detach().numpy(), k.detach().numpy(), cu, max_seqlen,
+                                    upstream.numpy(), block_size=block_size, scale=scale)
+    np.testing.assert_allclose(dq, q.grad.numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(dk, k.grad.numpy(), rtol=1e-12, atol=1e-12)
