@@ -77,21 +77,25 @@ int msa_score_bwd(const void* index_q, const void* index_k, int32_t dtype,
  * Replaces triton/sparse_attention.py:35-84 (_forward_kernel; launch :336-359).
  * out [T,Hq,D] in the input dtype; lse [T,Hq] fp32 (natural log, -inf for rows
  * without keys, whose output is 0). Slots with id < 0 or id > qb(t) are ignored;
- * keys after the query inside its own block are masked. */
+ * keys after the query inside its own block are masked.
+ * row_state (nullable): private fp64 [T,Hq,4] consumed by the backward; slot 0
+ * receives the full-precision lse (the reference keeps (max, denominator),
+ * sparse_attention.py:83-84). */
 int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t dtype, const int32_t* indices,
                  const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
                  int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
-                 int64_t block_size, double scale, void* out, float* lse, void* stream);
+                 int64_t block_size, double scale, void* out, float* lse, double* row_state,
+                 void* stream);
 
-/* Stage 3 backward, query pass: dQ (nullable) and per-(t,h) statistics
- * stats [T,Hq,3] fp32 = (probability mass, center, centered delta) consumed by
- * the KV pass. Replaces sparse_attention.py:87-198 (_backward_kernel with
+/* Stage 3 backward, query pass: dQ (nullable) and the per-(t,h) statistics
+ * row_state[...,1:4] = (probability mass, center O.dO, centered delta) consumed
+ * by the KV pass. Replaces sparse_attention.py:87-198 (_backward_kernel with
  * ACCUMULATE_KV=False; launch :376-385). */
 int msa_attn_bwd_dq(const void* q, const void* k, const void* v, int32_t dtype, const void* out,
-                    const void* grad_out, const float* lse, const int32_t* indices,
+                    const void* grad_out, double* row_state, const int32_t* indices,
                     const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
                     int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
-                    int64_t block_size, double scale, void* grad_q, float* stats, void* stream);
+                    int64_t block_size, double scale, void* grad_q, void* stream);
 
 /* Stage 3 backward workspace in bytes for msa_attn_bwd_dkdv. */
 int64_t msa_attn_bwd_workspace_bytes(int64_t total_tokens, int64_t q_heads, int64_t kv_groups,
@@ -102,12 +106,12 @@ int64_t msa_attn_bwd_workspace_bytes(int64_t total_tokens, int64_t q_heads, int6
  * row of the k2q CSR, no floating-point atomics. Replaces
  * sparse_attention.py:223-295 (_backward_kv_kernel; launch :386-393). */
 int msa_attn_bwd_dkdv(const void* q, const void* k, const void* v, int32_t dtype,
-                      const void* grad_out, const float* lse, const float* stats,
-                      const int32_t* cu_seqlens, const int32_t* cu_block_lens,
-                      const int32_t* row_ptr, const int32_t* query_indices, int64_t num_seqs,
-                      int64_t total_tokens, int64_t q_heads, int64_t kv_groups, int64_t head_dim,
-                      int64_t total_blocks, int64_t block_size, double scale, void* grad_k,
-                      void* grad_v, void* workspace, int64_t workspace_bytes, void* stream);
+                      const void* grad_out, const double* row_state, const int32_t* cu_seqlens,
+                      const int32_t* cu_block_lens, const int32_t* row_ptr,
+                      const int32_t* query_indices, int64_t num_seqs, int64_t total_tokens,
+                      int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t total_blocks,
+                      int64_t block_size, double scale, void* grad_k, void* grad_v, void* workspace,
+                      int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -8,15 +8,14 @@ namespace msa {
 
 template <int DT>
 int attn_fwd_valu_dispatch(const void*, const void*, const void*, const int32_t*, const int32_t*, int, int64_t, int,
-                           int, int, int, int, double, void*, float*, hipStream_t);
+                           int, int, int, int, double, void*, float*, double*, hipStream_t);
 template <int DT>
-int attn_dq_valu_dispatch(const void*, const void*, const void*, const void*, const void*, const float*,
-                          const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*,
-                          float*, hipStream_t);
+int attn_dq_valu_dispatch(const void*, const void*, const void*, const void*, const void*, double*, const int32_t*,
+                          const int32_t*, int, int64_t, int, int, int, int, int, double, void*, hipStream_t);
 template <int DT>
-int attn_dkdv_valu_dispatch(const void*, const void*, const void*, const void*, const float*, const float*,
-                            const int32_t*, const int32_t*, const int32_t*, const int32_t*, int, int64_t, int, int,
-                            int, int, double, void*, void*, hipStream_t);
+int attn_dkdv_valu_dispatch(const void*, const void*, const void*, const void*, const double*, const int32_t*,
+                            const int32_t*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, double,
+                            void*, void*, hipStream_t);
 
 static bool valid_common(int64_t num_seqs, int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t B) {
   return num_seqs > 0 && T >= 0 && Hq > 0 && G > 0 && Hq % G == 0 && D > 0 && B > 0;
@@ -29,7 +28,7 @@ using namespace msa;
 extern "C" int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t dtype, const int32_t* indices,
                             const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens, int64_t q_heads,
                             int64_t kv_groups, int64_t head_dim, int64_t topk_slots, int64_t block_size,
-                            double scale, void* out, float* lse, void* stream) {
+                            double scale, void* out, float* lse, double* row_state, void* stream) {
   if (!valid_common(num_seqs, total_tokens, q_heads, kv_groups, head_dim, block_size) || topk_slots < 0)
     return kErrInvalidArgument;
   if (total_tokens == 0) return kOk;
@@ -37,39 +36,39 @@ extern "C" int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nseq = static_cast<int>(num_seqs), Hq = static_cast<int>(q_heads), G = static_cast<int>(kv_groups);
   const int D = static_cast<int>(head_dim), K = static_cast<int>(topk_slots), B = static_cast<int>(block_size);
-  const float sc = static_cast<float>(scale);
-  if (dtype == kBF16 && attn_mfma_supported(Hq / G, D)) {
-    return attn_fwd_mfma(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, sc, out, lse, st);
+  if (dtype == kBF16 && attn_mfma_supported(Hq / G, D, B)) {
+    return attn_fwd_mfma(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, static_cast<float>(scale),
+                         out, lse, row_state, st);
   }
   switch (dtype) {
-    case kF32: return attn_fwd_valu_dispatch<kF32>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, st);
-    case kF16: return attn_fwd_valu_dispatch<kF16>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, st);
-    case kBF16: return attn_fwd_valu_dispatch<kBF16>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, st);
+    case kF32: return attn_fwd_valu_dispatch<kF32>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, row_state, st);
+    case kF16: return attn_fwd_valu_dispatch<kF16>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, row_state, st);
+    case kBF16: return attn_fwd_valu_dispatch<kBF16>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, row_state, st);
     default: return kErrInvalidArgument;
   }
 }
 
 extern "C" int msa_attn_bwd_dq(const void* q, const void* k, const void* v, int32_t dtype, const void* out,
-                               const void* grad_out, const float* lse, const int32_t* indices,
+                               const void* grad_out, double* row_state, const int32_t* indices,
                                const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens, int64_t q_heads,
                                int64_t kv_groups, int64_t head_dim, int64_t topk_slots, int64_t block_size,
-                               double scale, void* grad_q, float* stats, void* stream) {
-  if (!valid_common(num_seqs, total_tokens, q_heads, kv_groups, head_dim, block_size) || topk_slots < 0)
+                               double scale, void* grad_q, void* stream) {
+  if (!valid_common(num_seqs, total_tokens, q_heads, kv_groups, head_dim, block_size) || topk_slots < 0 ||
+      row_state == nullptr)
     return kErrInvalidArgument;
   if (total_tokens == 0) return kOk;
   if (head_dim > 512) return kErrUnsupported;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nseq = static_cast<int>(num_seqs), Hq = static_cast<int>(q_heads), G = static_cast<int>(kv_groups);
   const int D = static_cast<int>(head_dim), K = static_cast<int>(topk_slots), B = static_cast<int>(block_size);
-  const float sc = static_cast<float>(scale);
-  if (dtype == kBF16 && attn_mfma_supported(Hq / G, D)) {
-    return attn_bwd_dq_mfma(q, k, v, out, grad_out, lse, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, sc,
-                            grad_q, stats, st);
+  if (dtype == kBF16 && attn_mfma_supported(Hq / G, D, B)) {
+    return attn_bwd_dq_mfma(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B,
+                            static_cast<float>(scale), grad_q, st);
   }
   switch (dtype) {
-    case kF32: return attn_dq_valu_dispatch<kF32>(q, k, v, out, grad_out, lse, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, stats, st);
-    case kF16: return attn_dq_valu_dispatch<kF16>(q, k, v, out, grad_out, lse, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, stats, st);
-    case kBF16: return attn_dq_valu_dispatch<kBF16>(q, k, v, out, grad_out, lse, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, stats, st);
+    case kF32: return attn_dq_valu_dispatch<kF32>(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, st);
+    case kF16: return attn_dq_valu_dispatch<kF16>(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, st);
+    case kBF16: return attn_dq_valu_dispatch<kBF16>(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, st);
     default: return kErrInvalidArgument;
   }
 }
@@ -78,35 +77,34 @@ extern "C" int64_t msa_attn_bwd_workspace_bytes(int64_t total_tokens, int64_t q_
                                                 int64_t head_dim, int64_t topk_slots, int64_t total_blocks,
                                                 int64_t block_size) {
   if (q_heads <= 0 || kv_groups <= 0 || q_heads % kv_groups) return 256;
-  if (!attn_mfma_supported(q_heads / kv_groups, head_dim)) return 256;
+  if (!attn_mfma_supported(q_heads / kv_groups, head_dim, block_size)) return 256;
   return attn_dkdv_mfma_workspace_bytes(total_tokens, q_heads, kv_groups, head_dim, topk_slots, total_blocks,
                                         block_size);
 }
 
 extern "C" int msa_attn_bwd_dkdv(const void* q, const void* k, const void* v, int32_t dtype, const void* grad_out,
-                                 const float* lse, const float* stats, const int32_t* cu_seqlens,
-                                 const int32_t* cu_block_lens, const int32_t* row_ptr, const int32_t* query_indices,
-                                 int64_t num_seqs, int64_t total_tokens, int64_t q_heads, int64_t kv_groups,
-                                 int64_t head_dim, int64_t total_blocks, int64_t block_size, double scale,
-                                 void* grad_k, void* grad_v, void* workspace, int64_t workspace_bytes,
-                                 void* stream) {
-  if (!valid_common(num_seqs, total_tokens, q_heads, kv_groups, head_dim, block_size) || total_blocks < 0)
+                                 const double* row_state, const int32_t* cu_seqlens, const int32_t* cu_block_lens,
+                                 const int32_t* row_ptr, const int32_t* query_indices, int64_t num_seqs,
+                                 int64_t total_tokens, int64_t q_heads, int64_t kv_groups, int64_t head_dim,
+                                 int64_t total_blocks, int64_t block_size, double scale, void* grad_k, void* grad_v,
+                                 void* workspace, int64_t workspace_bytes, void* stream) {
+  if (!valid_common(num_seqs, total_tokens, q_heads, kv_groups, head_dim, block_size) || total_blocks < 0 ||
+      row_state == nullptr)
     return kErrInvalidArgument;
   if (total_tokens == 0 || (!grad_k && !grad_v)) return kOk;
   if (head_dim > 512) return kErrUnsupported;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nseq = static_cast<int>(num_seqs), Hq = static_cast<int>(q_heads), G = static_cast<int>(kv_groups);
   const int D = static_cast<int>(head_dim), B = static_cast<int>(block_size);
-  const float sc = static_cast<float>(scale);
-  if (dtype == kBF16 && attn_mfma_supported(Hq / G, D)) {
-    return attn_bwd_dkdv_mfma(q, k, v, grad_out, lse, stats, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq,
-                              total_tokens, Hq, G, D, total_blocks, B, sc, grad_k, grad_v, workspace,
-                              workspace_bytes, st);
+  if (dtype == kBF16 && attn_mfma_supported(Hq / G, D, B)) {
+    return attn_bwd_dkdv_mfma(q, k, v, grad_out, row_state, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq,
+                              total_tokens, Hq, G, D, total_blocks, B, static_cast<float>(scale), grad_k, grad_v,
+                              workspace, workspace_bytes, st);
   }
   switch (dtype) {
-    case kF32: return attn_dkdv_valu_dispatch<kF32>(q, k, v, grad_out, lse, stats, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq, total_tokens, Hq, G, D, B, scale, grad_k, grad_v, st);
-    case kF16: return attn_dkdv_valu_dispatch<kF16>(q, k, v, grad_out, lse, stats, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq, total_tokens, Hq, G, D, B, scale, grad_k, grad_v, st);
-    case kBF16: return attn_dkdv_valu_dispatch<kBF16>(q, k, v, grad_out, lse, stats, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq, total_tokens, Hq, G, D, B, scale, grad_k, grad_v, st);
+    case kF32: return attn_dkdv_valu_dispatch<kF32>(q, k, v, grad_out, row_state, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq, total_tokens, Hq, G, D, B, scale, grad_k, grad_v, st);
+    case kF16: return attn_dkdv_valu_dispatch<kF16>(q, k, v, grad_out, row_state, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq, total_tokens, Hq, G, D, B, scale, grad_k, grad_v, st);
+    case kBF16: return attn_dkdv_valu_dispatch<kBF16>(q, k, v, grad_out, row_state, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq, total_tokens, Hq, G, D, B, scale, grad_k, grad_v, st);
     default: return kErrInvalidArgument;
   }
 }

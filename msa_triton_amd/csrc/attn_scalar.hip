@@ -42,7 +42,8 @@ __global__ __launch_bounds__(256) void attn_fwd_valu(const void* __restrict__ q,
                                                      const int32_t* __restrict__ indices,
                                                      const int32_t* __restrict__ cu, int nseq, int64_t T,
                                                      int Hq, int G, int D, int K, int B, double scale,
-                                                     void* __restrict__ out, float* __restrict__ lse) {
+                                                     void* __restrict__ out, float* __restrict__ lse,
+                                                     double* __restrict__ row_state) {
   extern __shared__ float smem[];
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t th = static_cast<int64_t>(blockIdx.x) * 4 + wid;
@@ -100,16 +101,20 @@ __global__ __launch_bounds__(256) void attn_fwd_valu(const void* __restrict__ q,
     const int d = lane + j * kWave;
     if (d < D) store_from_f32<DT>(out, th * D + d, l > 0.0 ? static_cast<float>(o[j] / l) : 0.f);
   }
-  if (lane == 0) lse[th] = l > 0.0 ? static_cast<float>(m + log(l)) : -__builtin_inff();
+  if (lane == 0) {
+    const double full = l > 0.0 ? m + log(l) : -__builtin_inf();
+    lse[th] = static_cast<float>(full);
+    if (row_state) row_state[th * 4] = full;
+  }
 }
 
 // Query-pass backward: one wavefront per (t, h).
 template <int DT, int DPL>
 __global__ __launch_bounds__(256) void attn_bwd_dq_valu(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
-    const void* __restrict__ out, const void* __restrict__ dout, const float* __restrict__ lse,
+    const void* __restrict__ out, const void* __restrict__ dout, double* __restrict__ row_state,
     const int32_t* __restrict__ indices, const int32_t* __restrict__ cu, int nseq, int64_t T, int Hq, int G,
-    int D, int K, int B, double scale, void* __restrict__ dq, float* __restrict__ stats) {
+    int D, int K, int B, double scale, void* __restrict__ dq) {
   extern __shared__ float smem[];
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t th = static_cast<int64_t>(blockIdx.x) * 4 + wid;
@@ -132,7 +137,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_valu(
   const int g = h / (Hq / G);
   const RowCtx rc = row_ctx(cu, nseq, t, B);
   const double c = wave_sum_f64(cpart);
-  const double row_lse = lse[th];
+  const double row_lse = row_state[th * 4];
   double mass = 0.0, delta = 0.0;
   double a[DPL], bsum[DPL];
 #pragma unroll
@@ -191,10 +196,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_valu(
       }
     }
   }
-  if (lane == 0 && stats) {
-    stats[th * 3 + 0] = has ? static_cast<float>(msum) : 1.f;
-    stats[th * 3 + 1] = static_cast<float>(c);
-    stats[th * 3 + 2] = static_cast<float>(dhat);
+  if (lane == 0) {
+    row_state[th * 4 + 1] = has ? msum : 1.0;
+    row_state[th * 4 + 2] = c;
+    row_state[th * 4 + 3] = dhat;
   }
 }
 
@@ -203,8 +208,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_valu(
 template <int DT, int DPL>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_valu(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
-    const void* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ stats,
-    const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ row_ptr,
+    const void* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ row_ptr,
     const int32_t* __restrict__ qidx, int nseq, int64_t T, int Hq, int G, int D, int B, double scale,
     void* __restrict__ dk, void* __restrict__ dv) {
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -243,8 +247,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_valu(
       }
       sp = wave_sum_f64(sp);
       dp = wave_sum_f64(dp);
-      const double mass = stats[th * 3 + 0], c = stats[th * 3 + 1], dhat = stats[th * 3 + 2];
-      const double p = exp(sp * scale - static_cast<double>(lse[th])) / mass;
+      const double* rs = row_state + th * 4;
+      const double mass = rs[1], c = rs[2], dhat = rs[3];
+      const double p = exp(sp * scale - rs[0]) / mass;
       const double dsv = p * ((dp - c) - dhat) * scale;
 #pragma unroll
       for (int i = 0; i < DPL; ++i) {
@@ -266,70 +271,74 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_valu(
 template <int DT, int DPL>
 int attn_valu_launch_fwd(const void* q, const void* k, const void* v, const int32_t* idx, const int32_t* cu,
                          int nseq, int64_t T, int Hq, int G, int D, int K, int B, double scale, void* out,
-                         float* lse, hipStream_t st) {
+                         float* lse, double* rs, hipStream_t st) {
   hipLaunchKernelGGL((attn_fwd_valu<DT, DPL>), dim3(grid_1d(T * Hq, 4)), dim3(256), 4 * D * sizeof(float), st, q,
-                     k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse);
+                     k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse, rs);
   return status_from(hipGetLastError());
 }
 
 template <int DT, int DPL>
-int attn_valu_launch_dq(const void* q, const void* k, const void* v, const void* out, const void* dout,
-                        const float* lse, const int32_t* idx, const int32_t* cu, int nseq, int64_t T, int Hq,
-                        int G, int D, int K, int B, double scale, void* dq, float* stats, hipStream_t st) {
+int attn_valu_launch_dq(const void* q, const void* k, const void* v, const void* out, const void* dout, double* rs,
+                        const int32_t* idx, const int32_t* cu, int nseq, int64_t T, int Hq, int G, int D, int K,
+                        int B, double scale, void* dq, hipStream_t st) {
   hipLaunchKernelGGL((attn_bwd_dq_valu<DT, DPL>), dim3(grid_1d(T * Hq, 4)), dim3(256), 8 * D * sizeof(float),
-                     st, q, k, v, out, dout, lse, idx, cu, nseq, T, Hq, G, D, K, B, scale, dq, stats);
+                     st, q, k, v, out, dout, rs, idx, cu, nseq, T, Hq, G, D, K, B, scale, dq);
   return status_from(hipGetLastError());
 }
 
 template <int DT, int DPL>
-int attn_valu_launch_dkdv(const void* q, const void* k, const void* v, const void* dout, const float* lse,
-                          const float* stats, const int32_t* cu, const int32_t* cu_blocks, const int32_t* row_ptr,
-                          const int32_t* qidx, int nseq, int64_t T, int Hq, int G, int D, int B, double scale,
-                          void* dk, void* dv, hipStream_t st) {
-  hipLaunchKernelGGL((attn_bwd_dkdv_valu<DT, DPL>), dim3(grid_1d(T * G, 4)), dim3(256), 0, st, q, k, v, dout,
-                     lse, stats, cu, cu_blocks, row_ptr, qidx, nseq, T, Hq, G, D, B, scale, dk, dv);
+int attn_valu_launch_dkdv(const void* q, const void* k, const void* v, const void* dout, const double* rs,
+                          const int32_t* cu, const int32_t* cu_blocks, const int32_t* row_ptr, const int32_t* qidx,
+                          int nseq, int64_t T, int Hq, int G, int D, int B, double scale, void* dk, void* dv,
+                          hipStream_t st) {
+  hipLaunchKernelGGL((attn_bwd_dkdv_valu<DT, DPL>), dim3(grid_1d(T * G, 4)), dim3(256), 0, st, q, k, v, dout, rs,
+                     cu, cu_blocks, row_ptr, qidx, nseq, T, Hq, G, D, B, scale, dk, dv);
   return status_from(hipGetLastError());
 }
 
-#define MSA_DPL_DISPATCH(D, FN, ...)                     \
-  ((D) <= 64    ? FN<DT, 1>(__VA_ARGS__)                 \
-   : (D) <= 128 ? FN<DT, 2>(__VA_ARGS__)                 \
-   : (D) <= 256 ? FN<DT, 4>(__VA_ARGS__)                 \
+#define MSA_DPL_DISPATCH(D, FN, ...)     \
+  ((D) <= 64    ? FN<DT, 1>(__VA_ARGS__) \
+   : (D) <= 128 ? FN<DT, 2>(__VA_ARGS__) \
+   : (D) <= 256 ? FN<DT, 4>(__VA_ARGS__) \
                 : FN<DT, 8>(__VA_ARGS__))
 
 template <int DT>
 int attn_fwd_valu_dispatch(const void* q, const void* k, const void* v, const int32_t* idx, const int32_t* cu,
                            int nseq, int64_t T, int Hq, int G, int D, int K, int B, double scale, void* out,
-                           float* lse, hipStream_t st) {
-  return MSA_DPL_DISPATCH(D, attn_valu_launch_fwd, q, k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse, st);
+                           float* lse, double* rs, hipStream_t st) {
+  return MSA_DPL_DISPATCH(D, attn_valu_launch_fwd, q, k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse, rs,
+                          st);
 }
 
 template <int DT>
-int attn_dq_valu_dispatch(const void* q, const void* k, const void* v, const void* out, const void* dout,
-                          const float* lse, const int32_t* idx, const int32_t* cu, int nseq, int64_t T, int Hq,
-                          int G, int D, int K, int B, double scale, void* dq, float* stats, hipStream_t st) {
-  return MSA_DPL_DISPATCH(D, attn_valu_launch_dq, q, k, v, out, dout, lse, idx, cu, nseq, T, Hq, G, D, K, B, scale,
-                          dq, stats, st);
+int attn_dq_valu_dispatch(const void* q, const void* k, const void* v, const void* out, const void* dout, double* rs,
+                          const int32_t* idx, const int32_t* cu, int nseq, int64_t T, int Hq, int G, int D, int K,
+                          int B, double scale, void* dq, hipStream_t st) {
+  return MSA_DPL_DISPATCH(D, attn_valu_launch_dq, q, k, v, out, dout, rs, idx, cu, nseq, T, Hq, G, D, K, B, scale,
+                          dq, st);
 }
 
 template <int DT>
-int attn_dkdv_valu_dispatch(const void* q, const void* k, const void* v, const void* dout, const float* lse,
-                            const float* stats, const int32_t* cu, const int32_t* cu_blocks,
-                            const int32_t* row_ptr, const int32_t* qidx, int nseq, int64_t T, int Hq, int G, int D,
-                            int B, double scale, void* dk, void* dv, hipStream_t st) {
-  return MSA_DPL_DISPATCH(D, attn_valu_launch_dkdv, q, k, v, dout, lse, stats, cu, cu_blocks, row_ptr, qidx, nseq,
-                          T, Hq, G, D, B, scale, dk, dv, st);
+int attn_dkdv_valu_dispatch(const void* q, const void* k, const void* v, const void* dout, const double* rs,
+                            const int32_t* cu, const int32_t* cu_blocks, const int32_t* row_ptr, const int32_t* qidx,
+                            int nseq, int64_t T, int Hq, int G, int D, int B, double scale, void* dk, void* dv,
+                            hipStream_t st) {
+  return MSA_DPL_DISPATCH(D, attn_valu_launch_dkdv, q, k, v, dout, rs, cu, cu_blocks, row_ptr, qidx, nseq, T, Hq, G,
+                          D, B, scale, dk, dv, st);
 }
 
-// Explicit instantiations used by attn_api.hip.
-template int attn_fwd_valu_dispatch<kF32>(const void*, const void*, const void*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
-template int attn_fwd_valu_dispatch<kF16>(const void*, const void*, const void*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
-template int attn_fwd_valu_dispatch<kBF16>(const void*, const void*, const void*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
-template int attn_dq_valu_dispatch<kF32>(const void*, const void*, const void*, const void*, const void*, const float*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
-template int attn_dq_valu_dispatch<kF16>(const void*, const void*, const void*, const void*, const void*, const float*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
-template int attn_dq_valu_dispatch<kBF16>(const void*, const void*, const void*, const void*, const void*, const float*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int, double, void*, float*, hipStream_t);
-template int attn_dkdv_valu_dispatch<kF32>(const void*, const void*, const void*, const void*, const float*, const float*, const int32_t*, const int32_t*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, double, void*, void*, hipStream_t);
-template int attn_dkdv_valu_dispatch<kF16>(const void*, const void*, const void*, const void*, const float*, const float*, const int32_t*, const int32_t*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, double, void*, void*, hipStream_t);
-template int attn_dkdv_valu_dispatch<kBF16>(const void*, const void*, const void*, const void*, const float*, const float*, const int32_t*, const int32_t*, const int32_t*, const int32_t*, int, int64_t, int, int, int, int, double, void*, void*, hipStream_t);
+#define MSA_INSTANTIATE_VALU(DT)                                                                                    \
+  template int attn_fwd_valu_dispatch<DT>(const void*, const void*, const void*, const int32_t*, const int32_t*, int, \
+                                          int64_t, int, int, int, int, int, double, void*, float*, double*,          \
+                                          hipStream_t);                                                              \
+  template int attn_dq_valu_dispatch<DT>(const void*, const void*, const void*, const void*, const void*, double*,   \
+                                         const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int,      \
+                                         double, void*, hipStream_t);                                                \
+  template int attn_dkdv_valu_dispatch<DT>(const void*, const void*, const void*, const void*, const double*,       \
+                                           const int32_t*, const int32_t*, const int32_t*, const int32_t*, int,      \
+                                           int64_t, int, int, int, int, double, void*, void*, hipStream_t);
+MSA_INSTANTIATE_VALU(kF32)
+MSA_INSTANTIATE_VALU(kF16)
+MSA_INSTANTIATE_VALU(kBF16)
 
 }  // namespace msa

@@ -11,7 +11,8 @@ Execution: ``msa_attn_fwd`` (online softmax, saves lse), ``msa_attn_bwd_dq``
 (dQ and per-row statistics: probability mass, center, centered delta),
 ``build_k2q_csr`` and ``msa_attn_bwd_dkdv`` (dK/dV owned per key block and
 group, no floating-point atomics). Saved state is q, k, v, out and lse in the
-input dtype / fp32; no fp32 staging copies of q/k/v/out are made.
+input dtype plus an fp64 [T,Hq,4] per-row state (full-precision lse, then the
+backward's mass / center / delta); no fp32 staging copies of q/k/v/out.
 """
 
 from __future__ import annotations
@@ -35,15 +36,17 @@ class _SparseAttention(torch.autograd.Function):
         groups = k.shape[1]
         out = torch.empty_like(q)
         lse = torch.empty((total, heads), device=q.device, dtype=torch.float32)
+        # Private fp64 per-row state shared by the three kernels: lse, mass, center, delta.
+        row_state = torch.empty((total, heads, 4), device=q.device, dtype=torch.float64)
         if total:
             with torch.cuda.device(q.device):
                 status = _lib.lib().msa_attn_fwd(
                     q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[q.dtype], indices.data_ptr(),
                     cu.data_ptr(), meta.num_seqs, total, heads, groups, dim, indices.shape[2], block_size,
-                    scale, out.data_ptr(), lse.data_ptr(), _lib.stream_of(q.device),
+                    scale, out.data_ptr(), lse.data_ptr(), row_state.data_ptr(), _lib.stream_of(q.device),
                 )
             _lib.check(status, "msa_attn_fwd")
-        ctx.save_for_backward(q, k, v, indices, cu, out, lse)
+        ctx.save_for_backward(q, k, v, indices, cu, out, row_state)
         ctx.meta = meta
         ctx.scale = scale
         ctx.block_size = block_size
@@ -52,7 +55,7 @@ class _SparseAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output, grad_lse):
-        q, k, v, indices, cu, out, lse = ctx.saved_tensors
+        q, k, v, indices, cu, out, row_state = ctx.saved_tensors
         meta = ctx.meta
         need_q, need_k, need_v = ctx.needs_input_grad[:3]
         need_kv = need_k or need_v
@@ -68,13 +71,11 @@ class _SparseAttention(torch.autograd.Function):
             if grad_output is None:
                 grad_output = torch.zeros_like(out)
             dout = grad_output.to(q.dtype).contiguous()
-            stats = torch.empty((total, heads, 3), device=device, dtype=torch.float32) if need_kv else None
             with torch.cuda.device(device):
                 status = lib.msa_attn_bwd_dq(
                     q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[q.dtype], out.data_ptr(),
-                    dout.data_ptr(), lse.data_ptr(), indices.data_ptr(), cu.data_ptr(), meta.num_seqs, total,
-                    heads, groups, dim, indices.shape[2], ctx.block_size, ctx.scale, _lib.ptr(dq),
-                    _lib.ptr(stats), stream,
+                    dout.data_ptr(), row_state.data_ptr(), indices.data_ptr(), cu.data_ptr(), meta.num_seqs,
+                    total, heads, groups, dim, indices.shape[2], ctx.block_size, ctx.scale, _lib.ptr(dq), stream,
                 )
             _lib.check(status, "msa_attn_bwd_dq")
             if need_kv:
@@ -87,7 +88,7 @@ class _SparseAttention(torch.autograd.Function):
                 with torch.cuda.device(device):
                     status = lib.msa_attn_bwd_dkdv(
                         q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[q.dtype], dout.data_ptr(),
-                        lse.data_ptr(), stats.data_ptr(), cu.data_ptr(), csr.cu_block_lens.data_ptr(),
+                        row_state.data_ptr(), cu.data_ptr(), csr.cu_block_lens.data_ptr(),
                         csr.row_ptr.data_ptr(), csr.query_indices.data_ptr(), meta.num_seqs, total, heads,
                         groups, dim, meta.total_blocks, ctx.block_size, ctx.scale, _lib.ptr(dk), _lib.ptr(dv),
                         workspace.data_ptr(), ws_bytes, stream,
