@@ -7,8 +7,8 @@
 // with a compensated (hi, lo) FP32 dot and publishes fl32(hi*|s| + lo*|s|); for
 // finite bf16/fp16/fp32 inputs that is the correctly rounded exact block max.
 // Here the winning dot is evaluated in FP64 (bf16/fp16/fp32 products are exact
-// in FP64; the accumulation order is fixed: sequential FMA over the index dim,
-// see exact_dot) and rounded once to FP32. Winners are compared on the exact
+// in FP64; the accumulation order is fixed, see exact_dot) and rounded once to
+// FP32. Winners are compared on the exact
 // (directed) dot, ties are exact equality: tie_info = offset+1 for a unique
 // winner, -count for ties (index_score.py:128-136).
 //
@@ -219,7 +219,7 @@ __global__ __launch_bounds__(64) void score_bwd_dk(const void* __restrict__ iq,
 template <int DT>
 int score_fwd_launch(const void* iq, const void* ik, const int32_t* cu, int nseq, int64_t rows, int G,
                      int Di, int NB, int B, double scale, float* scores, int32_t* tie, hipStream_t st) {
-  if (DT == kBF16 && score_mfma_supported(Di, B)) {
+  if (DT == kBF16 && score_mfma_supported(Di, B, scale)) {
     return score_fwd_mfma_launch(iq, ik, cu, nseq, rows, G, Di, NB, B, scale, scores, tie, st);
   }
   const int64_t waves = rows * NB;

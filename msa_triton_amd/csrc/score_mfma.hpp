@@ -1,10 +1,12 @@
 // Exact FP64 evaluation helpers for the indexer score, shared by the exact
 // kernel, the MFMA kernel's certification step and the backward tie paths.
 //
-// All exact dots use ONE summation order (sequential FMA over the index dim in
-// one lane), so every kernel that re-evaluates a (query, key) dot reproduces
-// the same FP64 bits and tie membership is consistent between forward and
-// backward.
+// All exact dots use ONE summation order -- two sequential FMA chains over the
+// halves [0, h) and [h, n) of the index dim (h = n/2), added at the end -- so
+// every kernel that re-evaluates a (query, key) dot reproduces the same FP64
+// bits and tie membership is consistent between forward and backward. (For
+// bf16/fp16 inputs the FP64 sum is exact in practice, so the order only matters
+// in pathological exponent ranges.)
 #pragma once
 #include "common.hpp"
 
@@ -21,12 +23,19 @@ __device__ __forceinline__ double directed(double dot, double scale) {
 }
 
 template <int DT>
-__device__ __forceinline__ double exact_dot(const void* __restrict__ a, int64_t ia,
-                                            const void* __restrict__ b, int64_t ib, int n) {
+__device__ __forceinline__ double exact_half_dot(const void* __restrict__ a, int64_t ia,
+                                                 const void* __restrict__ b, int64_t ib, int d0, int d1) {
   double acc = 0.0;
-  for (int d = 0; d < n; ++d)
+  for (int d = d0; d < d1; ++d)
     acc = fma(static_cast<double>(load_as_f32<DT>(a, ia + d)), static_cast<double>(load_as_f32<DT>(b, ib + d)), acc);
   return acc;
+}
+
+template <int DT>
+__device__ __forceinline__ double exact_dot(const void* __restrict__ a, int64_t ia,
+                                            const void* __restrict__ b, int64_t ib, int n) {
+  const int h = n / 2;
+  return exact_half_dot<DT>(a, ia, b, ib, 0, h) + exact_half_dot<DT>(a, ia, b, ib, h, n);
 }
 
 // Wave-cooperative exact block max over keys [k0, k1) for query row offset qoff.
@@ -76,7 +85,7 @@ __device__ void for_each_winner(const void* __restrict__ iq, int64_t qoff, const
 }
 
 // MFMA score path (bf16). Declared here, defined in score_mfma.hip.
-bool score_mfma_supported(int Di, int B);
+bool score_mfma_supported(int Di, int B, double scale);
 int score_fwd_mfma_launch(const void* iq, const void* ik, const int32_t* cu, int nseq, int64_t rows, int G,
                           int Di, int NB, int B, double scale, float* scores, int32_t* tie, hipStream_t st);
 
