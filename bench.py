@@ -105,6 +105,9 @@ class Harness:
         self.dk = torch.empty_like(k)
         self.dv = torch.empty_like(v)
         self.csr = build_k2q_csr(ids, cu, block_size=cfg["block"])
+        self.fws_bytes = self.lib.msa_attn_fwd_workspace_bytes(2, self.T, cfg["hq"], cfg["g"], cfg["d"], cfg["topk"],
+                                                               self.meta.total_blocks, cfg["block"])
+        self.fws = torch.empty(max(1, self.fws_bytes), dtype=torch.uint8, device=device)
         self.ws_bytes = self.lib.msa_attn_bwd_workspace_bytes(self.T, cfg["hq"], cfg["g"], cfg["d"], cfg["topk"],
                                                               self.meta.total_blocks, cfg["block"])
         self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
@@ -112,9 +115,12 @@ class Harness:
 
     def fwd(self):
         c = self.cfg
+        csr = self.csr
         st = self.lib.msa_attn_fwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), 2, self.ids.data_ptr(),
                                    self.cu.data_ptr(), self.meta.num_seqs, self.T, c["hq"], c["g"], c["d"], c["topk"],
-                                   c["block"], self.scale, self.out.data_ptr(), self.lse.data_ptr(),
+                                   c["block"], self.scale, csr.cu_block_lens.data_ptr(), self.meta.total_blocks,
+                                   csr.row_ptr.data_ptr(), csr.query_indices.data_ptr(), csr.slot_indices.data_ptr(),
+                                   self.fws.data_ptr(), self.fws_bytes, self.out.data_ptr(), self.lse.data_ptr(),
                                    self.rs.data_ptr(), self.stream)
         assert st == 0
 

@@ -73,19 +73,31 @@ int msa_score_bwd(const void* index_q, const void* index_k, int32_t dtype,
                   int64_t index_dim, int64_t num_blocks, int64_t block_size, int64_t total_blocks,
                   double scale, void* grad_q, void* grad_k, void* workspace, void* stream);
 
-/* Stage 3 forward: online-softmax sparse GQA attention over the selected blocks.
+/* Stage 3 forward workspace in bytes; 0 means this configuration runs the VALU
+ * kernels, which need neither the CSR nor a workspace. */
+int64_t msa_attn_fwd_workspace_bytes(int32_t dtype, int64_t total_tokens, int64_t q_heads,
+                                     int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
+                                     int64_t total_blocks, int64_t block_size);
+
+/* Stage 3 forward: sparse GQA attention over the selected blocks.
  * Replaces triton/sparse_attention.py:35-84 (_forward_kernel; launch :336-359).
  * out [T,Hq,D] in the input dtype; lse [T,Hq] fp32 (natural log, -inf for rows
  * without keys, whose output is 0). Slots with id < 0 or id > qb(t) are ignored;
  * keys after the query inside its own block are masked.
+ * The bf16 path is KV-major: it consumes the k2q CSR of `indices`
+ * (msa_k2q_build: cu_block_lens, row_ptr, query_indices, slot_indices) and a
+ * workspace of msa_attn_fwd_workspace_bytes(...) bytes; these may be NULL / 0
+ * when that query returns 0.
  * row_state (nullable): private fp64 [T,Hq,4] consumed by the backward; slot 0
  * receives the full-precision lse (the reference keeps (max, denominator),
  * sparse_attention.py:83-84). */
 int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t dtype, const int32_t* indices,
                  const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
                  int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
-                 int64_t block_size, double scale, void* out, float* lse, double* row_state,
-                 void* stream);
+                 int64_t block_size, double scale, const int32_t* cu_block_lens,
+                 int64_t total_blocks, const int32_t* row_ptr, const int32_t* query_indices,
+                 const int32_t* slot_indices, void* workspace, int64_t workspace_bytes, void* out,
+                 float* lse, double* row_state, void* stream);
 
 /* Stage 3 backward, query pass: dQ (nullable) and the per-(t,h) statistics
  * row_state[...,1:4] = (probability mass, center O.dO, centered delta) consumed

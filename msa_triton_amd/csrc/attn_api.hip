@@ -25,10 +25,20 @@ static bool valid_common(int64_t num_seqs, int64_t T, int64_t Hq, int64_t G, int
 
 using namespace msa;
 
+extern "C" int64_t msa_attn_fwd_workspace_bytes(int32_t dtype, int64_t total_tokens, int64_t q_heads,
+                                                int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
+                                                int64_t total_blocks, int64_t block_size) {
+  if (q_heads <= 0 || kv_groups <= 0 || q_heads % kv_groups || total_tokens <= 0) return 0;
+  if (dtype != kBF16 || !attn_mfma_supported(q_heads / kv_groups, head_dim, block_size)) return 0;
+  return attn_fwd_kv_workspace_bytes(total_tokens, q_heads, kv_groups, head_dim, topk_slots, total_blocks);
+}
+
 extern "C" int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t dtype, const int32_t* indices,
                             const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens, int64_t q_heads,
                             int64_t kv_groups, int64_t head_dim, int64_t topk_slots, int64_t block_size,
-                            double scale, void* out, float* lse, double* row_state, void* stream) {
+                            double scale, const int32_t* cu_block_lens, int64_t total_blocks, const int32_t* row_ptr,
+                            const int32_t* query_indices, const int32_t* slot_indices, void* workspace,
+                            int64_t workspace_bytes, void* out, float* lse, double* row_state, void* stream) {
   if (!valid_common(num_seqs, total_tokens, q_heads, kv_groups, head_dim, block_size) || topk_slots < 0)
     return kErrInvalidArgument;
   if (total_tokens == 0) return kOk;
@@ -37,8 +47,10 @@ extern "C" int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t
   const int nseq = static_cast<int>(num_seqs), Hq = static_cast<int>(q_heads), G = static_cast<int>(kv_groups);
   const int D = static_cast<int>(head_dim), K = static_cast<int>(topk_slots), B = static_cast<int>(block_size);
   if (dtype == kBF16 && attn_mfma_supported(Hq / G, D, B)) {
-    return attn_fwd_mfma(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, static_cast<float>(scale),
-                         out, lse, row_state, st);
+    if (!cu_block_lens || !row_ptr || !query_indices || !slot_indices || !workspace) return kErrInvalidArgument;
+    return attn_fwd_kv(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, static_cast<float>(scale),
+                       cu_block_lens, total_blocks, row_ptr, query_indices, slot_indices, workspace, workspace_bytes,
+                       out, lse, row_state, st);
   }
   switch (dtype) {
     case kF32: return attn_fwd_valu_dispatch<kF32>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, row_state, st);

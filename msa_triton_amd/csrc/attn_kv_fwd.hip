@@ -1,0 +1,484 @@
+// Stage 3 forward, KV-major (bf16 inputs).
+//
+// Query-major attention streams each token's selected K/V blocks (K/V bytes
+// gathered per token = #slots x block x D x 4: ~137 GB at 32K tokens). Here the
+// k2q CSR (built from the indices) drives the work instead: a workgroup owns a
+// (key block, group) row -- its K block (row-major) and V block (transposed)
+// sit in LDS -- and streams the row's edges, i.e. the (query token, slot) pairs
+// that selected the block, 128 (edge, head) rows per tile. Each (edge, head)
+// row yields a partial softmax over the block in base 2:
+//   m = max_j s_j, l = sum_j 2^(s_j - m), O = sum_j 2^(s_j - m) v_j   (fp32),
+// with s_j = fl(q.k_j * scale * log2(e)), stored per (token, head, slot). A
+// combine kernel then merges the <= K partials of each (token, head) in slot
+// order in FP64:
+//   M = max m_s, L = sum 2^(m_s - M) l_s, out = sum 2^(m_s - M) O_s / L,
+//   lse = (M + log2 L) ln 2.
+// Query tokens are processed in chunks so the partial buffer stays bounded;
+// inside each CSR row the edges of a chunk form a contiguous range because rows
+// are ordered by query token.
+//
+// The logits use the K row fragment and the Q row fragment over the same dims
+// in the same k order as the backward kernels. P.V is computed exactly in its
+// products: P is split into three bf16 terms (hi + mid + lo == P).
+#include "attn_mfma.hpp"
+#include "mfma_util.hpp"
+
+namespace msa {
+
+namespace {
+
+constexpr int kRowsPerTile = 128;  // (edge, head) rows per tile: 4 waves x 32
+constexpr int kTilesPerItem = 4;   // tiles per work item
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <int NK>
+struct FwdSmem {
+  static constexpr int DP = 32 * NK;
+  static constexpr int KS = DP + 8;   // row stride of the K block (bf16)
+  static constexpr int VS = 128 + 8;  // key stride of the transposed V block (bf16)
+  uint16_t k[128 * KS];
+  uint16_t vt[DP * VS];
+  int32_t th[kRowsPerTile];   // token * Hq + head, -1 for padding rows
+  int32_t tok[kRowsPerTile];  // query token
+  int32_t rec[kRowsPerTile];  // partial record ((token - t0) * Hq + head) * K + slot
+};
+
+// Two 8-byte reads of tile[row][base + pi(q4, j)] where pi(q4, j) = 16*(j/4) + 4*q4 + j%4.
+__device__ __forceinline__ bf16x8 read_keys_pi(const uint16_t* tile, int stride, int row, int base, int q4) {
+  const uint16_t* p = tile + row * stride + base + 4 * q4;
+  const uint2 a = *reinterpret_cast<const uint2*>(p);
+  const uint2 b = *reinterpret_cast<const uint2*>(p + 16);
+  return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
+
+struct RowGeom {
+  int64_t kb;  // first key of the block
+  int nk;      // keys in the block
+  int g;
+};
+
+__device__ __forceinline__ RowGeom row_geom(const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks,
+                                            int nseq, int64_t row, int G, int B) {
+  const int64_t gb = row / G;
+  int s = upper_index(cu_blocks, nseq + 1, gb);
+  while (s < nseq && cu_blocks[s + 1] <= gb) ++s;
+  RowGeom r;
+  r.g = static_cast<int>(row % G);
+  r.kb = cu[s] + (gb - cu_blocks[s]) * B;
+  const int64_t end = cu[s + 1];
+  r.nk = static_cast<int>(end - r.kb < B ? end - r.kb : B);
+  return r;
+}
+
+}  // namespace
+
+// Per row, the first edge whose query token is >= c * tc, for c = 0..nch
+// (bounds[c * rows + row]); bound nch is the row end.
+__global__ __launch_bounds__(256) void fwd_chunk_bounds(const int32_t* __restrict__ row_ptr,
+                                                        const int32_t* __restrict__ qidx, int64_t rows, int64_t T,
+                                                        int64_t tc, int nch, int32_t* __restrict__ bounds) {
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (r >= rows) return;
+  const int32_t a = row_ptr[r], b = row_ptr[r + 1];
+  int32_t lo = a;
+  for (int c = 0; c <= nch; ++c) {
+    const int64_t t = c * tc < T ? c * tc : T;
+    int32_t hi = b;
+    while (lo < hi) {
+      const int32_t mid = (lo + hi) >> 1;
+      if (qidx[mid] < t) lo = mid + 1; else hi = mid;
+    }
+    bounds[c * rows + r] = (c == nch) ? b : lo;
+  }
+}
+
+// For chunk blockIdx.x: the exclusive prefix over rows of ceil(edges / epi) work
+// items, item_start[c * (rows + 1) + row], with the chunk total at index rows.
+__global__ __launch_bounds__(1024) void fwd_item_scan(const int32_t* __restrict__ bounds, int64_t rows, int epi,
+                                                      int32_t* __restrict__ item_start) {
+  __shared__ int32_t wsum[16];
+  __shared__ int32_t carry_s;
+  const int64_t c = blockIdx.x;
+  const int32_t* lo_b = bounds + c * rows;
+  const int32_t* hi_b = bounds + (c + 1) * rows;
+  int32_t* out = item_start + c * (rows + 1);
+  if (threadIdx.x == 0) carry_s = 0;
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  for (int64_t base = 0; base < rows; base += 1024) {
+    const int64_t r = base + threadIdx.x;
+    const int32_t n = r < rows ? (hi_b[r] - lo_b[r] + epi - 1) / epi : 0;
+    int32_t x = n;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int32_t y = __shfl_up(x, o, kWave);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) wsum[wid] = x;
+    __syncthreads();
+    if (threadIdx.x < 16) {
+      int32_t w = wsum[threadIdx.x];
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const int32_t y = __shfl_up(w, o, 16);
+        if (static_cast<int>(threadIdx.x) >= o) w += y;
+      }
+      wsum[threadIdx.x] = w;
+    }
+    __syncthreads();
+    const int32_t carry = carry_s;
+    if (r < rows) out[r] = carry + (wid > 0 ? wsum[wid - 1] : 0) + x - n;
+    __syncthreads();
+    if (threadIdx.x == 0) carry_s = carry + wsum[15];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[rows] = carry_s;
+}
+
+template <int NK>
+__global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
+    const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx,
+    const int32_t* __restrict__ sidx, const int32_t* __restrict__ e_lo, const int32_t* __restrict__ e_hi,
+    const int32_t* __restrict__ item_start, int nseq, int rows, int Hq, int G, int D, int K, int B, float scale2,
+    int epi, int t0, float* __restrict__ opart, float2* __restrict__ mlpart) {
+  constexpr int DP = 32 * NK, NDT = DP / 16, KS = FwdSmem<NK>::KS, VS = FwdSmem<NK>::VS;
+  __shared__ FwdSmem<NK> sm;
+  const int item = blockIdx.x;
+  if (item >= item_start[rows]) return;
+  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
+  const int row = upper_index(item_start, rows + 1, item);
+  const int chunk = item - item_start[row];
+  const RowGeom rg = row_geom(cu, cu_blocks, nseq, row, G, B);
+  const int R = Hq / G;
+  const int e_begin = e_lo[row] + chunk * epi;
+  const int e_end = e_begin + epi < e_hi[row] ? e_begin + epi : e_hi[row];
+  const int nrows = (e_end - e_begin) * R;
+
+  // ---- K block row-major, V block transposed, zero-padded to 128 keys x DP dims
+  for (int e = tid; e < 128 * (DP / 8); e += 256) {
+    const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));
+    uint4 kw = make_uint4(0u, 0u, 0u, 0u), vw = kw;
+    if (kl < rg.nk && d0 < D) {
+      const int64_t off = ((rg.kb + kl) * G + rg.g) * D + d0;
+      kw = *reinterpret_cast<const uint4*>(k + off);
+      vw = *reinterpret_cast<const uint4*>(v + off);
+    }
+    *reinterpret_cast<uint4*>(sm.k + kl * KS + d0) = kw;
+    const uint32_t w4[4] = {vw.x, vw.y, vw.z, vw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sm.vt[(d0 + 2 * i) * VS + kl] = static_cast<uint16_t>(w4[i] & 0xffffu);
+      sm.vt[(d0 + 2 * i + 1) * VS + kl] = static_cast<uint16_t>(w4[i] >> 16);
+    }
+  }
+
+  for (int r0 = 0; r0 < nrows; r0 += kRowsPerTile) {
+    if (r0 > 0) __syncthreads();  // the previous tile's row metadata is no longer read
+    if (tid < kRowsPerTile) {
+      const int rho = r0 + tid;
+      int32_t th = -1, tk = -1, rc = 0;
+      if (rho < nrows) {
+        const int eo = rho / R;
+        const int h = rg.g * R + (rho - eo * R);
+        tk = qidx[e_begin + eo];
+        th = tk * Hq + h;
+        rc = ((tk - t0) * Hq + h) * K + sidx[e_begin + eo];
+      }
+      sm.th[tid] = th;
+      sm.tok[tid] = tk;
+      sm.rec[tid] = rc;
+    }
+    __syncthreads();  // also publishes the K/V block on the first tile
+
+    // ---- Q fragments: lane row c of row tile rt is tile row 32*wid + 16*rt + c
+    bf16x8 qf[2][NK];
+    int lim[2];  // visible keys of the lane's row
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int mi = 32 * wid + 16 * rt + c;
+      const int32_t th = sm.th[mi];
+      const int64_t vis = static_cast<int64_t>(sm.tok[mi]) - rg.kb + 1;
+      lim[rt] = th < 0 ? 0 : (vis < rg.nk ? static_cast<int>(vis) : rg.nk);
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) {
+        const int d0 = 32 * kk + 8 * q4;
+        qf[rt][kk] = (th >= 0 && d0 < D) ? load_frag(q + static_cast<int64_t>(th) * D + d0) : zero_frag();
+      }
+    }
+    // ---- logits S^T = K Q^T: lane holds S[row 16*rt + c][key 16*kt + 4*q4 + i]
+    f32x4 s[2][8];
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+      bf16x8 kf[NK];
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk)
+        kf[kk] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(sm.k + (16 * kt + c) * KS + 32 * kk + 8 * q4));
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) a = mfma(kf[kk], qf[rt][kk], a);
+        s[rt][kt] = a;
+      }
+    }
+    // ---- base-2 partial softmax per row (rows of the lane's quad share c)
+    const bool full = __ballot(lim[0] < 128 || lim[1] < 128) == 0;
+    float mrow[2], lrow[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float m = -__builtin_inff();
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float x = s[rt][kt][i] * scale2;
+          if (!full) x = (16 * kt + 4 * q4 + i < lim[rt]) ? x : -__builtin_inff();
+          s[rt][kt][i] = x;
+          m = fmaxf(m, x);
+        }
+      m = quad_max(m);
+      const float base = m == -__builtin_inff() ? 0.f : m;
+      float l = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = __builtin_amdgcn_exp2f(s[rt][kt][i] - base);
+          s[rt][kt][i] = p;
+          l += p;
+        }
+      l += __shfl_xor(l, 16, kWave);
+      l += __shfl_xor(l, 32, kWave);
+      mrow[rt] = m;
+      lrow[rt] = l;
+    }
+    // ---- O = P V over 4 chunks of 32 keys: A = P[row c][keys pi], B = V[keys pi][dim c]
+    f32x4 o[2][NDT];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      bf16x8 ph[2], pm[2], pl[2];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        uint32_t wh[4], wm[4], wl[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          // elements j = 2*jj, 2*jj + 1 -> C tile 2*kc + j/4, entry j%4
+          const int j0 = 2 * jj, j1 = 2 * jj + 1;
+          uint32_t h0, m0, l0, h1, m1, l1;
+          split3_bits(s[rt][2 * kc + j0 / 4][j0 % 4], h0, m0, l0);
+          split3_bits(s[rt][2 * kc + j1 / 4][j1 % 4], h1, m1, l1);
+          wh[jj] = pack_hi16(h0, h1);
+          wm[jj] = pack_hi16(m0, m1);
+          wl[jj] = pack_hi16(l0, l1);
+        }
+        ph[rt] = __builtin_bit_cast(bf16x8, make_uint4(wh[0], wh[1], wh[2], wh[3]));
+        pm[rt] = __builtin_bit_cast(bf16x8, make_uint4(wm[0], wm[1], wm[2], wm[3]));
+        pl[rt] = __builtin_bit_cast(bf16x8, make_uint4(wl[0], wl[1], wl[2], wl[3]));
+      }
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const bf16x8 vb = read_keys_pi(sm.vt, VS, dt * 16 + c, 32 * kc, q4);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          o[rt][dt] = mfma(pl[rt], vb, o[rt][dt]);
+          o[rt][dt] = mfma(pm[rt], vb, o[rt][dt]);
+          o[rt][dt] = mfma(ph[rt], vb, o[rt][dt]);
+        }
+      }
+    }
+    // ---- store partials: o lane holds O[row 16*rt + 4*q4 + i][dim 16*dt + c]
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int mi = 32 * wid + 16 * rt + 4 * q4 + i;
+        if (sm.th[mi] < 0) continue;
+        float* dst = opart + static_cast<int64_t>(sm.rec[mi]) * D;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const int d = 16 * dt + c;
+          if (d < D) dst[d] = o[rt][dt][i];
+        }
+      }
+      if (q4 == 0) {
+        const int mi = 32 * wid + 16 * rt + c;
+        if (sm.th[mi] >= 0) mlpart[sm.rec[mi]] = make_float2(mrow[rt], lrow[rt]);
+      }
+    }
+  }
+}
+
+// 32 lanes per (token, head) of the chunk, 4 dims each (D <= 128): merge the
+// valid slots' partials in slot order in FP64.
+__global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restrict__ indices,
+                                                        const int32_t* __restrict__ cu, int nseq, int64_t t0,
+                                                        int64_t t1, int Hq, int G, int D, int K, int B,
+                                                        const float* __restrict__ opart,
+                                                        const float2* __restrict__ mlpart, uint16_t* __restrict__ out,
+                                                        float* __restrict__ lse, double* __restrict__ row_state) {
+  const int sub = threadIdx.x & 31;
+  const int64_t th = t0 * Hq + static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
+  if (th >= t1 * Hq) return;  // whole 32-lane segments exit together
+  const int64_t t = th / Hq;
+  const int h = static_cast<int>(th % Hq);
+  const int g = h / (Hq / G);
+  const int s = find_seq(cu, nseq, t);
+  const int64_t qb = (t - cu[s]) / B;
+  const int32_t* sel = indices + (t * G + g) * K;
+  const int64_t rec0 = ((t - t0) * Hq + h) * static_cast<int64_t>(K);
+
+  float M = -__builtin_inff();
+  for (int s0 = 0; s0 < K; s0 += 32) {
+    const int slot = s0 + sub;
+    if (slot < K) {
+      const int id = sel[slot];
+      if (id >= 0 && id <= qb) M = fmaxf(M, mlpart[rec0 + slot].x);
+    }
+  }
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 32));
+
+  double L = 0.0;
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  const bool has_dims = 4 * sub < D;
+  if (M != -__builtin_inff()) {
+    for (int s0 = 0; s0 < K; s0 += 32) {
+      const int slot = s0 + sub;
+      double w = 0.0;
+      if (slot < K) {
+        const int id = sel[slot];
+        if (id >= 0 && id <= qb) {
+          const float2 ml = mlpart[rec0 + slot];
+          w = exp2(static_cast<double>(ml.x) - static_cast<double>(M));
+          L = fma(w, static_cast<double>(ml.y), L);
+        }
+      }
+      const int n = K - s0 < 32 ? K - s0 : 32;
+      for (int j = 0; j < n; ++j) {
+        const double wj = __shfl(w, j, 32);
+        if (wj == 0.0) continue;  // invalid slot (or a weight that underflowed to zero)
+        if (has_dims) {
+          const float4 op = *reinterpret_cast<const float4*>(opart + (rec0 + s0 + j) * D + 4 * sub);
+          acc[0] = fma(wj, static_cast<double>(op.x), acc[0]);
+          acc[1] = fma(wj, static_cast<double>(op.y), acc[1]);
+          acc[2] = fma(wj, static_cast<double>(op.z), acc[2]);
+          acc[3] = fma(wj, static_cast<double>(op.w), acc[3]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) L += __shfl_xor(L, o, 32);
+  const bool has = L > 0.0;
+  if (has_dims) {
+    uint32_t w2[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t a = f32_to_bf16_bits(has ? static_cast<float>(acc[2 * i] / L) : 0.f);
+      const uint32_t b = f32_to_bf16_bits(has ? static_cast<float>(acc[2 * i + 1] / L) : 0.f);
+      w2[i] = a | (b << 16);
+    }
+    *reinterpret_cast<uint2*>(out + th * D + 4 * sub) = make_uint2(w2[0], w2[1]);
+  }
+  if (sub == 0) {
+    const double full = has ? (static_cast<double>(M) + log2(L)) * 0.6931471805599453 : -__builtin_inf();
+    lse[th] = static_cast<float>(full);
+    if (row_state) row_state[th * 4] = full;
+  }
+}
+
+// ---------------------------------------------------------------------------- host side
+
+static int nk_of_dim(int D) { return D <= 32 ? 1 : (D <= 64 ? 2 : 4); }
+
+static int64_t fwd_epi(int R) {
+  const int64_t e = static_cast<int64_t>(kRowsPerTile) * kTilesPerItem / R;
+  return e < 1 ? 1 : e;
+}
+
+static int64_t fwd_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t D) {
+  // partial budget: opart + mlpart per token, capped at ~256 MiB
+  const int64_t per_token = Hq * K * (D + 2) * 4;
+  int64_t tc = (int64_t(256) << 20) / (per_token > 0 ? per_token : 1);
+  if (tc < 64) tc = 64;
+  return tc < T ? tc : (T > 0 ? T : 1);
+}
+
+static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+struct FwdLayout {
+  int64_t tc, nch, bounds, items, opart, ml, total;
+};
+
+static FwdLayout fwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks) {
+  FwdLayout f;
+  const int64_t rows = total_blocks * G;
+  f.tc = fwd_chunk_tokens(T, Hq, K, D);
+  f.nch = (T + f.tc - 1) / f.tc;
+  f.bounds = 0;
+  f.items = align256((f.nch + 1) * rows * 4);
+  f.opart = f.items + align256(f.nch * (rows + 1) * 4);
+  f.ml = f.opart + align256(f.tc * Hq * K * D * 4);
+  f.total = f.ml + align256(f.tc * Hq * K * 8);
+  return f;
+}
+
+int64_t attn_fwd_kv_workspace_bytes(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks) {
+  return fwd_layout(T, Hq, G, D, K, total_blocks).total;
+}
+
+int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indices, const int32_t* cu, int nseq,
+                int64_t T, int Hq, int G, int D, int K, int B, float scale, const int32_t* cu_blocks,
+                int64_t total_blocks, const int32_t* row_ptr, const int32_t* qidx, const int32_t* sidx, void* ws,
+                int64_t ws_bytes, void* out, float* lse, double* rs, hipStream_t st) {
+  const int64_t rows = total_blocks * G;
+  const FwdLayout f = fwd_layout(T, Hq, G, D, K, total_blocks);
+  if (ws_bytes < f.total) return kErrInvalidArgument;
+  // 32-bit token-head, record and row arithmetic inside the kernels
+  if (T * Hq * (K > 0 ? K : 1) >= (int64_t(1) << 31) || rows >= (int64_t(1) << 31)) return kErrUnsupported;
+  if (T == 0) return kOk;
+  char* base = static_cast<char*>(ws);
+  int32_t* bounds = reinterpret_cast<int32_t*>(base + f.bounds);
+  int32_t* items = reinterpret_cast<int32_t*>(base + f.items);
+  float* opart = reinterpret_cast<float*>(base + f.opart);
+  float2* ml = reinterpret_cast<float2*>(base + f.ml);
+  const int R = Hq / G;
+  const int epi = static_cast<int>(fwd_epi(R));
+  const float scale2 = scale * kLog2e;
+  const auto* qb = static_cast<const uint16_t*>(q);
+  const auto* kb = static_cast<const uint16_t*>(k);
+  const auto* vb = static_cast<const uint16_t*>(v);
+  auto* ob = static_cast<uint16_t*>(out);
+  if (rows > 0) {
+    hipLaunchKernelGGL(fwd_chunk_bounds, dim3(grid_1d(rows, 256)), dim3(256), 0, st, row_ptr, qidx, rows, T, f.tc,
+                       static_cast<int>(f.nch), bounds);
+    hipLaunchKernelGGL(fwd_item_scan, dim3(static_cast<unsigned>(f.nch)), dim3(1024), 0, st, bounds, rows, epi, items);
+  }
+  for (int64_t c = 0; c < f.nch; ++c) {
+    const int64_t t0 = c * f.tc, t1 = t0 + f.tc < T ? t0 + f.tc : T;
+    if (rows > 0) {
+      // upper bound on items: one per row plus one per epi edges of the chunk
+      const int64_t max_items = rows + ((t1 - t0) * G * K) / epi + 1;
+      const dim3 grid(static_cast<unsigned>(max_items)), block(256);
+      const int32_t* lo = bounds + c * rows;
+      const int32_t* hi = bounds + (c + 1) * rows;
+      const int32_t* is = items + c * (rows + 1);
+      const int ir = static_cast<int>(rows), it0 = static_cast<int>(t0);
+      switch (nk_of_dim(D)) {
+        case 1: hipLaunchKernelGGL(attn_fwd_partial_kernel<1>, grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, lo, hi, is, nseq, ir, Hq, G, D, K, B, scale2, epi, it0, opart, ml); break;
+        case 2: hipLaunchKernelGGL(attn_fwd_partial_kernel<2>, grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, lo, hi, is, nseq, ir, Hq, G, D, K, B, scale2, epi, it0, opart, ml); break;
+        default: hipLaunchKernelGGL(attn_fwd_partial_kernel<4>, grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, lo, hi, is, nseq, ir, Hq, G, D, K, B, scale2, epi, it0, opart, ml); break;
+      }
+    }
+    hipLaunchKernelGGL(attn_fwd_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu, nseq, t0, t1,
+                       Hq, G, D, K, B, opart, ml, ob, lse, rs);
+  }
+  return status_from(hipGetLastError());
+}
+
+}  // namespace msa

@@ -42,6 +42,22 @@ __device__ __forceinline__ void split3(float x, uint16_t& hi, uint16_t& mid, uin
   lo = f32_to_bf16_bits(r1 - bf16_bits_to_f32(mid));
 }
 
+// Exact split of an fp32 value into three bf16 terms by truncation: hi keeps the
+// top 8 significant bits of x, mid the top 8 of x - hi, lo the remaining <= 8
+// bits, so x == hi + mid + lo exactly (24 = 3 x 8) for normal x. The terms are
+// returned as fp32 bit patterns whose low 16 bits are ignored by pack_hi16.
+__device__ __forceinline__ void split3_bits(float x, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+  hi = __float_as_uint(x);
+  const float r1 = x - __uint_as_float(hi & 0xffff0000u);
+  mid = __float_as_uint(r1);
+  lo = __float_as_uint(r1 - __uint_as_float(mid & 0xffff0000u));
+}
+
+// One 32-bit word holding the bf16 truncations (upper halves) of a (low half) and b (high half).
+__device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
 // Write a row fragment (8 dims of one key / row) transposed into tile[dim][key].
 __device__ __forceinline__ void store_transposed(uint16_t* tile, int dim0, int key, bf16x8 f) {
   const uint4 raw = __builtin_bit_cast(uint4, f);

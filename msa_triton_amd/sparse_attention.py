@@ -7,7 +7,8 @@ defaults, validation order, messages and exception types) and the
 (it produces the per-row statistics the KV pass consumes); the k2q CSR is
 built only when dK or dV is needed; lse is non-differentiable.
 
-Execution: ``msa_attn_fwd`` (online softmax, saves lse), ``msa_attn_bwd_dq``
+Execution: ``msa_attn_fwd`` (KV-major over the selection's k2q CSR for bf16:
+per-block partial softmax + ordered combine; saves lse), ``msa_attn_bwd_dq``
 (dQ and per-row statistics: probability mass, center, centered delta),
 ``build_k2q_csr`` and ``msa_attn_bwd_dkdv`` (dK/dV owned per key block and
 group, no floating-point atomics). Saved state is q, k, v, out and lse in the
@@ -39,11 +40,26 @@ class _SparseAttention(torch.autograd.Function):
         # Private fp64 per-row state shared by the three kernels: lse, mass, center, delta.
         row_state = torch.empty((total, heads, 4), device=q.device, dtype=torch.float64)
         if total:
+            lib = _lib.lib()
+            dtype = _lib.DTYPE_CODE[q.dtype]
+            slots = indices.shape[2]
+            ws_bytes = lib.msa_attn_fwd_workspace_bytes(dtype, total, heads, groups, dim, slots,
+                                                        meta.total_blocks, block_size)
+            csr = None
+            workspace = None
+            if ws_bytes > 0:
+                # The KV-major forward walks the block->query CSR of the selection.
+                csr = _k2q._build_device(indices, cu, meta, groups, slots)
+                workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
             with torch.cuda.device(q.device):
-                status = _lib.lib().msa_attn_fwd(
-                    q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[q.dtype], indices.data_ptr(),
-                    cu.data_ptr(), meta.num_seqs, total, heads, groups, dim, indices.shape[2], block_size,
-                    scale, out.data_ptr(), lse.data_ptr(), row_state.data_ptr(), _lib.stream_of(q.device),
+                status = lib.msa_attn_fwd(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), dtype, indices.data_ptr(), cu.data_ptr(),
+                    meta.num_seqs, total, heads, groups, dim, slots, block_size, scale,
+                    _lib.ptr(None if csr is None else csr.cu_block_lens), meta.total_blocks,
+                    _lib.ptr(None if csr is None else csr.row_ptr),
+                    _lib.ptr(None if csr is None else csr.query_indices),
+                    _lib.ptr(None if csr is None else csr.slot_indices), _lib.ptr(workspace), ws_bytes,
+                    out.data_ptr(), lse.data_ptr(), row_state.data_ptr(), _lib.stream_of(q.device),
                 )
             _lib.check(status, "msa_attn_fwd")
         ctx.save_for_backward(q, k, v, indices, cu, out, row_state)
