@@ -29,6 +29,7 @@ namespace {
 
 constexpr int kRowsPerTile = 128;  // (edge, head) rows per tile: 4 waves x 32
 constexpr int kTilesPerItem = 4;   // tiles per work item
+constexpr int kItemRows = kRowsPerTile * kTilesPerItem;
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <int NK>
@@ -36,11 +37,11 @@ struct FwdSmem {
   static constexpr int DP = 32 * NK;
   static constexpr int KS = DP + 8;   // row stride of the K block (bf16)
   static constexpr int VS = 128 + 8;  // key stride of the transposed V block (bf16)
-  uint16_t k[128 * KS];
-  uint16_t vt[DP * VS];
-  int32_t th[kRowsPerTile];   // token * Hq + head, -1 for padding rows
-  int32_t tok[kRowsPerTile];  // query token
-  int32_t rec[kRowsPerTile];  // partial record ((token - t0) * Hq + head) * K + slot
+  alignas(16) uint16_t k[128 * KS];
+  alignas(16) uint16_t vt[DP * VS];
+  int32_t th[kItemRows];   // token * Hq + head
+  int32_t tok[kItemRows];  // query token
+  int32_t rec[kItemRows];  // partial record ((token - t0) * Hq + head) * K + slot
 };
 
 // Two 8-byte reads of tile[row][base + pi(q4, j)] where pi(q4, j) = 16*(j/4) + 4*q4 + j%4.
@@ -93,9 +94,11 @@ __global__ __launch_bounds__(256) void fwd_chunk_bounds(const int32_t* __restric
 }
 
 // For chunk blockIdx.x: the exclusive prefix over rows of ceil(edges / epi) work
-// items, item_start[c * (rows + 1) + row], with the chunk total at index rows.
+// items, item_start[c * (rows + 1) + row], with the chunk total at index rows,
+// and the item table items[c * max_items + i] = (row, first edge of the item).
 __global__ __launch_bounds__(1024) void fwd_item_scan(const int32_t* __restrict__ bounds, int64_t rows, int epi,
-                                                      int32_t* __restrict__ item_start) {
+                                                      int64_t max_items, int32_t* __restrict__ item_start,
+                                                      int2* __restrict__ items) {
   __shared__ int32_t wsum[16];
   __shared__ int32_t carry_s;
   const int64_t c = blockIdx.x;
@@ -127,7 +130,12 @@ __global__ __launch_bounds__(1024) void fwd_item_scan(const int32_t* __restrict_
     }
     __syncthreads();
     const int32_t carry = carry_s;
-    if (r < rows) out[r] = carry + (wid > 0 ? wsum[wid - 1] : 0) + x - n;
+    if (r < rows) {
+      const int32_t first = carry + (wid > 0 ? wsum[wid - 1] : 0) + x - n;
+      out[r] = first;
+      int2* dst = items + c * max_items + first;  // first + n <= chunk total <= max_items
+      for (int32_t j = 0; j < n; ++j) dst[j] = make_int2(static_cast<int32_t>(r), lo_b[r] + j * epi);
+    }
     __syncthreads();
     if (threadIdx.x == 0) carry_s = carry + wsum[15];
     __syncthreads();
@@ -135,76 +143,112 @@ __global__ __launch_bounds__(1024) void fwd_item_scan(const int32_t* __restrict_
   if (threadIdx.x == 0) out[rows] = carry_s;
 }
 
-template <int NK>
+template <int NK, bool FULLD>
 __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx,
-    const int32_t* __restrict__ sidx, const int32_t* __restrict__ e_lo, const int32_t* __restrict__ e_hi,
-    const int32_t* __restrict__ item_start, int nseq, int rows, int Hq, int G, int D, int K, int B, float scale2,
-    int epi, int t0, float* __restrict__ opart, float2* __restrict__ mlpart) {
+    const int32_t* __restrict__ sidx, const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items,
+    const int2* __restrict__ items, int nseq, int Hq, int G, int D, int K, int B, float scale2, int epi, int t0,
+    float* __restrict__ opart, float2* __restrict__ mlpart) {
   constexpr int DP = 32 * NK, NDT = DP / 16, KS = FwdSmem<NK>::KS, VS = FwdSmem<NK>::VS;
   __shared__ FwdSmem<NK> sm;
   const int item = blockIdx.x;
-  if (item >= item_start[rows]) return;
+  if (item >= *n_items) return;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
-  const int row = upper_index(item_start, rows + 1, item);
-  const int chunk = item - item_start[row];
+  const int2 it = items[item];
+  const int row = it.x, e_begin = it.y;
   const RowGeom rg = row_geom(cu, cu_blocks, nseq, row, G, B);
   const int R = Hq / G;
-  const int e_begin = e_lo[row] + chunk * epi;
   const int e_end = e_begin + epi < e_hi[row] ? e_begin + epi : e_hi[row];
-  const int nrows = (e_end - e_begin) * R;
+  const int nrows = (e_end - e_begin) * R;  // <= kItemRows
 
-  // ---- K block row-major, V block transposed, zero-padded to 128 keys x DP dims
-  for (int e = tid; e < 128 * (DP / 8); e += 256) {
+  // ---- stage the K block (row-major), the V block (transposed) and the item's
+  // row metadata in LDS. All global loads are issued before any LDS store.
+  constexpr int KVI = 128 * (DP / 8) / 256;  // 16-byte K (and V) loads per thread
+  uint4 kw[KVI], vw[KVI];
+#pragma unroll
+  for (int it = 0; it < KVI; ++it) {
+    const int e = tid + 256 * it;
+    const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));  // lanes along dims
+    // unconditional loads from clamped (in-bounds) addresses; out-of-range lanes are zeroed at the store
+    const int klc = kl < rg.nk ? kl : rg.nk - 1, d0c = (FULLD || d0 < D) ? d0 : D - 8;
+    kw[it] = *reinterpret_cast<const uint4*>(k + ((rg.kb + klc) * G + rg.g) * D + d0c);
+  }
+#pragma unroll
+  for (int it = 0; it < KVI; ++it) {
+    const int e = tid + 256 * it;
+    const int kl = e & 127, d0 = 8 * (e >> 7);  // lanes along keys: conflict-free transposed writes
+    const int klc = kl < rg.nk ? kl : rg.nk - 1, d0c = (FULLD || d0 < D) ? d0 : D - 8;
+    vw[it] = *reinterpret_cast<const uint4*>(v + ((rg.kb + klc) * G + rg.g) * D + d0c);
+  }
+  constexpr int MI = kItemRows / 256;
+  int32_t mtok[MI], mslot[MI];
+#pragma unroll
+  for (int j = 0; j < MI; ++j) {
+    const int rho = tid + 256 * j;
+    const int eo = (rho < nrows ? rho : nrows - 1) / R;  // nrows >= 1
+    mtok[j] = qidx[e_begin + eo];
+    mslot[j] = sidx[e_begin + eo];
+  }
+#pragma unroll
+  for (int it = 0; it < KVI; ++it) {
+    const int e = tid + 256 * it;
     const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));
-    uint4 kw = make_uint4(0u, 0u, 0u, 0u), vw = kw;
-    if (kl < rg.nk && d0 < D) {
-      const int64_t off = ((rg.kb + kl) * G + rg.g) * D + d0;
-      kw = *reinterpret_cast<const uint4*>(k + off);
-      vw = *reinterpret_cast<const uint4*>(v + off);
-    }
-    *reinterpret_cast<uint4*>(sm.k + kl * KS + d0) = kw;
-    const uint32_t w4[4] = {vw.x, vw.y, vw.z, vw.w};
+    const bool ok = kl < rg.nk && (FULLD || d0 < D);
+    *reinterpret_cast<uint4*>(sm.k + kl * KS + d0) = ok ? kw[it] : make_uint4(0u, 0u, 0u, 0u);
+  }
+#pragma unroll
+  for (int it = 0; it < KVI; ++it) {
+    const int e = tid + 256 * it;
+    const int kl = e & 127, d0 = 8 * (e >> 7);
+    const bool ok = kl < rg.nk && (FULLD || d0 < D);
+    const uint32_t w4[4] = {ok ? vw[it].x : 0u, ok ? vw[it].y : 0u, ok ? vw[it].z : 0u, ok ? vw[it].w : 0u};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       sm.vt[(d0 + 2 * i) * VS + kl] = static_cast<uint16_t>(w4[i] & 0xffffu);
       sm.vt[(d0 + 2 * i + 1) * VS + kl] = static_cast<uint16_t>(w4[i] >> 16);
     }
   }
-
-  for (int r0 = 0; r0 < nrows; r0 += kRowsPerTile) {
-    if (r0 > 0) __syncthreads();  // the previous tile's row metadata is no longer read
-    if (tid < kRowsPerTile) {
-      const int rho = r0 + tid;
-      int32_t th = -1, tk = -1, rc = 0;
-      if (rho < nrows) {
-        const int eo = rho / R;
-        const int h = rg.g * R + (rho - eo * R);
-        tk = qidx[e_begin + eo];
-        th = tk * Hq + h;
-        rc = ((tk - t0) * Hq + h) * K + sidx[e_begin + eo];
-      }
-      sm.th[tid] = th;
-      sm.tok[tid] = tk;
-      sm.rec[tid] = rc;
+#pragma unroll
+  for (int j = 0; j < MI; ++j) {
+    const int rho = tid + 256 * j;
+    if (rho < nrows) {
+      const int eo = rho / R;
+      const int h = rg.g * R + (rho - eo * R);
+      sm.th[rho] = mtok[j] * Hq + h;
+      sm.tok[rho] = mtok[j];
+      sm.rec[rho] = ((mtok[j] - t0) * Hq + h) * K + mslot[j];
     }
-    __syncthreads();  // also publishes the K/V block on the first tile
+  }
+  __syncthreads();
 
-    // ---- Q fragments: lane row c of row tile rt is tile row 32*wid + 16*rt + c
-    bf16x8 qf[2][NK];
-    int lim[2];  // visible keys of the lane's row
+  // Waves are independent from here on. Wave wid owns rows r0 + 32*wid + 16*rt + c of each tile.
+  const int ntiles = (nrows + kRowsPerTile - 1) / kRowsPerTile;
+  bf16x8 qf[2][NK];
+  auto load_q = [&](int r0) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      const int mi = 32 * wid + 16 * rt + c;
-      const int32_t th = sm.th[mi];
-      const int64_t vis = static_cast<int64_t>(sm.tok[mi]) - rg.kb + 1;
-      lim[rt] = th < 0 ? 0 : (vis < rg.nk ? static_cast<int>(vis) : rg.nk);
+      const int rho = r0 + 32 * wid + 16 * rt + c;
+      const bool ok = rho < nrows;
+      const int64_t th = ok ? sm.th[rho] : 0;
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) {
         const int d0 = 32 * kk + 8 * q4;
-        qf[rt][kk] = (th >= 0 && d0 < D) ? load_frag(q + static_cast<int64_t>(th) * D + d0) : zero_frag();
+        qf[rt][kk] = (ok && (FULLD || d0 < D)) ? load_frag(q + th * D + d0) : zero_frag();
       }
+    }
+  };
+  load_q(0);
+  for (int tile = 0; tile < ntiles; ++tile) {
+    const int r0 = tile * kRowsPerTile;
+    const int rbase = r0 + 32 * wid;
+    if (rbase >= nrows) break;  // wave-uniform: no rows of this wave are left
+    int lim[2];  // visible keys of the lane's rows
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int rho = rbase + 16 * rt + c;
+      const int64_t vis = rho < nrows ? static_cast<int64_t>(sm.tok[rho]) - rg.kb + 1 : 0;
+      lim[rt] = vis < rg.nk ? static_cast<int>(vis) : rg.nk;
     }
     // ---- logits S^T = K Q^T: lane holds S[row 16*rt + c][key 16*kt + 4*q4 + i]
     f32x4 s[2][8];
@@ -222,29 +266,57 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
         s[rt][kt] = a;
       }
     }
-    // ---- base-2 partial softmax per row (rows of the lane's quad share c)
+    // Q fragments are dead: prefetch the next tile's rows.
+    if (tile + 1 < ntiles) load_q(r0 + kRowsPerTile);
+    // ---- base-2 partial softmax per row (rows of the lane's quad share c).
+    // m = fl(scale2 * a*) where a* is the max (scale2 > 0) or min (scale2 < 0) raw
+    // logit; p = 2^(scale2 * a - m) with one rounding (fma). The rounding of m is a
+    // common factor of the row's p, l and O, so it cancels in O / l.
     const bool full = __ballot(lim[0] < 128 || lim[1] < 128) == 0;
     float mrow[2], lrow[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      float m = -__builtin_inff();
+      float a = scale2 >= 0.f ? -__builtin_inff() : __builtin_inff();
+      if (full) {
+        if (scale2 >= 0.f) {
 #pragma unroll
-      for (int kt = 0; kt < 8; ++kt)
+          for (int kt = 0; kt < 8; ++kt)
+            a = fmaxf(a, fmaxf(fmaxf(s[rt][kt][0], s[rt][kt][1]), fmaxf(s[rt][kt][2], s[rt][kt][3])));
+        } else {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float x = s[rt][kt][i] * scale2;
-          if (!full) x = (16 * kt + 4 * q4 + i < lim[rt]) ? x : -__builtin_inff();
-          s[rt][kt][i] = x;
-          m = fmaxf(m, x);
+          for (int kt = 0; kt < 8; ++kt)
+            a = fminf(a, fminf(fminf(s[rt][kt][0], s[rt][kt][1]), fminf(s[rt][kt][2], s[rt][kt][3])));
         }
-      m = quad_max(m);
-      const float base = m == -__builtin_inff() ? 0.f : m;
+      } else {
+        // invisible keys get a raw logit that loses the max/min and underflows 2^(...)
+        const float hide = scale2 >= 0.f ? -__builtin_inff() : __builtin_inff();
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float x = (16 * kt + 4 * q4 + i < lim[rt]) ? s[rt][kt][i] : hide;
+            s[rt][kt][i] = x;
+            a = scale2 >= 0.f ? fmaxf(a, x) : fminf(a, x);
+          }
+      }
+      if (scale2 >= 0.f) {
+        a = fmaxf(a, __shfl_xor(a, 16, kWave));
+        a = fmaxf(a, __shfl_xor(a, 32, kWave));
+      } else {
+        a = fminf(a, __shfl_xor(a, 16, kWave));
+        a = fminf(a, __shfl_xor(a, 32, kWave));
+      }
+      const bool none = (a == -__builtin_inff() || a == __builtin_inff());  // row without visible keys
+      const float m = none ? -__builtin_inff() : a * scale2;
+      const float nm = none ? 0.f : -m;
       float l = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(s[rt][kt][i] - base);
+          // hidden keys: scale2 * (-+inf) = -inf (or NaN when scale2 == 0, mapped to 0 below)
+          float p = __builtin_amdgcn_exp2f(fmaf(s[rt][kt][i], scale2, nm));
+          if (!full) p = (16 * kt + 4 * q4 + i < lim[rt]) ? p : 0.f;
           s[rt][kt][i] = p;
           l += p;
         }
@@ -253,12 +325,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
       mrow[rt] = m;
       lrow[rt] = l;
     }
-    // ---- O = P V over 4 chunks of 32 keys: A = P[row c][keys pi], B = V[keys pi][dim c]
+    // ---- O^T = V^T P^T over 4 chunks of 32 keys: A = V^T[dim c][keys pi], B = P^T[keys pi][row c]
     f32x4 o[2][NDT];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       bf16x8 ph[2], pm[2], pl[2];
@@ -285,30 +353,24 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
         const bf16x8 vb = read_keys_pi(sm.vt, VS, dt * 16 + c, 32 * kc, q4);
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
-          o[rt][dt] = mfma(pl[rt], vb, o[rt][dt]);
-          o[rt][dt] = mfma(pm[rt], vb, o[rt][dt]);
-          o[rt][dt] = mfma(ph[rt], vb, o[rt][dt]);
+          f32x4 acc = kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : o[rt][dt];
+          acc = mfma(vb, pl[rt], acc);
+          acc = mfma(vb, pm[rt], acc);
+          o[rt][dt] = mfma(vb, ph[rt], acc);
         }
       }
     }
-    // ---- store partials: o lane holds O[row 16*rt + 4*q4 + i][dim 16*dt + c]
+    // ---- store partials: o lane holds O[row 16*rt + c][dims 16*dt + 4*q4 + 0..3]
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
+      const int rho = rbase + 16 * rt + c;
+      if (rho < nrows) {
+        float* dst = opart + static_cast<int64_t>(sm.rec[rho]) * D + 4 * q4;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int mi = 32 * wid + 16 * rt + 4 * q4 + i;
-        if (sm.th[mi] < 0) continue;
-        float* dst = opart + static_cast<int64_t>(sm.rec[mi]) * D;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const int d = 16 * dt + c;
-          if (d < D) dst[d] = o[rt][dt][i];
-        }
+        for (int dt = 0; dt < NDT; ++dt)
+          if (FULLD || 16 * dt + 4 * q4 < D) *reinterpret_cast<f32x4*>(dst + 16 * dt) = o[rt][dt];
       }
-      if (q4 == 0) {
-        const int mi = 32 * wid + 16 * rt + c;
-        if (sm.th[mi] >= 0) mlpart[sm.rec[mi]] = make_float2(mrow[rt], lrow[rt]);
-      }
+      if (q4 == 0 && rho < nrows) mlpart[sm.rec[rho]] = make_float2(mrow[rt], lrow[rt]);
     }
   }
 }
@@ -402,9 +464,9 @@ static int64_t fwd_epi(int R) {
 }
 
 static int64_t fwd_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t D) {
-  // partial budget: opart + mlpart per token, capped at ~256 MiB
+  // partial budget: opart + mlpart per token, capped at ~1 GiB (fewer, fuller work items per row)
   const int64_t per_token = Hq * K * (D + 2) * 4;
-  int64_t tc = (int64_t(256) << 20) / (per_token > 0 ? per_token : 1);
+  int64_t tc = (int64_t(1) << 30) / (per_token > 0 ? per_token : 1);
   if (tc < 64) tc = 64;
   return tc < T ? tc : (T > 0 ? T : 1);
 }
@@ -412,7 +474,7 @@ static int64_t fwd_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t D) {
 static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 struct FwdLayout {
-  int64_t tc, nch, bounds, items, opart, ml, total;
+  int64_t tc, nch, max_items, bounds, starts, items, opart, ml, total;
 };
 
 static FwdLayout fwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks) {
@@ -420,9 +482,12 @@ static FwdLayout fwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t
   const int64_t rows = total_blocks * G;
   f.tc = fwd_chunk_tokens(T, Hq, K, D);
   f.nch = (T + f.tc - 1) / f.tc;
+  // upper bound on a chunk's work items: one per row plus one per epi edges of the chunk
+  f.max_items = rows + (f.tc * G * K) / fwd_epi(static_cast<int>(Hq / (G > 0 ? G : 1))) + 1;
   f.bounds = 0;
-  f.items = align256((f.nch + 1) * rows * 4);
-  f.opart = f.items + align256(f.nch * (rows + 1) * 4);
+  f.starts = align256((f.nch + 1) * rows * 4);
+  f.items = f.starts + align256(f.nch * (rows + 1) * 4);
+  f.opart = f.items + align256(f.nch * f.max_items * 8);
   f.ml = f.opart + align256(f.tc * Hq * K * D * 4);
   f.total = f.ml + align256(f.tc * Hq * K * 8);
   return f;
@@ -444,7 +509,8 @@ int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indi
   if (T == 0) return kOk;
   char* base = static_cast<char*>(ws);
   int32_t* bounds = reinterpret_cast<int32_t*>(base + f.bounds);
-  int32_t* items = reinterpret_cast<int32_t*>(base + f.items);
+  int32_t* starts = reinterpret_cast<int32_t*>(base + f.starts);
+  int2* items = reinterpret_cast<int2*>(base + f.items);
   float* opart = reinterpret_cast<float*>(base + f.opart);
   float2* ml = reinterpret_cast<float2*>(base + f.ml);
   const int R = Hq / G;
@@ -457,23 +523,24 @@ int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indi
   if (rows > 0) {
     hipLaunchKernelGGL(fwd_chunk_bounds, dim3(grid_1d(rows, 256)), dim3(256), 0, st, row_ptr, qidx, rows, T, f.tc,
                        static_cast<int>(f.nch), bounds);
-    hipLaunchKernelGGL(fwd_item_scan, dim3(static_cast<unsigned>(f.nch)), dim3(1024), 0, st, bounds, rows, epi, items);
+    hipLaunchKernelGGL(fwd_item_scan, dim3(static_cast<unsigned>(f.nch)), dim3(1024), 0, st, bounds, rows, epi,
+                       f.max_items, starts, items);
   }
   for (int64_t c = 0; c < f.nch; ++c) {
     const int64_t t0 = c * f.tc, t1 = t0 + f.tc < T ? t0 + f.tc : T;
     if (rows > 0) {
-      // upper bound on items: one per row plus one per epi edges of the chunk
-      const int64_t max_items = rows + ((t1 - t0) * G * K) / epi + 1;
-      const dim3 grid(static_cast<unsigned>(max_items)), block(256);
-      const int32_t* lo = bounds + c * rows;
+      const dim3 grid(static_cast<unsigned>(f.max_items)), block(256);
       const int32_t* hi = bounds + (c + 1) * rows;
-      const int32_t* is = items + c * (rows + 1);
-      const int ir = static_cast<int>(rows), it0 = static_cast<int>(t0);
-      switch (nk_of_dim(D)) {
-        case 1: hipLaunchKernelGGL(attn_fwd_partial_kernel<1>, grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, lo, hi, is, nseq, ir, Hq, G, D, K, B, scale2, epi, it0, opart, ml); break;
-        case 2: hipLaunchKernelGGL(attn_fwd_partial_kernel<2>, grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, lo, hi, is, nseq, ir, Hq, G, D, K, B, scale2, epi, it0, opart, ml); break;
-        default: hipLaunchKernelGGL(attn_fwd_partial_kernel<4>, grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, lo, hi, is, nseq, ir, Hq, G, D, K, B, scale2, epi, it0, opart, ml); break;
-      }
+      const int32_t* nit = starts + c * (rows + 1) + rows;
+      const int2* its = items + c * f.max_items;
+      const int it0 = static_cast<int>(t0);
+#define MSA_FWD_PARTIAL(NKV, FD) hipLaunchKernelGGL((attn_fwd_partial_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, epi, it0, opart, ml)
+      const int nk = nk_of_dim(D);
+      const bool fd = D == 32 * nk;
+      if (nk == 1) { if (fd) MSA_FWD_PARTIAL(1, true); else MSA_FWD_PARTIAL(1, false); }
+      else if (nk == 2) { if (fd) MSA_FWD_PARTIAL(2, true); else MSA_FWD_PARTIAL(2, false); }
+      else { if (fd) MSA_FWD_PARTIAL(4, true); else MSA_FWD_PARTIAL(4, false); }
+#undef MSA_FWD_PARTIAL
     }
     hipLaunchKernelGGL(attn_fwd_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu, nseq, t0, t1,
                        Hq, G, D, K, B, opart, ml, ob, lse, rs);

@@ -639,7 +639,8 @@ __global__ __launch_bounds__(256) void attn_dkdv_finalize(const int32_t* __restr
 // ---------------------------------------------------------------------------- host side
 
 bool attn_mfma_supported(int64_t ratio, int64_t head_dim, int64_t block_size) {
-  return ratio >= 1 && head_dim >= 8 && head_dim <= 128 && head_dim % 8 == 0 && block_size >= 1 &&
+  // ratio <= 512: one (edge, head) work item holds whole edges of at most 512 rows
+  return ratio >= 1 && ratio <= 512 && head_dim >= 8 && head_dim <= 128 && head_dim % 8 == 0 && block_size >= 1 &&
          block_size <= 128;
 }
 
