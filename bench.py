@@ -108,9 +108,9 @@ class Harness:
         self.fws_bytes = self.lib.msa_attn_fwd_workspace_bytes(2, self.T, cfg["hq"], cfg["g"], cfg["d"], cfg["topk"],
                                                                self.meta.total_blocks, cfg["block"])
         self.fws = torch.empty(max(1, self.fws_bytes), dtype=torch.uint8, device=device)
-        self.ws_bytes = self.lib.msa_attn_bwd_workspace_bytes(self.T, cfg["hq"], cfg["g"], cfg["d"], cfg["topk"],
+        self.ws_bytes = self.lib.msa_attn_bwd_workspace_bytes(2, self.T, cfg["hq"], cfg["g"], cfg["d"], cfg["topk"],
                                                               self.meta.total_blocks, cfg["block"])
-        self.ws = torch.empty(self.ws_bytes, dtype=torch.uint8, device=device)
+        self.ws = torch.empty(max(1, self.ws_bytes), dtype=torch.uint8, device=device)
         self.stream = torch.cuda.current_stream(device).cuda_stream
 
     def fwd(self):
@@ -124,23 +124,16 @@ class Harness:
                                    self.rs.data_ptr(), self.stream)
         assert st == 0
 
-    def bwd_dq(self):
+    def bwd(self):
         c = self.cfg
-        st = self.lib.msa_attn_bwd_dq(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), 2, self.out.data_ptr(),
-                                      self.dout.data_ptr(), self.rs.data_ptr(), self.ids.data_ptr(),
-                                      self.cu.data_ptr(), self.meta.num_seqs, self.T, c["hq"], c["g"], c["d"],
-                                      c["topk"], c["block"], self.scale, self.dq.data_ptr(), self.stream)
-        assert st == 0
-
-    def bwd_dkdv(self):
-        c = self.cfg
-        st = self.lib.msa_attn_bwd_dkdv(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), 2,
-                                        self.dout.data_ptr(), self.rs.data_ptr(), self.cu.data_ptr(),
-                                        self.csr.cu_block_lens.data_ptr(), self.csr.row_ptr.data_ptr(),
-                                        self.csr.query_indices.data_ptr(), self.meta.num_seqs, self.T, c["hq"],
-                                        c["g"], c["d"], self.meta.total_blocks, c["block"], self.scale,
-                                        self.dk.data_ptr(), self.dv.data_ptr(), self.ws.data_ptr(), self.ws_bytes,
-                                        self.stream)
+        csr = self.csr
+        st = self.lib.msa_attn_bwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), 2, self.out.data_ptr(),
+                                   self.dout.data_ptr(), self.rs.data_ptr(), self.ids.data_ptr(), self.cu.data_ptr(),
+                                   self.meta.num_seqs, self.T, c["hq"], c["g"], c["d"], c["topk"], c["block"],
+                                   self.scale, csr.cu_block_lens.data_ptr(), self.meta.total_blocks,
+                                   csr.row_ptr.data_ptr(), csr.query_indices.data_ptr(), csr.slot_indices.data_ptr(),
+                                   self.dq.data_ptr(), self.dk.data_ptr(), self.dv.data_ptr(), self.ws.data_ptr(),
+                                   self.ws_bytes, self.stream)
         assert st == 0
 
 
@@ -274,11 +267,9 @@ def main():
     h = Harness(cfg, (iq, ik, q, k, v, dout), ids, cu, device)
     kern = {
         "attn_fwd": (h.fwd, fwd_flops),
-        "attn_bwd_dq": (h.bwd_dq, 1.5 * fwd_flops),
-        "attn_bwd_dkdv": (h.bwd_dkdv, 1.0 * fwd_flops),
+        "attn_bwd": (h.bwd, 2.5 * fwd_flops),
     }
     h.fwd()
-    h.bwd_dq()
     kt = {name: time_events(fn, args.repeats) for name, (fn, _) in kern.items()}
     dom = max(kt, key=lambda n: kt[n]["median"])
     achieved = kern[dom][1] / (kt[dom]["median"] * 1e-3) / 1e12
@@ -322,8 +313,7 @@ def main():
             stages[name] = round(time_events(fn, reps)["median"], 4)
             log(f"{name}: {stages[name]:.3f}")
         stages["attention_fwd_bwd_ms"] = round(ms, 4)
-        stages["attention_bwd_dq_ms"] = round(kt["attn_bwd_dq"]["median"], 4)
-        stages["attention_bwd_dkdv_ms"] = round(kt["attn_bwd_dkdv"]["median"], 4)
+        stages["attention_bwd_kernel_ms"] = round(kt["attn_bwd"]["median"], 4)
         stages["attention_fwd_kernel_ms"] = round(kt["attn_fwd"]["median"], 4)
 
     baseline = None

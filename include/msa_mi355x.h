@@ -88,9 +88,9 @@ int64_t msa_attn_fwd_workspace_bytes(int32_t dtype, int64_t total_tokens, int64_
  * (msa_k2q_build: cu_block_lens, row_ptr, query_indices, slot_indices) and a
  * workspace of msa_attn_fwd_workspace_bytes(...) bytes; these may be NULL / 0
  * when that query returns 0.
- * row_state (nullable): private fp64 [T,Hq,4] consumed by the backward; slot 0
- * receives the full-precision lse (the reference keeps (max, denominator),
- * sparse_attention.py:83-84). */
+ * row_state (nullable): private fp64 [T,Hq,4] consumed by msa_attn_bwd; slot 0
+ * receives the full-precision lse in the path's own convention (the reference
+ * keeps (max, denominator), sparse_attention.py:83-84); treat it as opaque. */
 int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t dtype, const int32_t* indices,
                  const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
                  int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
@@ -99,31 +99,31 @@ int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t dtype, con
                  const int32_t* slot_indices, void* workspace, int64_t workspace_bytes, void* out,
                  float* lse, double* row_state, void* stream);
 
-/* Stage 3 backward, query pass: dQ (nullable) and the per-(t,h) statistics
- * row_state[...,1:4] = (probability mass, center O.dO, centered delta) consumed
- * by the KV pass. Replaces sparse_attention.py:87-198 (_backward_kernel with
- * ACCUMULATE_KV=False; launch :376-385). */
-int msa_attn_bwd_dq(const void* q, const void* k, const void* v, int32_t dtype, const void* out,
-                    const void* grad_out, double* row_state, const int32_t* indices,
-                    const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
-                    int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
-                    int64_t block_size, double scale, void* grad_q, void* stream);
+/* Stage 3 backward workspace in bytes; 0 means this configuration runs the VALU
+ * kernels, which need no workspace. */
+int64_t msa_attn_bwd_workspace_bytes(int32_t dtype, int64_t total_tokens, int64_t q_heads,
+                                     int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
+                                     int64_t total_blocks, int64_t block_size);
 
-/* Stage 3 backward workspace in bytes for msa_attn_bwd_dkdv. */
-int64_t msa_attn_bwd_workspace_bytes(int64_t total_tokens, int64_t q_heads, int64_t kv_groups,
-                                     int64_t head_dim, int64_t topk_slots, int64_t total_blocks,
-                                     int64_t block_size);
-
-/* Stage 3 backward, KV pass: dK/dV (either nullable) owned per (key block, group)
- * row of the k2q CSR, no floating-point atomics. Replaces
- * sparse_attention.py:223-295 (_backward_kv_kernel; launch :386-393). */
-int msa_attn_bwd_dkdv(const void* q, const void* k, const void* v, int32_t dtype,
-                      const void* grad_out, const double* row_state, const int32_t* cu_seqlens,
-                      const int32_t* cu_block_lens, const int32_t* row_ptr,
-                      const int32_t* query_indices, int64_t num_seqs, int64_t total_tokens,
-                      int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t total_blocks,
-                      int64_t block_size, double scale, void* grad_k, void* grad_v, void* workspace,
-                      int64_t workspace_bytes, void* stream);
+/* Stage 3 backward: dQ, dK, dV (each nullable; all NULL is a no-op) of the
+ * attention computed by msa_attn_fwd with the same row_state. Replaces the
+ * autograd backward of triton/sparse_attention.py:361-394 (_backward_kernel,
+ * :87-198, with the dK/dV pass _backward_kv_kernel, :223-295, over
+ * build_k2q_csr). Softmax derivative centred as in the reference
+ * (:119-158): delta = sum p (dp - c) / mass from the same p and dp as dS.
+ * The bf16 path is KV-major and needs the k2q CSR (cu_block_lens, row_ptr,
+ * query_indices, slot_indices) and msa_attn_bwd_workspace_bytes(...) bytes of
+ * workspace for every gradient set; the VALU path needs the CSR only when
+ * grad_k or grad_v is requested. row_state slots 1..3 are (re)written.
+ * Deterministic: no floating-point atomics. */
+int msa_attn_bwd(const void* q, const void* k, const void* v, int32_t dtype, const void* out,
+                 const void* grad_out, double* row_state, const int32_t* indices,
+                 const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
+                 int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
+                 int64_t block_size, double scale, const int32_t* cu_block_lens,
+                 int64_t total_blocks, const int32_t* row_ptr, const int32_t* query_indices,
+                 const int32_t* slot_indices, void* grad_q, void* grad_k, void* grad_v,
+                 void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,6 +1,7 @@
 // C ABI for stage 3 (sparse GQA attention forward / backward).
-// bf16 inputs whose shape fits the MFMA templates run the MFMA kernels
-// (attn_mfma.hip); other dtypes/shapes run the VALU kernels (attn_scalar.hip).
+// bf16 inputs whose shape fits the MFMA templates run the KV-major MFMA kernels
+// (attn_kv_fwd.hip, attn_kv_bwd.hip); other dtypes/shapes run the VALU kernels
+// (attn_scalar.hip).
 #include "attn_mfma.hpp"
 #include "common.hpp"
 
@@ -47,7 +48,9 @@ extern "C" int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t
   const int nseq = static_cast<int>(num_seqs), Hq = static_cast<int>(q_heads), G = static_cast<int>(kv_groups);
   const int D = static_cast<int>(head_dim), K = static_cast<int>(topk_slots), B = static_cast<int>(block_size);
   if (dtype == kBF16 && attn_mfma_supported(Hq / G, D, B)) {
-    if (!cu_block_lens || !row_ptr || !query_indices || !slot_indices || !workspace) return kErrInvalidArgument;
+    // the edge arrays are empty (and may be NULL) when there are no slots
+    if (!cu_block_lens || !row_ptr || !workspace || (K > 0 && (!query_indices || !slot_indices)))
+      return kErrInvalidArgument;
     return attn_fwd_kv(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, static_cast<float>(scale),
                        cu_block_lens, total_blocks, row_ptr, query_indices, slot_indices, workspace, workspace_bytes,
                        out, lse, row_state, st);
@@ -60,63 +63,50 @@ extern "C" int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t
   }
 }
 
-extern "C" int msa_attn_bwd_dq(const void* q, const void* k, const void* v, int32_t dtype, const void* out,
-                               const void* grad_out, double* row_state, const int32_t* indices,
-                               const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens, int64_t q_heads,
-                               int64_t kv_groups, int64_t head_dim, int64_t topk_slots, int64_t block_size,
-                               double scale, void* grad_q, void* stream) {
+extern "C" int64_t msa_attn_bwd_workspace_bytes(int32_t dtype, int64_t total_tokens, int64_t q_heads,
+                                                int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
+                                                int64_t total_blocks, int64_t block_size) {
+  if (q_heads <= 0 || kv_groups <= 0 || q_heads % kv_groups || total_tokens <= 0) return 0;
+  if (dtype != kBF16 || !attn_mfma_supported(q_heads / kv_groups, head_dim, block_size)) return 0;
+  return attn_bwd_kv_workspace_bytes(total_tokens, q_heads, kv_groups, head_dim, topk_slots, total_blocks);
+}
+
+extern "C" int msa_attn_bwd(const void* q, const void* k, const void* v, int32_t dtype, const void* out,
+                            const void* grad_out, double* row_state, const int32_t* indices,
+                            const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens, int64_t q_heads,
+                            int64_t kv_groups, int64_t head_dim, int64_t topk_slots, int64_t block_size,
+                            double scale, const int32_t* cu_block_lens, int64_t total_blocks, const int32_t* row_ptr,
+                            const int32_t* query_indices, const int32_t* slot_indices, void* grad_q, void* grad_k,
+                            void* grad_v, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!valid_common(num_seqs, total_tokens, q_heads, kv_groups, head_dim, block_size) || topk_slots < 0 ||
-      row_state == nullptr)
+      total_blocks < 0 || row_state == nullptr)
     return kErrInvalidArgument;
-  if (total_tokens == 0) return kOk;
+  if (total_tokens == 0 || (!grad_q && !grad_k && !grad_v)) return kOk;
   if (head_dim > 512) return kErrUnsupported;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nseq = static_cast<int>(num_seqs), Hq = static_cast<int>(q_heads), G = static_cast<int>(kv_groups);
   const int D = static_cast<int>(head_dim), K = static_cast<int>(topk_slots), B = static_cast<int>(block_size);
+  const bool need_kv = grad_k != nullptr || grad_v != nullptr;
   if (dtype == kBF16 && attn_mfma_supported(Hq / G, D, B)) {
-    return attn_bwd_dq_mfma(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B,
-                            static_cast<float>(scale), grad_q, st);
+    if (!cu_block_lens || !row_ptr || !workspace || (K > 0 && (!query_indices || !slot_indices)))
+      return kErrInvalidArgument;
+    return attn_bwd_kv(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B,
+                       static_cast<float>(scale), cu_block_lens, total_blocks, row_ptr, query_indices, slot_indices,
+                       grad_q, grad_k, grad_v, workspace, workspace_bytes, st);
   }
+  if (need_kv && (!cu_block_lens || !row_ptr || (K > 0 && !query_indices))) return kErrInvalidArgument;
+  // VALU path: the query pass (dQ and the row statistics), then the KV pass.
+  int rc = kErrInvalidArgument;
   switch (dtype) {
-    case kF32: return attn_dq_valu_dispatch<kF32>(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, st);
-    case kF16: return attn_dq_valu_dispatch<kF16>(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, st);
-    case kBF16: return attn_dq_valu_dispatch<kBF16>(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, st);
+    case kF32: rc = attn_dq_valu_dispatch<kF32>(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, st); break;
+    case kF16: rc = attn_dq_valu_dispatch<kF16>(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, st); break;
+    case kBF16: rc = attn_dq_valu_dispatch<kBF16>(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, grad_q, st); break;
     default: return kErrInvalidArgument;
   }
-}
-
-extern "C" int64_t msa_attn_bwd_workspace_bytes(int64_t total_tokens, int64_t q_heads, int64_t kv_groups,
-                                                int64_t head_dim, int64_t topk_slots, int64_t total_blocks,
-                                                int64_t block_size) {
-  if (q_heads <= 0 || kv_groups <= 0 || q_heads % kv_groups) return 256;
-  if (!attn_mfma_supported(q_heads / kv_groups, head_dim, block_size)) return 256;
-  return attn_dkdv_mfma_workspace_bytes(total_tokens, q_heads, kv_groups, head_dim, topk_slots, total_blocks,
-                                        block_size);
-}
-
-extern "C" int msa_attn_bwd_dkdv(const void* q, const void* k, const void* v, int32_t dtype, const void* grad_out,
-                                 const double* row_state, const int32_t* cu_seqlens, const int32_t* cu_block_lens,
-                                 const int32_t* row_ptr, const int32_t* query_indices, int64_t num_seqs,
-                                 int64_t total_tokens, int64_t q_heads, int64_t kv_groups, int64_t head_dim,
-                                 int64_t total_blocks, int64_t block_size, double scale, void* grad_k, void* grad_v,
-                                 void* workspace, int64_t workspace_bytes, void* stream) {
-  if (!valid_common(num_seqs, total_tokens, q_heads, kv_groups, head_dim, block_size) || total_blocks < 0 ||
-      row_state == nullptr)
-    return kErrInvalidArgument;
-  if (total_tokens == 0 || (!grad_k && !grad_v)) return kOk;
-  if (head_dim > 512) return kErrUnsupported;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const int nseq = static_cast<int>(num_seqs), Hq = static_cast<int>(q_heads), G = static_cast<int>(kv_groups);
-  const int D = static_cast<int>(head_dim), B = static_cast<int>(block_size);
-  if (dtype == kBF16 && attn_mfma_supported(Hq / G, D, B)) {
-    return attn_bwd_dkdv_mfma(q, k, v, grad_out, row_state, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq,
-                              total_tokens, Hq, G, D, total_blocks, B, static_cast<float>(scale), grad_k, grad_v,
-                              workspace, workspace_bytes, st);
-  }
+  if (rc != kOk || !need_kv) return rc;
   switch (dtype) {
     case kF32: return attn_dkdv_valu_dispatch<kF32>(q, k, v, grad_out, row_state, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq, total_tokens, Hq, G, D, B, scale, grad_k, grad_v, st);
     case kF16: return attn_dkdv_valu_dispatch<kF16>(q, k, v, grad_out, row_state, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq, total_tokens, Hq, G, D, B, scale, grad_k, grad_v, st);
-    case kBF16: return attn_dkdv_valu_dispatch<kBF16>(q, k, v, grad_out, row_state, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq, total_tokens, Hq, G, D, B, scale, grad_k, grad_v, st);
-    default: return kErrInvalidArgument;
+    default: return attn_dkdv_valu_dispatch<kBF16>(q, k, v, grad_out, row_state, cu_seqlens, cu_block_lens, row_ptr, query_indices, nseq, total_tokens, Hq, G, D, B, scale, grad_k, grad_v, st);
   }
 }

@@ -1,0 +1,82 @@
+// Shared pieces of the KV-major stage-3 kernels (bf16 MFMA path).
+//
+// The k2q CSR has one row per (key block, group); its edges are the (query
+// token, slot) pairs that selected the block, ordered by query token. KV-major
+// passes walk the edges of a row with the row's K/V block resident on chip.
+// Query tokens are cut into chunks of tc tokens so that per-(token, head, slot)
+// partial buffers stay bounded; within a row, the edges of one chunk form a
+// contiguous range. A plan lists, per chunk, work items (row, first edge) of at
+// most `epi` edges each.
+#pragma once
+#include "attn_mfma.hpp"
+#include "mfma_util.hpp"
+
+namespace msa {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr double kLn2 = 0.6931471805599453;
+
+// Two 8-byte reads of tile[row][base + pi(q4, j)] where pi(q4, j) = 16*(j/4) + 4*q4 + j%4.
+__device__ __forceinline__ bf16x8 read_keys_pi(const uint16_t* tile, int stride, int row, int base, int q4) {
+  const uint16_t* p = tile + row * stride + base + 4 * q4;
+  const uint2 a = *reinterpret_cast<const uint2*>(p);
+  const uint2 b = *reinterpret_cast<const uint2*>(p + 16);
+  return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
+
+struct RowGeom {
+  int64_t kb;  // first key of the block
+  int nk;      // keys in the block
+  int g;
+};
+
+// Geometry of CSR row (global block gb = row / G, group row % G).
+__device__ __forceinline__ RowGeom row_geom(const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks,
+                                            int nseq, int64_t row, int G, int B) {
+  const int64_t gb = row / G;
+  int s = upper_index(cu_blocks, nseq + 1, gb);
+  while (s < nseq && cu_blocks[s + 1] <= gb) ++s;
+  RowGeom r;
+  r.g = static_cast<int>(row % G);
+  r.kb = cu[s] + (gb - cu_blocks[s]) * B;
+  const int64_t end = cu[s + 1];
+  r.nk = static_cast<int>(end - r.kb < B ? end - r.kb : B);
+  return r;
+}
+
+inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+// Query tokens per chunk: per-(token, head, slot) records of `record_bytes`
+// each, within ~1 GiB.
+int64_t kv_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t record_bytes);
+
+struct KvPlan {
+  int64_t rows, tc, nch, epi, max_items;  // max_items: per-chunk upper bound on work items
+  int64_t bounds, starts, items, bytes;   // byte offsets of the arrays inside the plan area, total size
+};
+
+KvPlan kv_plan_layout(int64_t T, int64_t rows, int64_t G, int64_t K, int64_t tc, int64_t epi);
+
+// Fills bounds[(nch + 1) x rows], starts[nch x (rows + 1)] and items[nch x max_items]
+// (int2: row, first edge) in the plan area at `base`.
+void kv_plan_launch(const KvPlan& p, const int32_t* row_ptr, const int32_t* qidx, int64_t T, void* base,
+                    hipStream_t st);
+
+// Per chunk views of a launched plan.
+inline const int32_t* kv_plan_hi(const KvPlan& p, const void* base, int64_t c) {
+  return reinterpret_cast<const int32_t*>(static_cast<const char*>(base) + p.bounds) + (c + 1) * p.rows;
+}
+inline const int32_t* kv_plan_lo(const KvPlan& p, const void* base, int64_t c) {
+  return reinterpret_cast<const int32_t*>(static_cast<const char*>(base) + p.bounds) + c * p.rows;
+}
+inline const int32_t* kv_plan_count(const KvPlan& p, const void* base, int64_t c) {
+  return reinterpret_cast<const int32_t*>(static_cast<const char*>(base) + p.starts) + c * (p.rows + 1) + p.rows;
+}
+inline const int32_t* kv_plan_starts(const KvPlan& p, const void* base, int64_t c) {
+  return reinterpret_cast<const int32_t*>(static_cast<const char*>(base) + p.starts) + c * (p.rows + 1);
+}
+inline const int2* kv_plan_items(const KvPlan& p, const void* base, int64_t c) {
+  return reinterpret_cast<const int2*>(static_cast<const char*>(base) + p.items) + c * p.max_items;
+}
+
+}  // namespace msa

@@ -20,8 +20,11 @@
 // The logits use the K row fragment and the Q row fragment over the same dims
 // in the same k order as the backward kernels. P.V is computed exactly in its
 // products: P is split into three bf16 terms (hi + mid + lo == P).
-#include "attn_mfma.hpp"
-#include "mfma_util.hpp"
+#include "attn_kv_common.hpp"
+
+// Logits are x = fl(acc * scale2) with their own rounding, and exponent arguments
+// x - m with another: no fused multiply-adds, so a row's maximum gets p == 1 exactly.
+#pragma clang fp contract(off)
 
 namespace msa {
 
@@ -30,7 +33,6 @@ namespace {
 constexpr int kRowsPerTile = 128;  // (edge, head) rows per tile: 4 waves x 32
 constexpr int kTilesPerItem = 4;   // tiles per work item
 constexpr int kItemRows = kRowsPerTile * kTilesPerItem;
-constexpr float kLog2e = 1.4426950408889634f;
 
 template <int NK>
 struct FwdSmem {
@@ -44,40 +46,13 @@ struct FwdSmem {
   int32_t rec[kItemRows];  // partial record ((token - t0) * Hq + head) * K + slot
 };
 
-// Two 8-byte reads of tile[row][base + pi(q4, j)] where pi(q4, j) = 16*(j/4) + 4*q4 + j%4.
-__device__ __forceinline__ bf16x8 read_keys_pi(const uint16_t* tile, int stride, int row, int base, int q4) {
-  const uint16_t* p = tile + row * stride + base + 4 * q4;
-  const uint2 a = *reinterpret_cast<const uint2*>(p);
-  const uint2 b = *reinterpret_cast<const uint2*>(p + 16);
-  return __builtin_bit_cast(bf16x8, make_uint4(a.x, a.y, b.x, b.y));
-}
-
-struct RowGeom {
-  int64_t kb;  // first key of the block
-  int nk;      // keys in the block
-  int g;
-};
-
-__device__ __forceinline__ RowGeom row_geom(const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks,
-                                            int nseq, int64_t row, int G, int B) {
-  const int64_t gb = row / G;
-  int s = upper_index(cu_blocks, nseq + 1, gb);
-  while (s < nseq && cu_blocks[s + 1] <= gb) ++s;
-  RowGeom r;
-  r.g = static_cast<int>(row % G);
-  r.kb = cu[s] + (gb - cu_blocks[s]) * B;
-  const int64_t end = cu[s + 1];
-  r.nk = static_cast<int>(end - r.kb < B ? end - r.kb : B);
-  return r;
-}
-
 }  // namespace
 
 // Per row, the first edge whose query token is >= c * tc, for c = 0..nch
 // (bounds[c * rows + row]); bound nch is the row end.
-__global__ __launch_bounds__(256) void fwd_chunk_bounds(const int32_t* __restrict__ row_ptr,
-                                                        const int32_t* __restrict__ qidx, int64_t rows, int64_t T,
-                                                        int64_t tc, int nch, int32_t* __restrict__ bounds) {
+__global__ __launch_bounds__(256) void kv_chunk_bounds(const int32_t* __restrict__ row_ptr,
+                                                       const int32_t* __restrict__ qidx, int64_t rows, int64_t T,
+                                                       int64_t tc, int nch, int32_t* __restrict__ bounds) {
   const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (r >= rows) return;
   const int32_t a = row_ptr[r], b = row_ptr[r + 1];
@@ -96,7 +71,7 @@ __global__ __launch_bounds__(256) void fwd_chunk_bounds(const int32_t* __restric
 // For chunk blockIdx.x: the exclusive prefix over rows of ceil(edges / epi) work
 // items, item_start[c * (rows + 1) + row], with the chunk total at index rows,
 // and the item table items[c * max_items + i] = (row, first edge of the item).
-__global__ __launch_bounds__(1024) void fwd_item_scan(const int32_t* __restrict__ bounds, int64_t rows, int epi,
+__global__ __launch_bounds__(1024) void kv_item_scan(const int32_t* __restrict__ bounds, int64_t rows, int epi,
                                                       int64_t max_items, int32_t* __restrict__ item_start,
                                                       int2* __restrict__ items) {
   __shared__ int32_t wsum[16];
@@ -268,55 +243,30 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     }
     // Q fragments are dead: prefetch the next tile's rows.
     if (tile + 1 < ntiles) load_q(r0 + kRowsPerTile);
-    // ---- base-2 partial softmax per row (rows of the lane's quad share c).
-    // m = fl(scale2 * a*) where a* is the max (scale2 > 0) or min (scale2 < 0) raw
-    // logit; p = 2^(scale2 * a - m) with one rounding (fma). The rounding of m is a
-    // common factor of the row's p, l and O, so it cancels in O / l.
+    // ---- base-2 partial softmax per row (rows of the lane's quad share c):
+    // x = fl(acc * scale2), m = max x, p = 2^(x - m) (exactly 1 at the maximum).
     const bool full = __ballot(lim[0] < 128 || lim[1] < 128) == 0;
     float mrow[2], lrow[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      float a = scale2 >= 0.f ? -__builtin_inff() : __builtin_inff();
-      if (full) {
-        if (scale2 >= 0.f) {
+      float m = -__builtin_inff();
 #pragma unroll
-          for (int kt = 0; kt < 8; ++kt)
-            a = fmaxf(a, fmaxf(fmaxf(s[rt][kt][0], s[rt][kt][1]), fmaxf(s[rt][kt][2], s[rt][kt][3])));
-        } else {
+      for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
-          for (int kt = 0; kt < 8; ++kt)
-            a = fminf(a, fminf(fminf(s[rt][kt][0], s[rt][kt][1]), fminf(s[rt][kt][2], s[rt][kt][3])));
+        for (int i = 0; i < 4; ++i) {
+          float x = s[rt][kt][i] * scale2;
+          if (!full) x = (16 * kt + 4 * q4 + i < lim[rt]) ? x : -__builtin_inff();
+          s[rt][kt][i] = x;
+          m = fmaxf(m, x);
         }
-      } else {
-        // invisible keys get a raw logit that loses the max/min and underflows 2^(...)
-        const float hide = scale2 >= 0.f ? -__builtin_inff() : __builtin_inff();
-#pragma unroll
-        for (int kt = 0; kt < 8; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float x = (16 * kt + 4 * q4 + i < lim[rt]) ? s[rt][kt][i] : hide;
-            s[rt][kt][i] = x;
-            a = scale2 >= 0.f ? fmaxf(a, x) : fminf(a, x);
-          }
-      }
-      if (scale2 >= 0.f) {
-        a = fmaxf(a, __shfl_xor(a, 16, kWave));
-        a = fmaxf(a, __shfl_xor(a, 32, kWave));
-      } else {
-        a = fminf(a, __shfl_xor(a, 16, kWave));
-        a = fminf(a, __shfl_xor(a, 32, kWave));
-      }
-      const bool none = (a == -__builtin_inff() || a == __builtin_inff());  // row without visible keys
-      const float m = none ? -__builtin_inff() : a * scale2;
-      const float nm = none ? 0.f : -m;
+      m = quad_max(m);
+      const float base = m == -__builtin_inff() ? 0.f : m;
       float l = 0.f;
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          // hidden keys: scale2 * (-+inf) = -inf (or NaN when scale2 == 0, mapped to 0 below)
-          float p = __builtin_amdgcn_exp2f(fmaf(s[rt][kt][i], scale2, nm));
-          if (!full) p = (16 * kt + 4 * q4 + i < lim[rt]) ? p : 0.f;
+          const float p = __builtin_amdgcn_exp2f(s[rt][kt][i] - base);
           s[rt][kt][i] = p;
           l += p;
         }
@@ -448,9 +398,11 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
     *reinterpret_cast<uint2*>(out + th * D + 4 * sub) = make_uint2(w2[0], w2[1]);
   }
   if (sub == 0) {
-    const double full = has ? (static_cast<double>(M) + log2(L)) * 0.6931471805599453 : -__builtin_inf();
-    lse[th] = static_cast<float>(full);
-    if (row_state) row_state[th * 4] = full;
+    // row_state keeps the base-2 lse (the backward's p = 2^(x - lse2) is then exactly
+    // 1 for a row whose only visible key attains it); the public lse is natural.
+    const double lse2 = has ? static_cast<double>(M) + log2(L) : -__builtin_inf();
+    lse[th] = static_cast<float>(lse2 * kLn2);
+    if (row_state) row_state[th * 4] = lse2;
   }
 }
 
@@ -458,38 +410,57 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
 
 static int nk_of_dim(int D) { return D <= 32 ? 1 : (D <= 64 ? 2 : 4); }
 
-static int64_t fwd_epi(int R) {
+static int64_t fwd_epi(int64_t R) {
   const int64_t e = static_cast<int64_t>(kRowsPerTile) * kTilesPerItem / R;
   return e < 1 ? 1 : e;
 }
 
-static int64_t fwd_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t D) {
-  // partial budget: opart + mlpart per token, capped at ~1 GiB (fewer, fuller work items per row)
-  const int64_t per_token = Hq * K * (D + 2) * 4;
+int64_t kv_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t record_bytes) {
+  const int64_t per_token = Hq * (K > 0 ? K : 1) * record_bytes;
   int64_t tc = (int64_t(1) << 30) / (per_token > 0 ? per_token : 1);
   if (tc < 64) tc = 64;
   return tc < T ? tc : (T > 0 ? T : 1);
 }
 
-static int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+KvPlan kv_plan_layout(int64_t T, int64_t rows, int64_t G, int64_t K, int64_t tc, int64_t epi) {
+  KvPlan p;
+  p.rows = rows;
+  p.tc = tc;
+  p.nch = (T + tc - 1) / tc;
+  p.epi = epi;
+  // one item per row plus one per epi edges of the chunk (a chunk holds <= tc * G * K edges)
+  p.max_items = rows + (tc * G * K) / epi + 1;
+  p.bounds = 0;
+  p.starts = align256((p.nch + 1) * rows * 4);
+  p.items = p.starts + align256(p.nch * (rows + 1) * 4);
+  p.bytes = p.items + align256(p.nch * p.max_items * 8);
+  return p;
+}
+
+void kv_plan_launch(const KvPlan& p, const int32_t* row_ptr, const int32_t* qidx, int64_t T, void* base,
+                    hipStream_t st) {
+  if (p.rows <= 0) return;
+  char* b = static_cast<char*>(base);
+  int32_t* bounds = reinterpret_cast<int32_t*>(b + p.bounds);
+  hipLaunchKernelGGL(kv_chunk_bounds, dim3(grid_1d(p.rows, 256)), dim3(256), 0, st, row_ptr, qidx, p.rows, T, p.tc,
+                     static_cast<int>(p.nch), bounds);
+  hipLaunchKernelGGL(kv_item_scan, dim3(static_cast<unsigned>(p.nch)), dim3(1024), 0, st, bounds, p.rows,
+                     static_cast<int>(p.epi), p.max_items, reinterpret_cast<int32_t*>(b + p.starts),
+                     reinterpret_cast<int2*>(b + p.items));
+}
 
 struct FwdLayout {
-  int64_t tc, nch, max_items, bounds, starts, items, opart, ml, total;
+  KvPlan plan;
+  int64_t opart, ml, total;
 };
 
 static FwdLayout fwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks) {
   FwdLayout f;
-  const int64_t rows = total_blocks * G;
-  f.tc = fwd_chunk_tokens(T, Hq, K, D);
-  f.nch = (T + f.tc - 1) / f.tc;
-  // upper bound on a chunk's work items: one per row plus one per epi edges of the chunk
-  f.max_items = rows + (f.tc * G * K) / fwd_epi(static_cast<int>(Hq / (G > 0 ? G : 1))) + 1;
-  f.bounds = 0;
-  f.starts = align256((f.nch + 1) * rows * 4);
-  f.items = f.starts + align256(f.nch * (rows + 1) * 4);
-  f.opart = f.items + align256(f.nch * f.max_items * 8);
-  f.ml = f.opart + align256(f.tc * Hq * K * D * 4);
-  f.total = f.ml + align256(f.tc * Hq * K * 8);
+  const int64_t tc = kv_chunk_tokens(T, Hq, K, (D + 2) * 4);
+  f.plan = kv_plan_layout(T, total_blocks * G, G, K, tc, fwd_epi(Hq / (G > 0 ? G : 1)));
+  f.opart = f.plan.bytes;
+  f.ml = f.opart + align256(tc * Hq * K * D * 4);
+  f.total = f.ml + align256(tc * Hq * K * 8);
   return f;
 }
 
@@ -508,31 +479,23 @@ int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indi
   if (T * Hq * (K > 0 ? K : 1) >= (int64_t(1) << 31) || rows >= (int64_t(1) << 31)) return kErrUnsupported;
   if (T == 0) return kOk;
   char* base = static_cast<char*>(ws);
-  int32_t* bounds = reinterpret_cast<int32_t*>(base + f.bounds);
-  int32_t* starts = reinterpret_cast<int32_t*>(base + f.starts);
-  int2* items = reinterpret_cast<int2*>(base + f.items);
   float* opart = reinterpret_cast<float*>(base + f.opart);
   float2* ml = reinterpret_cast<float2*>(base + f.ml);
-  const int R = Hq / G;
-  const int epi = static_cast<int>(fwd_epi(R));
+  const KvPlan& pl = f.plan;
+  const int epi = static_cast<int>(pl.epi);
   const float scale2 = scale * kLog2e;
   const auto* qb = static_cast<const uint16_t*>(q);
   const auto* kb = static_cast<const uint16_t*>(k);
   const auto* vb = static_cast<const uint16_t*>(v);
   auto* ob = static_cast<uint16_t*>(out);
-  if (rows > 0) {
-    hipLaunchKernelGGL(fwd_chunk_bounds, dim3(grid_1d(rows, 256)), dim3(256), 0, st, row_ptr, qidx, rows, T, f.tc,
-                       static_cast<int>(f.nch), bounds);
-    hipLaunchKernelGGL(fwd_item_scan, dim3(static_cast<unsigned>(f.nch)), dim3(1024), 0, st, bounds, rows, epi,
-                       f.max_items, starts, items);
-  }
-  for (int64_t c = 0; c < f.nch; ++c) {
-    const int64_t t0 = c * f.tc, t1 = t0 + f.tc < T ? t0 + f.tc : T;
+  kv_plan_launch(pl, row_ptr, qidx, T, base, st);
+  for (int64_t c = 0; c < pl.nch; ++c) {
+    const int64_t t0 = c * pl.tc, t1 = t0 + pl.tc < T ? t0 + pl.tc : T;
     if (rows > 0) {
-      const dim3 grid(static_cast<unsigned>(f.max_items)), block(256);
-      const int32_t* hi = bounds + (c + 1) * rows;
-      const int32_t* nit = starts + c * (rows + 1) + rows;
-      const int2* its = items + c * f.max_items;
+      const dim3 grid(static_cast<unsigned>(pl.max_items)), block(256);
+      const int32_t* hi = kv_plan_hi(pl, base, c);
+      const int32_t* nit = kv_plan_count(pl, base, c);
+      const int2* its = kv_plan_items(pl, base, c);
       const int it0 = static_cast<int>(t0);
 #define MSA_FWD_PARTIAL(NKV, FD) hipLaunchKernelGGL((attn_fwd_partial_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, epi, it0, opart, ml)
       const int nk = nk_of_dim(D);

@@ -24,6 +24,14 @@ int attn_bwd_dkdv_mfma(const void* q, const void* k, const void* v, const void* 
 
 int64_t attn_fwd_kv_workspace_bytes(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks);
 
+int64_t attn_bwd_kv_workspace_bytes(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks);
+
+int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, const void* dout, double* rs,
+                const int32_t* indices, const int32_t* cu, int nseq, int64_t T, int Hq, int G, int D, int K, int B,
+                float scale, const int32_t* cu_blocks, int64_t total_blocks, const int32_t* row_ptr,
+                const int32_t* qidx, const int32_t* sidx, void* dq, void* dk, void* dv, void* ws, int64_t ws_bytes,
+                hipStream_t st);
+
 int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indices, const int32_t* cu, int nseq,
                 int64_t T, int Hq, int G, int D, int K, int B, float scale, const int32_t* cu_blocks,
                 int64_t total_blocks, const int32_t* row_ptr, const int32_t* qidx, const int32_t* sidx, void* ws,

@@ -3,17 +3,15 @@
 Mirrors triton/sparse_attention.py:429-485 of the reference (signature,
 defaults, validation order, messages and exception types) and the
 ``_SparseAttention`` autograd contract (:334-395): per-input
-``needs_input_grad``; the query pass always runs when any grad is needed
-(it produces the per-row statistics the KV pass consumes); the k2q CSR is
-built only when dK or dV is needed; lse is non-differentiable.
+``needs_input_grad``; the public ``build_k2q_csr`` is invoked by the backward
+exactly when dK or dV is needed; lse is non-differentiable.
 
-Execution: ``msa_attn_fwd`` (KV-major over the selection's k2q CSR for bf16:
-per-block partial softmax + ordered combine; saves lse), ``msa_attn_bwd_dq``
-(dQ and per-row statistics: probability mass, center, centered delta),
-``build_k2q_csr`` and ``msa_attn_bwd_dkdv`` (dK/dV owned per key block and
-group, no floating-point atomics). Saved state is q, k, v, out and lse in the
-input dtype plus an fp64 [T,Hq,4] per-row state (full-precision lse, then the
-backward's mass / center / delta); no fp32 staging copies of q/k/v/out.
+Execution: ``msa_attn_fwd`` and ``msa_attn_bwd``. For bf16 both are KV-major
+over the selection's k2q CSR (per-block partials merged in slot order, dK/dV
+owned per key block, no floating-point atomics); the forward builds the CSR
+itself and keeps it for a backward that needs only dQ. Saved state is q, k, v,
+out in the input dtype plus an fp64 [T,Hq,4] per-row state (full-precision
+lse, then the backward's mass / center / delta); no fp32 staging copies.
 """
 
 from __future__ import annotations
@@ -37,15 +35,15 @@ class _SparseAttention(torch.autograd.Function):
         groups = k.shape[1]
         out = torch.empty_like(q)
         lse = torch.empty((total, heads), device=q.device, dtype=torch.float32)
-        # Private fp64 per-row state shared by the three kernels: lse, mass, center, delta.
+        # Private fp64 per-row state shared by forward and backward: lse, mass, center, delta.
         row_state = torch.empty((total, heads, 4), device=q.device, dtype=torch.float64)
+        csr = None
         if total:
             lib = _lib.lib()
             dtype = _lib.DTYPE_CODE[q.dtype]
             slots = indices.shape[2]
             ws_bytes = lib.msa_attn_fwd_workspace_bytes(dtype, total, heads, groups, dim, slots,
                                                         meta.total_blocks, block_size)
-            csr = None
             workspace = None
             if ws_bytes > 0:
                 # The KV-major forward walks the block->query CSR of the selection.
@@ -63,6 +61,10 @@ class _SparseAttention(torch.autograd.Function):
                 )
             _lib.check(status, "msa_attn_fwd")
         ctx.save_for_backward(q, k, v, indices, cu, out, row_state)
+        # A backward that needs dK or dV rebuilds the CSR through the public builder
+        # (as the reference does); a dQ-only backward reuses the forward's.
+        need_kv = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
+        ctx.csr = None if need_kv else csr
         ctx.meta = meta
         ctx.scale = scale
         ctx.block_size = block_size
@@ -80,36 +82,37 @@ class _SparseAttention(torch.autograd.Function):
         dv = torch.empty_like(v) if need_v else None
         total, heads, dim = q.shape
         groups = k.shape[1]
+        slots = indices.shape[2]
         if total and (need_q or need_kv):
             lib = _lib.lib()
             device = q.device
-            stream = _lib.stream_of(device)
+            dtype = _lib.DTYPE_CODE[q.dtype]
             if grad_output is None:
                 grad_output = torch.zeros_like(out)
             dout = grad_output.to(q.dtype).contiguous()
-            with torch.cuda.device(device):
-                status = lib.msa_attn_bwd_dq(
-                    q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[q.dtype], out.data_ptr(),
-                    dout.data_ptr(), row_state.data_ptr(), indices.data_ptr(), cu.data_ptr(), meta.num_seqs,
-                    total, heads, groups, dim, indices.shape[2], ctx.block_size, ctx.scale, _lib.ptr(dq), stream,
-                )
-            _lib.check(status, "msa_attn_bwd_dq")
+            ws_bytes = lib.msa_attn_bwd_workspace_bytes(dtype, total, heads, groups, dim, slots, meta.total_blocks,
+                                                        ctx.block_size)
             if need_kv:
                 # Looked up through the module so the CSR build stays observable.
                 csr = _k2q.build_k2q_csr(indices, cu, block_size=ctx.block_size)
-                ws_bytes = lib.msa_attn_bwd_workspace_bytes(
-                    total, heads, groups, dim, indices.shape[2], meta.total_blocks, ctx.block_size
+            elif ws_bytes > 0:
+                csr = ctx.csr if ctx.csr is not None else _k2q._build_device(indices, cu, meta, groups, slots)
+            else:
+                csr = None
+            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
+            with torch.cuda.device(device):
+                status = lib.msa_attn_bwd(
+                    q.data_ptr(), k.data_ptr(), v.data_ptr(), dtype, out.data_ptr(), dout.data_ptr(),
+                    row_state.data_ptr(), indices.data_ptr(), cu.data_ptr(), meta.num_seqs, total, heads, groups,
+                    dim, slots, ctx.block_size, ctx.scale,
+                    _lib.ptr(None if csr is None else csr.cu_block_lens), meta.total_blocks,
+                    _lib.ptr(None if csr is None else csr.row_ptr),
+                    _lib.ptr(None if csr is None else csr.query_indices),
+                    _lib.ptr(None if csr is None else csr.slot_indices), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+                    _lib.ptr(workspace), ws_bytes, _lib.stream_of(device),
                 )
-                workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
-                with torch.cuda.device(device):
-                    status = lib.msa_attn_bwd_dkdv(
-                        q.data_ptr(), k.data_ptr(), v.data_ptr(), _lib.DTYPE_CODE[q.dtype], dout.data_ptr(),
-                        row_state.data_ptr(), cu.data_ptr(), csr.cu_block_lens.data_ptr(),
-                        csr.row_ptr.data_ptr(), csr.query_indices.data_ptr(), meta.num_seqs, total, heads,
-                        groups, dim, meta.total_blocks, ctx.block_size, ctx.scale, _lib.ptr(dk), _lib.ptr(dv),
-                        workspace.data_ptr(), ws_bytes, stream,
-                    )
-                _lib.check(status, "msa_attn_bwd_dkdv")
+            _lib.check(status, "msa_attn_bwd")
+        ctx.csr = None
         return dq, dk, dv, None, None, None, None, None
 
 
