@@ -52,15 +52,12 @@ struct StatSmem {
 template <int NK>
 struct MainSmem {
   static constexpr int DP = 32 * NK;
-  static constexpr int KS = DP + 8;   // row stride of the Q / dO row tiles
-  static constexpr int TS = 128 + 8;  // key stride of K^T and of the dS planes
-  static constexpr int RS = 32 + 8;   // row stride of the transposed Q / dO tiles
-  alignas(16) uint16_t kt[DP * TS];   // K^T [dim][key]
+  static constexpr int KS = DP + 8;   // row stride of the K block and of the Q / dO row tiles
+  static constexpr int PS = 32 + 16;  // row stride of the dS planes [key][row]
+  alignas(16) uint16_t k[128 * KS];   // K block [key][dim]
   alignas(16) uint16_t qs[32 * KS];   // Q rows [row][dim]
   alignas(16) uint16_t gs[32 * KS];   // dO rows
-  alignas(16) uint16_t qt[DP * RS];   // Q^T [dim][row]
-  alignas(16) uint16_t gt[DP * RS];   // dO^T
-  alignas(16) uint16_t ds[3][32 * TS];  // dS split planes [row][key]
+  alignas(16) uint16_t ds[3][128 * PS];  // dS split planes (hi, mid, lo) [key][row]
   float4 stats[kMetaRows];            // lse2, 1 / mass, c, delta
   int32_t th[kMetaRows];
   int32_t tok[kMetaRows];
@@ -263,9 +260,10 @@ __global__ __launch_bounds__(256) void kv_bwd_stats_combine(const int32_t* __res
 // B2: one workgroup per work item (key block row, <= kMainEdges edges); wave w owns
 // keys 32w .. 32w + 31 of the block. Per 32-row tile (all waves, same rows):
 //   S = Q K^T, dP = dO V^T (C[row][key]: lane = key c, rows 4*q4 + i),
-//   dV += P^T dO and dK += dS^T Q (B operands from the transposed row tiles),
-//   dS -> three bf16 planes in LDS, then dQ^T = K^T dS^T over all 128 keys for the
-//   wave's dims (lane: row c, 4 consecutive dims) -> per-(row, block) partial.
+//   dV += P^T dO and dK += dS^T Q (B operands read transposed from the row tiles),
+//   dS -> three bf16 planes [key][row] in LDS, then dQ^T = K^T dS^T over all 128
+//   keys for the wave's dim tiles (lane: row c, 4 consecutive dims) -> per-(row,
+//   block) partial. The next tile's Q / dO rows are loaded during the current one.
 template <int NK, bool FULLD>
 __global__ __launch_bounds__(256, 1) void kv_bwd_main_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
@@ -274,7 +272,9 @@ __global__ __launch_bounds__(256, 1) void kv_bwd_main_kernel(
     const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items, const int2* __restrict__ items, int nseq,
     int Hq, int G, int D, int K, int B, float scale2, float scale, int epi, int t0, float* __restrict__ dqpart,
     float* __restrict__ kvpart) {
-  constexpr int DP = 32 * NK, NDT = DP / 16, KS = MainSmem<NK>::KS, TS = MainSmem<NK>::TS, RS = MainSmem<NK>::RS;
+  constexpr int DP = 32 * NK, NDT = DP / 16, KS = MainSmem<NK>::KS, PS = MainSmem<NK>::PS;
+  constexpr int NQT = (NDT + 3) / 4;  // dQ dim tiles per wave
+  constexpr int SI = 32 * (DP / 8) / 256 > 0 ? 32 * (DP / 8) / 256 : 1;  // 16-byte row loads per thread
   __shared__ MainSmem<NK> sm;
   const int item = blockIdx.x;
   if (item >= *n_items) return;
@@ -286,7 +286,7 @@ __global__ __launch_bounds__(256, 1) void kv_bwd_main_kernel(
   const int e_end = e_begin + epi < e_hi[row] ? e_begin + epi : e_hi[row];
   const int nrows = (e_end - e_begin) * R;
 
-  // ---- K / V fragments of this wave's keys (B operands of S and dP) and K^T in LDS
+  // ---- K / V fragments of this wave's keys (B operands of S and dP); K block in LDS
   bf16x8 kf[2][NK], vf[2][NK];
 #pragma unroll
   for (int kt = 0; kt < 2; ++kt) {
@@ -309,21 +309,16 @@ __global__ __launch_bounds__(256, 1) void kv_bwd_main_kernel(
 #pragma unroll
     for (int i = 0; i < KVI; ++i) {
       const int e = tid + 256 * i;
-      const int kl = e & 127, d0 = 8 * (e >> 7);
+      const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));
       const int klc = kl < rg.nk ? kl : rg.nk - 1, d0c = (FULLD || d0 < D) ? d0 : D - 8;
       kw[i] = *reinterpret_cast<const uint4*>(k + ((rg.kb + klc) * G + rg.g) * D + d0c);
     }
 #pragma unroll
     for (int i = 0; i < KVI; ++i) {
       const int e = tid + 256 * i;
-      const int kl = e & 127, d0 = 8 * (e >> 7);
+      const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));
       const bool ok = kl < rg.nk && (FULLD || d0 < D);
-      const uint32_t w4[4] = {ok ? kw[i].x : 0u, ok ? kw[i].y : 0u, ok ? kw[i].z : 0u, ok ? kw[i].w : 0u};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        sm.kt[(d0 + 2 * j) * TS + kl] = static_cast<uint16_t>(w4[j] & 0xffffu);
-        sm.kt[(d0 + 2 * j + 1) * TS + kl] = static_cast<uint16_t>(w4[j] >> 16);
-      }
+      *reinterpret_cast<uint4*>(sm.k + kl * KS + d0) = ok ? kw[i] : make_uint4(0u, 0u, 0u, 0u);
     }
   }
 
@@ -333,9 +328,36 @@ __global__ __launch_bounds__(256, 1) void kv_bwd_main_kernel(
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) dk[kt][dt] = dv[kt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // 32 Q / dO rows of a tile: thread e covers row e % 32, dims 8 * (e / 32) .. +7
+  uint4 qw[SI], gw[SI];
+  auto load_rows = [&](int r0, int mb, int mend) {
+#pragma unroll
+    for (int i = 0; i < SI; ++i) {
+      const int e = tid + 256 * i;
+      const int rr = e & 31, d0 = 8 * (e >> 5);
+      const int rho = r0 + rr < mend ? r0 + rr : mend - 1;
+      const int d0c = d0 < DP ? ((FULLD || d0 < D) ? d0 : D - 8) : 0;
+      const int64_t off = static_cast<int64_t>(sm.th[rho - mb]) * D + d0c;
+      qw[i] = *reinterpret_cast<const uint4*>(q + off);
+      gw[i] = *reinterpret_cast<const uint4*>(dout + off);
+    }
+  };
+  auto store_rows = [&](int r0, int mend) {
+#pragma unroll
+    for (int i = 0; i < SI; ++i) {
+      const int e = tid + 256 * i;
+      const int rr = e & 31, d0 = 8 * (e >> 5);
+      if (d0 < DP) {
+        const bool ok = r0 + rr < mend && (FULLD || d0 < D);
+        *reinterpret_cast<uint4*>(sm.qs + rr * KS + d0) = ok ? qw[i] : make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(sm.gs + rr * KS + d0) = ok ? gw[i] : make_uint4(0u, 0u, 0u, 0u);
+      }
+    }
+  };
+
   for (int mb = 0; mb < nrows; mb += kMetaRows) {
     const int mend = mb + kMetaRows < nrows ? mb + kMetaRows : nrows;
-    __syncthreads();  // previous metadata block no longer read (also publishes K^T on entry)
+    __syncthreads();  // previous metadata block no longer read (also publishes the K block on entry)
     if (tid < kMetaRows) {
       const int rho = mb + tid;
       if (rho < mend) {
@@ -352,44 +374,13 @@ __global__ __launch_bounds__(256, 1) void kv_bwd_main_kernel(
       }
     }
     __syncthreads();
+    load_rows(mb, mb, mend);
 
     for (int r0 = mb; r0 < mend; r0 += 32) {
-      // ---- stage 32 Q / dO rows, row-major and transposed (lanes along rows)
-      {
-        constexpr int SI = 32 * (DP / 8) / 256 > 0 ? 32 * (DP / 8) / 256 : 1;
-        uint4 qw[SI], gw[SI];
-#pragma unroll
-        for (int i = 0; i < SI; ++i) {
-          const int e = tid + 256 * i;
-          const int rr = e & 31, d0 = 8 * (e >> 5);
-          const int rho = r0 + rr < mend ? r0 + rr : mend - 1;
-          const int d0c = (FULLD || d0 < D) ? d0 : D - 8;
-          const int64_t off = static_cast<int64_t>(sm.th[rho - mb]) * D + (d0 < DP ? d0c : 0);
-          qw[i] = *reinterpret_cast<const uint4*>(q + off);
-          gw[i] = *reinterpret_cast<const uint4*>(dout + off);
-        }
-#pragma unroll
-        for (int i = 0; i < SI; ++i) {
-          const int e = tid + 256 * i;
-          const int rr = e & 31, d0 = 8 * (e >> 5);
-          if (d0 < DP) {
-            const bool ok = r0 + rr < mend && (FULLD || d0 < D);
-            const uint4 a = ok ? qw[i] : make_uint4(0u, 0u, 0u, 0u);
-            const uint4 b = ok ? gw[i] : make_uint4(0u, 0u, 0u, 0u);
-            *reinterpret_cast<uint4*>(sm.qs + rr * KS + d0) = a;
-            *reinterpret_cast<uint4*>(sm.gs + rr * KS + d0) = b;
-            const uint32_t a4[4] = {a.x, a.y, a.z, a.w}, b4[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              sm.qt[(d0 + 2 * j) * RS + rr] = static_cast<uint16_t>(a4[j] & 0xffffu);
-              sm.qt[(d0 + 2 * j + 1) * RS + rr] = static_cast<uint16_t>(a4[j] >> 16);
-              sm.gt[(d0 + 2 * j) * RS + rr] = static_cast<uint16_t>(b4[j] & 0xffffu);
-              sm.gt[(d0 + 2 * j + 1) * RS + rr] = static_cast<uint16_t>(b4[j] >> 16);
-            }
-          }
-        }
-      }
+      // All waves passed the previous tile's mid barrier: the row tiles are free.
+      store_rows(r0, mend);
       __syncthreads();
+      if (r0 + 32 < mend) load_rows(r0 + 32, mb, mend);
 
       // ---- S and dP: C[row 16*rt + 4*q4 + i][key 32*wid + 16*kt + c]
       f32x4 s[2][2], dp[2][2];
@@ -413,86 +404,102 @@ __global__ __launch_bounds__(256, 1) void kv_bwd_main_kernel(
           dp[rt][kt] = b;
         }
       }
-      // ---- P and dS (masked), split into bf16 planes
-      uint32_t ph[2][8], pm[2][8], pl[2][8], dh[2][8], dm[2][8], dl[2][8];  // [kt][j], j = 4*rt + i
+      // ---- P and dS (masked) as split bf16 A operands [key c][rows pi(q4, j)], j = 4*rt + i
+      bf16x8 ap[2][3], ad[2][3];  // [kt][hi, mid, lo]
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
+      for (int kt = 0; kt < 2; ++kt) {
+        uint32_t ph[8], pm[8], pl[8], dh[8], dm[8], dl[8];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int rl = 16 * rt + 4 * q4 + i;  // row inside the tile
-          const int rho = r0 + rl;
-          const bool rok = rho < mend;
-          const float4 st = sm.stats[(rok ? rho : mend - 1) - mb];
-          const int64_t vis = rok ? static_cast<int64_t>(sm.tok[rho - mb]) - rg.kb + 1 : 0;
+        for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt) {
+          for (int i = 0; i < 4; ++i) {
+            const int rho = r0 + 16 * rt + 4 * q4 + i;
+            const bool rok = rho < mend;
+            const float4 st = sm.stats[(rok ? rho : mend - 1) - mb];
+            const int64_t vis = rok ? static_cast<int64_t>(sm.tok[rho - mb]) - rg.kb + 1 : 0;
             const int kl = 32 * wid + 16 * kt + c;
             const bool ok = kl < vis && kl < rg.nk;
             const float p = ok ? __builtin_amdgcn_exp2f(s[rt][kt][i] * scale2 - st.x) : 0.f;
             const float P = p * st.y;
             const float dS = ok ? P * ((dp[rt][kt][i] - st.z) - st.w) * scale : 0.f;
-            split3_bits(P, ph[kt][4 * rt + i], pm[kt][4 * rt + i], pl[kt][4 * rt + i]);
-            split3_bits(dS, dh[kt][4 * rt + i], dm[kt][4 * rt + i], dl[kt][4 * rt + i]);
-            uint16_t* plane0 = sm.ds[0] + rl * TS + kl;
-            plane0[0] = static_cast<uint16_t>(dh[kt][4 * rt + i] >> 16);
-            plane0[32 * TS] = static_cast<uint16_t>(dm[kt][4 * rt + i] >> 16);
-            plane0[64 * TS] = static_cast<uint16_t>(dl[kt][4 * rt + i] >> 16);
+            split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
+            split3_bits(dS, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
           }
+        uint32_t w[3][4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          w[0][jj] = pack_hi16(dh[2 * jj], dh[2 * jj + 1]);
+          w[1][jj] = pack_hi16(dm[2 * jj], dm[2 * jj + 1]);
+          w[2][jj] = pack_hi16(dl[2 * jj], dl[2 * jj + 1]);
         }
-      // ---- dV += P^T dO, dK += dS^T Q: A = [key c][rows pi(q4, j)], B = X^T[dim 16*dt + c][rows pi]
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const bf16x8 aph = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(ph[kt][0], ph[kt][1]), pack_hi16(ph[kt][2], ph[kt][3]), pack_hi16(ph[kt][4], ph[kt][5]), pack_hi16(ph[kt][6], ph[kt][7])));
-        const bf16x8 apm = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pm[kt][0], pm[kt][1]), pack_hi16(pm[kt][2], pm[kt][3]), pack_hi16(pm[kt][4], pm[kt][5]), pack_hi16(pm[kt][6], pm[kt][7])));
-        const bf16x8 apl = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pl[kt][0], pl[kt][1]), pack_hi16(pl[kt][2], pl[kt][3]), pack_hi16(pl[kt][4], pl[kt][5]), pack_hi16(pl[kt][6], pl[kt][7])));
-        const bf16x8 adh = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(dh[kt][0], dh[kt][1]), pack_hi16(dh[kt][2], dh[kt][3]), pack_hi16(dh[kt][4], dh[kt][5]), pack_hi16(dh[kt][6], dh[kt][7])));
-        const bf16x8 adm = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(dm[kt][0], dm[kt][1]), pack_hi16(dm[kt][2], dm[kt][3]), pack_hi16(dm[kt][4], dm[kt][5]), pack_hi16(dm[kt][6], dm[kt][7])));
-        const bf16x8 adl = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(dl[kt][0], dl[kt][1]), pack_hi16(dl[kt][2], dl[kt][3]), pack_hi16(dl[kt][4], dl[kt][5]), pack_hi16(dl[kt][6], dl[kt][7])));
+        for (int pl3 = 0; pl3 < 3; ++pl3) {
+          ad[kt][pl3] = __builtin_bit_cast(bf16x8, make_uint4(w[pl3][0], w[pl3][1], w[pl3][2], w[pl3][3]));
+          // dS plane rows: key 32*wid + 16*kt + c, columns (rows) 16*rt + 4*q4 .. +3
+          uint16_t* dst = sm.ds[pl3] + (32 * wid + 16 * kt + c) * PS + 4 * q4;
+          *reinterpret_cast<uint2*>(dst) = make_uint2(w[pl3][0], w[pl3][1]);
+          *reinterpret_cast<uint2*>(dst + 16) = make_uint2(w[pl3][2], w[pl3][3]);
+        }
+        ap[kt][0] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(ph[0], ph[1]), pack_hi16(ph[2], ph[3]), pack_hi16(ph[4], ph[5]), pack_hi16(ph[6], ph[7])));
+        ap[kt][1] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pm[0], pm[1]), pack_hi16(pm[2], pm[3]), pack_hi16(pm[4], pm[5]), pack_hi16(pm[6], pm[7])));
+        ap[kt][2] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pl[0], pl[1]), pack_hi16(pl[2], pl[3]), pack_hi16(pl[4], pl[5]), pack_hi16(pl[6], pl[7])));
+      }
+      // ---- dV += P^T dO, dK += dS^T Q: B = X[rows pi(q4, j)][dim 16*dt + c], read transposed
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const bf16x8 gb = read_keys_pi(sm.gt, RS, 16 * dt + c, 0, q4);
-          const bf16x8 qb = read_keys_pi(sm.qt, RS, 16 * dt + c, 0, q4);
+      for (int dt = 0; dt < NDT; ++dt) {
+        const bf16x8 gb = frag_tr(sm.gs, KS, 4 * q4, 16 + 4 * q4, 16 * dt, c);
+        const bf16x8 qb = frag_tr(sm.qs, KS, 4 * q4, 16 + 4 * q4, 16 * dt, c);
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
           f32x4 a = dv[kt][dt];
-          a = mfma(apl, gb, a);
-          a = mfma(apm, gb, a);
-          dv[kt][dt] = mfma(aph, gb, a);
+          a = mfma(ap[kt][2], gb, a);
+          a = mfma(ap[kt][1], gb, a);
+          dv[kt][dt] = mfma(ap[kt][0], gb, a);
           f32x4 b = dk[kt][dt];
-          b = mfma(adl, qb, b);
-          b = mfma(adm, qb, b);
-          dk[kt][dt] = mfma(adh, qb, b);
+          b = mfma(ad[kt][2], qb, b);
+          b = mfma(ad[kt][1], qb, b);
+          dk[kt][dt] = mfma(ad[kt][0], qb, b);
         }
       }
-      __syncthreads();  // dS planes complete
-      // ---- dQ^T = K^T dS^T for dim tiles dt = wid, wid + 4, ...: C[dim 4*q4 + i][row c]
+      __syncthreads();  // dS planes complete; row tiles no longer read
+      // ---- dQ^T = K^T dS^T for dim tiles dt = wid + 4 * n: C[dim 16*dt + 4*q4 + i][row 16*rt + c]
+      if (wid < NDT) {
+        f32x4 acc[NQT][2];
 #pragma unroll
-      for (int dq_i = 0; dq_i < (NDT + 3) / 4; ++dq_i) {
-        const int dt = wid + 4 * dq_i;
-        if (dt < NDT) {
-          f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        for (int n = 0; n < NQT; ++n) acc[n][0] = acc[n][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int kc = 0; kc < 4; ++kc) {
-            const bf16x8 ka = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(sm.kt + (16 * dt + c) * TS + 32 * kc + 8 * q4));
+        for (int kc = 0; kc < 4; ++kc) {
+          bf16x8 ka[NQT];
 #pragma unroll
-            for (int rt = 0; rt < 2; ++rt) {
-              const uint16_t* dsr = sm.ds[0] + (16 * rt + c) * TS + 32 * kc + 8 * q4;
-              const bf16x8 bl = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(dsr + 64 * TS));
-              const bf16x8 bm = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(dsr + 32 * TS));
-              const bf16x8 bh = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(dsr));
-              acc[rt] = mfma(ka, bl, acc[rt]);
-              acc[rt] = mfma(ka, bm, acc[rt]);
-              acc[rt] = mfma(ka, bh, acc[rt]);
+          for (int n = 0; n < NQT; ++n) {
+            const int dt = wid + 4 * n;
+            ka[n] = dt < NDT ? frag_tr(sm.k, KS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * dt, c) : zero_frag();
+          }
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) {
+            const bf16x8 bl = frag_tr(sm.ds[2], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rt, c);
+            const bf16x8 bm = frag_tr(sm.ds[1], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rt, c);
+            const bf16x8 bh = frag_tr(sm.ds[0], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rt, c);
+#pragma unroll
+            for (int n = 0; n < NQT; ++n) {
+              acc[n][rt] = mfma(ka[n], bl, acc[n][rt]);
+              acc[n][rt] = mfma(ka[n], bm, acc[n][rt]);
+              acc[n][rt] = mfma(ka[n], bh, acc[n][rt]);
             }
           }
+        }
+#pragma unroll
+        for (int n = 0; n < NQT; ++n) {
+          const int dt = wid + 4 * n;
 #pragma unroll
           for (int rt = 0; rt < 2; ++rt) {
             const int rho = r0 + 16 * rt + c;
             const int d0 = 16 * dt + 4 * q4;
-            if (rho < mend && (FULLD || d0 < D))
-              *reinterpret_cast<f32x4*>(dqpart + static_cast<int64_t>(sm.rec[rho - mb]) * D + d0) = acc[rt];
+            if (dt < NDT && rho < mend && (FULLD || d0 < D))
+              *reinterpret_cast<f32x4*>(dqpart + static_cast<int64_t>(sm.rec[rho - mb]) * D + d0) = acc[n][rt];
           }
         }
       }
-      __syncthreads();  // row tiles and dS planes are rewritten by the next tile
     }
   }
 

@@ -3,8 +3,7 @@
 // Query-major attention streams each token's selected K/V blocks (K/V bytes
 // gathered per token = #slots x block x D x 4: ~137 GB at 32K tokens). Here the
 // k2q CSR (built from the indices) drives the work instead: a workgroup owns a
-// (key block, group) row -- its K block (row-major) and V block (transposed)
-// sit in LDS -- and streams the row's edges, i.e. the (query token, slot) pairs
+// (key block, group) row -- its K and V blocks sit in LDS, row-major -- and streams the row's edges, i.e. the (query token, slot) pairs
 // that selected the block, 128 (edge, head) rows per tile. Each (edge, head)
 // row yields a partial softmax over the block in base 2:
 //   m = max_j s_j, l = sum_j 2^(s_j - m), O = sum_j 2^(s_j - m) v_j   (fp32),
@@ -37,10 +36,9 @@ constexpr int kItemRows = kRowsPerTile * kTilesPerItem;
 template <int NK>
 struct FwdSmem {
   static constexpr int DP = 32 * NK;
-  static constexpr int KS = DP + 8;   // row stride of the K block (bf16)
-  static constexpr int VS = 128 + 8;  // key stride of the transposed V block (bf16)
+  static constexpr int KS = DP + 8;   // row stride of the K and V blocks (bf16)
   alignas(16) uint16_t k[128 * KS];
-  alignas(16) uint16_t vt[DP * VS];
+  alignas(16) uint16_t v[128 * KS];
   int32_t th[kItemRows];   // token * Hq + head
   int32_t tok[kItemRows];  // query token
   int32_t rec[kItemRows];  // partial record ((token - t0) * Hq + head) * K + slot
@@ -125,7 +123,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     const int32_t* __restrict__ sidx, const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items,
     const int2* __restrict__ items, int nseq, int Hq, int G, int D, int K, int B, float scale2, int epi, int t0,
     float* __restrict__ opart, float2* __restrict__ mlpart) {
-  constexpr int DP = 32 * NK, NDT = DP / 16, KS = FwdSmem<NK>::KS, VS = FwdSmem<NK>::VS;
+  constexpr int DP = 32 * NK, NDT = DP / 16, KS = FwdSmem<NK>::KS;
   __shared__ FwdSmem<NK> sm;
   const int item = blockIdx.x;
   if (item >= *n_items) return;
@@ -137,8 +135,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
   const int e_end = e_begin + epi < e_hi[row] ? e_begin + epi : e_hi[row];
   const int nrows = (e_end - e_begin) * R;  // <= kItemRows
 
-  // ---- stage the K block (row-major), the V block (transposed) and the item's
-  // row metadata in LDS. All global loads are issued before any LDS store.
+  // ---- stage the K and V blocks (row-major) and the item's row metadata in LDS.
+  // All global loads are issued before any LDS store.
   constexpr int KVI = 128 * (DP / 8) / 256;  // 16-byte K (and V) loads per thread
   uint4 kw[KVI], vw[KVI];
 #pragma unroll
@@ -147,14 +145,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));  // lanes along dims
     // unconditional loads from clamped (in-bounds) addresses; out-of-range lanes are zeroed at the store
     const int klc = kl < rg.nk ? kl : rg.nk - 1, d0c = (FULLD || d0 < D) ? d0 : D - 8;
-    kw[it] = *reinterpret_cast<const uint4*>(k + ((rg.kb + klc) * G + rg.g) * D + d0c);
-  }
-#pragma unroll
-  for (int it = 0; it < KVI; ++it) {
-    const int e = tid + 256 * it;
-    const int kl = e & 127, d0 = 8 * (e >> 7);  // lanes along keys: conflict-free transposed writes
-    const int klc = kl < rg.nk ? kl : rg.nk - 1, d0c = (FULLD || d0 < D) ? d0 : D - 8;
-    vw[it] = *reinterpret_cast<const uint4*>(v + ((rg.kb + klc) * G + rg.g) * D + d0c);
+    const int64_t off = ((rg.kb + klc) * G + rg.g) * D + d0c;
+    kw[it] = *reinterpret_cast<const uint4*>(k + off);
+    vw[it] = *reinterpret_cast<const uint4*>(v + off);
   }
   constexpr int MI = kItemRows / 256;
   int32_t mtok[MI], mslot[MI];
@@ -171,18 +164,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));
     const bool ok = kl < rg.nk && (FULLD || d0 < D);
     *reinterpret_cast<uint4*>(sm.k + kl * KS + d0) = ok ? kw[it] : make_uint4(0u, 0u, 0u, 0u);
-  }
-#pragma unroll
-  for (int it = 0; it < KVI; ++it) {
-    const int e = tid + 256 * it;
-    const int kl = e & 127, d0 = 8 * (e >> 7);
-    const bool ok = kl < rg.nk && (FULLD || d0 < D);
-    const uint32_t w4[4] = {ok ? vw[it].x : 0u, ok ? vw[it].y : 0u, ok ? vw[it].z : 0u, ok ? vw[it].w : 0u};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sm.vt[(d0 + 2 * i) * VS + kl] = static_cast<uint16_t>(w4[i] & 0xffffu);
-      sm.vt[(d0 + 2 * i + 1) * VS + kl] = static_cast<uint16_t>(w4[i] >> 16);
-    }
+    *reinterpret_cast<uint4*>(sm.v + kl * KS + d0) = ok ? vw[it] : make_uint4(0u, 0u, 0u, 0u);
   }
 #pragma unroll
   for (int j = 0; j < MI; ++j) {
@@ -300,7 +282,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
       }
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        const bf16x8 vb = read_keys_pi(sm.vt, VS, dt * 16 + c, 32 * kc, q4);
+        // V^T[dim 16*dt + c][keys pi(q4, j)] read transposed from the row-major V block
+        const bf16x8 vb = frag_tr(sm.v, KS, 32 * kc + 4 * q4, 32 * kc + 16 + 4 * q4, 16 * dt, c);
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
           f32x4 acc = kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : o[rt][dt];

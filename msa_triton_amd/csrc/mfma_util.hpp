@@ -80,6 +80,27 @@ __device__ __forceinline__ bf16x8 read_transposed(const uint16_t* tile, int row,
   return __builtin_bit_cast(bf16x8, raw);
 }
 
+// gfx950 LDS transpose read (ds_read_b64_tr_b16). Within each 16-lane group the
+// lanes' 8-byte reads form M[lane][e] (e = 0..3), and lane 4a + b receives
+// M[4j + a][b] as element j. For a row-major tile T[k][n], a lane (c = lane % 16)
+// pointing at &T[k0 + c/4][n0 + 4 (c%4)] therefore receives T[k0 + j][n0 + c]:
+// the MFMA operand layout (n = c, 4 consecutive k) of the transposed tile.
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+  const v4i16 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((v4i16 __attribute__((address_space(3)))*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
+// Operand fragment from a row-major LDS tile T[k][n] (row stride `stride`): element
+// j of lane (c, q4) is T[ka + j][n0 + c] for j < 4 and T[kb + j - 4][n0 + c] for j >= 4.
+__device__ __forceinline__ bf16x8 frag_tr(const uint16_t* tile, int stride, int ka, int kb, int n0, int c) {
+  const uint16_t* base = tile + (c >> 2) * stride + n0 + 4 * (c & 3);
+  const uint2 lo = lds_read_tr16(base + ka * stride);
+  const uint2 hi = lds_read_tr16(base + kb * stride);
+  return __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+
 __device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
 
 __device__ __forceinline__ float quad_max(float v) {
