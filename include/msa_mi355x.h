@@ -58,9 +58,10 @@ int msa_score_fwd(const void* index_q, const void* index_k, int32_t dtype,
                   int64_t groups, int64_t index_dim, int64_t num_blocks, int64_t block_size,
                   double scale, float* scores, int32_t* tie_info, void* stream);
 
-/* Score backward workspace in bytes (transposed tie/grad staging). */
+/* Score backward workspace in bytes (block-major tie/grad copies and the FP64
+ * per-segment dk sums). */
 int64_t msa_score_bwd_workspace_bytes(int64_t total_tokens, int64_t groups, int64_t num_blocks,
-                                      int64_t index_dim);
+                                      int64_t index_dim, int64_t block_size, int64_t total_blocks);
 
 /* Stage 1 backward (amax subgradient: unique winner gets ds*scale, exact ties
  * split it evenly). Replaces index_score.py:139-232 (_index_score_backward_q,

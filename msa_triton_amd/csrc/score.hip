@@ -13,8 +13,8 @@
 // winner, -count for ties (index_score.py:128-136).
 //
 // Backward (index_score.py:139-232): ds*scale goes to the unique winner or is
-// split evenly across exact ties. dq is a per-row gather; dk inverts the winner
-// map per key block. Both accumulate in FP64 in a fixed order (no float
+// split evenly across exact ties. dq is a per-row gather; dk scans each key
+// block's rows for the winners it owns (row segments, summed in order). Both accumulate in FP64 in a fixed order (no float
 // atomics), then round to the input dtype.
 #include "common.hpp"
 #include "score_mfma.hpp"
@@ -148,72 +148,162 @@ __global__ __launch_bounds__(256) void score_bwd_dq(const void* __restrict__ iq,
   }
 }
 
-// dk for one (key block, 128-key chunk, 64-dim chunk): one wavefront scans the
-// block's rows (t, g) with t in the block's sequence and t >= block start, in
-// row order, and adds w * q[row] into the winner's FP64 accumulator in LDS.
-// Lanes own index dims, so every row update is a whole-wave, conflict-free
-// read-modify-write; the fixed row order makes the sum deterministic.
+// dk, partial sums. One wavefront per (key block gb, 8 keys, row segment, 128-dim
+// chunk): it scans the segment's rows (t, g) of gb's sequence with t >= block
+// start, 64 per step (lanes = rows, block-major tie/ds), and adds w * q[row] for
+// rows whose unique winner is one of its keys (lanes = dims, FP64, row order;
+// q rows are loaded four at a time). Exact ties add w / count to every tied key
+// among its keys (exact recomputation). The per-segment sums go to
+// part[((wave * dchunks + dc) * 8 + key) * 128 + dim]; score_bwd_dk_reduce adds
+// the segments in order.
+constexpr int kDkKeys = 8;
+
 template <int DT>
-__global__ __launch_bounds__(64) void score_bwd_dk(const void* __restrict__ iq,
-                                                   const void* __restrict__ ik,
-                                                   const int32_t* __restrict__ cu,
-                                                   const int32_t* __restrict__ cu_blocks, int nseq,
-                                                   const int32_t* __restrict__ tie_t,
-                                                   const float* __restrict__ ds_t, int64_t rows, int G,
-                                                   int Di, int B, double scale, void* __restrict__ dk) {
-  __shared__ double acc[128][64];
-  const int lane = threadIdx.x;
-  const int64_t gb = blockIdx.x;
-  const int kc = blockIdx.y;  // key chunk of 128
-  const int d = blockIdx.z * 64 + lane;
+__global__ __launch_bounds__(256) void score_bwd_dk_part(
+    const void* __restrict__ iq, const void* __restrict__ ik, const int32_t* __restrict__ cu,
+    const int32_t* __restrict__ cu_blocks, int nseq, const int32_t* __restrict__ tie_t,
+    const float* __restrict__ ds_t, int64_t rows, int G, int Di, int B, int kgroups, int nseg, int64_t seg_rows,
+    int64_t total_blocks, double scale, double* __restrict__ part) {
+  const int lane = threadIdx.x & 63;
+  const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (w >= total_blocks * kgroups * nseg) return;
+  const int sg = static_cast<int>(w % nseg);
+  const int kg = static_cast<int>((w / nseg) % kgroups);
+  const int64_t gb = w / nseg / kgroups;
+  const int dc = blockIdx.y, dchunks = gridDim.y;
   int s = upper_index(cu_blocks, nseq + 1, gb);
   while (s < nseq && cu_blocks[s + 1] <= gb) ++s;
   const int b = static_cast<int>(gb - cu_blocks[s]);
   const int64_t start = cu[s], end = cu[s + 1];
   const int64_t k0 = start + static_cast<int64_t>(b) * B;
   const int64_t kend = k0 + B < end ? k0 + B : end;
-  const int64_t c0 = k0 + static_cast<int64_t>(kc) * 128;
-  if (c0 >= kend) return;
-  const int nk = static_cast<int>(kend - c0 < 128 ? kend - c0 : 128);
-  for (int i = 0; i < nk; ++i) acc[i][lane] = 0.0;
-  const int64_t r_begin = k0 * G, r_end = end * G;
-  const int32_t* tcol = tie_t + static_cast<int64_t>(b) * rows;
-  const float* dcol = ds_t + static_cast<int64_t>(b) * rows;
-  const int64_t qoff = static_cast<int64_t>(kc) * 128 + 1;  // tie value of this chunk's first key
-  for (int64_t r0 = r_begin; r0 < r_end; r0 += 64) {
-    const int64_t r = r0 + lane;
-    const int32_t my_tie = r < r_end ? tcol[r] : 0;
-    const float my_ds = r < r_end ? dcol[r] : 0.f;
-    const bool mine = my_tie < 0 || (my_tie >= qoff && my_tie < qoff + nk);
-    uint64_t mask = __ballot(mine);
-    while (mask) {
-      const int i = __builtin_ctzll(mask);
-      mask &= mask - 1;
-      const int32_t ti = __shfl(my_tie, i, kWave);
-      const float di = __shfl(my_ds, i, kWave);
-      const int64_t row = r0 + i;
-      const float qv = d < Di ? load_as_f32<DT>(iq, row * Di + d) : 0.f;
-      if (ti > 0) {
-        const int o = static_cast<int>(ti - qoff);
-        acc[o][lane] = fma(static_cast<double>(di) * scale, static_cast<double>(qv), acc[o][lane]);
-      } else {
+  const int o0 = kg * kDkKeys;
+  const int64_t kA = k0 + o0;
+  const int nk = static_cast<int>(kend - kA < kDkKeys ? kend - kA : kDkKeys);
+  const int64_t r_begin = k0 * G + sg * seg_rows;
+  const int64_t r_stop = (k0 * G + (sg + 1) * seg_rows) < end * G ? k0 * G + (sg + 1) * seg_rows : end * G;
+  double acc[kDkKeys][2];
+#pragma unroll
+  for (int kk = 0; kk < kDkKeys; ++kk) acc[kk][0] = acc[kk][1] = 0.0;
+  const int d0 = dc * 128 + lane, d1 = d0 + 64;
+  if (nk > 0) {
+    const int32_t* tcol = tie_t + static_cast<int64_t>(b) * rows;
+    const float* dcol = ds_t + static_cast<int64_t>(b) * rows;
+    int32_t tie_n = 0;
+    float ds_n = 0.f;
+    if (r_begin + lane < r_stop) {
+      tie_n = tcol[r_begin + lane];
+      ds_n = dcol[r_begin + lane];
+    }
+    for (int64_t r0 = r_begin; r0 < r_stop; r0 += 64) {
+      const int32_t tie = tie_n;
+      const float dsv = ds_n;
+      if (r0 + 64 + lane < r_stop) {  // prefetch the next step
+        tie_n = tcol[r0 + 64 + lane];
+        ds_n = dcol[r0 + 64 + lane];
+      }
+      const int rel = tie - 1 - o0;  // winner offset relative to this wave's first key
+      uint64_t m = __ballot(tie > 0 && rel >= 0 && rel < nk);
+      while (m) {
+        int idx[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          idx[u] = -1;
+          if (m) {
+            idx[u] = __builtin_ctzll(m);
+            m &= m - 1;
+          }
+        }
+        float qv[4][2];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          qv[u][0] = qv[u][1] = 0.f;
+          if (idx[u] >= 0) {
+            const int64_t row = r0 + idx[u];
+            if (d0 < Di) qv[u][0] = load_as_f32<DT>(iq, row * Di + d0);
+            if (d1 < Di) qv[u][1] = load_as_f32<DT>(iq, row * Di + d1);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (idx[u] < 0) continue;
+          const int ru = __shfl(rel, idx[u], kWave);
+          const double wgt = static_cast<double>(__shfl(dsv, idx[u], kWave)) * scale;
+#pragma unroll
+          for (int kk = 0; kk < kDkKeys; ++kk) {
+            if (kk == ru) {
+              acc[kk][0] = fma(wgt, static_cast<double>(qv[u][0]), acc[kk][0]);
+              acc[kk][1] = fma(wgt, static_cast<double>(qv[u][1]), acc[kk][1]);
+            }
+          }
+        }
+      }
+      // exact ties (rare): recompute the block maximum and test this wave's keys
+      uint64_t tm = __ballot(tie < 0);
+      while (tm) {
+        const int i = __builtin_ctzll(tm);
+        tm &= tm - 1;
+        const int64_t row = r0 + i;
         const int64_t t = row / G;
         const int64_t k1 = (k0 + B < t + 1) ? k0 + B : t + 1;
+        const int64_t hi = k1 < kA + nk ? k1 : kA + nk;
+        if (hi <= kA) continue;
         const BlockMax bm = block_max_exact<DT>(iq, row * Di, ik, k0, k1, Di, scale, lane);
-        const double wgt = static_cast<double>(di) * scale / static_cast<double>(bm.count);
-        const int64_t hi = k1 < c0 + nk ? k1 : c0 + nk;
-        if (hi > c0) {
-          for_each_winner<DT>(iq, row * Di, ik, c0, hi, Di, scale, bm.best, lane, [&](int64_t kk) {
-            const int o = static_cast<int>(kk - c0);
-            acc[o][lane] = fma(wgt, static_cast<double>(qv), acc[o][lane]);
-          });
-        }
+        const double wgt = static_cast<double>(__shfl(dsv, i, kWave)) * scale / static_cast<double>(bm.count);
+        const float q0 = d0 < Di ? load_as_f32<DT>(iq, row * Di + d0) : 0.f;
+        const float q1 = d1 < Di ? load_as_f32<DT>(iq, row * Di + d1) : 0.f;
+        for_each_winner<DT>(iq, row * Di, ik, kA, hi, Di, scale, bm.best, lane, [&](int64_t kk_abs) {
+          const int kr = static_cast<int>(kk_abs - kA);
+#pragma unroll
+          for (int kk = 0; kk < kDkKeys; ++kk) {
+            if (kk == kr) {
+              acc[kk][0] = fma(wgt, static_cast<double>(q0), acc[kk][0]);
+              acc[kk][1] = fma(wgt, static_cast<double>(q1), acc[kk][1]);
+            }
+          }
+        });
       }
     }
   }
-  if (d < Di) {
-    for (int i = 0; i < nk; ++i) store_from_f32<DT>(dk, (c0 + i) * Di + d, static_cast<float>(acc[i][lane]));
+  double* dst = part + (w * dchunks + dc) * kDkKeys * 128;
+#pragma unroll
+  for (int kk = 0; kk < kDkKeys; ++kk) {
+    dst[kk * 128 + lane] = acc[kk][0];
+    dst[kk * 128 + 64 + lane] = acc[kk][1];
   }
+}
+
+// dk[key][d] = sum over the key block's row segments (in order) of the partial sums.
+template <int DT>
+__global__ __launch_bounds__(256) void score_bwd_dk_reduce(const int32_t* __restrict__ cu,
+                                                           const int32_t* __restrict__ cu_blocks, int nseq,
+                                                           int64_t T, int G, int Di, int B, int kgroups, int nseg,
+                                                           int64_t seg_rows, const double* __restrict__ part,
+                                                           void* __restrict__ dk) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= T * Di) return;
+  const int64_t key = i / Di;
+  const int d = static_cast<int>(i % Di);
+  const int s = find_seq(cu, nseq, key);
+  const int64_t start = cu[s], end = cu[s + 1];
+  const int b = static_cast<int>((key - start) / B);
+  const int o = static_cast<int>((key - start) % B);
+  const int64_t gb = cu_blocks[s] + b;
+  const int64_t k0 = start + static_cast<int64_t>(b) * B;
+  const int kg = o / kDkKeys, kk = o % kDkKeys;
+  const int dc = d / 128, dl = d % 128, dchunks = (Di + 127) / 128;
+  double sum = 0.0;
+  for (int sg = 0; sg < nseg; ++sg) {
+    if (k0 * G + sg * seg_rows >= end * G) break;  // empty segment (no partial written work)
+    const int64_t w = (gb * kgroups + kg) * nseg + sg;
+    sum += part[((w * dchunks + dc) * kDkKeys + kk) * 128 + dl];
+  }
+  store_from_f32<DT>(dk, i, static_cast<float>(sum));
+}
+
+static int64_t dk_seg_rows(int64_t rows) {
+  const int64_t s = (rows + 7) / 8;
+  return s > 16384 ? s : 16384;
 }
 
 template <int DT>
@@ -242,12 +332,20 @@ int score_bwd_launch(const void* iq, const void* ik, const int32_t* cu, const in
   if (dk && total_blocks > 0) {
     int32_t* tie_t = static_cast<int32_t*>(ws);
     float* ds_t = reinterpret_cast<float*>(tie_t + rows * NB);
+    double* part = reinterpret_cast<double*>(ds_t + rows * NB);  // 8 * rows * NB bytes in: 8-byte aligned
     const dim3 tgrid(grid_1d(rows, 64), static_cast<unsigned>((NB + 63) / 64));
     hipLaunchKernelGGL(score_bwd_transpose, tgrid, dim3(256), 0, st, tie, ds, rows, NB, tie_t, ds_t);
-    const dim3 grid(static_cast<unsigned>(total_blocks), static_cast<unsigned>((B + 127) / 128),
-                    static_cast<unsigned>((Di + 63) / 64));
-    hipLaunchKernelGGL(score_bwd_dk<DT>, grid, dim3(64), 0, st, iq, ik, cu, cu_blocks, nseq, tie_t, ds_t, rows,
-                       G, Di, B, scale, dk);
+    const int kgroups = (B + kDkKeys - 1) / kDkKeys;
+    const int64_t seg_rows = dk_seg_rows(rows);
+    const int nseg = static_cast<int>((rows + seg_rows - 1) / seg_rows);
+    const int dchunks = (Di + 127) / 128;
+    const int64_t waves = total_blocks * kgroups * nseg;
+    const dim3 grid(grid_1d(waves, 4), static_cast<unsigned>(dchunks));
+    hipLaunchKernelGGL(score_bwd_dk_part<DT>, grid, dim3(256), 0, st, iq, ik, cu, cu_blocks, nseq, tie_t, ds_t, rows,
+                       G, Di, B, kgroups, nseg, seg_rows, total_blocks, scale, part);
+    const int64_t T = rows / G;
+    hipLaunchKernelGGL(score_bwd_dk_reduce<DT>, dim3(grid_1d(T * Di, 256)), dim3(256), 0, st, cu, cu_blocks, nseq, T,
+                       G, Di, B, kgroups, nseg, seg_rows, part, dk);
   }
   return status_from(hipGetLastError());
 }
@@ -279,9 +377,17 @@ extern "C" int msa_score_fwd(const void* index_q, const void* index_k, int32_t d
 }
 
 extern "C" int64_t msa_score_bwd_workspace_bytes(int64_t total_tokens, int64_t groups, int64_t num_blocks,
-                                                 int64_t index_dim) {
-  (void)index_dim;
-  return total_tokens * groups * num_blocks * 8 + 256;
+                                                 int64_t index_dim, int64_t block_size, int64_t total_blocks) {
+  if (total_tokens <= 0 || groups <= 0 || num_blocks <= 0 || index_dim <= 0 || block_size <= 0) return 256;
+  const int64_t rows = total_tokens * groups;
+  // block-major tie / ds copies, then the dk partial sums (FP64)
+  const int64_t tr = rows * num_blocks * 8 + 8;
+  const int64_t seg_rows = dk_seg_rows(rows);
+  const int64_t nseg = (rows + seg_rows - 1) / seg_rows;
+  const int64_t kgroups = (block_size + kDkKeys - 1) / kDkKeys;
+  const int64_t dchunks = (index_dim + 127) / 128;
+  const int64_t part = total_blocks * kgroups * nseg * dchunks * kDkKeys * 128 * 8;
+  return tr + part + 256;
 }
 
 extern "C" int msa_score_bwd(const void* index_q, const void* index_k, int32_t dtype,

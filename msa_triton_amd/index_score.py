@@ -58,7 +58,8 @@ class _IndexScore(torch.autograd.Function):
             ds = grad_scores.to(torch.float32).contiguous()
             cu_blocks = torch.tensor(meta.cu_block_lens, dtype=torch.int32, device=q.device)
             lib = _lib.lib()
-            ws_bytes = lib.msa_score_bwd_workspace_bytes(total, groups, ctx.blocks, dim) if dk is not None else 0
+            ws_bytes = (lib.msa_score_bwd_workspace_bytes(total, groups, ctx.blocks, dim, meta.block_size,
+                                                         meta.total_blocks) if dk is not None else 0)
             workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
             with torch.cuda.device(q.device):
                 status = lib.msa_score_bwd(
