@@ -115,29 +115,61 @@ __global__ __launch_bounds__(256) void score_bwd_dq(const void* __restrict__ iq,
     const int32_t my_tie = bl < nvalid ? tie[row * NB + bl] : 0;
     const float my_ds = bl < nvalid ? ds[row * NB + bl] : 0.f;
     const int n = nvalid - b0 < 64 ? nvalid - b0 : 64;
-    for (int i = 0; i < n; ++i) {
+    // blocks in order; unique winners' key rows are loaded four at a time
+    int i = 0;
+    while (i < n) {
+      int bi[4];
+      int cnt = 0;
+      while (cnt < 4 && i < n) {
+        if (__shfl(my_tie, i, kWave) <= 0) break;  // a tie (or an empty block) is handled alone, in order
+        bi[cnt++] = i++;
+      }
+      if (cnt > 0) {
+        float kv[4][DPL];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (u < cnt) {
+            const int32_t ti = __shfl(my_tie, bi[u], kWave);
+            const int64_t key = start + static_cast<int64_t>(b0 + bi[u]) * B + ti - 1;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) {
+              const int d = lane + j * kWave;
+              kv[u][j] = d < Di ? load_as_f32<DT>(ik, key * Di + d) : 0.f;
+            }
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          if (u < cnt) {
+            const double wgt = static_cast<double>(__shfl(my_ds, bi[u], kWave)) * scale;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) acc[j] = fma(wgt, static_cast<double>(kv[u][j]), acc[j]);
+          }
+        }
+        continue;
+      }
       const int32_t ti = __shfl(my_tie, i, kWave);
       const float di = __shfl(my_ds, i, kWave);
       const int64_t k0 = start + static_cast<int64_t>(b0 + i) * B;
-      if (ti > 0) {
-        const double wgt = static_cast<double>(di) * scale;
-        const int64_t key = k0 + ti - 1;
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) {
-          const int d = lane + j * kWave;
-          if (d < Di) acc[j] = fma(wgt, static_cast<double>(load_as_f32<DT>(ik, key * Di + d)), acc[j]);
-        }
-      } else if (ti < 0) {
+      ++i;
+      if (ti < 0) {
         const int64_t k1 = (k0 + B < t + 1) ? k0 + B : t + 1;
         const BlockMax bm = block_max_exact<DT>(iq, row * Di, ik, k0, k1, Di, scale, lane);
         const double wgt = static_cast<double>(di) * scale / static_cast<double>(bm.count);
-        for_each_winner<DT>(iq, row * Di, ik, k0, k1, Di, scale, bm.best, lane, [&](int64_t kk) {
+        for (int64_t base = k0; base < k1; base += kWave) {
+          const int64_t kk = base + lane;
+          const bool win = kk < k1 && directed(exact_dot<DT>(iq, row * Di, ik, kk * Di, Di), scale) == bm.best;
+          uint64_t mask = __ballot(win);
+          while (mask) {
+            const int wl = __builtin_ctzll(mask);
+            mask &= mask - 1;
 #pragma unroll
-          for (int j = 0; j < DPL; ++j) {
-            const int d = lane + j * kWave;
-            if (d < Di) acc[j] = fma(wgt, static_cast<double>(load_as_f32<DT>(ik, kk * Di + d)), acc[j]);
+            for (int j = 0; j < DPL; ++j) {
+              const int d = lane + j * kWave;
+              if (d < Di) acc[j] = fma(wgt, static_cast<double>(load_as_f32<DT>(ik, (base + wl) * Di + d)), acc[j]);
+            }
           }
-        });
+        }
       }
     }
   }
@@ -250,18 +282,19 @@ __global__ __launch_bounds__(256) void score_bwd_dk_part(
         if (hi <= kA) continue;
         const BlockMax bm = block_max_exact<DT>(iq, row * Di, ik, k0, k1, Di, scale, lane);
         const double wgt = static_cast<double>(__shfl(dsv, i, kWave)) * scale / static_cast<double>(bm.count);
+        // lanes 0 .. hi - kA - 1 test this wave's visible keys against the exact maximum
+        const bool win = lane < hi - kA &&
+                         directed(exact_dot<DT>(iq, row * Di, ik, (kA + lane) * Di, Di), scale) == bm.best;
+        const uint32_t wmask = static_cast<uint32_t>(__ballot(win));
         const float q0 = d0 < Di ? load_as_f32<DT>(iq, row * Di + d0) : 0.f;
         const float q1 = d1 < Di ? load_as_f32<DT>(iq, row * Di + d1) : 0.f;
-        for_each_winner<DT>(iq, row * Di, ik, kA, hi, Di, scale, bm.best, lane, [&](int64_t kk_abs) {
-          const int kr = static_cast<int>(kk_abs - kA);
 #pragma unroll
-          for (int kk = 0; kk < kDkKeys; ++kk) {
-            if (kk == kr) {
-              acc[kk][0] = fma(wgt, static_cast<double>(q0), acc[kk][0]);
-              acc[kk][1] = fma(wgt, static_cast<double>(q1), acc[kk][1]);
-            }
+        for (int kk = 0; kk < kDkKeys; ++kk) {
+          if ((wmask >> kk) & 1u) {
+            acc[kk][0] = fma(wgt, static_cast<double>(q0), acc[kk][0]);
+            acc[kk][1] = fma(wgt, static_cast<double>(q1), acc[kk][1]);
           }
-        });
+        }
       }
     }
   }
