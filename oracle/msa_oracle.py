@@ -151,6 +151,49 @@ def topk(scores, cu, *, block_size=128, topk_blocks=16, local_blocks=1):
     return result
 
 
+def topk_rows(score_rows, positions, *, block_size=128, topk_blocks=16, local_blocks=1):
+    """``topk`` for a subset of rows: score_rows [n, G, NB] of tokens whose
+    sequence-local positions are ``positions`` [n]. Same masking, boost, order."""
+    scores = np.asarray(score_rows, dtype=np.float32)
+    n, groups, nb = scores.shape
+    result = np.full((n, groups, topk_blocks), -1, dtype=np.int32)
+    if n == 0 or topk_blocks == 0:
+        return result
+    qb = np.asarray(positions, dtype=np.int64) // block_size
+    blocks = np.arange(nb)
+    valid = blocks[None, :] <= qb[:, None]
+    ranked = np.where(valid[:, None, :], scores.astype(np.float64), -np.inf)
+    if local_blocks:
+        local = valid & (blocks[None, :] > qb[:, None] - local_blocks)
+        ranked = np.where(local[:, None, :], np.inf, ranked)
+    count = min(topk_blocks, nb)
+    order = np.argsort(-ranked, axis=-1, kind="stable")[..., :count]
+    values = np.take_along_axis(ranked, order, axis=-1)
+    result[..., :count] = np.where(values == -np.inf, -1, order).astype(np.int32)
+    return result
+
+
+def index_score_rows(iq, ik, cu, tokens, nb, *, block_size=128, scale=1.0):
+    """``index_score`` (f64 scores, f32 scores) for the given query tokens only: [n, G, nb]."""
+    q = np.asarray(iq, dtype=np.float64)
+    k = np.asarray(ik, dtype=np.float64)[:, 0, :]
+    bounds = bounds_of(cu)
+    _, start = _token_positions(bounds)
+    tokens = np.asarray(tokens, dtype=np.int64)
+    groups = q.shape[1]
+    out = np.full((len(tokens), groups, nb), -np.inf)
+    sign = 1.0 if scale > 0 else (-1.0 if scale < 0 else 0.0)
+    for i, t in enumerate(tokens):
+        a = int(start[t])
+        pos = int(t) - a
+        dots = q[t] @ k[a : t + 1].T  # [G, pos + 1]
+        for blk in range(pos // block_size + 1):
+            lo, hi = blk * block_size, min((blk + 1) * block_size, pos + 1)
+            with np.errstate(invalid="ignore"):
+                out[i, :, blk] = np.abs(scale) * (sign * dots[:, lo:hi]).max(-1)
+    return out, out.astype(np.float32)
+
+
 # --------------------------------------------------------------------------- k2q CSR
 
 
@@ -328,9 +371,9 @@ def attention_kv_rows(q, k, v, indices, cu, dout, keys, *, block_size=128, scale
         a, b = bounds[s], bounds[s + 1]
         blk = (j - a) // block_size
         for g in range(groups):
-            for t in range(j, b):
-                if not np.any(ids[t, g] == blk):
-                    continue
+            hits = np.nonzero((ids[j:b, g, :] == blk).any(-1))[0] + j  # query tokens that selected j's block
+            for t in hits:
+                t = int(t)
                 if (t, g) not in cache:
                     row = attention_rows(q, k, v, ids, cu, [t], block_size=block_size, scale=scale, dout=do)
                     cache[(t, g)] = (row["lse"][0], row["delta"][0])

@@ -158,3 +158,17 @@ def test_backward_matches_torch_amax_autograd(lengths, groups, dim, block_size, 
                                     upstream.numpy(), block_size=block_size, scale=scale)
     np.testing.assert_allclose(dq, q.grad.numpy(), rtol=1e-12, atol=1e-12)
     np.testing.assert_allclose(dk, k.grad.numpy(), rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize("scale", [1.0, -0.5])
+def test_index_score_rows_matches_full(scale):
+    """The row-subset score restatement used at large sizes agrees with ``index_score`` bit for bit."""
+    rng = np.random.default_rng(5)
+    cu = np.array([0, 19, 19, 60], dtype=np.int32)
+    iq = torch.from_numpy(rng.standard_normal((60, 2, 16))).bfloat16().float().numpy()
+    ik = torch.from_numpy(rng.standard_normal((60, 1, 16))).bfloat16().float().numpy()
+    f64, f32, _ = O.index_score(iq, ik, cu, 41, block_size=8, scale=scale)
+    rows = np.array([0, 7, 8, 18, 19, 30, 59])
+    r64, r32 = O.index_score_rows(iq, ik, cu, rows, f64.shape[2], block_size=8, scale=scale)
+    np.testing.assert_array_equal(r64, f64[rows])
+    np.testing.assert_array_equal(r32, f32[rows])

@@ -151,3 +151,19 @@ def test_k2q_all_invalid():
     ids[:, :, 0] = -1
     result = O.k2q_csr(ids, [0, 3, 7], block_size=2)
     assert np.count_nonzero(result[0]) == 0 and (result[1] == -1).all()
+
+
+@pytest.mark.parametrize("local_blocks", [0, 1, 2])
+def test_topk_rows_matches_full_topk(local_blocks):
+    """The row-subset restatement used at large sizes agrees with ``topk`` row by row."""
+    rng = np.random.default_rng(11)
+    lengths, groups, block = [37, 0, 70], 3, 8
+    cu = np.array([0, 37, 37, 107], dtype=np.int32)
+    nb = (70 + block - 1) // block
+    scores = rng.standard_normal((107, groups, nb)).astype(np.float32)
+    scores[5, 1, 2] = scores[5, 1, 0]  # an exact tie
+    full = O.topk(scores, cu, block_size=block, topk_blocks=5, local_blocks=local_blocks)
+    rows = np.array([0, 5, 36, 37, 40, 99, 106])
+    starts = np.where(rows < 37, 0, 37)
+    part = O.topk_rows(scores[rows], rows - starts, block_size=block, topk_blocks=5, local_blocks=local_blocks)
+    np.testing.assert_array_equal(part, full[rows])
