@@ -28,6 +28,7 @@ if ROOT not in sys.path:
 
 MFMA_BF16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 FLOP/clk (dense bf16)
 HBM_PEAK_GBPS = 8000.0
+ENTRY_NAMES = {"attn_fwd": "msa_attn_fwd", "attn_bwd": "msa_attn_bwd"}
 
 # BASELINE.json configs (c1 is the reference's CPU-runnable case).
 CONFIGS = {
@@ -74,6 +75,35 @@ def visible_keys(cfg):
             qb = pos // b
             total += (pos % b + 1) + (min(k, qb + 1) - 1) * b
     return total * cfg["g"]
+
+
+def stage_work(cfg):
+    """Algorithmic work of the non-attention stages (closed forms of the measurement spec):
+    score fwd FLOP, top-k / CSR / score-bwd bytes."""
+    b, k, g, di = cfg["block"], cfg["topk"], cfg["g"], cfg["di"]
+    T = sum(cfg["lengths"])
+    pairs = sum(n * (n + 1) // 2 for n in cfg["lengths"])
+    score_flops = 2.0 * di * g * pairs
+    causal_blocks = sum(sum(p // b + 1 for p in range(n)) for n in cfg["lengths"])  # valid (t, b) per group
+    topk_bytes = causal_blocks * g * 4 + T * g * k * 4
+    rows = sum((n + b - 1) // b for n in cfg["lengths"]) * g
+    csr_bytes = T * g * k * 4 + (rows + 1) * 4 + 2 * T * g * k * 4 + (len(cfg["lengths"]) + 1) * 4
+    # score backward: read ds and the tie codes of every valid (t, g, b), gather one index_k row
+    # (dq) and one index_q row (dk) per valid entry, write dq and dk
+    score_bwd_bytes = causal_blocks * g * (4 + 4 + 2 * di * 2) + T * g * di * 2 + T * di * 2
+    return score_flops, topk_bytes, csr_bytes, score_bwd_bytes
+
+
+def measured_traffic(config, entry):
+    """HBM bytes per call of a C-ABI entry point from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE, calibrated against a copy of known size), if present."""
+    path = os.path.join(ROOT, "profiles", f"attn_{config}_traffic.json")
+    try:
+        with open(path) as f:
+            data = json.load(f)
+        return data["entries"][entry]["bytes_per_call"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 class Harness:
@@ -206,6 +236,9 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--no-stages", action="store_true")
+    parser.add_argument("--pmc-pass", action="store_true",
+                        help="for rocprofv3 --pmc: a 256 MiB calibration copy, then one attention forward and one "
+                             "backward call (direct C ABI) and exit")
     args = parser.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (this path does not shard "
@@ -241,6 +274,21 @@ def main():
     assert int(valid.sum()) == sum(min(topk, p // block + 1) for n in cfg["lengths"] for p in range(n)) * cfg["g"]
     fwd_flops = 4.0 * cfg["d"] * (cfg["hq"] // cfg["g"]) * keys
     step_flops = 3.5 * fwd_flops
+
+    if args.pmc_pass:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)  # 256 MiB read + 256 MiB written: calibrates FETCH_SIZE / WRITE_SIZE
+        torch.cuda.synchronize()
+        h = Harness(cfg, (iq, ik, q, k, v, dout), ids, cu, device)
+        torch.cuda.synchronize()
+        h.fwd()
+        torch.cuda.synchronize()
+        h.bwd()
+        torch.cuda.synchronize()
+        log("pmc pass done")
+        return
 
     qg, kg, vg = (x.detach().clone().requires_grad_() for x in (q, k, v))
 
@@ -315,6 +363,25 @@ def main():
         stages["attention_fwd_bwd_ms"] = round(ms, 4)
         stages["attention_bwd_kernel_ms"] = round(kt["attn_bwd"]["median"], 4)
         stages["attention_fwd_kernel_ms"] = round(kt["attn_fwd"]["median"], 4)
+        score_flops, topk_bytes, csr_bytes, score_bwd_bytes = stage_work(cfg)
+        score_bwd_ms = max(stages["score_fwd_bwd_ms"] - stages["score_fwd_ms"], 1e-6)
+
+        def frac(work, ms_, peak, scale):
+            achieved_ = work / (ms_ * 1e-3) / scale
+            return {"achieved": round(achieved_, 2), "peak": peak, "frac": round(achieved_ / peak, 4)}
+
+        stages["roofline"] = {
+            "score_fwd": {"bound": "mfma", "unit": "TFLOP/s", **frac(score_flops, stages["score_fwd_ms"],
+                                                                      MFMA_BF16_PEAK_TFLOPS, 1e12)},
+            "score_bwd": {"bound": "hbm", "unit": "GB/s", **frac(score_bwd_bytes, score_bwd_ms, HBM_PEAK_GBPS, 1e9)},
+            "topk": {"bound": "hbm", "unit": "GB/s", **frac(topk_bytes, stages["topk_ms"], HBM_PEAK_GBPS, 1e9)},
+            "k2q_csr": {"bound": "hbm", "unit": "GB/s", **frac(csr_bytes, stages["k2q_csr_ms"], HBM_PEAK_GBPS, 1e9)},
+            "attention_fwd": {"bound": "mfma", "unit": "TFLOP/s",
+                              **frac(fwd_flops, stages["attention_fwd_kernel_ms"], MFMA_BF16_PEAK_TFLOPS, 1e12)},
+            "attention_bwd": {"bound": "mfma", "unit": "TFLOP/s",
+                              **frac(2.5 * fwd_flops, stages["attention_bwd_kernel_ms"], MFMA_BF16_PEAK_TFLOPS,
+                                     1e12)},
+        }
 
     baseline = None
     if not args.no_cpu_baseline:
@@ -339,9 +406,10 @@ def main():
                                f"D={cfg['d']} Di={cfg['di']} block={block} topk={topk} local={local}; "
                                "step = m3_sparse_attention fwd+bwd (dQ,dK,dV)",
                    "effective_tflop_per_step": round(step_flops / 1e12, 4)},
-        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
+        "roofline": {"bound": "mfma", "kernel": ENTRY_NAMES[dom], "achieved": round(achieved, 2),
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic(args.config, ENTRY_NAMES[dom]),
                      "kernel_ms": round(kt[dom]["median"], 4)},
         "cpu_baseline": baseline,
         "stages": stages,

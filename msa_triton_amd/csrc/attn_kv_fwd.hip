@@ -391,6 +391,11 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
 
 // ---------------------------------------------------------------------------- host side
 
+bool attn_mfma_supported(int64_t ratio, int64_t head_dim, int64_t block_size) {
+  return ratio >= 1 && ratio <= kItemRows && head_dim >= 8 && head_dim <= 128 && head_dim % 8 == 0 &&
+         block_size >= 1 && block_size <= 128;
+}
+
 static int nk_of_dim(int D) { return D <= 32 ? 1 : (D <= 64 ? 2 : 4); }
 
 static int64_t fwd_epi(int64_t R) {

@@ -1,26 +1,13 @@
-// MFMA (bf16) kernels of stage 3; see attn_mfma.hip.
+// MFMA (bf16) kernels of stage 3: KV-major forward (attn_kv_fwd.hip) and backward
+// (attn_kv_bwd.hip).
 #pragma once
 #include "common.hpp"
 
 namespace msa {
 
+// Shapes the MFMA kernels cover: head ratio <= 512 (a work item holds whole edges of
+// at most 512 rows), 8 <= D <= 128 with D % 8 == 0, block <= 128.
 bool attn_mfma_supported(int64_t ratio, int64_t head_dim, int64_t block_size);
-
-int attn_fwd_mfma(const void* q, const void* k, const void* v, const int32_t* indices, const int32_t* cu, int nseq,
-                  int64_t T, int Hq, int G, int D, int K, int B, float scale, void* out, float* lse, double* rs,
-                  hipStream_t st);
-
-int attn_bwd_dq_mfma(const void* q, const void* k, const void* v, const void* out, const void* dout, double* rs,
-                     const int32_t* indices, const int32_t* cu, int nseq, int64_t T, int Hq, int G, int D, int K,
-                     int B, float scale, void* dq, hipStream_t st);
-
-int64_t attn_dkdv_mfma_workspace_bytes(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks,
-                                       int64_t B);
-
-int attn_bwd_dkdv_mfma(const void* q, const void* k, const void* v, const void* dout, const double* rs,
-                       const int32_t* cu, const int32_t* cu_blocks, const int32_t* row_ptr, const int32_t* qidx,
-                       int nseq, int64_t T, int Hq, int G, int D, int64_t total_blocks, int B, float scale, void* dk,
-                       void* dv, void* ws, int64_t ws_bytes, hipStream_t st);
 
 int64_t attn_fwd_kv_workspace_bytes(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks);
 

@@ -3,13 +3,12 @@
 // Lane l (c = l % 16, q4 = l / 16) holds A[c][8*q4 + j], B[8*q4 + j][c] (j = 0..7)
 // and C[4*q4 + i][c] (i = 0..3). Fragments are assembled in 32-bit words: the
 // 8-wide __bf16 vector type is only used as the MFMA operand container (element
-// access on it is avoided).
+// extraction from it is avoided: it yields element 0 for every index on this
+// toolchain).
 #pragma once
 #include "common.hpp"
 
 namespace msa {
-
-constexpr int kTS = 40;  // padded key stride (bf16 elements) of the transposed LDS tiles
 
 __device__ __forceinline__ bf16x8 zero_frag() { return __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u)); }
 
@@ -20,26 +19,6 @@ __device__ __forceinline__ bf16x8 load_frag(const uint16_t* __restrict__ p) {
 
 __device__ __forceinline__ f32x4 mfma(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-// Operand fragments are assembled from 16-bit patterns in 32-bit words; the
-// __bf16 vector type is only used as the MFMA operand container.
-struct Frag8 {
-  uint32_t w[4];
-  __device__ __forceinline__ void set(int j, uint16_t bits) {
-    const int k = j >> 1;
-    w[k] = (j & 1) ? ((w[k] & 0x0000ffffu) | (static_cast<uint32_t>(bits) << 16))
-                   : ((w[k] & 0xffff0000u) | bits);
-  }
-  __device__ __forceinline__ bf16x8 vec() const { return __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3])); }
-};
-
-// x = hi + mid + lo with three RNE bf16 terms (24 significant bits in total).
-__device__ __forceinline__ void split3(float x, uint16_t& hi, uint16_t& mid, uint16_t& lo) {
-  hi = f32_to_bf16_bits(x);
-  const float r1 = x - bf16_bits_to_f32(hi);
-  mid = f32_to_bf16_bits(r1);
-  lo = f32_to_bf16_bits(r1 - bf16_bits_to_f32(mid));
 }
 
 // Exact split of an fp32 value into three bf16 terms by truncation: hi keeps the
@@ -56,28 +35,6 @@ __device__ __forceinline__ void split3_bits(float x, uint32_t& hi, uint32_t& mid
 // One 32-bit word holding the bf16 truncations (upper halves) of a (low half) and b (high half).
 __device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
-}
-
-// Write a row fragment (8 dims of one key / row) transposed into tile[dim][key].
-__device__ __forceinline__ void store_transposed(uint16_t* tile, int dim0, int key, bf16x8 f) {
-  const uint4 raw = __builtin_bit_cast(uint4, f);
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    tile[(dim0 + 2 * i) * kTS + key] = static_cast<uint16_t>(w[i] & 0xffffu);
-    tile[(dim0 + 2 * i + 1) * kTS + key] = static_cast<uint16_t>(w[i] >> 16);
-  }
-}
-
-// Operand for a key-contraction MFMA from tile[dim][key]: element j of lane
-// (c, q4) is tile[row][pi(q4, j)], pi(q4, j) = 16*(j/4) + 4*q4 + j%4, which is
-// the key order of the lane's two 16-key C tiles.
-__device__ __forceinline__ bf16x8 read_transposed(const uint16_t* tile, int row, int q4) {
-  const uint16_t* p = tile + row * kTS + 4 * q4;
-  const uint2 a = *reinterpret_cast<const uint2*>(p);
-  const uint2 b = *reinterpret_cast<const uint2*>(p + 16);
-  const uint4 raw = make_uint4(a.x, a.y, b.x, b.y);
-  return __builtin_bit_cast(bf16x8, raw);
 }
 
 // gfx950 LDS transpose read (ds_read_b64_tr_b16). Within each 16-lane group the
@@ -101,16 +58,9 @@ __device__ __forceinline__ bf16x8 frag_tr(const uint16_t* tile, int stride, int 
   return __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
 }
 
-__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
-
 __device__ __forceinline__ float quad_max(float v) {
   v = fmaxf(v, __shfl_xor(v, 16, kWave));
   return fmaxf(v, __shfl_xor(v, 32, kWave));
-}
-
-__device__ __forceinline__ double quad_sum(double v) {
-  v += __shfl_xor(v, 16, kWave);
-  return v + __shfl_xor(v, 32, kWave);
 }
 
 

@@ -16,6 +16,8 @@ Functions and the reference code they restate:
   attention_rows / attention_kv_rows   the same math restricted to sampled
                        query rows / key rows, gathering only selected blocks,
                        for parity at sizes where the dense form does not fit.
+  index_score_rows / topk_rows   index_score / topk for a subset of query
+                       rows (pinned against the full restatements).
 
 Pinning (see tests/test_oracle_*.py): every function is checked against the
 reference's known-answer cases (tests/test_eager.py:143-170,
