@@ -4,8 +4,8 @@
 // (scale2 = scale * log2 e), p_j = 2^(x_j - lse2) with the forward's base-2 lse,
 // dp_j = dO . v_j, c = O . dO (bf16 output, fp64), and
 //   mass = sum_j p_j,  delta = sum_j p_j (dp_j - c) / mass,
-//   P_j = p_j / mass,  dS_j = P_j ((dp_j - c) - delta) * scale,
-//   dQ = sum_j dS_j k_j,  dK_j = sum_rows dS_j q,  dV_j = sum_rows P_j dO.
+//   P_j = p_j / mass,  dS_j = P_j ((dp_j - c) - delta),
+//   dQ = scale sum_j dS_j k_j,  dK_j = scale sum_rows dS_j q,  dV_j = sum_rows P_j dO.
 // This is the reference's centred softmax derivative (tests/reference_fp64.py,
 // triton/sparse_attention.py:96-197): delta is formed from the same p_j and dp_j
 // as dS, so sum_j dS_j vanishes to rounding even when dp_j are large and close.
@@ -15,10 +15,10 @@
 //   stats   (B1)  per (row, block): sum p, sum p (dp - c)    KV-major, rows per wave
 //   combine       mass, delta per row (FP64, slot order)
 //   main    (B2)  dK, dV per key block (registers) and dQ per (row, block)
-//                 partials                                  KV-major, keys per wave
+//                 partials                                  KV-major, 16 keys per wave
 //   accumulate    dK, dV item partials -> FP32 key accumulators (item order)
-//   dq combine    dQ = sum of the row's block partials (FP64, slot order)
-//   finalize      FP32 key accumulators -> bf16 dK, dV
+//   dq combine    dQ = scale * sum of the row's block partials (FP64, slot order)
+//   finalize      FP32 key accumulators -> bf16 dK (times scale), dV
 // No floating-point atomics; every sum has a fixed order.
 #include "attn_kv_common.hpp"
 
@@ -34,7 +34,8 @@ constexpr int kStatRowsPerTile = 128;  // B1: (edge, head) rows per tile (4 wave
 constexpr int kStatTilesPerItem = 4;
 constexpr int kStatItemRows = kStatRowsPerTile * kStatTilesPerItem;
 constexpr int kMainEdges = 512;        // B2: CSR edges per work item
-constexpr int kMetaRows = 256;         // B2: row metadata staged per block of 8 tiles
+constexpr int kMainThreads = 512;      // B2: 8 waves, 16 keys each (S, dP, dV, dK), 16 rows x 32 dims each (dQ)
+constexpr int kPlaneStride = 40;       // B2: halves per key of a dS plane [key][row] (32 + 8: conflict-free b64 writes)
 
 template <int NK>
 struct StatSmem {
@@ -52,16 +53,16 @@ struct StatSmem {
 template <int NK>
 struct MainSmem {
   static constexpr int DP = 32 * NK;
-  static constexpr int KS = DP + 8;   // row stride of the K block and of the Q / dO row tiles
-  static constexpr int PS = 32 + 16;  // row stride of the dS planes [key][row]
-  alignas(16) uint16_t k[128 * KS];   // K block [key][dim]
-  alignas(16) uint16_t qs[32 * KS];   // Q rows [row][dim]
-  alignas(16) uint16_t gs[32 * KS];   // dO rows
-  alignas(16) uint16_t ds[3][128 * PS];  // dS split planes (hi, mid, lo) [key][row]
-  float4 stats[kMetaRows];            // lse2, 1 / mass, c, delta
-  int32_t th[kMetaRows];
-  int32_t tok[kMetaRows];
-  int32_t rec[kMetaRows];
+  static constexpr int KS = DP + 8;                     // row stride of the K block and the Q / dO row tiles
+  alignas(16) uint16_t k[128 * KS];                     // K block [key][dim]
+  alignas(16) uint16_t qs[2][32 * KS];                  // Q rows of a tile [row][dim], double-buffered
+  alignas(16) uint16_t gs[2][32 * KS];                  // dO rows
+  alignas(16) uint16_t ds[2][3][128 * kPlaneStride];    // dS split planes (hi, mid, lo) [key][row]
+  alignas(16) float4 st[2][32];                         // (lse2, 1 / mass, c, delta) per tile row
+  alignas(16) int32_t vis[2][32];                       // visible keys of the block per tile row (0 past the end)
+  alignas(16) int32_t rec[2][32];                       // dQ partial record per tile row (-1 past the end)
+  int32_t etok[kMainEdges];                             // the item's edges: query token and slot
+  int32_t eslot[kMainEdges];
 };
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -257,24 +258,32 @@ __global__ __launch_bounds__(256) void kv_bwd_stats_combine(const int32_t* __res
   }
 }
 
-// B2: one workgroup per work item (key block row, <= kMainEdges edges); wave w owns
-// keys 32w .. 32w + 31 of the block. Per 32-row tile (all waves, same rows):
-//   S = Q K^T, dP = dO V^T (C[row][key]: lane = key c, rows 4*q4 + i),
-//   dV += P^T dO and dK += dS^T Q (B operands read transposed from the row tiles),
-//   dS -> three bf16 planes [key][row] in LDS, then dQ^T = K^T dS^T over all 128
-//   keys for the wave's dim tiles (lane: row c, 4 consecutive dims) -> per-(row,
-//   block) partial. The next tile's Q / dO rows are loaded during the current one.
+// One workgroup (8 waves) per work item: a key block row and <= kMainEdges of its
+// edges, i.e. nrows = edges x (Hq / G) query rows, processed in tiles of 32 rows.
+// Wave w owns keys 16w .. 16w + 15 of the block. Per tile:
+//   S = Q K^T, dP = dO V^T     C[row 16 rt + 4 q4 + i][key c] (A: Q / dO rows from LDS,
+//                              B: this wave's K / V fragments, in registers)
+//   P = p / mass, dS           exact 3-way bf16 splits; A operands of dV / dK come
+//                              straight from the C registers (rows permuted by pi)
+//   dV += P^T dO, dK += dS^T Q B operands read transposed from the row tiles
+//   dS planes -> LDS [key][row]; barrier
+//   dQ^T = K^T dS^T            wave (rh, dq): rows 16 rh .. +15, dims 32 dq .. +31,
+//                              K^T fragments in registers -> per-(row, block) partial
+// Row tiles and dS planes are double-buffered, so one barrier per tile orders all
+// LDS traffic; the next tile's rows are committed before it and the one after is
+// loaded from memory during the current tile.
 template <int NK, bool FULLD>
-__global__ __launch_bounds__(256, 1) void kv_bwd_main_kernel(
+__global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx, const int32_t* __restrict__ sidx,
     const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items, const int2* __restrict__ items, int nseq,
-    int Hq, int G, int D, int K, int B, float scale2, float scale, int epi, int t0, float* __restrict__ dqpart,
+    int Hq, int G, int D, int K, int B, float scale2, int epi, int t0, float* __restrict__ dqpart,
     float* __restrict__ kvpart) {
-  constexpr int DP = 32 * NK, NDT = DP / 16, KS = MainSmem<NK>::KS, PS = MainSmem<NK>::PS;
-  constexpr int NQT = (NDT + 3) / 4;  // dQ dim tiles per wave
-  constexpr int SI = 32 * (DP / 8) / 256 > 0 ? 32 * (DP / 8) / 256 : 1;  // 16-byte row loads per thread
+  constexpr int DP = 32 * NK, NDT = DP / 16, KS = MainSmem<NK>::KS, PS = kPlaneStride;
+  constexpr int RV = DP / 8;             // 16-byte chunks per row
+  constexpr int TV = 32 * RV;            // chunks per tile and tensor
+  constexpr int SI = (TV + 255) / 256;   // chunks per staging thread (threads 0-255: Q, 256-511: dO)
   __shared__ MainSmem<NK> sm;
   const int item = blockIdx.x;
   if (item >= *n_items) return;
@@ -284,237 +293,257 @@ __global__ __launch_bounds__(256, 1) void kv_bwd_main_kernel(
   const RowGeom rg = row_geom(cu, cu_blocks, nseq, row, G, B);
   const int R = Hq / G;
   const int e_end = e_begin + epi < e_hi[row] ? e_begin + epi : e_hi[row];
-  const int nrows = (e_end - e_begin) * R;
+  const int ne = e_end - e_begin;
+  const int nrows = ne * R;
+  const int ntiles = (nrows + 31) >> 5;
+  if (nrows <= 0) return;  // (the plan emits no empty items; whole workgroup)
 
-  // ---- K / V fragments of this wave's keys (B operands of S and dP); K block in LDS
-  bf16x8 kf[2][NK], vf[2][NK];
-#pragma unroll
-  for (int kt = 0; kt < 2; ++kt) {
-    const int kl = 32 * wid + 16 * kt + c;
-    const int klc = kl < rg.nk ? kl : rg.nk - 1;
-#pragma unroll
-    for (int kk = 0; kk < NK; ++kk) {
-      const int d0 = 32 * kk + 8 * q4;
-      const int d0c = (FULLD || d0 < D) ? d0 : D - 8;
-      const int64_t off = ((rg.kb + klc) * G + rg.g) * D + d0c;
-      const bool ok = kl < rg.nk && (FULLD || d0 < D);
-      const bf16x8 kx = load_frag(k + off), vx = load_frag(v + off);
-      kf[kt][kk] = ok ? kx : zero_frag();
-      vf[kt][kk] = ok ? vx : zero_frag();
-    }
+  // ---- item set-up: edges and the K block in LDS, V fragments of this wave's keys
+  for (int e = tid; e < ne; e += kMainThreads) {
+    sm.etok[e] = qidx[e_begin + e];
+    sm.eslot[e] = sidx[e_begin + e];
   }
   {
-    constexpr int KVI = 128 * (DP / 8) / 256;
+    constexpr int KVI = (128 * RV + kMainThreads - 1) / kMainThreads;
     uint4 kw[KVI];
 #pragma unroll
     for (int i = 0; i < KVI; ++i) {
-      const int e = tid + 256 * i;
-      const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));
+      const int e = tid + kMainThreads * i;
+      const int kl = (e < 128 * RV ? e : 0) / RV, d0 = 8 * (e % RV);
       const int klc = kl < rg.nk ? kl : rg.nk - 1, d0c = (FULLD || d0 < D) ? d0 : D - 8;
       kw[i] = *reinterpret_cast<const uint4*>(k + ((rg.kb + klc) * G + rg.g) * D + d0c);
     }
 #pragma unroll
     for (int i = 0; i < KVI; ++i) {
-      const int e = tid + 256 * i;
-      const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));
-      const bool ok = kl < rg.nk && (FULLD || d0 < D);
-      *reinterpret_cast<uint4*>(sm.k + kl * KS + d0) = ok ? kw[i] : make_uint4(0u, 0u, 0u, 0u);
-    }
-  }
-
-  f32x4 dk[2][NDT], dv[2][NDT];
-#pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) dk[kt][dt] = dv[kt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // 32 Q / dO rows of a tile: thread e covers row e % 32, dims 8 * (e / 32) .. +7
-  uint4 qw[SI], gw[SI];
-  auto load_rows = [&](int r0, int mb, int mend) {
-#pragma unroll
-    for (int i = 0; i < SI; ++i) {
-      const int e = tid + 256 * i;
-      const int rr = e & 31, d0 = 8 * (e >> 5);
-      const int rho = r0 + rr < mend ? r0 + rr : mend - 1;
-      const int d0c = d0 < DP ? ((FULLD || d0 < D) ? d0 : D - 8) : 0;
-      const int64_t off = static_cast<int64_t>(sm.th[rho - mb]) * D + d0c;
-      qw[i] = *reinterpret_cast<const uint4*>(q + off);
-      gw[i] = *reinterpret_cast<const uint4*>(dout + off);
-    }
-  };
-  auto store_rows = [&](int r0, int mend) {
-#pragma unroll
-    for (int i = 0; i < SI; ++i) {
-      const int e = tid + 256 * i;
-      const int rr = e & 31, d0 = 8 * (e >> 5);
-      if (d0 < DP) {
-        const bool ok = r0 + rr < mend && (FULLD || d0 < D);
-        *reinterpret_cast<uint4*>(sm.qs + rr * KS + d0) = ok ? qw[i] : make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(sm.gs + rr * KS + d0) = ok ? gw[i] : make_uint4(0u, 0u, 0u, 0u);
-      }
-    }
-  };
-
-  for (int mb = 0; mb < nrows; mb += kMetaRows) {
-    const int mend = mb + kMetaRows < nrows ? mb + kMetaRows : nrows;
-    __syncthreads();  // previous metadata block no longer read (also publishes the K block on entry)
-    if (tid < kMetaRows) {
-      const int rho = mb + tid;
-      if (rho < mend) {
-        const int eo = rho / R;
-        const int h = rg.g * R + (rho - eo * R);
-        const int32_t tk = qidx[e_begin + eo];
-        const int th = tk * Hq + h;
-        const double* rs = row_state + static_cast<int64_t>(th) * 4;
-        sm.th[tid] = th;
-        sm.tok[tid] = tk;
-        sm.rec[tid] = ((tk - t0) * Hq + h) * K + sidx[e_begin + eo];
-        sm.stats[tid] = make_float4(static_cast<float>(rs[0]), static_cast<float>(1.0 / rs[1]),
-                                    static_cast<float>(rs[2]), static_cast<float>(rs[3]));
-      }
-    }
-    __syncthreads();
-    load_rows(mb, mb, mend);
-
-    for (int r0 = mb; r0 < mend; r0 += 32) {
-      // All waves passed the previous tile's mid barrier: the row tiles are free.
-      store_rows(r0, mend);
-      __syncthreads();
-      if (r0 + 32 < mend) load_rows(r0 + 32, mb, mend);
-
-      // ---- S and dP: C[row 16*rt + 4*q4 + i][key 32*wid + 16*kt + c]
-      f32x4 s[2][2], dp[2][2];
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        bf16x8 qa[NK], ga[NK];
-#pragma unroll
-        for (int kk = 0; kk < NK; ++kk) {
-          qa[kk] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(sm.qs + (16 * rt + c) * KS + 32 * kk + 8 * q4));
-          ga[kk] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(sm.gs + (16 * rt + c) * KS + 32 * kk + 8 * q4));
-        }
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int kk = 0; kk < NK; ++kk) {
-            a = mfma(qa[kk], kf[kt][kk], a);
-            b = mfma(ga[kk], vf[kt][kk], b);
-          }
-          s[rt][kt] = a;
-          dp[rt][kt] = b;
-        }
-      }
-      // ---- P and dS (masked) as split bf16 A operands [key c][rows pi(q4, j)], j = 4*rt + i
-      bf16x8 ap[2][3], ad[2][3];  // [kt][hi, mid, lo]
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        uint32_t ph[8], pm[8], pl[8], dh[8], dm[8], dl[8];
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int rho = r0 + 16 * rt + 4 * q4 + i;
-            const bool rok = rho < mend;
-            const float4 st = sm.stats[(rok ? rho : mend - 1) - mb];
-            const int64_t vis = rok ? static_cast<int64_t>(sm.tok[rho - mb]) - rg.kb + 1 : 0;
-            const int kl = 32 * wid + 16 * kt + c;
-            const bool ok = kl < vis && kl < rg.nk;
-            const float p = ok ? __builtin_amdgcn_exp2f(s[rt][kt][i] * scale2 - st.x) : 0.f;
-            const float P = p * st.y;
-            const float dS = ok ? P * ((dp[rt][kt][i] - st.z) - st.w) * scale : 0.f;
-            split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
-            split3_bits(dS, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
-          }
-        uint32_t w[3][4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          w[0][jj] = pack_hi16(dh[2 * jj], dh[2 * jj + 1]);
-          w[1][jj] = pack_hi16(dm[2 * jj], dm[2 * jj + 1]);
-          w[2][jj] = pack_hi16(dl[2 * jj], dl[2 * jj + 1]);
-        }
-#pragma unroll
-        for (int pl3 = 0; pl3 < 3; ++pl3) {
-          ad[kt][pl3] = __builtin_bit_cast(bf16x8, make_uint4(w[pl3][0], w[pl3][1], w[pl3][2], w[pl3][3]));
-          // dS plane rows: key 32*wid + 16*kt + c, columns (rows) 16*rt + 4*q4 .. +3
-          uint16_t* dst = sm.ds[pl3] + (32 * wid + 16 * kt + c) * PS + 4 * q4;
-          *reinterpret_cast<uint2*>(dst) = make_uint2(w[pl3][0], w[pl3][1]);
-          *reinterpret_cast<uint2*>(dst + 16) = make_uint2(w[pl3][2], w[pl3][3]);
-        }
-        ap[kt][0] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(ph[0], ph[1]), pack_hi16(ph[2], ph[3]), pack_hi16(ph[4], ph[5]), pack_hi16(ph[6], ph[7])));
-        ap[kt][1] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pm[0], pm[1]), pack_hi16(pm[2], pm[3]), pack_hi16(pm[4], pm[5]), pack_hi16(pm[6], pm[7])));
-        ap[kt][2] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pl[0], pl[1]), pack_hi16(pl[2], pl[3]), pack_hi16(pl[4], pl[5]), pack_hi16(pl[6], pl[7])));
-      }
-      // ---- dV += P^T dO, dK += dS^T Q: B = X[rows pi(q4, j)][dim 16*dt + c], read transposed
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        const bf16x8 gb = frag_tr(sm.gs, KS, 4 * q4, 16 + 4 * q4, 16 * dt, c);
-        const bf16x8 qb = frag_tr(sm.qs, KS, 4 * q4, 16 + 4 * q4, 16 * dt, c);
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          f32x4 a = dv[kt][dt];
-          a = mfma(ap[kt][2], gb, a);
-          a = mfma(ap[kt][1], gb, a);
-          dv[kt][dt] = mfma(ap[kt][0], gb, a);
-          f32x4 b = dk[kt][dt];
-          b = mfma(ad[kt][2], qb, b);
-          b = mfma(ad[kt][1], qb, b);
-          dk[kt][dt] = mfma(ad[kt][0], qb, b);
-        }
-      }
-      __syncthreads();  // dS planes complete; row tiles no longer read
-      // ---- dQ^T = K^T dS^T for dim tiles dt = wid + 4 * n: C[dim 16*dt + 4*q4 + i][row 16*rt + c]
-      if (wid < NDT) {
-        f32x4 acc[NQT][2];
-#pragma unroll
-        for (int n = 0; n < NQT; ++n) acc[n][0] = acc[n][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kc = 0; kc < 4; ++kc) {
-          bf16x8 ka[NQT];
-#pragma unroll
-          for (int n = 0; n < NQT; ++n) {
-            const int dt = wid + 4 * n;
-            ka[n] = dt < NDT ? frag_tr(sm.k, KS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * dt, c) : zero_frag();
-          }
-#pragma unroll
-          for (int rt = 0; rt < 2; ++rt) {
-            const bf16x8 bl = frag_tr(sm.ds[2], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rt, c);
-            const bf16x8 bm = frag_tr(sm.ds[1], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rt, c);
-            const bf16x8 bh = frag_tr(sm.ds[0], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rt, c);
-#pragma unroll
-            for (int n = 0; n < NQT; ++n) {
-              acc[n][rt] = mfma(ka[n], bl, acc[n][rt]);
-              acc[n][rt] = mfma(ka[n], bm, acc[n][rt]);
-              acc[n][rt] = mfma(ka[n], bh, acc[n][rt]);
-            }
-          }
-        }
-#pragma unroll
-        for (int n = 0; n < NQT; ++n) {
-          const int dt = wid + 4 * n;
-#pragma unroll
-          for (int rt = 0; rt < 2; ++rt) {
-            const int rho = r0 + 16 * rt + c;
-            const int d0 = 16 * dt + 4 * q4;
-            if (dt < NDT && rho < mend && (FULLD || d0 < D))
-              *reinterpret_cast<f32x4*>(dqpart + static_cast<int64_t>(sm.rec[rho - mb]) * D + d0) = acc[n][rt];
-          }
-        }
+      const int e = tid + kMainThreads * i;
+      if ((128 * RV) % kMainThreads == 0 || e < 128 * RV) {
+        const int kl = e / RV, d0 = 8 * (e % RV);
+        const bool ok = kl < rg.nk && (FULLD || d0 < D);
+        *reinterpret_cast<uint4*>(sm.k + kl * KS + d0) = ok ? kw[i] : make_uint4(0u, 0u, 0u, 0u);
       }
     }
   }
+  bf16x8 vf[NK];
+  {
+    const int kl = 16 * wid + c;
+    const int klc = kl < rg.nk ? kl : rg.nk - 1;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) {
+      const int d0 = 32 * kk + 8 * q4;
+      const int d0c = (FULLD || d0 < D) ? d0 : D - 8;
+      const bf16x8 x = load_frag(v + ((rg.kb + klc) * G + rg.g) * D + d0c);
+      vf[kk] = kl < rg.nk && (FULLD || d0 < D) ? x : zero_frag();
+    }
+  }
+  __syncthreads();  // K block and edges visible
+
+  bf16x8 kf[NK];  // B operand of S: K[key 16 w + c][dims 32 kk + 8 q4 + j]
+#pragma unroll
+  for (int kk = 0; kk < NK; ++kk) kf[kk] = load_frag(sm.k + (16 * wid + c) * KS + 32 * kk + 8 * q4);
+  const int rh = wid >> 2, dq = wid & 3;
+  const bool dq_active = 32 * dq < DP;
+  bf16x8 kt[2][4];  // A operand of dQ^T: K^T[dim 32 dq + 16 dt2 + c][keys 32 kc + 8 q4 + j]
+#pragma unroll
+  for (int dt2 = 0; dt2 < 2; ++dt2)
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+      kt[dt2][kc] = dq_active ? frag_tr(sm.k, KS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 32 * dq + 16 * dt2, c)
+                              : zero_frag();
+
+  // ---- row staging: thread tid loads 16-byte chunks of Q (tid < 256) or dO rows of a
+  // tile; threads 0-31 also fetch the per-row statistics, visible keys and record.
+  const uint16_t* src = tid < 256 ? q : dout;
+  uint4 pf[SI];
+  double4 pst = make_double4(0.0, 1.0, 0.0, 0.0);
+  int prec = -1, pvis = 0;
+#define MSA_MAIN_ISSUE(R0)                                                                                  \
+  {                                                                                                         \
+    _Pragma("unroll") for (int i = 0; i < SI; ++i) {                                                        \
+      const int idx = (tid & 255) + 256 * i;                                                                \
+      if (TV % 256 == 0 || idx < TV) {                                                                      \
+        const int rr = idx / RV, d0 = 8 * (idx % RV);                                                       \
+        const int rho = (R0) + rr < nrows ? (R0) + rr : nrows - 1;                                          \
+        const int eo = rho / R;                                                                             \
+        const int64_t th = static_cast<int64_t>(sm.etok[eo]) * Hq + rg.g * R + (rho - eo * R);              \
+        const int d0c = (FULLD || d0 < D) ? d0 : D - 8;                                                     \
+        pf[i] = *reinterpret_cast<const uint4*>(src + th * D + d0c);                                        \
+      }                                                                                                     \
+    }                                                                                                       \
+    if (tid < 32) {                                                                                         \
+      const int rho = (R0) + tid;                                                                           \
+      if (rho < nrows) {                                                                                    \
+        const int eo = rho / R;                                                                             \
+        const int h = rg.g * R + (rho - eo * R);                                                            \
+        const int tk = sm.etok[eo];                                                                         \
+        pst = *reinterpret_cast<const double4*>(row_state + (static_cast<int64_t>(tk) * Hq + h) * 4);       \
+        prec = ((tk - t0) * Hq + h) * K + sm.eslot[eo];                                                     \
+        const int64_t vk = static_cast<int64_t>(tk) - rg.kb + 1;                                            \
+        pvis = vk < rg.nk ? static_cast<int>(vk) : rg.nk;                                                   \
+      } else {                                                                                              \
+        pst = make_double4(0.0, 1.0, 0.0, 0.0);                                                             \
+        prec = -1;                                                                                          \
+        pvis = 0;                                                                                           \
+      }                                                                                                     \
+    }                                                                                                       \
+  }
+#define MSA_MAIN_COMMIT(R0, BUF)                                                                            \
+  {                                                                                                         \
+    uint16_t* dstt = tid < 256 ? sm.qs[BUF] : sm.gs[BUF];                                                   \
+    _Pragma("unroll") for (int i = 0; i < SI; ++i) {                                                        \
+      const int idx = (tid & 255) + 256 * i;                                                                \
+      if (TV % 256 == 0 || idx < TV) {                                                                      \
+        const int rr = idx / RV, d0 = 8 * (idx % RV);                                                       \
+        const bool ok = (R0) + rr < nrows && (FULLD || d0 < D);                                             \
+        *reinterpret_cast<uint4*>(dstt + rr * KS + d0) = ok ? pf[i] : make_uint4(0u, 0u, 0u, 0u);          \
+      }                                                                                                     \
+    }                                                                                                       \
+    if (tid < 32) {                                                                                         \
+      sm.st[BUF][tid] = make_float4(static_cast<float>(pst.x), static_cast<float>(1.0 / pst.y),              \
+                                    static_cast<float>(pst.z), static_cast<float>(pst.w));                   \
+      sm.vis[BUF][tid] = pvis;                                                                              \
+      sm.rec[BUF][tid] = prec;                                                                              \
+    }                                                                                                       \
+  }
+
+  f32x4 dk[NDT], dv[NDT];  // C[key 16 w + 4 q4 + i][dim 16 dt + c]
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) dk[dt] = dv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  MSA_MAIN_ISSUE(0)
+  MSA_MAIN_COMMIT(0, 0)
+  if (ntiles > 1) MSA_MAIN_ISSUE(32)
+  __syncthreads();
+
+  const int key = 16 * wid + c;
+  for (int t = 0; t < ntiles; ++t) {
+    const int b = t & 1;
+    // ---- S and dP: C[row 16 rt + 4 q4 + i][key c]
+    f32x4 s[2], dp[2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      f32x4 a = {0.f, 0.f, 0.f, 0.f}, g = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) {
+        const bf16x8 qa = load_frag(sm.qs[b] + (16 * rt + c) * KS + 32 * kk + 8 * q4);
+        const bf16x8 ga = load_frag(sm.gs[b] + (16 * rt + c) * KS + 32 * kk + 8 * q4);
+        a = mfma(qa, kf[kk], a);
+        g = mfma(ga, vf[kk], g);
+      }
+      s[rt] = a;
+      dp[rt] = g;
+    }
+    // ---- P and dS, split into three bf16 terms; element j = 4 rt + i is row pi(q4, j)
+    const int myrec = sm.rec[b][16 * rh + c];  // read before the barrier: the buffer is refilled after it
+    const bool full = 32 * t + 32 <= nrows && sm.vis[b][0] >= 16 * wid + 16;  // rows are in token order
+    uint32_t ph[8], pm[8], pl[8], dh[8], dm[8], dl[8];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float4 stv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) stv[i] = sm.st[b][16 * rt + 4 * q4 + i];
+      if (full) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float P = __builtin_amdgcn_exp2f(s[rt][i] * scale2 - stv[i].x) * stv[i].y;
+          const float d = P * ((dp[rt][i] - stv[i].z) - stv[i].w);
+          split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
+          split3_bits(d, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
+        }
+      } else {
+        const int4 vis = *reinterpret_cast<const int4*>(&sm.vis[b][16 * rt + 4 * q4]);
+        const int vv[4] = {vis.x, vis.y, vis.z, vis.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool ok = key < vv[i];
+          const float P = ok ? __builtin_amdgcn_exp2f(s[rt][i] * scale2 - stv[i].x) * stv[i].y : 0.f;
+          const float d = ok ? P * ((dp[rt][i] - stv[i].z) - stv[i].w) : 0.f;
+          split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
+          split3_bits(d, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
+        }
+      }
+    }
+    bf16x8 ap[3], ad[3];  // [hi, mid, lo]
+    {
+      uint32_t w[3][4];
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        w[0][jj] = pack_hi16(dh[2 * jj], dh[2 * jj + 1]);
+        w[1][jj] = pack_hi16(dm[2 * jj], dm[2 * jj + 1]);
+        w[2][jj] = pack_hi16(dl[2 * jj], dl[2 * jj + 1]);
+      }
+#pragma unroll
+      for (int p3 = 0; p3 < 3; ++p3) {
+        ad[p3] = __builtin_bit_cast(bf16x8, make_uint4(w[p3][0], w[p3][1], w[p3][2], w[p3][3]));
+        // plane rows: key 16 w + c, columns (tile rows) 4 q4 .. +3 and 16 + 4 q4 .. +3
+        uint16_t* dst = sm.ds[b][p3] + key * PS + 4 * q4;
+        *reinterpret_cast<uint2*>(dst) = make_uint2(w[p3][0], w[p3][1]);
+        *reinterpret_cast<uint2*>(dst + 16) = make_uint2(w[p3][2], w[p3][3]);
+      }
+      ap[0] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(ph[0], ph[1]), pack_hi16(ph[2], ph[3]),
+                                                    pack_hi16(ph[4], ph[5]), pack_hi16(ph[6], ph[7])));
+      ap[1] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pm[0], pm[1]), pack_hi16(pm[2], pm[3]),
+                                                    pack_hi16(pm[4], pm[5]), pack_hi16(pm[6], pm[7])));
+      ap[2] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pl[0], pl[1]), pack_hi16(pl[2], pl[3]),
+                                                    pack_hi16(pl[4], pl[5]), pack_hi16(pl[6], pl[7])));
+    }
+    // ---- dV += P^T dO, dK += dS^T Q: B = X[rows pi(q4, j)][dim 16 dt + c], read transposed
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const bf16x8 gb = frag_tr(sm.gs[b], KS, 4 * q4, 16 + 4 * q4, 16 * dt, c);
+      const bf16x8 qb = frag_tr(sm.qs[b], KS, 4 * q4, 16 + 4 * q4, 16 * dt, c);
+      f32x4 x = dv[dt];
+      x = mfma(ap[2], gb, x);
+      x = mfma(ap[1], gb, x);
+      dv[dt] = mfma(ap[0], gb, x);
+      f32x4 y = dk[dt];
+      y = mfma(ad[2], qb, y);
+      y = mfma(ad[1], qb, y);
+      dk[dt] = mfma(ad[0], qb, y);
+    }
+    // ---- stage the next tile, start loading the one after
+    if (t + 1 < ntiles) {
+      MSA_MAIN_COMMIT(32 * (t + 1), b ^ 1)
+      if (t + 2 < ntiles) MSA_MAIN_ISSUE(32 * (t + 2))
+    }
+    __syncthreads();  // dS planes of this tile and rows of the next one complete
+    // ---- dQ^T = K^T dS^T: C[dim 32 dq + 16 dt2 + 4 q4 + i][row 16 rh + c]
+    if (dq_active) {
+      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        const bf16x8 bl = frag_tr(sm.ds[b][2], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rh, c);
+        const bf16x8 bm = frag_tr(sm.ds[b][1], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rh, c);
+        const bf16x8 bh = frag_tr(sm.ds[b][0], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rh, c);
+#pragma unroll
+        for (int dt2 = 0; dt2 < 2; ++dt2) {
+          acc[dt2] = mfma(kt[dt2][kc], bl, acc[dt2]);
+          acc[dt2] = mfma(kt[dt2][kc], bm, acc[dt2]);
+          acc[dt2] = mfma(kt[dt2][kc], bh, acc[dt2]);
+        }
+      }
+      if (myrec >= 0) {
+#pragma unroll
+        for (int dt2 = 0; dt2 < 2; ++dt2) {
+          const int d0 = 32 * dq + 16 * dt2 + 4 * q4;
+          if (FULLD || d0 < D)
+            *reinterpret_cast<f32x4*>(dqpart + static_cast<int64_t>(myrec) * D + d0) = acc[dt2];
+        }
+      }
+    }
+  }
+#undef MSA_MAIN_ISSUE
+#undef MSA_MAIN_COMMIT
 
   // ---- this item's dK / dV contribution: kvpart[item][0 = dK, 1 = dV][key][dim]
   float* base = kvpart + static_cast<int64_t>(item) * 2 * 128 * DP;
 #pragma unroll
-  for (int kt = 0; kt < 2; ++kt)
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = 32 * wid + 16 * kt + 4 * q4 + i, d = 16 * dt + c;
-        base[key * DP + d] = dk[kt][dt][i];
-        base[128 * DP + key * DP + d] = dv[kt][dt][i];
-      }
+    for (int i = 0; i < 4; ++i) {
+      const int kr = 16 * wid + 4 * q4 + i, d = 16 * dt + c;
+      base[kr * DP + d] = dk[dt][i];
+      base[128 * DP + kr * DP + d] = dv[dt][i];
+    }
 }
 
 // For chunk c: add each row's item partials (in item order) into the FP32 key
@@ -543,10 +572,11 @@ __global__ __launch_bounds__(256) void kv_bwd_accumulate(const int32_t* __restri
   acc[T * G * D + off] += sv;
 }
 
-// dQ = sum of the row's block partials over its valid slots (FP64, slot order); 32 lanes per row.
+// dQ = scale * sum of the row's block partials over its valid slots (FP64, slot
+// order); 32 lanes per row.
 __global__ __launch_bounds__(256) void kv_bwd_dq_combine(const int32_t* __restrict__ indices,
                                                          const int32_t* __restrict__ cu, int nseq, int64_t t0,
-                                                         int64_t t1, int Hq, int G, int D, int K, int B,
+                                                         int64_t t1, int Hq, int G, int D, int K, int B, double scale,
                                                          const float* __restrict__ dqpart,
                                                          uint16_t* __restrict__ dq) {
   const int sub = threadIdx.x & 31;
@@ -570,8 +600,10 @@ __global__ __launch_bounds__(256) void kv_bwd_dq_combine(const int32_t* __restri
     a2 += static_cast<double>(x.z);
     a3 += static_cast<double>(x.w);
   }
-  const uint32_t w0 = f32_to_bf16_bits(static_cast<float>(a0)) | (static_cast<uint32_t>(f32_to_bf16_bits(static_cast<float>(a1))) << 16);
-  const uint32_t w1 = f32_to_bf16_bits(static_cast<float>(a2)) | (static_cast<uint32_t>(f32_to_bf16_bits(static_cast<float>(a3))) << 16);
+  const uint32_t w0 = f32_to_bf16_bits(static_cast<float>(a0 * scale)) |
+                      (static_cast<uint32_t>(f32_to_bf16_bits(static_cast<float>(a1 * scale))) << 16);
+  const uint32_t w1 = f32_to_bf16_bits(static_cast<float>(a2 * scale)) |
+                      (static_cast<uint32_t>(f32_to_bf16_bits(static_cast<float>(a3 * scale))) << 16);
   *reinterpret_cast<uint2*>(dq + th * D + 4 * sub) = make_uint2(w0, w1);
 }
 
@@ -580,16 +612,14 @@ __global__ __launch_bounds__(256) void kv_bwd_zero(float* __restrict__ p, int64_
   if (i < n) p[i] = 0.f;
 }
 
-// FP32 key accumulators -> bf16 dK (acc[0]) and dV (acc[1]).
-__global__ __launch_bounds__(256) void kv_bwd_finalize(const float* __restrict__ acc, int64_t n,
+// FP32 key accumulators -> bf16 dK = scale * acc[0] and dV = acc[1].
+__global__ __launch_bounds__(256) void kv_bwd_finalize(const float* __restrict__ acc, int64_t n, float scale,
                                                        uint16_t* __restrict__ dk, uint16_t* __restrict__ dv) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= n) return;
-  if (dk) dk[i] = f32_to_bf16_bits(acc[i]);
+  if (dk) dk[i] = f32_to_bf16_bits(acc[i] * scale);
   if (dv) dv[i] = f32_to_bf16_bits(acc[n + i]);
 }
-
-// ---------------------------------------------------------------------------- host side
 
 static int nk_of_dim(int D) { return D <= 32 ? 1 : (D <= 64 ? 2 : 4); }
 
@@ -678,8 +708,8 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       const int32_t* nit = kv_plan_count(mp, mbase, c);
       const int2* its = kv_plan_items(mp, mbase, c);
       const int mepi = static_cast<int>(mp.epi);
-      const dim3 grid(static_cast<unsigned>(mp.max_items)), block(256);
-#define MSA_BWD_MAIN(NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, scale, mepi, it0, dqpart, kvpart)
+      const dim3 grid(static_cast<unsigned>(mp.max_items)), block(kMainThreads);
+#define MSA_BWD_MAIN(NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, mepi, it0, dqpart, kvpart)
       if (nk == 1) { if (fd) MSA_BWD_MAIN(1, true); else MSA_BWD_MAIN(1, false); }
       else if (nk == 2) { if (fd) MSA_BWD_MAIN(2, true); else MSA_BWD_MAIN(2, false); }
       else { if (fd) MSA_BWD_MAIN(4, true); else MSA_BWD_MAIN(4, false); }
@@ -694,10 +724,10 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
     }
     if (dq)
       hipLaunchKernelGGL(kv_bwd_dq_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu, nseq, t0,
-                         t1, Hq, G, D, K, B, dqpart, static_cast<uint16_t*>(dq));
+                         t1, Hq, G, D, K, B, static_cast<double>(scale), dqpart, static_cast<uint16_t*>(dq));
   }
   if (need_kv)
-    hipLaunchKernelGGL(kv_bwd_finalize, dim3(grid_1d(nacc, 256)), dim3(256), 0, st, acc, nacc,
+    hipLaunchKernelGGL(kv_bwd_finalize, dim3(grid_1d(nacc, 256)), dim3(256), 0, st, acc, nacc, scale,
                        static_cast<uint16_t*>(dk), static_cast<uint16_t*>(dv));
   return status_from(hipGetLastError());
 }
