@@ -230,9 +230,12 @@ __global__ __launch_bounds__(256) void score_bwd_dk_part(
     for (int64_t r0 = r_begin; r0 < r_stop; r0 += 64) {
       const int32_t tie = tie_n;
       const float dsv = ds_n;
-      if (r0 + 64 + lane < r_stop) {  // prefetch the next step
+      if (r0 + 64 + lane < r_stop) {  // prefetch the next step; lanes past the segment end carry no row
         tie_n = tcol[r0 + 64 + lane];
         ds_n = dcol[r0 + 64 + lane];
+      } else {
+        tie_n = 0;
+        ds_n = 0.f;
       }
       const int rel = tie - 1 - o0;  // winner offset relative to this wave's first key
       uint64_t m = __ballot(tie > 0 && rel >= 0 && rel < nk);

@@ -2,20 +2,27 @@
 // certified exact winner.
 //
 // Work unit: a tile of 128 consecutive (t, g) rows of the flattened [T*G] row
-// space; the tile's query fragments stay in registers for its whole lifetime.
-// For every key block reachable by the tile's rows, the 4 waves each take 32 of
-// the block's (<= 128) keys and evaluate the 128 x 32 logits on
-// v_mfma_f32_16x16x32_bf16 (exact bf16 products, fp32 accumulation).
+// space, 4 waves x 32 rows. A wave keeps its rows' query fragments in
+// registers and, for every key block reachable by the tile, evaluates its
+// 32 x 128 logits on v_mfma_f32_16x16x32_bf16 (exact bf16 products, fp32
+// accumulation) against the block held in LDS. Key blocks are double-buffered:
+// the next block is fetched from memory while the current one is used, so one
+// barrier per block orders all LDS traffic. Tiles are issued heaviest first
+// (the last rows of a sequence see the most blocks).
 //
 // Exactness (the public score must equal fl32(scale * exact winning dot) and
 // the winner set must be the exact one, index_score.py:121-136): with
 //   E = (Di_pad + 8) * 2^-22 * ||q|| * max_k ||k||  >=  |s_mfma - s_exact|,
 // every key whose approximate directed logit is below (max_approx - 2E) is
 // certainly beaten by the approximate winner. If exactly one key survives,
-// it is the unique exact winner and only its dot is evaluated in FP64 (from LDS
-// copies of the tile rows and the key block, in the fixed summation order of
-// exact_dot). Otherwise the row takes the slow path: every key of the block is
-// re-evaluated in FP64 and max / tie count / first winner are taken exactly.
+// it is the unique exact winner and only its dot is evaluated in FP64: a lane
+// pair owns the row, each lane runs one half of exact_dot's fixed order (two
+// sequential FMA chains over the halves of the index dim) from the query half
+// it keeps in registers and the key row in LDS, and the halves are added in
+// that order. Otherwise the whole wave re-evaluates every visible key of the
+// block in FP64 (same order) and takes max / tie count / first winner exactly.
+// A negative scale flips the query signs once (exact), so every comparison is
+// on the directed dot.
 #include "mfma_util.hpp"
 #include "score_mfma.hpp"
 
@@ -23,292 +30,367 @@ namespace msa {
 
 namespace {
 
-constexpr int kTileRows = 128;
+constexpr int kTileRows = 128;  // 4 waves x 32 rows
+constexpr int kThreads = 256;
 
 template <int NK>
 struct ScoreSmem {
   static constexpr int DP = 32 * NK;
-  static constexpr int RS = DP + 8;
-  uint16_t q[kTileRows * RS];  // tile rows, raw bf16 (not sign-flipped)
-  uint16_t k[kTileRows * RS];  // current key block, raw bf16
-  float wmax[4][kTileRows];    // per-wave approximate row maximum
-  int widx[4][kTileRows];      // per-wave approximate argmax (key offset in block)
-  int wcnt[4][kTileRows];      // per-wave number of candidates
-  float kmax2[4];              // per-wave max key norm^2
-  float qnorm[kTileRows];
-  int qb[kTileRows];           // query block of each row (-1 if no row)
-  int seq_of[kTileRows];       // sequence of each row
-  double half[kTileRows];      // second-half partial dots
-  int slow[kTileRows];
-  int nslow;
-  double red_v[4];
-  int red_c[4];
-  int red_f[4];
+  static constexpr int RS = DP + 8;  // row stride (bf16) of a key block: conflict-free 16-byte row reads
+  alignas(16) uint16_t k[2][128 * RS];
+  float kmax2[2][4];  // per-wave max squared key norm of the buffered block
+  uint32_t qrow[4][DP / 2];  // per-wave query row of an ambiguous row (packed bf16)
 };
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// Half-dot over dims [d0, d1) of two LDS rows, sequential FMA (exact_dot order).
-__device__ __forceinline__ double lds_half_dot(const uint16_t* a, const uint16_t* b, int d0, int d1) {
-  double acc = 0.0;
-  for (int d = d0; d < d1; ++d)
-    acc = fma(static_cast<double>(bf16_bits_to_f32(a[d])), static_cast<double>(bf16_bits_to_f32(b[d])), acc);
-  return acc;
+// Iteration space of a tile: (sequence, block) pairs for every sequence overlapping
+// the tile rows [r0, r0 + nr), blocks 0 .. the last row's query block.
+struct BlockCursor {
+  int s;       // sequence
+  int b;       // sequence-local block
+  int b_last;  // last block of this sequence the tile needs
+};
+
+__device__ __forceinline__ int last_block_of(const int32_t* __restrict__ cu, int s, int64_t r0, int nr, int G,
+                                             int B) {
+  const int64_t start = cu[s], end = cu[s + 1];
+  const int64_t t_last = (r0 + nr - 1) / G;
+  const int64_t t = t_last < end - 1 ? t_last : end - 1;
+  return static_cast<int>((t - start) / B);
+}
+
+// Next (s, b) after c; s == nseq when the tile has no more blocks.
+__device__ __forceinline__ BlockCursor next_block(const int32_t* __restrict__ cu, int nseq, BlockCursor c,
+                                                  int64_t r0, int nr, int G, int B) {
+  if (c.b < c.b_last) {
+    ++c.b;
+    return c;
+  }
+  const int64_t t_last = (r0 + nr - 1) / G;
+  for (int s = c.s + 1; s < nseq && cu[s] <= t_last; ++s) {
+    if (cu[s + 1] > cu[s]) return BlockCursor{s, 0, last_block_of(cu, s, r0, nr, G, B)};
+  }
+  return BlockCursor{nseq, 0, -1};
 }
 
 }  // namespace
 
-template <int NK>
-__global__ __launch_bounds__(256) void score_fwd_mfma_kernel(const uint16_t* __restrict__ iq,
-                                                             const uint16_t* __restrict__ ik,
-                                                             const int32_t* __restrict__ cu, int nseq, int64_t rows,
-                                                             int G, int Di, int NB, int B, double scale,
-                                                             float* __restrict__ scores, int32_t* __restrict__ tie) {
+template <int NK, bool FULLD>
+__global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint16_t* __restrict__ iq,
+                                                                     const uint16_t* __restrict__ ik,
+                                                                     const int32_t* __restrict__ cu, int nseq,
+                                                                     int64_t rows, int G, int Di, int NB, int B,
+                                                                     double scale, float* __restrict__ scores,
+                                                                     int32_t* __restrict__ tie) {
   constexpr int DP = 32 * NK, RS = ScoreSmem<NK>::RS;
+  constexpr int CPK = DP / 8;                 // 16-byte chunks per key row
+  constexpr int KCH = 128 * CPK / kThreads;   // chunks per thread per key block
+  constexpr int HW = DP / 4;                  // max 32-bit words of a query half (Di / 2 <= DP / 2)
   __shared__ ScoreSmem<NK> sm;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
-  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kTileRows;
+  const int64_t r0 = static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * kTileRows;  // heaviest tiles first
   const int nr = static_cast<int>(rows - r0 < kTileRows ? rows - r0 : kTileRows);
   const bool neg = scale < 0.0;
   const double ascale = fabs(scale);
+  const uint32_t flip = neg ? 0x80008000u : 0u;
   const float cerr = static_cast<float>(DP + 8) * 0x1p-22f;
+  // exact_dot's split point (Di % 8 == 0, so h % 4 == 0); compile-time for Di == DP
+  const int h = FULLD ? DP / 2 : Di / 2;
 
-  // ---- stage the tile rows (raw) and per-row metadata
-  for (int e = tid; e < kTileRows * (DP / 8); e += 256) {
-    const int rr = e / (DP / 8), d0 = 8 * (e % (DP / 8));
-    uint4 val = make_uint4(0u, 0u, 0u, 0u);
-    if (rr < nr && d0 < Di) val = *reinterpret_cast<const uint4*>(iq + (r0 + rr) * Di + d0);
-    *reinterpret_cast<uint4*>(sm.q + rr * RS + d0) = val;
-  }
-  if (tid < kTileRows) {
-    if (tid < nr) {
-      const int64_t t = (r0 + tid) / G;
-      const int s = find_seq(cu, nseq, t);
-      sm.seq_of[tid] = s;
-      sm.qb[tid] = static_cast<int>((t - cu[s]) / B);
-    } else {
-      sm.seq_of[tid] = -1;
-      sm.qb[tid] = -1;
-    }
-  }
-  if (tid == 0) sm.nslow = 0;
-  __syncthreads();
-  if (tid < kTileRows) {
-    float s2 = 0.f;
-    for (int d = 0; d < Di; ++d) {
-      const float x = bf16_bits_to_f32(sm.q[tid * RS + d]);
-      s2 = fmaf(x, x, s2);
-    }
-    sm.qnorm[tid] = sqrtf(s2) * 1.0001f;
-  }
-  // B-operand fragments of the tile rows: row 16*rt + c, dims 32*kk + 8*q4 (sign-flipped if scale < 0).
-  bf16x8 qf[8][NK];
+  // ---- this wave's rows: MFMA B fragments (rows 16 rt + c) ...
+  const int wr0 = 32 * wid;  // first tile row of the wave
+  bf16x8 qf[2][NK];
+  int64_t mtok[2];
+  bool min_tile[2];
 #pragma unroll
-  for (int rt = 0; rt < 8; ++rt)
+  for (int rt = 0; rt < 2; ++rt) {
+    const int rr = wr0 + 16 * rt + c;
+    min_tile[rt] = rr < nr;
+    mtok[rt] = min_tile[rt] ? (r0 + rr) / G : -1;
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
-      uint4 w = *reinterpret_cast<const uint4*>(sm.q + (16 * rt + c) * RS + 32 * kk + 8 * q4);
-      if (neg) {
-        w.x ^= 0x80008000u;
-        w.y ^= 0x80008000u;
-        w.z ^= 0x80008000u;
-        w.w ^= 0x80008000u;
-      }
+      const int d0 = 32 * kk + 8 * q4;
+      uint4 w = make_uint4(0u, 0u, 0u, 0u);
+      if (min_tile[rt] && d0 < Di) w = *reinterpret_cast<const uint4*>(iq + (r0 + rr) * Di + d0);
+      w.x ^= flip;
+      w.y ^= flip;
+      w.z ^= flip;
+      w.w ^= flip;
       qf[rt][kk] = __builtin_bit_cast(bf16x8, w);
     }
+  }
+  // ... and the exact-dot layout: lane (pr = lane & 31, hf = lane >> 5) keeps half hf
+  // (dims [hf h, hf h + h)) of row wr0 + pr, sign-flipped, packed two per word.
+  const int pr = lane & 31, hf = lane >> 5;
+  const int prow = wr0 + pr;
+  const bool pin = prow < nr;
+  uint32_t qh[HW];
+  float pn2 = 0.f;
+#pragma unroll
+  for (int w4 = 0; w4 < HW / 2; ++w4) {  // 8-byte loads: 4 dims each
+    uint2 x = make_uint2(0u, 0u);
+    if (pin && 4 * w4 < h) x = *reinterpret_cast<const uint2*>(iq + (r0 + prow) * Di + hf * h + 4 * w4);
+    x.x ^= flip;
+    x.y ^= flip;
+    qh[2 * w4] = x.x;
+    qh[2 * w4 + 1] = x.y;
+    pn2 = fmaf(bf16_lo(x.x), bf16_lo(x.x), pn2);
+    pn2 = fmaf(bf16_hi(x.x), bf16_hi(x.x), pn2);
+    pn2 = fmaf(bf16_lo(x.y), bf16_lo(x.y), pn2);
+    pn2 = fmaf(bf16_hi(x.y), bf16_hi(x.y), pn2);
+  }
+  pn2 += __shfl_xor(pn2, 32, kWave);
+  const float pnorm = sqrtf(pn2) * 1.0001f;  // ||q|| of row prow, rounded up
+  float mnorm[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) mnorm[rt] = __shfl(pnorm, 16 * rt + c, kWave);
+  const int64_t ptok = pin ? (r0 + prow) / G : -1;
 
-  const int64_t t_first = r0 / G, t_last = (r0 + nr - 1) / G;
-  for (int s = find_seq(cu, nseq, t_first); s < nseq && cu[s] <= t_last; ++s) {
-    const int64_t start = cu[s], end = cu[s + 1];
-    const int64_t ra = start * G > r0 ? start * G : r0;
-    const int64_t rb = end * G < r0 + nr ? end * G : r0 + nr;
-    if (ra >= rb) continue;
-    const int qb_last = static_cast<int>(((rb - 1) / G - start) / B);
-    for (int b = 0; b <= qb_last; ++b) {
-      const int64_t kb = start + static_cast<int64_t>(b) * B;
-      const int nk = static_cast<int>(end - kb < B ? end - kb : B);
-      __syncthreads();  // previous block's LDS consumers are done
-      // ---- this wave's 32 keys: offsets 32*wid + 16*kt + c
-      bf16x8 kf[2][NK];
-      float kn2 = 0.f;
+  // ---- key block staging: thread tid holds KCH 16-byte chunks (keys (tid + 256 i) / CPK)
+  uint4 kreg[KCH];
+  auto fetch = [&](const BlockCursor& bc) {
+    if (bc.s >= nseq) return;
+    const int64_t kb = cu[bc.s] + static_cast<int64_t>(bc.b) * B;
+    const int64_t end = cu[bc.s + 1];
+    const int nk = static_cast<int>(end - kb < B ? end - kb : B);
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const int kl = 32 * wid + 16 * kt + c;
-        float part = 0.f;
+    for (int i = 0; i < KCH; ++i) {
+      const int e = tid + kThreads * i;
+      const int kl = e / CPK, d0 = 8 * (e % CPK);
+      kreg[i] = (kl < nk && d0 < Di) ? *reinterpret_cast<const uint4*>(ik + (kb + kl) * Di + d0)
+                                     : make_uint4(0u, 0u, 0u, 0u);
+    }
+  };
+  auto commit = [&](int buf) {
+    float n2 = 0.f;
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) {
-          const int d0 = 32 * kk + 8 * q4;
-          uint4 w = make_uint4(0u, 0u, 0u, 0u);
-          if (kl < nk && d0 < Di) w = *reinterpret_cast<const uint4*>(ik + (kb + kl) * Di + d0);
-          *reinterpret_cast<uint4*>(sm.k + kl * RS + d0) = w;
-          kf[kt][kk] = __builtin_bit_cast(bf16x8, w);
-          const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    for (int i = 0; i < KCH; ++i) {
+      const int e = tid + kThreads * i;
+      const int kl = e / CPK, d0 = 8 * (e % CPK);
+      *reinterpret_cast<uint4*>(sm.k[buf] + kl * RS + d0) = kreg[i];
+      float part = 0.f;
+      const uint32_t ws[4] = {kreg[i].x, kreg[i].y, kreg[i].z, kreg[i].w};
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            part = fmaf(bf16_lo(ws[j]), bf16_lo(ws[j]), part);
-            part = fmaf(bf16_hi(ws[j]), bf16_hi(ws[j]), part);
-          }
-        }
-        part += __shfl_xor(part, 16, kWave);
-        part += __shfl_xor(part, 32, kWave);
-        kn2 = fmaxf(kn2, part);
+      for (int j = 0; j < 4; ++j) {
+        part = fmaf(bf16_lo(ws[j]), bf16_lo(ws[j]), part);
+        part = fmaf(bf16_hi(ws[j]), bf16_hi(ws[j]), part);
       }
 #pragma unroll
-      for (int o = 1; o < 16; o <<= 1) kn2 = fmaxf(kn2, __shfl_xor(kn2, o, kWave));
-      if (lane == 0) sm.kmax2[wid] = kn2 * 1.0001f;
-      // ---- logits: C[key 16*kt + 4*q4 + i][row 16*rt + c]
-      f32x4 acc[8][2];
+      for (int o = 1; o < CPK; o <<= 1) part += __shfl_xor(part, o, kWave);  // CPK consecutive lanes per key
+      n2 = fmaxf(n2, part);
+    }
 #pragma unroll
-      for (int rt = 0; rt < 8; ++rt)
+    for (int o = 1; o < 64; o <<= 1) n2 = fmaxf(n2, __shfl_xor(n2, o, kWave));
+    if (lane == 0) sm.kmax2[buf][wid] = n2 * 1.0001f;
+  };
+
+  // first (sequence, block) of the tile
+  BlockCursor cur{nseq, 0, -1};
+  {
+    const int64_t t_first = r0 / G;
+    const int s0 = find_seq(cu, nseq, t_first);
+    cur = BlockCursor{s0, 0, last_block_of(cu, s0, r0, nr, G, B)};
+  }
+  fetch(cur);
+  commit(0);
+  __syncthreads();
+  int buf = 0;
+  while (cur.s < nseq) {
+    const BlockCursor nxt = next_block(cu, nseq, cur, r0, nr, G, B);
+    fetch(nxt);  // in flight while this block is evaluated
+
+    const int64_t start = cu[cur.s], end = cu[cur.s + 1];
+    const int64_t kb = start + static_cast<int64_t>(cur.b) * B;
+    const int nk = static_cast<int>(end - kb < B ? end - kb : B);
+    // visible keys of the lane's MFMA rows (0: row not in this sequence or block in its future)
+    int lim[2];
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
+    for (int rt = 0; rt < 2; ++rt) {
+      const int64_t t = mtok[rt];
+      const int64_t v = (t >= start && t < end) ? t - kb + 1 : 0;
+      lim[rt] = v <= 0 ? 0 : (v < nk ? static_cast<int>(v) : nk);
+    }
+    const bool wave_on = __ballot(lim[0] > 0 || lim[1] > 0) != 0;  // wave-uniform
+    const uint16_t* kt_base = sm.k[buf];
+    // approximate logits, 16 keys at a time, folded into a per-row running top 2:
+    // m1 the maximum, o1 the lane-local offset (16 kt + i) of its first key, m2 the
+    // largest other value (med3(m1, v, m2) is the new second largest)
+    float m1[2] = {-__builtin_inff(), -__builtin_inff()}, m2[2] = {-__builtin_inff(), -__builtin_inff()};
+    int o1[2] = {0, 0};
+    if (wave_on) {
+      const bool full = __ballot(lim[0] < 128 || lim[1] < 128) == 0;  // no key masked in the wave
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt) {
+        bf16x8 kf[NK];
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) kf[kk] = load_frag(kt_base + (16 * kt + c) * RS + 32 * kk + 8 * q4);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
           f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int kk = 0; kk < NK; ++kk) a = mfma(kf[kt][kk], qf[rt][kk], a);
-          acc[rt][kt] = a;
-        }
-      // ---- per-row approximate max / argmax over this wave's keys
-      bool rowok[8];
-      int64_t trow[8];
-#pragma unroll
-      for (int rt = 0; rt < 8; ++rt) {
-        const int rr = 16 * rt + c;
-        const int64_t r = r0 + rr;
-        rowok[rt] = r >= ra && r < rb && sm.qb[rr] >= b;
-        trow[rt] = r / G;
-        float m = -__builtin_inff();
-        int idx = 0x7fffffff;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
+          for (int kk = 0; kk < NK; ++kk) a = mfma(kf[kk], qf[rt][kk], a);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const int kl = 32 * wid + 16 * kt + 4 * q4 + i;
-            const bool ok = rowok[rt] && kl < nk && kb + kl <= trow[rt];
-            const float v = ok ? acc[rt][kt][i] : -__builtin_inff();
-            if (v > m) {
-              m = v;
-              idx = kl;
-            }
+            float v = a[i];
+            if (!full) v = 16 * kt + 4 * q4 + i < lim[rt] ? v : -__builtin_inff();
+            o1[rt] = v > m1[rt] ? 16 * kt + i : o1[rt];
+            m2[rt] = __builtin_amdgcn_fmed3f(m1[rt], v, m2[rt]);
+            m1[rt] = fmaxf(m1[rt], v);
           }
+        }
+      }
+    }
+    if (wave_on) {
+      const float kmax = sqrtf(fmaxf(fmaxf(sm.kmax2[buf][0], sm.kmax2[buf][1]),
+                                     fmaxf(sm.kmax2[buf][2], sm.kmax2[buf][3])));
+      // merge the four key quarters of each row; the winner is certified unique iff no
+      // other key comes within 2E of the maximum
+      int widx[2], wcnt[2];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        float a1 = m1[rt], a2 = m2[rt];
+        int ai = o1[rt] + 4 * q4;
 #pragma unroll
         for (int o = 16; o <= 32; o <<= 1) {
-          const float om = __shfl_xor(m, o, kWave);
-          const int oi = __shfl_xor(idx, o, kWave);
-          if (om > m || (om == m && oi < idx)) {
-            m = om;
-            idx = oi;
-          }
+          const float b1 = __shfl_xor(a1, o, kWave);
+          const float b2 = __shfl_xor(a2, o, kWave);
+          const int bi = __shfl_xor(ai, o, kWave);
+          a2 = fmaxf(fmaxf(a2, b2), fminf(a1, b1));
+          if (b1 > a1 || (b1 == a1 && bi < ai)) ai = bi;
+          a1 = fmaxf(a1, b1);
         }
-        if (q4 == 0) {
-          sm.wmax[wid][rr] = m;
-          sm.widx[wid][rr] = idx;
-        }
+        const float thr = a1 - 2.f * cerr * mnorm[rt] * kmax;
+        widx[rt] = ai;
+        wcnt[rt] = a2 >= thr ? 2 : 1;  // 2: at least two candidates
       }
-      __syncthreads();
-      // ---- candidates within 2E of the row maximum
-      const float kmax = sqrtf(fmaxf(fmaxf(sm.kmax2[0], sm.kmax2[1]), fmaxf(sm.kmax2[2], sm.kmax2[3])));
+      // lane pair (pr, hf): row wr0 + pr = 16 rt + c with rt = pr >> 4 -- this lane's c matches
+      const int prt = pr >> 4;
+      const int myidx = prt ? widx[1] : widx[0];
+      const int mycnt = prt ? wcnt[1] : wcnt[0];
+      const int mylim = prt ? lim[1] : lim[0];
+      const bool row_ok = pin && mylim > 0;
+      // unique winner: its exact dot, half per lane, in exact_dot's order
+      double half = 0.0;
+      if (row_ok && mycnt == 1) {
+        const uint16_t* krow = kt_base + myidx * RS + hf * h;
+        if constexpr (FULLD) {
 #pragma unroll
-      for (int rt = 0; rt < 8; ++rt) {
-        const int rr = 16 * rt + c;
-        const float gm = fmaxf(fmaxf(sm.wmax[0][rr], sm.wmax[1][rr]), fmaxf(sm.wmax[2][rr], sm.wmax[3][rr]));
-        const float thr = gm - 2.f * cerr * sm.qnorm[rr] * kmax;
-        int cnt = 0;
+          for (int j8 = 0; j8 < HW / 4; ++j8) {  // 8 dims per 16-byte read
+            // opaque to the optimiser: keeps the FP64 widening of the query inside the
+            // block loop instead of 2 x 64 hoisted registers
+            asm volatile("" : "+v"(qh[4 * j8]), "+v"(qh[4 * j8 + 1]), "+v"(qh[4 * j8 + 2]), "+v"(qh[4 * j8 + 3]));
+            const uint4 kw = *reinterpret_cast<const uint4*>(krow + 8 * j8);
+            const uint32_t kx[4] = {kw.x, kw.y, kw.z, kw.w};
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int kl = 32 * wid + 16 * kt + 4 * q4 + i;
-            const bool ok = rowok[rt] && kl < nk && kb + kl <= trow[rt];
-            cnt += (ok && acc[rt][kt][i] >= thr) ? 1 : 0;
+            for (int u = 0; u < 4; ++u) {
+              half = fma(static_cast<double>(bf16_lo(qh[4 * j8 + u])), static_cast<double>(bf16_lo(kx[u])), half);
+              half = fma(static_cast<double>(bf16_hi(qh[4 * j8 + u])), static_cast<double>(bf16_hi(kx[u])), half);
+            }
           }
-        cnt += __shfl_xor(cnt, 16, kWave);
-        cnt += __shfl_xor(cnt, 32, kWave);
-        if (q4 == 0) sm.wcnt[wid][rr] = cnt;
-      }
-      __syncthreads();
-      // ---- resolve rows: 2 threads per row evaluate the two halves of the winner's exact dot
-      const int rr = tid & (kTileRows - 1);
-      const int half = tid >> 7;
-      const int64_t r = r0 + rr;
-      const bool valid = r >= ra && r < rb && sm.qb[rr] >= b;
-      const int h = Di / 2;
-      int winner = -1;
-      bool unique = false;
-      if (valid) {
-        float gm = sm.wmax[0][rr];
-        int gw = 0;
-#pragma unroll
-        for (int w = 1; w < 4; ++w)
-          if (sm.wmax[w][rr] > gm) {
-            gm = sm.wmax[w][rr];
-            gw = w;
-          }
-        const int total = sm.wcnt[0][rr] + sm.wcnt[1][rr] + sm.wcnt[2][rr] + sm.wcnt[3][rr];
-        unique = total == 1;
-        winner = sm.widx[gw][rr];
-        if (unique && half == 1) sm.half[rr] = lds_half_dot(sm.q + rr * RS, sm.k + winner * RS, h, Di);
-      }
-      __syncthreads();
-      if (half == 0 && valid) {
-        if (unique) {
-          const double dot = lds_half_dot(sm.q + rr * RS, sm.k + winner * RS, 0, h) + sm.half[rr];
-          const double dv = neg ? -dot : dot;
-          scores[r * NB + b] = static_cast<float>(ascale * dv);
-          if (tie) tie[r * NB + b] = winner + 1;
         } else {
-          sm.slow[atomicAdd(&sm.nslow, 1)] = rr;
+#pragma unroll
+          for (int w4 = 0; w4 < HW / 2; ++w4) {
+            if (4 * w4 < h) {
+              asm volatile("" : "+v"(qh[2 * w4]), "+v"(qh[2 * w4 + 1]));
+              const uint2 kw = *reinterpret_cast<const uint2*>(krow + 4 * w4);
+              half = fma(static_cast<double>(bf16_lo(qh[2 * w4])), static_cast<double>(bf16_lo(kw.x)), half);
+              half = fma(static_cast<double>(bf16_hi(qh[2 * w4])), static_cast<double>(bf16_hi(kw.x)), half);
+              half = fma(static_cast<double>(bf16_lo(qh[2 * w4 + 1])), static_cast<double>(bf16_lo(kw.y)), half);
+              half = fma(static_cast<double>(bf16_hi(qh[2 * w4 + 1])), static_cast<double>(bf16_hi(kw.y)), half);
+            }
+          }
         }
       }
-      __syncthreads();
-      // ---- slow path: exact evaluation of every key of the block for the listed rows
-      const int nslow = sm.nslow;
-      for (int si = 0; si < nslow; ++si) {
-        const int sr = sm.slow[si];
-        const int64_t srow = r0 + sr;
-        const int64_t st = srow / G;
-        double v = -__builtin_inf();
-        int idx = 0x7fffffff;
-        if (tid < nk && kb + tid <= st) {
-          const double dot = lds_half_dot(sm.q + sr * RS, sm.k + tid * RS, 0, h) +
-                             lds_half_dot(sm.q + sr * RS, sm.k + tid * RS, h, Di);
-          v = neg ? -dot : dot;
-          idx = tid;
+      const double other = __shfl_xor(half, 32, kWave);
+      if (row_ok && mycnt == 1 && hf == 0) {
+        const int64_t out = (r0 + prow) * NB + cur.b;
+        scores[out] = static_cast<float>(ascale * (half + other));
+        if (tie) tie[out] = myidx + 1;
+      }
+      // ambiguous rows: every visible key of the block in FP64, whole wave (rare). The
+      // row's query (sign-flipped) goes through this wave's LDS slot; lane l takes keys
+      // l and l + 64 and runs exact_dot's two half chains for each.
+      uint64_t slow = __ballot(row_ok && mycnt != 1 && hf == 0);
+      while (slow) {
+        const int j = __builtin_ctzll(slow);
+        slow &= slow - 1;
+        if (pr == j) {
+#pragma unroll
+          for (int w = 0; w < HW; ++w)
+            if (2 * w < h) sm.qrow[wid][hf * (h / 2) + w] = qh[w];
         }
-        const double wbest = wave_max_f64(v);
-        int wc = wave_sum_i32((v == wbest && idx != 0x7fffffff) ? 1 : 0);
-        int wf = (v == wbest) ? idx : 0x7fffffff;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int64_t srow = r0 + wr0 + j;
+        const int64_t st = srow / G;
+        const int vis = static_cast<int>(st - kb + 1 < nk ? st - kb + 1 : nk);
+        const uint32_t* qw = sm.qrow[wid];
+        double best = -__builtin_inf();
+        int count = 0, first = 0x7fffffff;
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+          const int kl = lane + 64 * kh;
+          if (kl < vis) {
+            const uint16_t* krow = kt_base + kl * RS;
+            double a0 = 0.0, a1 = 0.0;
+#pragma unroll
+            for (int w4 = 0; w4 < HW / 2; ++w4) {
+              if (4 * w4 < h) {
+                const uint2 q0 = *reinterpret_cast<const uint2*>(qw + 2 * w4);
+                const uint2 q1 = *reinterpret_cast<const uint2*>(qw + h / 2 + 2 * w4);
+                const uint2 k0 = *reinterpret_cast<const uint2*>(krow + 4 * w4);
+                const uint2 k1 = *reinterpret_cast<const uint2*>(krow + h + 4 * w4);
+                a0 = fma(static_cast<double>(bf16_lo(q0.x)), static_cast<double>(bf16_lo(k0.x)), a0);
+                a1 = fma(static_cast<double>(bf16_lo(q1.x)), static_cast<double>(bf16_lo(k1.x)), a1);
+                a0 = fma(static_cast<double>(bf16_hi(q0.x)), static_cast<double>(bf16_hi(k0.x)), a0);
+                a1 = fma(static_cast<double>(bf16_hi(q1.x)), static_cast<double>(bf16_hi(k1.x)), a1);
+                a0 = fma(static_cast<double>(bf16_lo(q0.y)), static_cast<double>(bf16_lo(k0.y)), a0);
+                a1 = fma(static_cast<double>(bf16_lo(q1.y)), static_cast<double>(bf16_lo(k1.y)), a1);
+                a0 = fma(static_cast<double>(bf16_hi(q0.y)), static_cast<double>(bf16_hi(k0.y)), a0);
+                a1 = fma(static_cast<double>(bf16_hi(q1.y)), static_cast<double>(bf16_hi(k1.y)), a1);
+              }
+            }
+            const double v = a0 + a1;
+            if (v > best) {
+              best = v;
+              count = 1;
+              first = kl;
+            } else if (v == best) {
+              ++count;
+            }
+          }
+        }
+        const double wbest = wave_max_f64(best);
+        const int wc = wave_sum_i32((best == wbest && count > 0) ? count : 0);
+        int wf = (best == wbest && count > 0) ? first : 0x7fffffff;
 #pragma unroll
         for (int o = 32; o > 0; o >>= 1) wf = min(wf, __shfl_xor(wf, o, kWave));
         if (lane == 0) {
-          sm.red_v[wid] = wbest;
-          sm.red_c[wid] = wc;
-          sm.red_f[wid] = wf;
+          const int64_t out = srow * NB + cur.b;
+          scores[out] = static_cast<float>(ascale * wbest);
+          if (tie) tie[out] = wc == 1 ? wf + 1 : -wc;
         }
-        __syncthreads();
-        if (tid == 0) {
-          double best = sm.red_v[0];
-          for (int w = 1; w < 4; ++w) best = fmax(best, sm.red_v[w]);
-          int count = 0, first = 0x7fffffff;
-          for (int w = 0; w < 4; ++w)
-            if (sm.red_v[w] == best) {
-              count += sm.red_c[w];
-              first = min(first, sm.red_f[w]);
-            }
-          scores[srow * NB + b] = static_cast<float>(ascale * best);
-          if (tie) tie[srow * NB + b] = count == 1 ? first + 1 : -count;
-        }
-        __syncthreads();
       }
-      if (tid == 0) sm.nslow = 0;
     }
+    if (nxt.s < nseq) commit(buf ^ 1);  // that buffer's readers finished before the last barrier
+    __syncthreads();  // this block's readers are done; the next block is visible
+    buf ^= 1;
+    cur = nxt;
   }
-  // ---- blocks without a causal key: -inf, tie code 0
-  for (int e = tid; e < kTileRows * NB; e += 256) {
-    const int rr2 = e / NB, b = e % NB;
-    if (rr2 < nr && b > sm.qb[rr2]) {
-      scores[(r0 + rr2) * NB + b] = -__builtin_inff();
-      if (tie) tie[(r0 + rr2) * NB + b] = 0;
+
+  // ---- blocks without a causal key: -inf, tie code 0 (each wave fills its rows)
+  const int64_t pstart = pin ? cu[find_seq(cu, nseq, ptok)] : 0;
+  const int pqb = pin ? static_cast<int>((ptok - pstart) / B) : NB;
+  for (int j = 0; j < 32; ++j) {
+    const int qbj = __shfl(pqb, j, kWave);
+    if (wr0 + j >= nr) break;
+    const int64_t base = (r0 + wr0 + j) * NB;
+    for (int b = qbj + 1 + lane; b < NB; b += kWave) {
+      scores[base + b] = -__builtin_inff();
+      if (tie) tie[base + b] = 0;
     }
   }
 }
@@ -319,15 +401,16 @@ bool score_mfma_supported(int Di, int B, double scale) {
 
 int score_fwd_mfma_launch(const void* iq, const void* ik, const int32_t* cu, int nseq, int64_t rows, int G, int Di,
                           int NB, int B, double scale, float* scores, int32_t* tie, hipStream_t st) {
-  const dim3 grid(grid_1d(rows, kTileRows)), block(256);
+  const dim3 grid(grid_1d(rows, kTileRows)), block(kThreads);
   const auto* q = static_cast<const uint16_t*>(iq);
   const auto* k = static_cast<const uint16_t*>(ik);
-  if (Di <= 32)
-    hipLaunchKernelGGL(score_fwd_mfma_kernel<1>, grid, block, 0, st, q, k, cu, nseq, rows, G, Di, NB, B, scale, scores, tie);
-  else if (Di <= 64)
-    hipLaunchKernelGGL(score_fwd_mfma_kernel<2>, grid, block, 0, st, q, k, cu, nseq, rows, G, Di, NB, B, scale, scores, tie);
-  else
-    hipLaunchKernelGGL(score_fwd_mfma_kernel<4>, grid, block, 0, st, q, k, cu, nseq, rows, G, Di, NB, B, scale, scores, tie);
+#define MSA_SCORE_MFMA(NKV, FD) hipLaunchKernelGGL((score_fwd_mfma_kernel<NKV, FD>), grid, block, 0, st, q, k, cu, nseq, rows, G, Di, NB, B, scale, scores, tie)
+  const int nk = Di <= 32 ? 1 : (Di <= 64 ? 2 : 4);
+  const bool fd = Di == 32 * nk;
+  if (nk == 1) { if (fd) MSA_SCORE_MFMA(1, true); else MSA_SCORE_MFMA(1, false); }
+  else if (nk == 2) { if (fd) MSA_SCORE_MFMA(2, true); else MSA_SCORE_MFMA(2, false); }
+  else { if (fd) MSA_SCORE_MFMA(4, true); else MSA_SCORE_MFMA(4, false); }
+#undef MSA_SCORE_MFMA
   return status_from(hipGetLastError());
 }
 

@@ -125,6 +125,22 @@ def test_no_grad_with_trainable_inputs_preserves_score_values(device):
     torch.testing.assert_close(trainable, inference, atol=0, rtol=0)
 
 
+@pytest.mark.parametrize("scale", [1.0, -1.0, 0.5])
+@pytest.mark.parametrize("dim", [32, 64, 128])
+def test_score_mfma_path_exact_ties(dim, scale, device):
+    """Small-integer bf16 inputs make exact ties and near-ties common, so the MFMA
+    path's ambiguous-row branch (full FP64 re-evaluation of the block) and its tie
+    codes are exercised; the backward consumes those codes."""
+    gen = torch.Generator().manual_seed(dim + int(4 * scale))
+    lengths = [300, 77]
+    q_cpu = torch.randint(-2, 3, (sum(lengths), 2, dim), generator=gen).to(torch.bfloat16)
+    k_cpu = torch.randint(-2, 3, (sum(lengths), 1, dim), generator=gen).to(torch.bfloat16)
+    block = 32
+    nb = (max(lengths) + block - 1) // block
+    upstream = torch.randn((sum(lengths), 2, nb), generator=gen).to(torch.bfloat16).float()
+    _run(q_cpu, k_cpu, lengths, max(lengths), block, scale, upstream, device)
+
+
 @pytest.mark.parametrize("lengths,groups,dim,block,seed", [
     ([1280 - 512, 512], 2, 64, 128, 71), ([2048], 4, 128, 128, 3), ([300, 1, 777], 3, 96, 64, 4),
 ])
