@@ -573,12 +573,15 @@ __global__ __launch_bounds__(256) void kv_bwd_accumulate(const int32_t* __restri
 }
 
 // dQ = scale * sum of the row's block partials over its valid slots (FP64, slot
-// order); 32 lanes per row.
+// order); 32 lanes per row. Slots are taken 8 at a time with all of their
+// partial loads issued first (every slot's record is in bounds; invalid slots
+// are masked, never added).
 __global__ __launch_bounds__(256) void kv_bwd_dq_combine(const int32_t* __restrict__ indices,
                                                          const int32_t* __restrict__ cu, int nseq, int64_t t0,
                                                          int64_t t1, int Hq, int G, int D, int K, int B, double scale,
                                                          const float* __restrict__ dqpart,
                                                          uint16_t* __restrict__ dq) {
+  constexpr int kBatch = 8;
   const int sub = threadIdx.x & 31;
   const int64_t th = t0 * Hq + static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
   if (th >= t1 * Hq) return;
@@ -591,14 +594,25 @@ __global__ __launch_bounds__(256) void kv_bwd_dq_combine(const int32_t* __restri
   const int64_t rec0 = ((t - t0) * Hq + h) * static_cast<int64_t>(K);
   if (4 * sub >= D) return;
   double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
-  for (int slot = 0; slot < K; ++slot) {
-    const int id = sel[slot];
-    if (id < 0 || id > qb) continue;
-    const float4 x = *reinterpret_cast<const float4*>(dqpart + (rec0 + slot) * D + 4 * sub);
-    a0 += static_cast<double>(x.x);
-    a1 += static_cast<double>(x.y);
-    a2 += static_cast<double>(x.z);
-    a3 += static_cast<double>(x.w);
+  for (int s0 = 0; s0 < K; s0 += kBatch) {
+    float4 x[kBatch];
+    bool ok[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int slot = s0 + u < K ? s0 + u : K - 1;
+      const int id = sel[slot];
+      ok[u] = s0 + u < K && id >= 0 && id <= qb;
+      x[u] = *reinterpret_cast<const float4*>(dqpart + (rec0 + slot) * D + 4 * sub);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (ok[u]) {
+        a0 += static_cast<double>(x[u].x);
+        a1 += static_cast<double>(x[u].y);
+        a2 += static_cast<double>(x[u].z);
+        a3 += static_cast<double>(x[u].w);
+      }
+    }
   }
   const uint32_t w0 = f32_to_bf16_bits(static_cast<float>(a0 * scale)) |
                       (static_cast<uint32_t>(f32_to_bf16_bits(static_cast<float>(a1 * scale))) << 16);
@@ -633,7 +647,7 @@ static BwdLayout bwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t
   const int64_t rows = total_blocks * G;
   const int64_t R = Hq / (G > 0 ? G : 1);
   const int64_t DP = 32 * nk_of_dim(static_cast<int>(D));
-  const int64_t tc = kv_chunk_tokens(T, Hq, K, D * 4 + 8);
+  const int64_t tc = kv_chunk_tokens(T, Hq, K, D * 4 + 8, int64_t(1) << 32);
   int64_t sepi = static_cast<int64_t>(kStatItemRows) / (R > 0 ? R : 1);
   if (sepi < 1) sepi = 1;
   b.stat_plan = kv_plan_layout(T, rows, G, K, tc, sepi);

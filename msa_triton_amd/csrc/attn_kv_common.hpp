@@ -46,9 +46,11 @@ __device__ __forceinline__ RowGeom row_geom(const int32_t* __restrict__ cu, cons
 
 inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
-// Query tokens per chunk: per-(token, head, slot) records of `record_bytes`
-// each, within ~1 GiB.
-int64_t kv_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t record_bytes);
+// Query tokens per chunk: per-(token, head, slot) records of `record_bytes` each
+// within `budget` bytes, chunks of equal size. The forward partial pass runs
+// best with ~1 GiB chunks (its gathered query rows stay cache-resident), the
+// backward with ~4 GiB (fewer per-chunk key-block reloads and item tails).
+int64_t kv_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t record_bytes, int64_t budget);
 
 struct KvPlan {
   int64_t rows, tc, nch, epi, max_items;  // max_items: per-chunk upper bound on work items

@@ -309,7 +309,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
 }
 
 // 32 lanes per (token, head) of the chunk, 4 dims each (D <= 128): merge the
-// valid slots' partials in slot order in FP64.
+// valid slots' partials in slot order in FP64. Slots are taken 8 at a time with
+// all of their partial loads issued before any arithmetic (records are in bounds
+// for every slot, valid or not; invalid slots are masked, never multiplied).
+constexpr int kCombineBatch = 8;
+
 __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restrict__ indices,
                                                         const int32_t* __restrict__ cu, int nseq, int64_t t0,
                                                         int64_t t1, int Hq, int G, int D, int K, int B,
@@ -327,6 +331,7 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
   const int32_t* sel = indices + (t * G + g) * K;
   const int64_t rec0 = ((t - t0) * Hq + h) * static_cast<int64_t>(K);
 
+  // slot sub (and sub + 32, ...) of this row: validity and (m, l)
   float M = -__builtin_inff();
   for (int s0 = 0; s0 < K; s0 += 32) {
     const int slot = s0 + sub;
@@ -341,6 +346,7 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
   double L = 0.0;
   double acc[4] = {0.0, 0.0, 0.0, 0.0};
   const bool has_dims = 4 * sub < D;
+  const int dcol = has_dims ? 4 * sub : 0;  // lanes without dims read (and ignore) dims 0..3
   if (M != -__builtin_inff()) {
     for (int s0 = 0; s0 < K; s0 += 32) {
       const int slot = s0 + sub;
@@ -354,15 +360,22 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
         }
       }
       const int n = K - s0 < 32 ? K - s0 : 32;
-      for (int j = 0; j < n; ++j) {
-        const double wj = __shfl(w, j, 32);
-        if (wj == 0.0) continue;  // invalid slot (or a weight that underflowed to zero)
-        if (has_dims) {
-          const float4 op = *reinterpret_cast<const float4*>(opart + (rec0 + s0 + j) * D + 4 * sub);
-          acc[0] = fma(wj, static_cast<double>(op.x), acc[0]);
-          acc[1] = fma(wj, static_cast<double>(op.y), acc[1]);
-          acc[2] = fma(wj, static_cast<double>(op.z), acc[2]);
-          acc[3] = fma(wj, static_cast<double>(op.w), acc[3]);
+      for (int j0 = 0; j0 < n; j0 += kCombineBatch) {
+        float4 op[kCombineBatch];
+#pragma unroll
+        for (int u = 0; u < kCombineBatch; ++u) {
+          const int j = j0 + u < n ? j0 + u : n - 1;
+          op[u] = *reinterpret_cast<const float4*>(opart + (rec0 + s0 + j) * D + dcol);
+        }
+#pragma unroll
+        for (int u = 0; u < kCombineBatch; ++u) {
+          const double wj = __shfl(w, j0 + u < n ? j0 + u : 0, 32);
+          if (j0 + u < n && wj != 0.0) {  // invalid slot (or a weight that underflowed to zero)
+            acc[0] = fma(wj, static_cast<double>(op[u].x), acc[0]);
+            acc[1] = fma(wj, static_cast<double>(op[u].y), acc[1]);
+            acc[2] = fma(wj, static_cast<double>(op[u].z), acc[2]);
+            acc[3] = fma(wj, static_cast<double>(op[u].w), acc[3]);
+          }
         }
       }
     }
@@ -403,11 +416,13 @@ static int64_t fwd_epi(int64_t R) {
   return e < 1 ? 1 : e;
 }
 
-int64_t kv_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t record_bytes) {
+int64_t kv_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t record_bytes, int64_t budget) {
   const int64_t per_token = Hq * (K > 0 ? K : 1) * record_bytes;
-  int64_t tc = (int64_t(1) << 30) / (per_token > 0 ? per_token : 1);
+  int64_t tc = budget / (per_token > 0 ? per_token : 1);
   if (tc < 64) tc = 64;
-  return tc < T ? tc : (T > 0 ? T : 1);
+  if (T <= tc) return T > 0 ? T : 1;
+  const int64_t nch = (T + tc - 1) / tc;  // balanced chunks
+  return (T + nch - 1) / nch;
 }
 
 KvPlan kv_plan_layout(int64_t T, int64_t rows, int64_t G, int64_t K, int64_t tc, int64_t epi) {
@@ -444,7 +459,7 @@ struct FwdLayout {
 
 static FwdLayout fwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks) {
   FwdLayout f;
-  const int64_t tc = kv_chunk_tokens(T, Hq, K, (D + 2) * 4);
+  const int64_t tc = kv_chunk_tokens(T, Hq, K, (D + 2) * 4, int64_t(1) << 30);
   f.plan = kv_plan_layout(T, total_blocks * G, G, K, tc, fwd_epi(Hq / (G > 0 ? G : 1)));
   f.opart = f.plan.bytes;
   f.ml = f.opart + align256(tc * Hq * K * D * 4);
