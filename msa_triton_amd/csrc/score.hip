@@ -14,8 +14,9 @@
 //
 // Backward (index_score.py:139-232): ds*scale goes to the unique winner or is
 // split evenly across exact ties. dq is a per-row gather; dk scans each key
-// block's rows for the winners it owns (row segments, summed in order). Both accumulate in FP64 in a fixed order (no float
-// atomics), then round to the input dtype.
+// block's rows once per row segment and adds each row into its winner's FP64 LDS
+// row (rows in order; segments summed in order). Both accumulate in FP64 in a fixed
+// order (no float atomics), then round to the input dtype.
 #include "common.hpp"
 #include "score_mfma.hpp"
 
@@ -89,8 +90,37 @@ __global__ __launch_bounds__(256) void score_bwd_transpose(const int32_t* __rest
   }
 }
 
+__device__ __forceinline__ int lane_i32(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+
+// Element `hi` (0: low half, 1: high half) of a word holding two 2-byte values, as fp32.
+template <int DT>
+__device__ __forceinline__ float half_of(uint32_t w, int hi) {
+  if constexpr (DT == kBF16) {
+    return __uint_as_float(hi ? (w & 0xffff0000u) : (w << 16));
+  } else {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(hi ? (w >> 16) : (w & 0xffffu))));
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  if constexpr (DT == kBF16) {
+    return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+  } else {
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))) << 16);
+  }
+}
+__device__ __forceinline__ float lane_f32(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
 // dq[t,g] = sum over valid blocks of w * k[winner] (ties: w/count per tied key).
-// One wavefront per row, lanes over index dims, FP64 accumulation in block order.
+// One wavefront per row, lane j of the wave owns dims DPL j .. DPL j + DPL - 1. The
+// row's blocks are taken 64 at a time (lane = block); unique winners are added in
+// block order with kDqBatch key rows in flight (block / key broadcast by readlane),
+// then the chunk's exact ties (rare) in block order. FP64 accumulation.
+constexpr int kDqBatch = 16;
 template <int DT, int DPL>
 __global__ __launch_bounds__(256) void score_bwd_dq(const void* __restrict__ iq,
                                                     const void* __restrict__ ik,
@@ -110,64 +140,66 @@ __global__ __launch_bounds__(256) void score_bwd_dq(const void* __restrict__ iq,
   double acc[DPL];
 #pragma unroll
   for (int i = 0; i < DPL; ++i) acc[i] = 0.0;
+  const int dbase = DPL * lane;
   for (int b0 = 0; b0 < nvalid; b0 += 64) {
     const int bl = b0 + lane;
     const int32_t my_tie = bl < nvalid ? tie[row * NB + bl] : 0;
     const float my_ds = bl < nvalid ? ds[row * NB + bl] : 0.f;
-    const int n = nvalid - b0 < 64 ? nvalid - b0 : 64;
-    // blocks in order; unique winners' key rows are loaded four at a time
-    int i = 0;
-    while (i < n) {
-      int bi[4];
+    // winner key relative to the sequence start (< 2^31: it is a token of the sequence)
+    const int my_key = my_tie > 0 ? bl * B + my_tie - 1 : 0;
+    uint64_t um = __ballot(my_tie > 0);
+    while (um) {
+      int bi[kDqBatch];
       int cnt = 0;
-      while (cnt < 4 && i < n) {
-        if (__shfl(my_tie, i, kWave) <= 0) break;  // a tie (or an empty block) is handled alone, in order
-        bi[cnt++] = i++;
-      }
-      if (cnt > 0) {
-        float kv[4][DPL];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (u < cnt) {
-            const int32_t ti = __shfl(my_tie, bi[u], kWave);
-            const int64_t key = start + static_cast<int64_t>(b0 + bi[u]) * B + ti - 1;
-#pragma unroll
-            for (int j = 0; j < DPL; ++j) {
-              const int d = lane + j * kWave;
-              kv[u][j] = d < Di ? load_as_f32<DT>(ik, key * Di + d) : 0.f;
-            }
-          }
+      for (int u = 0; u < kDqBatch; ++u) {
+        bi[u] = 0;
+        if (um) {
+          bi[u] = __builtin_ctzll(um);
+          um &= um - 1;
+          cnt = u + 1;
         }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (u < cnt) {
-            const double wgt = static_cast<double>(__shfl(my_ds, bi[u], kWave)) * scale;
-#pragma unroll
-            for (int j = 0; j < DPL; ++j) acc[j] = fma(wgt, static_cast<double>(kv[u][j]), acc[j]);
-          }
-        }
-        continue;
       }
-      const int32_t ti = __shfl(my_tie, i, kWave);
-      const float di = __shfl(my_ds, i, kWave);
+      float kv[kDqBatch][DPL];
+#pragma unroll
+      for (int u = 0; u < kDqBatch; ++u) {
+        const int64_t key = start + lane_i32(my_key, bi[u]);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          const int d = dbase + j;
+          kv[u][j] = (u < cnt && d < Di) ? load_as_f32<DT>(ik, key * Di + d) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kDqBatch; ++u) {
+        if (u < cnt) {
+          const double wgt = static_cast<double>(lane_f32(my_ds, bi[u])) * scale;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) acc[j] = fma(wgt, static_cast<double>(kv[u][j]), acc[j]);
+        }
+      }
+    }
+    // exact ties of this chunk, in block order (rare)
+    uint64_t tm = __ballot(my_tie < 0);
+    while (tm) {
+      const int i = __builtin_ctzll(tm);
+      tm &= tm - 1;
+      const float di = lane_f32(my_ds, i);
       const int64_t k0 = start + static_cast<int64_t>(b0 + i) * B;
-      ++i;
-      if (ti < 0) {
-        const int64_t k1 = (k0 + B < t + 1) ? k0 + B : t + 1;
-        const BlockMax bm = block_max_exact<DT>(iq, row * Di, ik, k0, k1, Di, scale, lane);
-        const double wgt = static_cast<double>(di) * scale / static_cast<double>(bm.count);
-        for (int64_t base = k0; base < k1; base += kWave) {
-          const int64_t kk = base + lane;
-          const bool win = kk < k1 && directed(exact_dot<DT>(iq, row * Di, ik, kk * Di, Di), scale) == bm.best;
-          uint64_t mask = __ballot(win);
-          while (mask) {
-            const int wl = __builtin_ctzll(mask);
-            mask &= mask - 1;
+      const int64_t k1 = (k0 + B < t + 1) ? k0 + B : t + 1;
+      const BlockMax bm = block_max_exact<DT>(iq, row * Di, ik, k0, k1, Di, scale, lane);
+      const double wgt = static_cast<double>(di) * scale / static_cast<double>(bm.count);
+      for (int64_t base = k0; base < k1; base += kWave) {
+        const int64_t kk = base + lane;
+        const bool win = kk < k1 && directed(exact_dot<DT>(iq, row * Di, ik, kk * Di, Di), scale) == bm.best;
+        uint64_t mask = __ballot(win);
+        while (mask) {
+          const int wl = __builtin_ctzll(mask);
+          mask &= mask - 1;
 #pragma unroll
-            for (int j = 0; j < DPL; ++j) {
-              const int d = lane + j * kWave;
-              if (d < Di) acc[j] = fma(wgt, static_cast<double>(load_as_f32<DT>(ik, (base + wl) * Di + d)), acc[j]);
-            }
+          for (int j = 0; j < DPL; ++j) {
+            const int d = dbase + j;
+            if (d < Di) acc[j] = fma(wgt, static_cast<double>(load_as_f32<DT>(ik, (base + wl) * Di + d)), acc[j]);
           }
         }
       }
@@ -175,137 +207,386 @@ __global__ __launch_bounds__(256) void score_bwd_dq(const void* __restrict__ iq,
   }
 #pragma unroll
   for (int j = 0; j < DPL; ++j) {
-    const int d = lane + j * kWave;
+    const int d = dbase + j;
     if (d < Di) store_from_f32<DT>(dq, row * Di + d, static_cast<float>(acc[j]));
   }
 }
 
-// dk, partial sums. One wavefront per (key block gb, 8 keys, row segment, 128-dim
-// chunk): it scans the segment's rows (t, g) of gb's sequence with t >= block
-// start, 64 per step (lanes = rows, block-major tie/ds), and adds w * q[row] for
-// rows whose unique winner is one of its keys (lanes = dims, FP64, row order;
-// q rows are loaded four at a time). Exact ties add w / count to every tied key
-// among its keys (exact recomputation). The per-segment sums go to
-// part[((wave * dchunks + dc) * 8 + key) * 128 + dim]; score_bwd_dk_reduce adds
-// the segments in order.
-constexpr int kDkKeys = 8;
+// Wide-gather dq for 2-byte dtypes with Di = 32, 64 or 128: a row of Di
+// elements is LPR = Di / 8 lanes x 16 bytes, so one load instruction fetches RPI =
+// 64 / LPR winner rows. Per 64-block chunk the unique winners are compacted (in
+// block order) into the wave's LDS list; lane (slot, chunk) adds entries slot,
+// slot + RPI, ... of the list into FP64 sums of its 8 dims, and the RPI slot sums
+// are added in slot order at the end (a fixed order). Exact ties (rare) are added
+// by every slot-0 lane after the chunk's unique winners, in block order.
+template <int DT, int LPR>
+__global__ __launch_bounds__(256) void score_bwd_dq_wide(const void* __restrict__ iq,
+                                                         const void* __restrict__ ik,
+                                                         const int32_t* __restrict__ cu, int nseq,
+                                                         const int32_t* __restrict__ tie,
+                                                         const float* __restrict__ ds, int64_t rows, int G,
+                                                         int Di, int NB, int B, double scale,
+                                                         void* __restrict__ dq) {
+  constexpr int RPI = 64 / LPR;
+  __shared__ int32_t lkey[4][64];
+  __shared__ float lw[4][64];
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wid;
+  if (row >= rows) return;  // whole wave
+  const int slot = lane / LPR, dch = lane % LPR;
+  const int64_t t = row / G;
+  const int sq = find_seq(cu, nseq, t);
+  const int64_t start = cu[sq];
+  const int64_t pos = t - start;
+  const int nvalid = static_cast<int>(pos / B + 1 < NB ? pos / B + 1 : NB);
+  const uint16_t* kb16 = static_cast<const uint16_t*>(ik);
+  double acc[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = 0.0;
+  const uint64_t lt = (uint64_t(1) << lane) - 1;
+  for (int b0 = 0; b0 < nvalid; b0 += 64) {
+    const int bl = b0 + lane;
+    const int32_t my_tie = bl < nvalid ? tie[row * NB + bl] : 0;
+    const float my_ds = bl < nvalid ? ds[row * NB + bl] : 0.f;
+    const uint64_t um = __ballot(my_tie > 0);
+    if (my_tie > 0) {
+      const int p = __popcll(um & lt);
+      lkey[wid][p] = bl * B + my_tie - 1;  // winner key relative to the sequence start
+      lw[wid][p] = my_ds;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int n = __popcll(um);
+    for (int e0 = 0; e0 < n; e0 += 4 * RPI) {
+      uint4 kv[4];
+      double wv[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int e = e0 + u * RPI + slot;
+        const bool ok = e < n;
+        const int64_t key = start + lkey[wid][ok ? e : 0];
+        kv[u] = ok ? *reinterpret_cast<const uint4*>(kb16 + key * Di + 8 * dch) : make_uint4(0u, 0u, 0u, 0u);
+        wv[u] = ok ? static_cast<double>(lw[wid][e]) * scale : 0.0;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const uint32_t x[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) {
+          acc[2 * q2] = fma(wv[u], static_cast<double>(half_of<DT>(x[q2], 0)), acc[2 * q2]);
+          acc[2 * q2 + 1] = fma(wv[u], static_cast<double>(half_of<DT>(x[q2], 1)), acc[2 * q2 + 1]);
+        }
+      }
+    }
+    __builtin_amdgcn_wave_barrier();  // list reused by the next chunk
+    // exact ties of this chunk (rare), in block order: slot-0 lanes hold the sums they add to
+    uint64_t tm = __ballot(my_tie < 0);
+    while (tm) {
+      const int i = __builtin_ctzll(tm);
+      tm &= tm - 1;
+      const float di = lane_f32(my_ds, i);
+      const int64_t k0 = start + static_cast<int64_t>(b0 + i) * B;
+      const int64_t k1 = (k0 + B < t + 1) ? k0 + B : t + 1;
+      const BlockMax bm = block_max_exact<DT>(iq, row * Di, ik, k0, k1, Di, scale, lane);
+      const double wgt = static_cast<double>(di) * scale / static_cast<double>(bm.count);
+      for (int64_t base = k0; base < k1; base += kWave) {
+        const int64_t kk = base + lane;
+        const bool win = kk < k1 && directed(exact_dot<DT>(iq, row * Di, ik, kk * Di, Di), scale) == bm.best;
+        uint64_t mask = __ballot(win);
+        while (mask) {
+          const int wl = __builtin_ctzll(mask);
+          mask &= mask - 1;
+          if (slot == 0) {
+            const uint4 kw = *reinterpret_cast<const uint4*>(kb16 + (base + wl) * Di + 8 * dch);
+            const uint32_t x[4] = {kw.x, kw.y, kw.z, kw.w};
+#pragma unroll
+            for (int q2 = 0; q2 < 4; ++q2) {
+              acc[2 * q2] = fma(wgt, static_cast<double>(half_of<DT>(x[q2], 0)), acc[2 * q2]);
+              acc[2 * q2 + 1] = fma(wgt, static_cast<double>(half_of<DT>(x[q2], 1)), acc[2 * q2 + 1]);
+            }
+          }
+        }
+      }
+    }
+  }
+  // slot sums in slot order
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    double tot = 0.0;
+#pragma unroll
+    for (int sl = 0; sl < RPI; ++sl) tot += __shfl(acc[i], sl * LPR + dch, kWave);
+    acc[i] = tot;
+  }
+  if (slot == 0) {
+    uint32_t o[4];
+#pragma unroll
+    for (int q2 = 0; q2 < 4; ++q2)
+      o[q2] = pack2<DT>(static_cast<float>(acc[2 * q2]), static_cast<float>(acc[2 * q2 + 1]));
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(dq) + row * Di + 8 * dch) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
 
-template <int DT>
-__global__ __launch_bounds__(256) void score_bwd_dk_part(
+// dk, partial sums. One workgroup per (key block gb, segment of kDkSeg rows, chunk of
+// 128 keys). The segment's rows (t, g) of gb's sequence with t >= block start are
+// read once (block-major tie / ds) and bucketed by their unique winner with a stable
+// counting sort in LDS (per 64-row wave step the rank among equal winners comes from
+// seven ballots on the winner's bits; waves are merged in order), so each key's rows
+// stay in row order. Wave w then sums the keys w, w + 4, ...: lanes over dims, query
+// rows streamed kDkBatch at a time, FP64 accumulation in row order; the segment's
+// exact ties (rare) follow in row order. The sums go to
+// part[((gb * nseg + sg) * kchunks + kc) * 128 + key][Di]; score_bwd_dk_reduce adds
+// the segments in order.
+// acc += w * q[row] over this lane's dims (wide layout: 8 dims 8 dch .. +7, only the
+// slot-0 lanes' sums are kept; otherwise DPL dims from dbase).
+template <int DT, int DPL>
+__device__ __forceinline__ void dk_add_row(double (&acc)[8], double wgt, const void* __restrict__ iq, int64_t row,
+                                           int Di, bool wide, int dch, int dbase) {
+  if (wide) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      acc[j] = fma(wgt, static_cast<double>(load_as_f32<DT>(iq, row * Di + 8 * dch + j)), acc[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const int d = dbase + j;
+      if (d < Di) acc[j] = fma(wgt, static_cast<double>(load_as_f32<DT>(iq, row * Di + d)), acc[j]);
+    }
+  }
+}
+
+constexpr int kDkSeg = 8192;
+constexpr int kDkBatch = 16;
+constexpr int kDkTieCap = 256;
+
+template <int DT, int DPL>
+__global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
     const void* __restrict__ iq, const void* __restrict__ ik, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, int nseq, const int32_t* __restrict__ tie_t,
-    const float* __restrict__ ds_t, int64_t rows, int G, int Di, int B, int kgroups, int nseg, int64_t seg_rows,
-    int64_t total_blocks, double scale, double* __restrict__ part) {
-  const int lane = threadIdx.x & 63;
-  const int64_t w = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (w >= total_blocks * kgroups * nseg) return;
+    const float* __restrict__ ds_t, int64_t rows, int G, int Di, int B, int nseg, double scale,
+    double* __restrict__ part) {
+  __shared__ uint16_t lrow[kDkSeg];   // bucketed row offsets (within the segment)
+  __shared__ float lds_w[kDkSeg];     // their ds
+  __shared__ int32_t cnt[128], bstart[128], running[128];
+  __shared__ int32_t wcnt[4][128];
+  __shared__ int32_t tie_row[kDkTieCap];
+  __shared__ double tie_best[kDkTieCap];
+  __shared__ int32_t tie_count[kDkTieCap];
+  __shared__ int32_t ntie_s;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t w = blockIdx.x;  // (gb, sg)
   const int sg = static_cast<int>(w % nseg);
-  const int kg = static_cast<int>((w / nseg) % kgroups);
-  const int64_t gb = w / nseg / kgroups;
-  const int dc = blockIdx.y, dchunks = gridDim.y;
+  const int64_t gb = w / nseg;
+  const int kc = blockIdx.y, kchunks = gridDim.y;
   int s = upper_index(cu_blocks, nseq + 1, gb);
   while (s < nseq && cu_blocks[s + 1] <= gb) ++s;
   const int b = static_cast<int>(gb - cu_blocks[s]);
   const int64_t start = cu[s], end = cu[s + 1];
   const int64_t k0 = start + static_cast<int64_t>(b) * B;
-  const int64_t kend = k0 + B < end ? k0 + B : end;
-  const int o0 = kg * kDkKeys;
-  const int64_t kA = k0 + o0;
-  const int nk = static_cast<int>(kend - kA < kDkKeys ? kend - kA : kDkKeys);
-  const int64_t r_begin = k0 * G + sg * seg_rows;
-  const int64_t r_stop = (k0 * G + (sg + 1) * seg_rows) < end * G ? k0 * G + (sg + 1) * seg_rows : end * G;
-  double acc[kDkKeys][2];
-#pragma unroll
-  for (int kk = 0; kk < kDkKeys; ++kk) acc[kk][0] = acc[kk][1] = 0.0;
-  const int d0 = dc * 128 + lane, d1 = d0 + 64;
-  if (nk > 0) {
-    const int32_t* tcol = tie_t + static_cast<int64_t>(b) * rows;
-    const float* dcol = ds_t + static_cast<int64_t>(b) * rows;
-    int32_t tie_n = 0;
-    float ds_n = 0.f;
-    if (r_begin + lane < r_stop) {
-      tie_n = tcol[r_begin + lane];
-      ds_n = dcol[r_begin + lane];
-    }
-    for (int64_t r0 = r_begin; r0 < r_stop; r0 += 64) {
-      const int32_t tie = tie_n;
-      const float dsv = ds_n;
-      if (r0 + 64 + lane < r_stop) {  // prefetch the next step; lanes past the segment end carry no row
-        tie_n = tcol[r0 + 64 + lane];
-        ds_n = dcol[r0 + 64 + lane];
-      } else {
-        tie_n = 0;
-        ds_n = 0.f;
-      }
-      const int rel = tie - 1 - o0;  // winner offset relative to this wave's first key
-      uint64_t m = __ballot(tie > 0 && rel >= 0 && rel < nk);
-      while (m) {
-        int idx[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          idx[u] = -1;
-          if (m) {
-            idx[u] = __builtin_ctzll(m);
-            m &= m - 1;
-          }
-        }
-        float qv[4][2];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          qv[u][0] = qv[u][1] = 0.f;
-          if (idx[u] >= 0) {
-            const int64_t row = r0 + idx[u];
-            if (d0 < Di) qv[u][0] = load_as_f32<DT>(iq, row * Di + d0);
-            if (d1 < Di) qv[u][1] = load_as_f32<DT>(iq, row * Di + d1);
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (idx[u] < 0) continue;
-          const int ru = __shfl(rel, idx[u], kWave);
-          const double wgt = static_cast<double>(__shfl(dsv, idx[u], kWave)) * scale;
-#pragma unroll
-          for (int kk = 0; kk < kDkKeys; ++kk) {
-            if (kk == ru) {
-              acc[kk][0] = fma(wgt, static_cast<double>(qv[u][0]), acc[kk][0]);
-              acc[kk][1] = fma(wgt, static_cast<double>(qv[u][1]), acc[kk][1]);
-            }
-          }
-        }
-      }
-      // exact ties (rare): recompute the block maximum and test this wave's keys
-      uint64_t tm = __ballot(tie < 0);
-      while (tm) {
-        const int i = __builtin_ctzll(tm);
-        tm &= tm - 1;
-        const int64_t row = r0 + i;
-        const int64_t t = row / G;
-        const int64_t k1 = (k0 + B < t + 1) ? k0 + B : t + 1;
-        const int64_t hi = k1 < kA + nk ? k1 : kA + nk;
-        if (hi <= kA) continue;
-        const BlockMax bm = block_max_exact<DT>(iq, row * Di, ik, k0, k1, Di, scale, lane);
-        const double wgt = static_cast<double>(__shfl(dsv, i, kWave)) * scale / static_cast<double>(bm.count);
-        // lanes 0 .. hi - kA - 1 test this wave's visible keys against the exact maximum
-        const bool win = lane < hi - kA &&
-                         directed(exact_dot<DT>(iq, row * Di, ik, (kA + lane) * Di, Di), scale) == bm.best;
-        const uint32_t wmask = static_cast<uint32_t>(__ballot(win));
-        const float q0 = d0 < Di ? load_as_f32<DT>(iq, row * Di + d0) : 0.f;
-        const float q1 = d1 < Di ? load_as_f32<DT>(iq, row * Di + d1) : 0.f;
-#pragma unroll
-        for (int kk = 0; kk < kDkKeys; ++kk) {
-          if ((wmask >> kk) & 1u) {
-            acc[kk][0] = fma(wgt, static_cast<double>(q0), acc[kk][0]);
-            acc[kk][1] = fma(wgt, static_cast<double>(q1), acc[kk][1]);
-          }
-        }
-      }
+  const int64_t r_begin = k0 * G + static_cast<int64_t>(sg) * kDkSeg;
+  const int64_t r_stop = r_begin + kDkSeg < end * G ? r_begin + kDkSeg : end * G;
+  if (r_begin >= r_stop) return;  // whole workgroup: empty segment (the reduce skips it)
+  const int o_lo = 128 * kc;      // this chunk's first key offset in the block
+  const int nseg_rows = static_cast<int>(r_stop - r_begin);
+  const int32_t* tcol = tie_t + static_cast<int64_t>(b) * rows + r_begin;
+  const float* dcol = ds_t + static_cast<int64_t>(b) * rows + r_begin;
+  if (tid < 128) {
+    cnt[tid] = 0;
+    running[tid] = 0;
+    wcnt[0][tid] = wcnt[1][tid] = wcnt[2][tid] = wcnt[3][tid] = 0;
+  }
+  if (tid == 0) ntie_s = 0;
+  __syncthreads();
+  // ---- histogram of winners in this key chunk; list the exact ties
+  for (int i = tid; i < nseg_rows; i += 256) {
+    const int32_t tc = tcol[i];
+    const int o = tc - 1 - o_lo;
+    if (tc > 0 && o >= 0 && o < 128) atomicAdd(&cnt[o], 1);
+    if (tc < 0) {
+      const int slot = atomicAdd(&ntie_s, 1);
+      if (slot < kDkTieCap) tie_row[slot] = i;
     }
   }
-  double* dst = part + (w * dchunks + dc) * kDkKeys * 128;
+  __syncthreads();
+  if (tid < 64) {  // exclusive scan of the 128 bucket counts (two per lane)
+    const int a0 = cnt[2 * tid], a1 = cnt[2 * tid + 1];
+    int x = a0 + a1;
 #pragma unroll
-  for (int kk = 0; kk < kDkKeys; ++kk) {
-    dst[kk * 128 + lane] = acc[kk][0];
-    dst[kk * 128 + 64 + lane] = acc[kk][1];
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, kWave);
+      if (lane >= o) x += y;
+    }
+    bstart[2 * tid] = x - a0 - a1;
+    bstart[2 * tid + 1] = x - a1;
+  }
+  __syncthreads();
+  // ---- stable scatter, 256 rows per step
+  const uint64_t lt = (uint64_t(1) << lane) - 1;
+  for (int base = 0; base < nseg_rows; base += 256) {
+    const int i = base + tid;
+    int32_t tc = 0;
+    float dv = 0.f;
+    if (i < nseg_rows) {
+      tc = tcol[i];
+      dv = dcol[i];
+    }
+    const int o = tc - 1 - o_lo;
+    const bool on = tc > 0 && o >= 0 && o < 128;
+    uint64_t match = __ballot(on);
+#pragma unroll
+    for (int bit = 0; bit < 7; ++bit) {
+      const uint64_t m = __ballot(on && ((o >> bit) & 1));
+      match &= ((o >> bit) & 1) ? m : ~m;
+    }
+    const int rank = __popcll(match & lt);
+    const int total = __popcll(match);
+    if (on && rank == total - 1) wcnt[wid][o] = total;  // last lane of its group
+    __syncthreads();
+    if (on) {
+      int before = running[o] + rank;
+      for (int w2 = 0; w2 < wid; ++w2) before += wcnt[w2][o];
+      const int p = bstart[o] + before;
+      lrow[p] = static_cast<uint16_t>(i);
+      lds_w[p] = dv;
+    }
+    __syncthreads();
+    if (tid < 128) {
+      running[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
+      wcnt[0][tid] = wcnt[1][tid] = wcnt[2][tid] = wcnt[3][tid] = 0;
+    }
+    __syncthreads();
+  }
+  // ---- exact ties of the segment (rare): sort the listed rows, block maximum per row
+  const int ntie = ntie_s < kDkTieCap ? ntie_s : kDkTieCap;
+  const bool tie_overflow = ntie_s > kDkTieCap;
+  if (ntie > 1 && tid == 0) {  // insertion sort: row order
+    for (int x = 1; x < ntie; ++x) {
+      const int v = tie_row[x];
+      int y = x - 1;
+      while (y >= 0 && tie_row[y] > v) {
+        tie_row[y + 1] = tie_row[y];
+        --y;
+      }
+      tie_row[y + 1] = v;
+    }
+  }
+  __syncthreads();
+  for (int x = wid; x < ntie; x += 4) {
+    const int64_t row = r_begin + tie_row[x];
+    const int64_t t = row / G;
+    const int64_t k1 = (k0 + B < t + 1) ? k0 + B : t + 1;
+    const BlockMax bm = block_max_exact<DT>(iq, row * Di, ik, k0, k1, Di, scale, lane);
+    if (lane == 0) {
+      tie_best[x] = bm.best;
+      tie_count[x] = bm.count;
+    }
+  }
+  __syncthreads();
+  // ---- per-key sums: wave w takes keys w, w + 4, ...
+  const int dbase = DPL * lane;
+  const int64_t kchunk_end = k0 + B < end ? k0 + B : end;
+  constexpr int kWideLpr = 16;                  // lanes per 128-dim row (wide gathers, Di == 128)
+  constexpr int kWideRpi = 64 / kWideLpr;       // rows per load instruction
+  const bool wide = (DT != kF32) && Di == 128;  // 16-byte gathers
+  const int slot = lane / kWideLpr, dch = lane % kWideLpr;
+  for (int o = wid; o < 128; o += 4) {
+    const int64_t key = k0 + o_lo + o;
+    if (key >= kchunk_end || o_lo + o >= B) break;  // keys past the block (wave-uniform)
+    double acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0;
+    const int e0 = bstart[o], e1 = e0 + cnt[o];
+    if (wide) {
+      // lane (slot, dch) adds entries e0 + slot, e0 + slot + RPI, ... over dims 8 dch .. +7
+      const uint16_t* q16 = static_cast<const uint16_t*>(iq);
+      for (int e = e0; e < e1; e += 4 * kWideRpi) {
+        uint4 qw[4];
+        double wv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int ee = e + u * kWideRpi + slot;
+          const bool ok = ee < e1;
+          const int64_t row = r_begin + lrow[ok ? ee : e0];
+          qw[u] = ok ? *reinterpret_cast<const uint4*>(q16 + row * 128 + 8 * dch) : make_uint4(0u, 0u, 0u, 0u);
+          wv[u] = ok ? static_cast<double>(lds_w[ee]) * scale : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const uint32_t x[4] = {qw[u].x, qw[u].y, qw[u].z, qw[u].w};
+#pragma unroll
+          for (int q2 = 0; q2 < 4; ++q2) {
+            acc[2 * q2] = fma(wv[u], static_cast<double>(half_of<DT>(x[q2], 0)), acc[2 * q2]);
+            acc[2 * q2 + 1] = fma(wv[u], static_cast<double>(half_of<DT>(x[q2], 1)), acc[2 * q2 + 1]);
+          }
+        }
+      }
+      // slot sums in slot order; every lane then holds the key's sums of its chunk's 8 dims
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        double tot = 0.0;
+#pragma unroll
+        for (int sl = 0; sl < kWideRpi; ++sl) tot += __shfl(acc[j], sl * kWideLpr + dch, kWave);
+        acc[j] = tot;
+      }
+    } else {
+      for (int e = e0; e < e1; e += kDkBatch) {
+        float qv[kDkBatch][DPL];
+#pragma unroll
+        for (int u = 0; u < kDkBatch; ++u) {
+          const int64_t row = r_begin + lrow[e + u < e1 ? e + u : e0];
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) {
+            const int d = dbase + j;
+            qv[u][j] = (e + u < e1 && d < Di) ? load_as_f32<DT>(iq, row * Di + d) : 0.f;
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < kDkBatch; ++u) {
+          if (e + u < e1) {
+            const double wgt = static_cast<double>(lds_w[e + u]) * scale;
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) acc[j] = fma(wgt, static_cast<double>(qv[u][j]), acc[j]);
+          }
+        }
+      }
+    }
+    // exact ties: rows in order; the key takes w / count when its exact dot attains the maximum
+    if (!tie_overflow) {
+      for (int x = 0; x < ntie; ++x) {
+        const int64_t row = r_begin + tie_row[x];
+        const int64_t t = row / G;
+        if (key > t) continue;  // not visible from this row
+        if (directed(exact_dot<DT>(iq, row * Di, ik, key * Di, Di), scale) != tie_best[x]) continue;
+        const double wgt = static_cast<double>(dcol[tie_row[x]]) * scale / static_cast<double>(tie_count[x]);
+        dk_add_row<DT, DPL>(acc, wgt, iq, row, Di, wide, dch, dbase);
+      }
+    } else {
+      // more ties than the list holds: rescan the segment in row order
+      for (int i = 0; i < nseg_rows; ++i) {
+        if (tcol[i] >= 0) continue;
+        const int64_t row = r_begin + i;
+        const int64_t t = row / G;
+        if (key > t) continue;
+        const int64_t k1 = (k0 + B < t + 1) ? k0 + B : t + 1;
+        const BlockMax bm = block_max_exact<DT>(iq, row * Di, ik, k0, k1, Di, scale, lane);
+        if (directed(exact_dot<DT>(iq, row * Di, ik, key * Di, Di), scale) != bm.best) continue;
+        const double wgt = static_cast<double>(dcol[i]) * scale / static_cast<double>(bm.count);
+        dk_add_row<DT, DPL>(acc, wgt, iq, row, Di, wide, dch, dbase);
+      }
+    }
+    double* dst = part + ((w * kchunks + kc) * 128 + o) * static_cast<int64_t>(Di);
+    if (wide) {
+      if (slot == 0) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[8 * dch + j] = acc[j];
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        const int d = dbase + j;
+        if (d < Di) dst[d] = acc[j];
+      }
+    }
   }
 }
 
@@ -313,8 +594,8 @@ __global__ __launch_bounds__(256) void score_bwd_dk_part(
 template <int DT>
 __global__ __launch_bounds__(256) void score_bwd_dk_reduce(const int32_t* __restrict__ cu,
                                                            const int32_t* __restrict__ cu_blocks, int nseq,
-                                                           int64_t T, int G, int Di, int B, int kgroups, int nseg,
-                                                           int64_t seg_rows, const double* __restrict__ part,
+                                                           int64_t T, int G, int Di, int B, int nseg,
+                                                           const double* __restrict__ part,
                                                            void* __restrict__ dk) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= T * Di) return;
@@ -326,21 +607,17 @@ __global__ __launch_bounds__(256) void score_bwd_dk_reduce(const int32_t* __rest
   const int o = static_cast<int>((key - start) % B);
   const int64_t gb = cu_blocks[s] + b;
   const int64_t k0 = start + static_cast<int64_t>(b) * B;
-  const int kg = o / kDkKeys, kk = o % kDkKeys;
-  const int dc = d / 128, dl = d % 128, dchunks = (Di + 127) / 128;
+  const int kc = o / 128, kchunks = (B + 127) / 128;
   double sum = 0.0;
   for (int sg = 0; sg < nseg; ++sg) {
-    if (k0 * G + sg * seg_rows >= end * G) break;  // empty segment (no partial written work)
-    const int64_t w = (gb * kgroups + kg) * nseg + sg;
-    sum += part[((w * dchunks + dc) * kDkKeys + kk) * 128 + dl];
+    if (k0 * G + static_cast<int64_t>(sg) * kDkSeg >= end * G) break;  // empty segment (nothing written)
+    const int64_t w = gb * nseg + sg;
+    sum += part[((w * kchunks + kc) * 128 + o % 128) * static_cast<int64_t>(Di) + d];
   }
   store_from_f32<DT>(dk, i, static_cast<float>(sum));
 }
 
-static int64_t dk_seg_rows(int64_t rows) {
-  const int64_t s = (rows + 7) / 8;
-  return s > 16384 ? s : 16384;
-}
+static int64_t dk_nseg(int64_t rows) { return (rows + kDkSeg - 1) / kDkSeg; }
 
 template <int DT>
 int score_fwd_launch(const void* iq, const void* ik, const int32_t* cu, int nseq, int64_t rows, int G,
@@ -358,7 +635,14 @@ template <int DT>
 int score_bwd_launch(const void* iq, const void* ik, const int32_t* cu, const int32_t* cu_blocks, int nseq,
                      const int32_t* tie, const float* ds, int64_t rows, int G, int Di, int NB, int B,
                      int64_t total_blocks, double scale, void* dq, void* dk, void* ws, hipStream_t st) {
-  if (dq) {
+  if (dq && DT != kF32 && (Di == 32 || Di == 64 || Di == 128)) {
+    const dim3 grid(grid_1d(rows, 4)), block(256);
+    switch (Di / 8) {
+      case 4: hipLaunchKernelGGL((score_bwd_dq_wide<DT, 4>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq); break;
+      case 8: hipLaunchKernelGGL((score_bwd_dq_wide<DT, 8>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq); break;
+      default: hipLaunchKernelGGL((score_bwd_dq_wide<DT, 16>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq); break;
+    }
+  } else if (dq) {
     const dim3 grid(grid_1d(rows, 4)), block(256);
     if (Di <= 64) hipLaunchKernelGGL((score_bwd_dq<DT, 1>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq);
     else if (Di <= 128) hipLaunchKernelGGL((score_bwd_dq<DT, 2>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq);
@@ -371,17 +655,18 @@ int score_bwd_launch(const void* iq, const void* ik, const int32_t* cu, const in
     double* part = reinterpret_cast<double*>(ds_t + rows * NB);  // 8 * rows * NB bytes in: 8-byte aligned
     const dim3 tgrid(grid_1d(rows, 64), static_cast<unsigned>((NB + 63) / 64));
     hipLaunchKernelGGL(score_bwd_transpose, tgrid, dim3(256), 0, st, tie, ds, rows, NB, tie_t, ds_t);
-    const int kgroups = (B + kDkKeys - 1) / kDkKeys;
-    const int64_t seg_rows = dk_seg_rows(rows);
-    const int nseg = static_cast<int>((rows + seg_rows - 1) / seg_rows);
-    const int dchunks = (Di + 127) / 128;
-    const int64_t waves = total_blocks * kgroups * nseg;
-    const dim3 grid(grid_1d(waves, 4), static_cast<unsigned>(dchunks));
-    hipLaunchKernelGGL(score_bwd_dk_part<DT>, grid, dim3(256), 0, st, iq, ik, cu, cu_blocks, nseq, tie_t, ds_t, rows,
-                       G, Di, B, kgroups, nseg, seg_rows, total_blocks, scale, part);
+    const int nseg = static_cast<int>(dk_nseg(rows));
+    const int kchunks = (B + 127) / 128;
+    const dim3 grid(static_cast<unsigned>(total_blocks * nseg), static_cast<unsigned>(kchunks));
+#define MSA_DK_PART(DPLV) hipLaunchKernelGGL((score_bwd_dk_part<DT, DPLV>), grid, dim3(256), 0, st, iq, ik, cu, cu_blocks, nseq, tie_t, ds_t, rows, G, Di, B, nseg, scale, part)
+    if (Di <= 64) MSA_DK_PART(1);
+    else if (Di <= 128) MSA_DK_PART(2);
+    else if (Di <= 256) MSA_DK_PART(4);
+    else MSA_DK_PART(8);
+#undef MSA_DK_PART
     const int64_t T = rows / G;
     hipLaunchKernelGGL(score_bwd_dk_reduce<DT>, dim3(grid_1d(T * Di, 256)), dim3(256), 0, st, cu, cu_blocks, nseq, T,
-                       G, Di, B, kgroups, nseg, seg_rows, part, dk);
+                       G, Di, B, nseg, part, dk);
   }
   return status_from(hipGetLastError());
 }
@@ -418,11 +703,9 @@ extern "C" int64_t msa_score_bwd_workspace_bytes(int64_t total_tokens, int64_t g
   const int64_t rows = total_tokens * groups;
   // block-major tie / ds copies, then the dk partial sums (FP64)
   const int64_t tr = rows * num_blocks * 8 + 8;
-  const int64_t seg_rows = dk_seg_rows(rows);
-  const int64_t nseg = (rows + seg_rows - 1) / seg_rows;
-  const int64_t kgroups = (block_size + kDkKeys - 1) / kDkKeys;
-  const int64_t dchunks = (index_dim + 127) / 128;
-  const int64_t part = total_blocks * kgroups * nseg * dchunks * kDkKeys * 128 * 8;
+  const int64_t nseg = dk_nseg(rows);
+  const int64_t kchunks = (block_size + 127) / 128;
+  const int64_t part = total_blocks * nseg * kchunks * 128 * index_dim * 8;
   return tr + part + 256;
 }
 

@@ -141,6 +141,23 @@ def test_score_mfma_path_exact_ties(dim, scale, device):
     _run(q_cpu, k_cpu, lengths, max(lengths), block, scale, upstream, device)
 
 
+@pytest.mark.parametrize("integer", [False, True])
+def test_score_backward_blocks_wider_than_128_keys(integer, device):
+    """Key blocks of 200 keys (two key chunks in the dK pass); small-integer inputs
+    add exact ties in both chunks."""
+    gen = torch.Generator().manual_seed(200 + integer)
+    lengths, groups, dim, block = [450, 130], 2, 16, 200
+    if integer:
+        q_cpu = torch.randint(-1, 2, (sum(lengths), groups, dim), generator=gen).to(torch.bfloat16)
+        k_cpu = torch.randint(-1, 2, (sum(lengths), 1, dim), generator=gen).to(torch.bfloat16)
+    else:
+        q_cpu = torch.randn(sum(lengths), groups, dim, generator=gen).to(torch.bfloat16)
+        k_cpu = torch.randn(sum(lengths), 1, dim, generator=gen).to(torch.bfloat16)
+    nb = (max(lengths) + block - 1) // block
+    upstream = torch.randn((sum(lengths), groups, nb), generator=gen).to(torch.bfloat16).float()
+    _run(q_cpu, k_cpu, lengths, max(lengths), block, 1.0, upstream, device)
+
+
 @pytest.mark.parametrize("lengths,groups,dim,block,seed", [
     ([1280 - 512, 512], 2, 64, 128, 71), ([2048], 4, 128, 128, 3), ([300, 1, 777], 3, 96, 64, 4),
 ])
