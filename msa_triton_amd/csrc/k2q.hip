@@ -14,11 +14,10 @@
 //   2. k2q_rowscan : per row, exclusive prefix of the counts over the tiles
 //                    qb >= b (in qb order), giving the tile's start inside the row.
 //   3. k2q_ptrscan : exclusive scan of row totals -> row_ptr (one workgroup).
-//   4. k2q_scatter : each tile walks its tokens in order and places edges at
-//                    row_ptr[row] + tile offset + running count + duplicate rank.
+//   4. k2q_scatter_par : per (tile, group), a stable counting sort of the tile's
+//                    edges on their block id places each edge at row_ptr[row] +
+//                    tile offset + its rank among the tile's edges of that row.
 //   5. k2q_tail    : entries at or beyond row_ptr[rows] become -1.
-// The scatter is sequential over the B tokens of a tile but parallel over the
-// G*K edges of a token and over all tiles.
 #include "common.hpp"
 
 namespace msa {
@@ -134,58 +133,93 @@ __global__ __launch_bounds__(1024) void k2q_ptrscan(const int32_t* __restrict__ 
   if (threadIdx.x == 0) row_ptr[rows] = carry_s;
 }
 
-// One workgroup per tile; tokens processed in order, edges of a token in parallel.
-__global__ __launch_bounds__(1024) void k2q_scatter(const int32_t* __restrict__ indices,
-                                                    const int32_t* __restrict__ cu,
-                                                    const int32_t* __restrict__ cu_blocks,
-                                                    const int64_t* __restrict__ tri_prefix, int nseq,
-                                                    int G, int K, int B,
-                                                    const int32_t* __restrict__ row_ptr,
-                                                    int32_t* __restrict__ counters,
-                                                    int32_t* __restrict__ query_idx,
-                                                    int32_t* __restrict__ slot_idx) {
-  extern __shared__ int32_t ids[];  // G*K ids of the current token
+// Parallel scatter. One workgroup per (tile, group) for tiles with at most
+// kParIds ids (query blocks below kParIds; later tiles of longer sequences walk
+// their edges serially): the tile's edges of that group, taken in (token, slot) order 256
+// per step, are placed by a stable counting sort on the block id. Inside a 64-lane
+// wave the rank among equal ids comes from one ballot per id bit; waves are merged
+// in order through per-wave id counts, and a running count per id carries the
+// order across steps. The position is row_ptr[row] + the tile's offset in the row
+// (from k2q_rowscan) + that rank, i.e. the same (query, slot) order as the
+// sequential scatter, duplicates included.
+constexpr int kParIds = 1024;
+constexpr int kParIdBits = 10;
+
+__global__ __launch_bounds__(256) void k2q_scatter_par(const int32_t* __restrict__ indices,
+                                                       const int32_t* __restrict__ cu,
+                                                       const int32_t* __restrict__ cu_blocks,
+                                                       const int64_t* __restrict__ tri_prefix, int nseq, int G,
+                                                       int K, int B, const int32_t* __restrict__ row_ptr,
+                                                       int32_t* __restrict__ counters,
+                                                       int32_t* __restrict__ query_idx,
+                                                       int32_t* __restrict__ slot_idx) {
+  __shared__ int32_t running[kParIds];
+  __shared__ int32_t wcnt[4][kParIds];
   const TileInfo ti = tile_info(blockIdx.x, cu, cu_blocks, tri_prefix, nseq, G, B);
-  int32_t* cnt = counters + ti.counter_base;
+  const int g = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int nb = cu_blocks[ti.seq + 1] - cu_blocks[ti.seq];
-  const int64_t row_base = static_cast<int64_t>(cu_blocks[ti.seq]) * G;
-  const int GK = G * K;
-  for (int64_t t = ti.tok_begin; t < ti.tok_end; ++t) {
-    const int32_t* src = indices + t * GK;
-    for (int e = threadIdx.x; e < GK; e += blockDim.x) {
-      const int id = src[e];
-      ids[e] = (id >= 0 && id < nb && id <= ti.qb) ? id : -1;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < GK; e += blockDim.x) {
-      const int id = ids[e];
-      if (id >= 0) {
-        const int g = e / K, slot = e % K;
-        const int32_t* mine = ids + g * K;
-        int rank = 0;
-        for (int s2 = 0; s2 < slot; ++s2) rank += (mine[s2] == id);
-        const int64_t lr = static_cast<int64_t>(id) * G + g;
-        const int64_t pos = static_cast<int64_t>(row_ptr[row_base + lr]) + cnt[lr] + rank;
-        query_idx[pos] = static_cast<int32_t>(t);
-        slot_idx[pos] = slot;
-      }
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < GK; e += blockDim.x) {
-      const int id = ids[e];
-      if (id >= 0) {
-        const int g = e / K, slot = e % K;
-        const int32_t* mine = ids + g * K;
-        bool first = true;
-        int dup = 0;
-        for (int s2 = 0; s2 < K; ++s2) {
-          if (mine[s2] == id) {
-            if (s2 < slot) first = false;
-            ++dup;
-          }
+  const int nid = ti.qb + 1;  // ids of this tile: 0 .. qb
+  int32_t* cntw = counters + ti.counter_base;
+  if (nid > kParIds) {
+    // more ids than the LDS counters hold: one thread walks the edges in (token, slot)
+    // order, advancing the tile's offsets of this group's rows in place
+    if (tid == 0) {
+      const int64_t rb = static_cast<int64_t>(cu_blocks[ti.seq]) * G;
+      for (int64_t t = ti.tok_begin; t < ti.tok_end; ++t)
+        for (int slot = 0; slot < K; ++slot) {
+          const int v = indices[(t * G + g) * K + slot];
+          if (v < 0 || v >= nb || v > ti.qb) continue;
+          const int64_t lr = static_cast<int64_t>(v) * G + g;
+          const int64_t pos = static_cast<int64_t>(row_ptr[rb + lr]) + cntw[lr]++;
+          query_idx[pos] = static_cast<int32_t>(t);
+          slot_idx[pos] = slot;
         }
-        if (first) cnt[static_cast<int64_t>(id) * G + g] += dup;
-      }
+    }
+    return;
+  }
+  for (int i = tid; i < nid; i += 256) {
+    running[i] = 0;
+    wcnt[0][i] = wcnt[1][i] = wcnt[2][i] = wcnt[3][i] = 0;
+  }
+  __syncthreads();
+  const int32_t* cnt = counters + ti.counter_base;  // the tile's offset inside each row
+  const int64_t row_base = static_cast<int64_t>(cu_blocks[ti.seq]) * G;
+  const int64_t nedge = (ti.tok_end - ti.tok_begin) * K;
+  const uint64_t lt = (uint64_t(1) << lane) - 1;
+  for (int64_t base = 0; base < nedge; base += 256) {
+    const int64_t e = base + tid;
+    int id = -1, slot = 0;
+    int64_t t = 0;
+    if (e < nedge) {
+      t = ti.tok_begin + e / K;
+      slot = static_cast<int>(e % K);
+      const int v = indices[(t * G + g) * K + slot];
+      if (v >= 0 && v < nb && v <= ti.qb) id = v;
+    }
+    const bool on = id >= 0;
+    uint64_t match = __ballot(on);
+#pragma unroll
+    for (int bit = 0; bit < kParIdBits; ++bit) {
+      const uint64_t m = __ballot(on && ((id >> bit) & 1));
+      match &= ((id >> bit) & 1) ? m : ~m;
+    }
+    const int rank = __popcll(match & lt);
+    const int total = __popcll(match);
+    if (on && rank == total - 1) wcnt[wid][id] = total;
+    __syncthreads();
+    if (on) {
+      int before = running[id] + rank;
+      for (int w2 = 0; w2 < wid; ++w2) before += wcnt[w2][id];
+      const int64_t lr = static_cast<int64_t>(id) * G + g;
+      const int64_t pos = static_cast<int64_t>(row_ptr[row_base + lr]) + cnt[lr] + before;
+      query_idx[pos] = static_cast<int32_t>(t);
+      slot_idx[pos] = slot;
+    }
+    __syncthreads();
+    for (int i = tid; i < nid; i += 256) {
+      running[i] += wcnt[0][i] + wcnt[1][i] + wcnt[2][i] + wcnt[3][i];
+      wcnt[0][i] = wcnt[1][i] = wcnt[2][i] = wcnt[3][i] = 0;
     }
     __syncthreads();
   }
@@ -255,11 +289,9 @@ extern "C" int msa_k2q_build(const int32_t* indices, const int32_t* cu_seqlens,
   hipLaunchKernelGGL(k2q_rowscan, dim3(grid_1d(rows, 256)), dim3(256), 0, st, cu_block_lens, tri_prefix,
                      nseq, G, rows, counters, totals);
   hipLaunchKernelGGL(k2q_ptrscan, dim3(1), dim3(1024), 0, st, totals, rows, row_ptr);
-  const int GK = G * K;
-  const int threads = GK <= 64 ? 64 : (GK >= 1024 ? 1024 : ((GK + 63) / 64) * 64);
-  hipLaunchKernelGGL(k2q_scatter, dim3(static_cast<unsigned>(total_blocks)), dim3(threads),
-                     static_cast<size_t>(GK) * 4, st, indices, cu_seqlens, cu_block_lens, tri_prefix, nseq,
-                     G, K, B, row_ptr, counters, query_indices, slot_indices);
+  hipLaunchKernelGGL(k2q_scatter_par, dim3(static_cast<unsigned>(total_blocks), static_cast<unsigned>(G)),
+                     dim3(256), 0, st, indices, cu_seqlens, cu_block_lens, tri_prefix, nseq, G, K, B, row_ptr,
+                     counters, query_indices, slot_indices);
   hipLaunchKernelGGL(k2q_tail, dim3(capped_grid(capacity)), dim3(256), 0, st, row_ptr, rows, capacity,
                      query_indices, slot_indices);
   return status_from(hipGetLastError());

@@ -70,6 +70,19 @@ def test_topk_baseline_sized_rows(total, groups, nb, k, local, device):
     np.testing.assert_array_equal(got.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("tokens,block,k,local", [(2048, 2, 16, 1), (3000, 2, 32, 2), (4400, 2, 8, 0)])
+def test_topk_long_rows(tokens, block, k, local, device):
+    """Rows of 1024 blocks (sixteen lanes per row) and of 1500 / 2200 blocks (one
+    wavefront per row), with integer scores for ties."""
+    gen = torch.Generator().manual_seed(tokens)
+    nb = (tokens + block - 1) // block
+    scores = torch.randint(-4, 5, (tokens, 2, nb), generator=gen).float()
+    got = msa.m3_topk(scores.to(device), cu_tensor([tokens], device), block_size=block, topk_blocks=k,
+                      local_blocks=local)
+    ref = O.topk(scores.numpy(), [0, tokens], block_size=block, topk_blocks=k, local_blocks=local)
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
+
+
 def _check_csr(ids_cpu, lengths, block_size, device):
     ids = ids_cpu.to(device)
     original = ids.clone()
@@ -121,6 +134,15 @@ def test_k2q_hotspots_tail_block_noncontiguous_and_all_invalid(device):
     bad[:, :, 0] = -1
     result = _check_csr(bad, [3, 4], 2, device)
     assert result.row_ptr.count_nonzero().item() == 0
+
+
+def test_k2q_sequences_longer_than_1024_blocks(device):
+    """Query blocks 1024 and later take the serial path of the scatter; earlier ones
+    and the short second sequence the parallel one. Random ids include duplicates."""
+    generator = torch.Generator().manual_seed(1100)
+    lengths, groups, slots, block_size = [2200, 37], 2, 3, 2
+    ids = torch.randint(-1, 1101, (sum(lengths), groups, slots), generator=generator, dtype=torch.int32)
+    _check_csr(ids, lengths, block_size, device)
 
 
 @pytest.mark.parametrize("lengths,groups,k,block", [
