@@ -106,6 +106,74 @@ def measured_traffic(config, entry):
         return None
 
 
+def _pmc_rows(directory, counter):
+    """(dispatch id, kernel name, value in bytes) of one rocprofv3 counter pass, in dispatch order.
+    FETCH_SIZE / WRITE_SIZE are reported in KiB per dispatch."""
+    import csv
+    import glob
+
+    rows = []
+    for path in glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == counter:
+                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0))
+    rows.sort()
+    return rows
+
+
+def summarize_pmc(config, fetch_dir, write_dir):
+    """Per-entry HBM bytes of one msa_attn_fwd and one msa_attn_bwd call from two --pmc-pass runs.
+    The calibration copy (the largest copy dispatch) moves COPY bytes each way; each counter is scaled
+    so that it reads exactly that. The forward call's dispatches run from its first kv_chunk_bounds up
+    to the first backward kernel (kv_bwd_*), the backward call's from there to the end."""
+    copy_bytes = 64 << 22  # 256 MiB
+    out = {"config": config, "counters": ["FETCH_SIZE", "WRITE_SIZE"],
+           "command": [f"rocprofv3 --pmc FETCH_SIZE -d <out> -o f --output-format csv -- python bench.py --config "
+                       f"{config} --pmc-pass",
+                       f"rocprofv3 --pmc WRITE_SIZE -d <out> -o w --output-format csv -- python bench.py --config "
+                       f"{config} --pmc-pass"],
+           "calibration": {"copy_bytes": copy_bytes}, "entries": {}}
+    per_kernel = {}
+    for counter, directory, key in (("FETCH_SIZE", fetch_dir, "read"), ("WRITE_SIZE", write_dir, "write")):
+        rows = _pmc_rows(directory, counter)
+        calib = max(r[2] for r in rows if "copy" in r[1].lower())
+        scale = copy_bytes / calib
+        out["calibration"][f"{key}_reported_bytes"] = calib
+        out["calibration"][f"{key}_scale"] = round(scale, 4)
+        first_bwd = next(i for i, r in enumerate(rows) if "kv_bwd_" in r[1])
+        first_fwd = max(i for i, r in enumerate(rows[:first_bwd]) if "kv_chunk_bounds" in r[1])
+        for i, (_, name, value) in enumerate(rows[first_fwd:], start=first_fwd):
+            entry = "msa_attn_fwd" if i < first_bwd else "msa_attn_bwd"
+            short = name.split("(")[0].replace("void ", "").replace("msa::", "")
+            d = per_kernel.setdefault((entry, short), {"dispatches": 0, "read": 0.0, "write": 0.0})
+            if key == "read":
+                d["dispatches"] += 1
+            d[key] += value * scale
+            e = out["entries"].setdefault(entry, {"read_bytes": 0.0, "write_bytes": 0.0})
+            e[f"{key}_bytes"] += value * scale
+    for e in out["entries"].values():
+        e["read_bytes"] = int(e["read_bytes"])
+        e["write_bytes"] = int(e["write_bytes"])
+        e["bytes_per_call"] = e["read_bytes"] + e["write_bytes"]
+    path = os.path.join(ROOT, "profiles", f"attn_{config}_traffic.json")
+    with open(path, "w") as f:
+        json.dump(out, f, indent=1)
+    gib = float(1 << 30)
+    print("| entry | kernel | dispatches | read GiB | write GiB |")
+    print("|---|---|---:|---:|---:|")
+    for (entry, name), d in per_kernel.items():
+        print(f"| {entry} | `{name}` | {d['dispatches']} | {d['read'] / gib:.3f} | {d['write'] / gib:.3f} |")
+    print()
+    print("| entry | read GiB / call | write GiB / call | total GB / call | at 8 TB/s |")
+    print("|---|---:|---:|---:|---:|")
+    for entry, e in out["entries"].items():
+        tot = e["bytes_per_call"]
+        print(f"| {entry} | {e['read_bytes'] / gib:.2f} | {e['write_bytes'] / gib:.2f} | {tot / 1e9:.2f} | "
+              f"{tot / 8e12 * 1e3:.2f} ms |")
+    print(f"wrote {path}", file=sys.stderr)
+
+
 class Harness:
     """Direct C-ABI launches on preallocated buffers, for per-kernel timing."""
 
@@ -239,7 +307,13 @@ def main():
     parser.add_argument("--pmc-pass", action="store_true",
                         help="for rocprofv3 --pmc: a 256 MiB calibration copy, then one attention forward and one "
                              "backward call (direct C ABI) and exit")
+    parser.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                        help="read the counter CSVs of two --pmc-pass runs (FETCH_SIZE, WRITE_SIZE), write "
+                             "profiles/attn_<config>_traffic.json and print a markdown table; no GPU needed")
     args = parser.parse_args()
+    if args.pmc_summarize:
+        summarize_pmc(args.config, *args.pmc_summarize)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (this path does not shard "
               "across GPUs; see DESIGN.md for how it would).", file=sys.stderr)
