@@ -19,7 +19,8 @@
 //   accumulate    dK, dV item partials -> FP32 key accumulators (item order)
 //   dq combine    dQ = scale * sum of the row's block partials (FP64, slot order)
 //   finalize      FP32 key accumulators -> bf16 dK (times scale), dV
-// No floating-point atomics; every sum has a fixed order.
+// No floating-point atomics; every sum has a fixed order. Partial records are
+// written and read once each, with non-temporal (streaming) stores and loads.
 #include "attn_kv_common.hpp"
 
 // Logits are x = fl(acc * scale2) with their own rounding, and exponent arguments
@@ -526,7 +527,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
         for (int dt2 = 0; dt2 < 2; ++dt2) {
           const int d0 = 32 * dq + 16 * dt2 + 4 * q4;
           if (FULLD || d0 < D)
-            *reinterpret_cast<f32x4*>(dqpart + static_cast<int64_t>(myrec) * D + d0) = acc[dt2];
+            __builtin_nontemporal_store(acc[dt2], reinterpret_cast<f32x4*>(dqpart + static_cast<int64_t>(myrec) * D + d0));
         }
       }
     }
@@ -541,8 +542,8 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int kr = 16 * wid + 4 * q4 + i, d = 16 * dt + c;
-      base[kr * DP + d] = dk[dt][i];
-      base[128 * DP + kr * DP + d] = dv[dt][i];
+      __builtin_nontemporal_store(dk[dt][i], base + kr * DP + d);
+      __builtin_nontemporal_store(dv[dt][i], base + 128 * DP + kr * DP + d);
     }
 }
 
@@ -564,8 +565,8 @@ __global__ __launch_bounds__(256) void kv_bwd_accumulate(const int32_t* __restri
   float sk = 0.f, sv = 0.f;
   for (int i = i0; i < i1; ++i) {
     const float* p = kvpart + static_cast<int64_t>(i) * 2 * 128 * DP;
-    sk += p[kl * DP + d];
-    sv += p[128 * DP + kl * DP + d];
+    sk += __builtin_nontemporal_load(p + kl * DP + d);
+    sv += __builtin_nontemporal_load(p + 128 * DP + kl * DP + d);
   }
   const int64_t off = ((rg.kb + kl) * G + rg.g) * D + d;
   acc[off] += sk;
@@ -602,7 +603,8 @@ __global__ __launch_bounds__(256) void kv_bwd_dq_combine(const int32_t* __restri
       const int slot = s0 + u < K ? s0 + u : K - 1;
       const int id = sel[slot];
       ok[u] = s0 + u < K && id >= 0 && id <= qb;
-      x[u] = *reinterpret_cast<const float4*>(dqpart + (rec0 + slot) * D + 4 * sub);
+      const f32x4 y = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dqpart + (rec0 + slot) * D + 4 * sub));
+      x[u] = make_float4(y[0], y[1], y[2], y[3]);
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {

@@ -16,6 +16,9 @@
 // inside each CSR row the edges of a chunk form a contiguous range because rows
 // are ordered by query token.
 //
+// Partial records are written and read once each, with non-temporal (streaming)
+// stores and loads: the partial pass is bound by their write traffic.
+//
 // The logits use the K row fragment and the Q row fragment over the same dims
 // in the same k order as the backward kernels. P.V is computed exactly in its
 // products: P is split into three bf16 terms (hi + mid + lo == P).
@@ -301,7 +304,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
         float* dst = opart + static_cast<int64_t>(sm.rec[rho]) * D + 4 * q4;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt)
-          if (FULLD || 16 * dt + 4 * q4 < D) *reinterpret_cast<f32x4*>(dst + 16 * dt) = o[rt][dt];
+          if (FULLD || 16 * dt + 4 * q4 < D) __builtin_nontemporal_store(o[rt][dt], reinterpret_cast<f32x4*>(dst + 16 * dt));
       }
       if (q4 == 0 && rho < nrows) mlpart[sm.rec[rho]] = make_float2(mrow[rt], lrow[rt]);
     }
@@ -360,16 +363,26 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
         }
       }
       const int n = K - s0 < 32 ? K - s0 : 32;
+      // the two 32-lane halves of the wave hold two rows: slot j's weight comes from
+      // lane j of this half (wave-uniform readlanes of both halves, then a select)
+      const bool upper = (threadIdx.x & 32) != 0;
+      const uint64_t wbits = __double_as_longlong(w);
+      const uint32_t wlo = static_cast<uint32_t>(wbits), whi = static_cast<uint32_t>(wbits >> 32);
       for (int j0 = 0; j0 < n; j0 += kCombineBatch) {
         float4 op[kCombineBatch];
 #pragma unroll
         for (int u = 0; u < kCombineBatch; ++u) {
           const int j = j0 + u < n ? j0 + u : n - 1;
-          op[u] = *reinterpret_cast<const float4*>(opart + (rec0 + s0 + j) * D + dcol);
+          const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(opart + (rec0 + s0 + j) * D + dcol));
+          op[u] = make_float4(x[0], x[1], x[2], x[3]);
         }
 #pragma unroll
         for (int u = 0; u < kCombineBatch; ++u) {
-          const double wj = __shfl(w, j0 + u < n ? j0 + u : 0, 32);
+          const int j = j0 + u < n ? j0 + u : 0;
+          const uint32_t alo = __builtin_amdgcn_readlane(wlo, j), ahi = __builtin_amdgcn_readlane(whi, j);
+          const uint32_t blo = __builtin_amdgcn_readlane(wlo, 32 + j), bhi = __builtin_amdgcn_readlane(whi, 32 + j);
+          const double wj = __longlong_as_double(static_cast<long long>(
+              (static_cast<uint64_t>(upper ? bhi : ahi) << 32) | (upper ? blo : alo)));
           if (j0 + u < n && wj != 0.0) {  // invalid slot (or a weight that underflowed to zero)
             acc[0] = fma(wj, static_cast<double>(op[u].x), acc[0]);
             acc[1] = fma(wj, static_cast<double>(op[u].y), acc[1]);
