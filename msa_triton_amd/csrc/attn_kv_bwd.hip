@@ -23,8 +23,9 @@
 // written and read once each, with non-temporal (streaming) stores and loads.
 #include "attn_kv_common.hpp"
 
-// Logits are x = fl(acc * scale2) with their own rounding, and exponent arguments
-// x - m with another: no fused multiply-adds, so a row's maximum gets p == 1 exactly.
+// Logits are x = fl(acc * scale2) and exponent arguments fl(x - lse2), each with its
+// own rounding and formed identically in the stats and main passes, so the p_j
+// summed into mass and delta are the p_j of dS. Only explicit fmaf calls fuse.
 #pragma clang fp contract(off)
 
 namespace msa {
@@ -36,15 +37,26 @@ constexpr int kStatTilesPerItem = 4;
 constexpr int kStatItemRows = kStatRowsPerTile * kStatTilesPerItem;
 constexpr int kMainEdges = 512;        // B2: CSR edges per work item
 constexpr int kMainThreads = 512;      // B2: 8 waves, 16 keys each (S, dP, dV, dK), 16 rows x 32 dims each (dQ)
-constexpr int kPlaneStride = 40;       // B2: halves per key of a dS plane [key][row] (32 + 8: conflict-free b64 writes)
+
+// LDS rows of K / V blocks and of Q / dO tiles are DP + 16 halves apart (a 288-byte
+// stride at DP = 128): both the row-fragment reads (ds_read_b128, lane c -> row c)
+// and the transposed reads (ds_read_b64_tr_b16, four rows x 32 bytes per 16 lanes)
+// then spread over all 64 banks. A DP + 8 stride leaves both 2-way conflicted.
+template <int DP>
+constexpr int lds_row_stride() { return DP + 16; }
+
+// dS planes [key][tile row] are unpadded (64 bytes per key); the 8-byte piece p
+// (tile rows 4p .. 4p + 3) of key k sits at piece p ^ ((k >> 1) & 6). The writes
+// (lane c -> key c, pieces q4 and 4 + q4) and the transposed reads of the dQ pass
+// (lanes c / 4 + 8 q4 -> keys, c % 4 -> pieces) are then bank-conflict free.
+__device__ __forceinline__ int plane_offset(int key, int piece) { return key * 32 + 4 * (piece ^ ((key >> 1) & 6)); }
 
 template <int NK>
 struct StatSmem {
   static constexpr int DP = 32 * NK;
-  static constexpr int KS = DP + 8;
+  static constexpr int KS = lds_row_stride<DP>();
   alignas(16) uint16_t k[128 * KS];
   alignas(16) uint16_t v[128 * KS];
-  int32_t th[kStatItemRows];
   int32_t tok[kStatItemRows];
   int32_t rec[kStatItemRows];
   float lse2[kStatItemRows];
@@ -54,11 +66,11 @@ struct StatSmem {
 template <int NK>
 struct MainSmem {
   static constexpr int DP = 32 * NK;
-  static constexpr int KS = DP + 8;                     // row stride of the K block and the Q / dO row tiles
+  static constexpr int KS = lds_row_stride<DP>();       // row stride of the K block and the Q / dO row tiles
   alignas(16) uint16_t k[128 * KS];                     // K block [key][dim]
   alignas(16) uint16_t qs[2][32 * KS];                  // Q rows of a tile [row][dim], double-buffered
   alignas(16) uint16_t gs[2][32 * KS];                  // dO rows
-  alignas(16) uint16_t ds[2][3][128 * kPlaneStride];    // dS split planes (hi, mid, lo) [key][row]
+  alignas(16) uint16_t ds[2][3][128 * 32];              // dS split planes (hi, mid, lo) [key][row], swizzled
   alignas(16) float4 st[2][32];                         // (lse2, 1 / mass, c, delta) per tile row
   alignas(16) int32_t vis[2][32];                       // visible keys of the block per tile row (0 past the end)
   alignas(16) int32_t rec[2][32];                       // dQ partial record per tile row (-1 past the end)
@@ -149,7 +161,6 @@ __global__ __launch_bounds__(256, 2) void kv_bwd_stats_kernel(
       const int eo = rho / R;
       const int h = rg.g * R + (rho - eo * R);
       const int th = mtok[j] * Hq + h;
-      sm.th[rho] = th;
       sm.tok[rho] = mtok[j];
       sm.rec[rho] = ((mtok[j] - t0) * Hq + h) * K + mslot[j];
       sm.lse2[rho] = static_cast<float>(row_state[static_cast<int64_t>(th) * 4]);
@@ -169,7 +180,7 @@ __global__ __launch_bounds__(256, 2) void kv_bwd_stats_kernel(
     for (int rt = 0; rt < 2; ++rt) {
       const int rho = rbase + 16 * rt + c;
       const bool ok = rho < nrows;
-      const int64_t th = ok ? sm.th[rho] : 0;
+      const int64_t th = ok ? static_cast<int64_t>(sm.tok[rho]) * Hq + rg.g * R + rho % R : 0;
       const int64_t vis = ok ? static_cast<int64_t>(sm.tok[rho]) - rg.kb + 1 : 0;
       lim[rt] = vis < rg.nk ? static_cast<int>(vis) : rg.nk;
       lse2[rt] = ok ? sm.lse2[rho] : 0.f;
@@ -183,6 +194,8 @@ __global__ __launch_bounds__(256, 2) void kv_bwd_stats_kernel(
       }
     }
     float psum[2] = {0.f, 0.f}, usum[2] = {0.f, 0.f};
+    // rows are in token order: when every row of the wave sees all 128 keys, no masks
+    const bool full = __all(lim[0] >= 128 && lim[1] >= 128);
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
       bf16x8 kf[NK], vf[NK];
@@ -199,12 +212,21 @@ __global__ __launch_bounds__(256, 2) void kv_bwd_stats_kernel(
           sa = mfma(kf[kk], qf[rt][kk], sa);
           da = mfma(vf[kk], gf[rt][kk], da);
         }
+        if (full) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const bool vis = 16 * kt + 4 * q4 + i < lim[rt];
-          const float p = vis ? __builtin_amdgcn_exp2f(sa[i] * scale2 - lse2[rt]) : 0.f;
-          psum[rt] += p;
-          usum[rt] += p * (da[i] - cen[rt]);
+          for (int i = 0; i < 4; ++i) {
+            const float p = __builtin_amdgcn_exp2f(sa[i] * scale2 - lse2[rt]);
+            psum[rt] += p;
+            usum[rt] = __builtin_fmaf(p, da[i] - cen[rt], usum[rt]);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool vis = 16 * kt + 4 * q4 + i < lim[rt];
+            const float p = vis ? __builtin_amdgcn_exp2f(sa[i] * scale2 - lse2[rt]) : 0.f;
+            psum[rt] += p;
+            usum[rt] = __builtin_fmaf(p, da[i] - cen[rt], usum[rt]);
+          }
         }
       }
     }
@@ -281,7 +303,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items, const int2* __restrict__ items, int nseq,
     int Hq, int G, int D, int K, int B, float scale2, int epi, int t0, float* __restrict__ dqpart,
     float* __restrict__ kvpart) {
-  constexpr int DP = 32 * NK, NDT = DP / 16, KS = MainSmem<NK>::KS, PS = kPlaneStride;
+  constexpr int DP = 32 * NK, NDT = DP / 16, KS = MainSmem<NK>::KS;
   constexpr int RV = DP / 8;             // 16-byte chunks per row
   constexpr int TV = 32 * RV;            // chunks per tile and tensor
   constexpr int SI = (TV + 255) / 256;   // chunks per staging thread (threads 0-255: Q, 256-511: dO)
@@ -476,9 +498,8 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       for (int p3 = 0; p3 < 3; ++p3) {
         ad[p3] = __builtin_bit_cast(bf16x8, make_uint4(w[p3][0], w[p3][1], w[p3][2], w[p3][3]));
         // plane rows: key 16 w + c, columns (tile rows) 4 q4 .. +3 and 16 + 4 q4 .. +3
-        uint16_t* dst = sm.ds[b][p3] + key * PS + 4 * q4;
-        *reinterpret_cast<uint2*>(dst) = make_uint2(w[p3][0], w[p3][1]);
-        *reinterpret_cast<uint2*>(dst + 16) = make_uint2(w[p3][2], w[p3][3]);
+        *reinterpret_cast<uint2*>(sm.ds[b][p3] + plane_offset(key, q4)) = make_uint2(w[p3][0], w[p3][1]);
+        *reinterpret_cast<uint2*>(sm.ds[b][p3] + plane_offset(key, 4 + q4)) = make_uint2(w[p3][2], w[p3][3]);
       }
       ap[0] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(ph[0], ph[1]), pack_hi16(ph[2], ph[3]),
                                                     pack_hi16(ph[4], ph[5]), pack_hi16(ph[6], ph[7])));
@@ -512,9 +533,12 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        const bf16x8 bl = frag_tr(sm.ds[b][2], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rh, c);
-        const bf16x8 bm = frag_tr(sm.ds[b][1], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rh, c);
-        const bf16x8 bh = frag_tr(sm.ds[b][0], PS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * rh, c);
+        // B[keys 32 kc + 8 q4 + j][tile rows 16 rh + c]: lane c reads key (.. + c / 4), piece 4 rh + c % 4
+        const int ka = 32 * kc + 8 * q4 + (c >> 2), kb = ka + 4;
+        const int oa = plane_offset(ka, 4 * rh + (c & 3)), ob = plane_offset(kb, 4 * rh + (c & 3));
+        const bf16x8 bl = frag_tr_at(sm.ds[b][2] + oa, sm.ds[b][2] + ob);
+        const bf16x8 bm = frag_tr_at(sm.ds[b][1] + oa, sm.ds[b][1] + ob);
+        const bf16x8 bh = frag_tr_at(sm.ds[b][0] + oa, sm.ds[b][0] + ob);
 #pragma unroll
         for (int dt2 = 0; dt2 < 2; ++dt2) {
           acc[dt2] = mfma(kt[dt2][kc], bl, acc[dt2]);
@@ -535,20 +559,19 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
 #undef MSA_MAIN_ISSUE
 #undef MSA_MAIN_COMMIT
 
-  // ---- this item's dK / dV contribution: kvpart[item][0 = dK, 1 = dV][key][dim]
-  float* base = kvpart + static_cast<int64_t>(item) * 2 * 128 * DP;
+  // ---- this item's dK / dV contribution, in accumulator-fragment order:
+  // kvpart[item][0 = dK, 1 = dV][wave][dt][lane][i] holds key 16 wave + 4 q4 + i, dim 16 dt + c.
+  f32x4* base = reinterpret_cast<f32x4*>(kvpart + static_cast<int64_t>(item) * 2 * 128 * DP) + wid * NDT * 64 + lane;
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kr = 16 * wid + 4 * q4 + i, d = 16 * dt + c;
-      __builtin_nontemporal_store(dk[dt][i], base + kr * DP + d);
-      __builtin_nontemporal_store(dv[dt][i], base + 128 * DP + kr * DP + d);
-    }
+  for (int dt = 0; dt < NDT; ++dt) {
+    __builtin_nontemporal_store(dk[dt], base + dt * 64);
+    __builtin_nontemporal_store(dv[dt], base + 32 * DP + dt * 64);
+  }
 }
 
 // For chunk c: add each row's item partials (in item order) into the FP32 key
-// accumulators acc[0 = dK, 1 = dV][key][group][dim]. grid (rows, 128 * DP / 256).
+// accumulators acc[0 = dK, 1 = dV][key][group][dim]. Thread e owns fragment slot e
+// of the partial layout (four keys, one dim). grid (rows, DP / 8).
 template <int DP>
 __global__ __launch_bounds__(256) void kv_bwd_accumulate(const int32_t* __restrict__ cu,
                                                          const int32_t* __restrict__ cu_blocks,
@@ -559,18 +582,25 @@ __global__ __launch_bounds__(256) void kv_bwd_accumulate(const int32_t* __restri
   const int i0 = starts[row], i1 = starts[row + 1];
   if (i0 == i1) return;
   const RowGeom rg = row_geom(cu, cu_blocks, nseq, row, G, B);
-  const int e = blockIdx.y * 256 + threadIdx.x;  // element of the 128 x DP block
-  const int kl = e / DP, d = e % DP;
-  if (kl >= rg.nk || d >= D) return;
-  float sk = 0.f, sv = 0.f;
+  constexpr int NDT = DP / 16;
+  const int e = blockIdx.y * 256 + threadIdx.x;  // fragment slot: (wave, dt, lane)
+  const int w = e / (NDT * 64), dt = (e / 64) % NDT, ln = e % 64;
+  const int kl0 = 16 * w + 4 * (ln >> 4), d = 16 * dt + (ln & 15);
+  if (kl0 >= rg.nk || d >= D) return;
+  f32x4 sk = {0.f, 0.f, 0.f, 0.f}, sv = {0.f, 0.f, 0.f, 0.f};
   for (int i = i0; i < i1; ++i) {
-    const float* p = kvpart + static_cast<int64_t>(i) * 2 * 128 * DP;
-    sk += __builtin_nontemporal_load(p + kl * DP + d);
-    sv += __builtin_nontemporal_load(p + 128 * DP + kl * DP + d);
+    const f32x4* p = reinterpret_cast<const f32x4*>(kvpart + static_cast<int64_t>(i) * 2 * 128 * DP) + e;
+    sk += __builtin_nontemporal_load(p);
+    sv += __builtin_nontemporal_load(p + 32 * DP);
   }
-  const int64_t off = ((rg.kb + kl) * G + rg.g) * D + d;
-  acc[off] += sk;
-  acc[T * G * D + off] += sv;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (kl0 + i < rg.nk) {
+      const int64_t off = ((rg.kb + kl0 + i) * G + rg.g) * D + d;
+      acc[off] += sk[i];
+      acc[T * G * D + off] += sv[i];
+    }
+  }
 }
 
 // dQ = scale * sum of the row's block partials over its valid slots (FP64, slot
@@ -732,7 +762,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
 #undef MSA_BWD_MAIN
       if (need_kv) {
         const int32_t* starts = kv_plan_starts(mp, mbase, c);
-        const dim3 agrid(static_cast<unsigned>(rows), static_cast<unsigned>(128 * 32 * nk / 256));
+        const dim3 agrid(static_cast<unsigned>(rows), static_cast<unsigned>(32 * nk / 8));
         if (nk == 1) hipLaunchKernelGGL(kv_bwd_accumulate<32>, agrid, dim3(256), 0, st, cu, cu_blocks, starts, nseq, G, D, B, T, kvpart, acc);
         else if (nk == 2) hipLaunchKernelGGL(kv_bwd_accumulate<64>, agrid, dim3(256), 0, st, cu, cu_blocks, starts, nseq, G, D, B, T, kvpart, acc);
         else hipLaunchKernelGGL(kv_bwd_accumulate<128>, agrid, dim3(256), 0, st, cu, cu_blocks, starts, nseq, G, D, B, T, kvpart, acc);

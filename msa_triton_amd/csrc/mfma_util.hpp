@@ -58,6 +58,14 @@ __device__ __forceinline__ bf16x8 frag_tr(const uint16_t* tile, int stride, int 
   return __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
 }
 
+// frag_tr with the two 8-byte read addresses of this lane given directly (for
+// swizzled tiles): elements 0..3 from the read at lo, 4..7 from the read at hi.
+__device__ __forceinline__ bf16x8 frag_tr_at(const uint16_t* lo_p, const uint16_t* hi_p) {
+  const uint2 lo = lds_read_tr16(lo_p);
+  const uint2 hi = lds_read_tr16(hi_p);
+  return __builtin_bit_cast(bf16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+}
+
 __device__ __forceinline__ float quad_max(float v) {
   v = fmaxf(v, __shfl_xor(v, 16, kWave));
   return fmaxf(v, __shfl_xor(v, 32, kWave));
