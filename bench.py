@@ -235,6 +235,23 @@ class Harness:
         assert st == 0
 
 
+def time_loop(fn, steps, warmup=2):
+    """Milliseconds per call over `steps` back-to-back calls (one event pair, no
+    synchronisation in between), like the headline step timing."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
 def time_events(fn, repeats, warmup=1):
     """Median / min / p90 milliseconds per call, HIP events on the current stream."""
     import torch
@@ -435,6 +452,29 @@ def main():
             stages[name] = round(time_events(fn, reps)["median"], 4)
             log(f"{name}: {stages[name]:.3f}")
         stages["attention_fwd_bwd_ms"] = round(ms, 4)
+        # the same autograd step with prepared sequence metadata (no host reads of
+        # cu_seqlens), eager and replayed from a HIP graph capture
+        seqs = msa.prepare_sequences(cu, block_size=block)
+
+        def step_prepared():
+            qg.grad = kg.grad = vg.grad = None
+            msa.m3_sparse_attention(qg, kg, vg, ids, seqs, max_len, block_size=block).backward(dout)
+
+        stages["attention_fwd_bwd_prepared_ms"] = round(time_loop(step_prepared, args.steps), 4)
+        log(f"attention_fwd_bwd_prepared_ms: {stages['attention_fwd_bwd_prepared_ms']:.3f}")
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                step_prepared()
+        torch.cuda.current_stream().wait_stream(side)
+        qg.grad = kg.grad = vg.grad = None
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            msa.m3_sparse_attention(qg, kg, vg, ids, seqs, max_len, block_size=block).backward(dout)
+        stages["attention_fwd_bwd_graph_ms"] = round(time_loop(graph.replay, args.steps), 4)
+        log(f"attention_fwd_bwd_graph_ms: {stages['attention_fwd_bwd_graph_ms']:.3f}")
+        del graph
         stages["attention_bwd_kernel_ms"] = round(kt["attn_bwd"]["median"], 4)
         stages["attention_fwd_kernel_ms"] = round(kt["attn_fwd"]["median"], 4)
         score_flops, topk_bytes, csr_bytes, score_bwd_bytes = stage_work(cfg)

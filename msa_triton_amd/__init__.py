@@ -11,7 +11,16 @@ not load the native library.
 
 All three run as hand-written gfx950 HIP kernels behind the C ABI declared in
 ``include/msa_mi355x.h``; there is no CPU or eager fallback.
+
+    prepare_sequences(cu_seqlens, *, block_size=128) -> PackedSequences
+
+validates ``cu_seqlens`` once and returns immutable metadata with device copies;
+passed in place of ``cu_seqlens`` to any operator (and to ``build_k2q_csr``), it
+removes the operators' host reads of ``cu_seqlens``, so a layer's forward and
+backward run without host synchronisation and can be captured in a HIP graph.
 """
+
+from .layout import PackedSequences
 
 
 def m3_index_score(index_q, index_k, cu_seqlens, max_seqlen, *, block_size=128, scale=1.0):
@@ -39,4 +48,10 @@ def m3_sparse_attention(
     )
 
 
-__all__ = ["m3_index_score", "m3_topk", "m3_sparse_attention"]
+def prepare_sequences(cu_seqlens, *, block_size=128):
+    from .layout import prepare_sequences as implementation
+
+    return implementation(cu_seqlens, block_size=block_size)
+
+
+__all__ = ["m3_index_score", "m3_topk", "m3_sparse_attention", "prepare_sequences", "PackedSequences"]

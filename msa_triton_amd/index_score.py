@@ -19,12 +19,12 @@ import math
 import torch
 
 from . import _lib
-from .layout import sequence_meta
+from .layout import PackedSequences, prepared_for, sequence_meta
 
 
 class _IndexScore(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, index_q, index_k, cu_seqlens, max_seqlen, block_size, scale, save_state, meta):
+    def forward(ctx, index_q, index_k, cu_seqlens, max_seqlen, block_size, scale, save_state, meta, cu_blocks):
         q = index_q.contiguous()
         k = index_k.contiguous()
         cu = cu_seqlens.contiguous()
@@ -43,6 +43,7 @@ class _IndexScore(torch.autograd.Function):
         if save_state:
             ctx.save_for_backward(q, k, cu, tie)
         ctx.meta = meta
+        ctx.cu_blocks = cu_blocks  # prepared device copy of cu_block_lens, or None
         ctx.scale = scale
         ctx.blocks = blocks
         return scores
@@ -56,7 +57,9 @@ class _IndexScore(torch.autograd.Function):
         dk = torch.empty_like(k) if ctx.needs_input_grad[1] else None
         if total and (dq is not None or dk is not None):
             ds = grad_scores.to(torch.float32).contiguous()
-            cu_blocks = torch.tensor(meta.cu_block_lens, dtype=torch.int32, device=q.device)
+            cu_blocks = ctx.cu_blocks
+            if cu_blocks is None:
+                cu_blocks = torch.tensor(meta.cu_block_lens, dtype=torch.int32, device=q.device)
             lib = _lib.lib()
             ws_bytes = (lib.msa_score_bwd_workspace_bytes(total, groups, ctx.blocks, dim, meta.block_size,
                                                          meta.total_blocks) if dk is not None else 0)
@@ -69,7 +72,7 @@ class _IndexScore(torch.autograd.Function):
                     workspace.data_ptr(), _lib.stream_of(q.device),
                 )
             _lib.check(status, "msa_score_bwd")
-        return dq, dk, None, None, None, None, None, None
+        return dq, dk, None, None, None, None, None, None, None
 
 
 def m3_index_score(
@@ -98,27 +101,34 @@ def m3_index_score(
         raise TypeError("index_q must have BF16, FP16, or FP32 dtype")
     if index_k.dtype != index_q.dtype or index_k.device != index_q.device:
         raise ValueError("index_q and index_k must share dtype and device")
-    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2 or cu_seqlens.dtype != torch.int32:
+    seqs = cu_seqlens if isinstance(cu_seqlens, PackedSequences) else None
+    cu = seqs.cu_seqlens if seqs is not None else cu_seqlens
+    if cu.ndim != 1 or cu.numel() < 2 or cu.dtype != torch.int32:
         raise ValueError("cu_seqlens must be a rank-1 int32 tensor with at least two entries")
-    if cu_seqlens.device != index_q.device:
+    if cu.device != index_q.device:
         raise ValueError("cu_seqlens must be on the input device")
     if not isinstance(block_size, int) or block_size <= 0:
         raise ValueError("block_size must be a positive integer")
     if not isinstance(max_seqlen, int) or max_seqlen <= 0:
         raise ValueError("max_seqlen must be a positive integer")
-    if total > 2147483647 or cu_seqlens.numel() - 1 > 2147483647:
+    if total > 2147483647 or cu.numel() - 1 > 2147483647:
         raise ValueError("packed token and sequence counts must fit int32 metadata")
     if block_size > 2147483647 or max_seqlen > 2147483647:
         raise ValueError("block_size and max_seqlen must fit int32 metadata")
     if not math.isfinite(scale):
         raise ValueError("scale must be finite")
-    boundaries = cu_seqlens.detach().cpu().tolist()
-    lengths = [end - start for start, end in zip(boundaries, boundaries[1:])]
-    if boundaries[0] != 0 or boundaries[-1] != total or any(n < 0 for n in lengths):
-        raise ValueError("cu_seqlens must span T with nondecreasing boundaries starting at zero")
+    if seqs is None:
+        boundaries = cu.detach().cpu().tolist()
+        lengths = [end - start for start, end in zip(boundaries, boundaries[1:])]
+        if boundaries[0] != 0 or boundaries[-1] != total or any(n < 0 for n in lengths):
+            raise ValueError("cu_seqlens must span T with nondecreasing boundaries starting at zero")
+        meta = sequence_meta(boundaries, block_size)
+    else:  # prepared: no host read
+        meta = prepared_for(seqs, block_size=block_size, total_tokens=total, device=index_q.device)
+        lengths = list(meta.lengths)
     if max(lengths) > max_seqlen:
         raise ValueError("max_seqlen is smaller than a packed sequence")
     _lib.require_gpu(index_q, "m3_index_score")
-    meta = sequence_meta(boundaries, block_size)
     save_state = torch.is_grad_enabled() and (index_q.requires_grad or index_k.requires_grad)
-    return _IndexScore.apply(index_q, index_k, cu_seqlens, max_seqlen, block_size, float(scale), save_state, meta)
+    return _IndexScore.apply(index_q, index_k, cu, max_seqlen, block_size, float(scale), save_state, meta,
+                             None if seqs is None else seqs.cu_block_lens)

@@ -6,7 +6,8 @@ validation order, messages (``"span T"``, ``"nondecreasing"``, ``"block_size"``,
 int32 outputs. The build runs as HIP kernels (``msa_k2q_build``): a per-query-
 block histogram, a per-row prefix over tiles, a row-pointer scan and an ordered
 scatter, instead of the reference's int64 argsort. Sequence metadata is read on
-the host once, as in the reference.
+the host once, as in the reference, or taken from ``PackedSequences`` without a
+host read.
 """
 
 from __future__ import annotations
@@ -16,7 +17,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .layout import sequence_meta
+from .layout import PackedSequences, prepared_for, sequence_meta
 
 _INT32_MAX = 2**31 - 1
 
@@ -55,33 +56,42 @@ def build_k2q_csr(indices: torch.Tensor, cu_seqlens: torch.Tensor, *, block_size
         raise ValueError("indices must have at least one group")
     if not isinstance(block_size, int) or isinstance(block_size, bool) or block_size <= 0:
         raise ValueError("block_size must be a positive integer")
-    if cu_seqlens.ndim != 1 or cu_seqlens.dtype != torch.int32 or cu_seqlens.numel() < 2:
+    seqs = cu_seqlens if isinstance(cu_seqlens, PackedSequences) else None
+    cu = seqs.cu_seqlens if seqs is not None else cu_seqlens
+    if cu.ndim != 1 or cu.dtype != torch.int32 or cu.numel() < 2:
         raise ValueError("cu_seqlens must be a rank-1 int32 tensor with at least two entries")
-    if cu_seqlens.device != indices.device:
+    if cu.device != indices.device:
         raise ValueError("cu_seqlens and indices must be on the same device")
     capacity = total * groups * slots
     # Protects the int32 CSR counts and positions.
     if capacity > _INT32_MAX:
         raise OverflowError("T * G * K exceeds int32 edge capacity")
-    bounds = cu_seqlens.detach().cpu().tolist()
-    lengths = [end - start for start, end in zip(bounds[:-1], bounds[1:])]
-    if bounds[0] != 0 or bounds[-1] != total or any(length < 0 for length in lengths):
-        raise ValueError("cu_seqlens must span T with nondecreasing boundaries starting at zero")
-    meta = sequence_meta(bounds, block_size)
+    if seqs is None:
+        bounds = cu.detach().cpu().tolist()
+        lengths = [end - start for start, end in zip(bounds[:-1], bounds[1:])]
+        if bounds[0] != 0 or bounds[-1] != total or any(length < 0 for length in lengths):
+            raise ValueError("cu_seqlens must span T with nondecreasing boundaries starting at zero")
+        meta = sequence_meta(bounds, block_size)
+    else:  # prepared: no host read
+        meta = prepared_for(seqs, block_size=block_size, total_tokens=total, device=indices.device)
     num_rows = meta.total_blocks * groups
     if num_rows >= _INT32_MAX:
         raise OverflowError("block/group row pointer length exceeds int32 indexing capacity")
     _lib.require_gpu(indices, "build_k2q_csr")
-    return _build_device(indices.contiguous(), cu_seqlens.contiguous(), meta, groups, slots)
+    return _build_device(indices.contiguous(), cu.contiguous(), meta, groups, slots, seqs)
 
 
-def _build_device(indices, cu_seqlens, meta, groups, slots) -> K2QCSR:
+def _build_device(indices, cu_seqlens, meta, groups, slots, seqs=None) -> K2QCSR:
     device = indices.device
     total = indices.shape[0]
     capacity = total * groups * slots
     num_rows = meta.total_blocks * groups
-    cu_block_lens = torch.tensor(meta.cu_block_lens, dtype=torch.int32, device=device)
-    tri = torch.tensor([groups * x for x in meta.tri_prefix], dtype=torch.int64, device=device)
+    if seqs is None:
+        cu_block_lens = torch.tensor(meta.cu_block_lens, dtype=torch.int32, device=device)
+        tri = torch.tensor([groups * x for x in meta.tri_prefix], dtype=torch.int64, device=device)
+    else:  # prepared device copies (no host-to-device copy: capturable)
+        cu_block_lens = seqs.cu_block_lens
+        tri = seqs.tile_prefix * groups
     counter_elems = groups * meta.tri_prefix[-1]
     row_ptr = torch.empty(num_rows + 1, dtype=torch.int32, device=device)
     query_indices = torch.empty(capacity, dtype=torch.int32, device=device)

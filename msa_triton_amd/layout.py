@@ -5,6 +5,14 @@ messages and exception types); its messages are part of the attention error
 contract. ``SequenceMeta`` is the per-call host metadata every operator derives
 from ``cu_seqlens`` (block counts, per-sequence block prefix ``cu_block_lens``),
 computed once from the single host read of ``cu_seqlens``.
+
+``PackedSequences`` (from ``prepare_sequences``) is the prepared, immutable form:
+validated once, with its own device copies of ``cu_seqlens``, ``cu_block_lens``
+and the k2q tile prefix. Every operator accepts it in place of ``cu_seqlens`` and
+then reads nothing back from the device, so a layer's score, top-k, attention and
+backward issue no host synchronisation and can be captured in a HIP graph. Its
+device tensors are private clones: later writes to the caller's ``cu_seqlens``
+do not reach it (the stale-cache hazard of keying a cache on the caller's tensor).
 """
 
 from __future__ import annotations
@@ -63,3 +71,75 @@ def sequence_meta(bounds: list[int], block_size: int) -> SequenceMeta:
     for count in block_counts:
         cu_blocks.append(cu_blocks[-1] + count)
     return SequenceMeta(tuple(bounds), tuple(lengths), tuple(block_counts), tuple(cu_blocks), block_size)
+
+
+@dataclass(frozen=True, eq=False)
+class PackedSequences:
+    """Validated packed-sequence metadata for one block size, with device copies.
+
+    ``cu_seqlens`` (int32 ``[N+1]``), ``cu_block_lens`` (int32 ``[N+1]``) and
+    ``tile_prefix`` (int64 ``[N+1]``, the per-sequence start of the k2q
+    histogram's (query block, key block) counters, per group) live on the
+    device; ``meta`` holds the same numbers on the host.
+    """
+
+    cu_seqlens: torch.Tensor
+    cu_block_lens: torch.Tensor
+    tile_prefix: torch.Tensor
+    meta: SequenceMeta
+
+    @property
+    def device(self) -> torch.device:
+        return self.cu_seqlens.device
+
+    @property
+    def block_size(self) -> int:
+        return self.meta.block_size
+
+    @property
+    def total_tokens(self) -> int:
+        return self.meta.bounds[-1]
+
+    @property
+    def max_seqlen(self) -> int:
+        return max(self.meta.lengths)
+
+
+def prepare_sequences(cu_seqlens: torch.Tensor, *, block_size: int = 128) -> PackedSequences:
+    """Validate ``cu_seqlens`` once (one host read) and return ``PackedSequences``.
+
+    The checks and messages are those of ``sequence_lengths`` (zero start,
+    nondecreasing); the total token count is the last boundary.
+    """
+    if not isinstance(cu_seqlens, torch.Tensor):
+        raise TypeError("cu_seqlens must be a tensor")
+    if not isinstance(block_size, int) or isinstance(block_size, bool) or block_size <= 0:
+        raise ValueError("block_size must be a positive integer")
+    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2:
+        raise ValueError("cu_seqlens must be a vector with at least two entries")
+    if cu_seqlens.dtype != torch.int32:
+        raise TypeError("cu_seqlens must be int32")
+    bounds = cu_seqlens.detach().cpu().tolist()
+    if bounds[0] != 0:
+        raise ValueError("cu_seqlens must start at zero and end at total_tokens")
+    if any(b < a for a, b in zip(bounds, bounds[1:])):
+        raise ValueError("cu_seqlens must be nondecreasing")
+    meta = sequence_meta(bounds, block_size)
+    device = cu_seqlens.device
+    return PackedSequences(
+        cu_seqlens=cu_seqlens.detach().clone().contiguous(),
+        cu_block_lens=torch.tensor(meta.cu_block_lens, dtype=torch.int32, device=device),
+        tile_prefix=torch.tensor(meta.tri_prefix, dtype=torch.int64, device=device),
+        meta=meta,
+    )
+
+
+def prepared_for(seqs: PackedSequences, *, block_size: int, total_tokens: int, device: torch.device) -> SequenceMeta:
+    """Check that prepared metadata fits an operator call; return its host metadata."""
+    if seqs.block_size != block_size:
+        raise ValueError("block_size differs from the block_size the sequences were prepared with")
+    if seqs.total_tokens != total_tokens:
+        raise ValueError("cu_seqlens must start at zero and end at total_tokens")
+    if seqs.device != device:
+        raise ValueError("prepared sequences must be on the input device")
+    return seqs.meta

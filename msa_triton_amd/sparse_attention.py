@@ -9,7 +9,9 @@ exactly when dK or dV is needed; lse is non-differentiable.
 Execution: ``msa_attn_fwd`` and ``msa_attn_bwd``. For bf16 both are KV-major
 over the selection's k2q CSR (per-block partials merged in slot order, dK/dV
 owned per key block, no floating-point atomics); the forward builds the CSR
-itself and keeps it for a backward that needs only dQ. Saved state is q, k, v,
+itself and keeps it for a backward that needs only dQ. ``cu_seqlens`` may be a
+``PackedSequences`` (``prepare_sequences``): then neither pass reads metadata
+back from the device. Saved state is q, k, v,
 out in the input dtype plus an fp64 [T,Hq,4] per-row state (full-precision
 lse, then the backward's mass / center / delta); no fp32 staging copies.
 """
@@ -22,12 +24,12 @@ import torch
 
 from . import _lib
 from . import k2q as _k2q
-from .layout import sequence_lengths, sequence_meta
+from .layout import PackedSequences, prepared_for, sequence_lengths, sequence_meta
 
 
 class _SparseAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, indices, cu_seqlens, block_size, scale, meta):
+    def forward(ctx, q, k, v, indices, cu_seqlens, block_size, scale, meta, seqs):
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         indices = indices.contiguous()
         cu = cu_seqlens.contiguous()
@@ -47,7 +49,7 @@ class _SparseAttention(torch.autograd.Function):
             workspace = None
             if ws_bytes > 0:
                 # The KV-major forward walks the block->query CSR of the selection.
-                csr = _k2q._build_device(indices, cu, meta, groups, slots)
+                csr = _k2q._build_device(indices, cu, meta, groups, slots, seqs)
                 workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
             with torch.cuda.device(q.device):
                 status = lib.msa_attn_fwd(
@@ -66,6 +68,7 @@ class _SparseAttention(torch.autograd.Function):
         need_kv = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
         ctx.csr = None if need_kv else csr
         ctx.meta = meta
+        ctx.seqs = seqs
         ctx.scale = scale
         ctx.block_size = block_size
         ctx.mark_non_differentiable(lse)
@@ -94,9 +97,10 @@ class _SparseAttention(torch.autograd.Function):
                                                         ctx.block_size)
             if need_kv:
                 # Looked up through the module so the CSR build stays observable.
-                csr = _k2q.build_k2q_csr(indices, cu, block_size=ctx.block_size)
+                csr = _k2q.build_k2q_csr(indices, cu if ctx.seqs is None else ctx.seqs, block_size=ctx.block_size)
             elif ws_bytes > 0:
-                csr = ctx.csr if ctx.csr is not None else _k2q._build_device(indices, cu, meta, groups, slots)
+                csr = ctx.csr if ctx.csr is not None else _k2q._build_device(indices, cu, meta, groups, slots,
+                                                                             ctx.seqs)
             else:
                 csr = None
             workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
@@ -113,7 +117,7 @@ class _SparseAttention(torch.autograd.Function):
                 )
             _lib.check(status, "msa_attn_bwd")
         ctx.csr = None
-        return dq, dk, dv, None, None, None, None, None
+        return dq, dk, dv, None, None, None, None, None, None
 
 
 def m3_sparse_attention(
@@ -147,24 +151,32 @@ def m3_sparse_attention(
         raise TypeError("q/k/v must share a BF16, FP16, or FP32 dtype.")
     if indices.ndim != 3 or indices.shape[:2] != (q.shape[0], k.shape[1]) or indices.dtype != torch.int32:
         raise ValueError("indices must be int32 [T,G,K].")
-    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2 or cu_seqlens.dtype != torch.int32:
+    seqs = cu_seqlens if isinstance(cu_seqlens, PackedSequences) else None
+    cu = seqs.cu_seqlens if seqs is not None else cu_seqlens
+    if cu.ndim != 1 or cu.numel() < 2 or cu.dtype != torch.int32:
         raise ValueError("cu_seqlens must be int32 [num_sequences + 1].")
-    if any(x.device != q.device for x in (k, v, indices, cu_seqlens)):
+    if any(x.device != q.device for x in (k, v, indices, cu)):
         raise ValueError("All inputs must reside on the same device.")
     if not isinstance(block_size, int) or block_size <= 0:
         raise ValueError("block_size must be a positive integer.")
     if not isinstance(max_seqlen, int) or max_seqlen <= 0:
         raise ValueError("max_seqlen must be a positive integer.")
-    lengths = sequence_lengths(cu_seqlens, q.shape[0])
+    if seqs is None:
+        lengths = sequence_lengths(cu, q.shape[0])
+    else:  # prepared: no host read
+        lengths = list(prepared_for(seqs, block_size=block_size, total_tokens=q.shape[0], device=q.device).lengths)
     if max(lengths) > max_seqlen:
         raise ValueError("max_seqlen is smaller than an actual sequence.")
     effective_scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
     if not math.isfinite(effective_scale):
         raise ValueError("scale must be finite.")
     _lib.require_gpu(q, "m3_sparse_attention")
-    bounds = [0]
-    for length in lengths:
-        bounds.append(bounds[-1] + length)
-    meta = sequence_meta(bounds, block_size)
-    output, lse = _SparseAttention.apply(q, k, v, indices, cu_seqlens, block_size, effective_scale, meta)
+    if seqs is None:
+        bounds = [0]
+        for length in lengths:
+            bounds.append(bounds[-1] + length)
+        meta = sequence_meta(bounds, block_size)
+    else:
+        meta = seqs.meta
+    output, lse = _SparseAttention.apply(q, k, v, indices, cu, block_size, effective_scale, meta, seqs)
     return (output, lse) if return_lse else output

@@ -15,15 +15,18 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .layout import PackedSequences, prepared_for
 
 
 @torch.no_grad()
 def m3_topk(scores, cu_seqlens, *, block_size=128, topk_blocks=16, local_blocks=1):
     if scores.ndim != 3 or scores.dtype != torch.float32:
         raise ValueError("scores must be FP32 [T,G,Bmax]")
-    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2 or cu_seqlens.dtype != torch.int32:
+    seqs = cu_seqlens if isinstance(cu_seqlens, PackedSequences) else None
+    cu = seqs.cu_seqlens if seqs is not None else cu_seqlens
+    if cu.ndim != 1 or cu.numel() < 2 or cu.dtype != torch.int32:
         raise ValueError("cu_seqlens must be an int32 vector with at least two entries")
-    if cu_seqlens.device != scores.device:
+    if cu.device != scores.device:
         raise ValueError("scores and cu_seqlens must share a device")
     if not isinstance(block_size, int) or block_size <= 0:
         raise ValueError("block_size must be a positive integer")
@@ -32,9 +35,12 @@ def m3_topk(scores, cu_seqlens, *, block_size=128, topk_blocks=16, local_blocks=
     if not isinstance(local_blocks, int) or not 0 <= local_blocks <= topk_blocks:
         raise ValueError("local_blocks must satisfy 0 <= local_blocks <= topk_blocks")
     total, groups, blocks = scores.shape
-    boundaries = cu_seqlens.detach().cpu().tolist()
-    if boundaries[0] != 0 or boundaries[-1] != total or any(b < a for a, b in zip(boundaries, boundaries[1:])):
-        raise ValueError("cu_seqlens must start at 0, be nondecreasing, and end at T")
+    if seqs is None:
+        boundaries = cu.detach().cpu().tolist()
+        if boundaries[0] != 0 or boundaries[-1] != total or any(b < a for a, b in zip(boundaries, boundaries[1:])):
+            raise ValueError("cu_seqlens must start at 0, be nondecreasing, and end at T")
+    else:  # prepared: no host read
+        boundaries = list(prepared_for(seqs, block_size=block_size, total_tokens=total, device=scores.device).bounds)
     if groups <= 0 or blocks <= 0 or any(b - a > blocks * block_size for a, b in zip(boundaries, boundaries[1:])):
         raise ValueError("scores need positive G and enough block slots for every sequence")
     _lib.require_gpu(scores, "m3_topk")
@@ -44,7 +50,7 @@ def m3_topk(scores, cu_seqlens, *, block_size=128, topk_blocks=16, local_blocks=
     if blocks > 4096:
         raise NotImplementedError("m3_topk supports at most 4096 block columns")
     scores = scores.contiguous()
-    cu = cu_seqlens.contiguous()
+    cu = cu.contiguous()
     with torch.cuda.device(scores.device):
         status = _lib.lib().msa_topk(
             scores.data_ptr(), cu.data_ptr(), len(boundaries) - 1, total, groups, blocks, block_size,
