@@ -22,56 +22,67 @@ from . import _lib
 from .layout import PackedSequences, prepared_for, sequence_meta
 
 
+def _score_forward(q, k, cu, meta, max_seqlen, block_size, scale, save_state):
+    """Forward launch on contiguous inputs: (scores, tie codes or None)."""
+    total, groups, dim = q.shape
+    blocks = (max_seqlen + block_size - 1) // block_size
+    scores = torch.empty((total, groups, blocks), dtype=torch.float32, device=q.device)
+    tie = torch.empty((total, groups, blocks), dtype=torch.int32, device=q.device) if save_state else None
+    if total:
+        with torch.cuda.device(q.device):
+            status = _lib.lib().msa_score_fwd(
+                q.data_ptr(), k.data_ptr(), _lib.DTYPE_CODE[q.dtype], cu.data_ptr(), meta.num_seqs,
+                total, groups, dim, blocks, block_size, scale, scores.data_ptr(),
+                None if tie is None else tie.data_ptr(), _lib.stream_of(q.device),
+            )
+        _lib.check(status, "msa_score_fwd")
+    return scores, tie
+
+
+def _score_backward(q, k, cu, tie, grad_scores, meta, blocks, scale, need_q, need_k, cu_blocks=None):
+    """Backward launch: (dq, dk), None where not needed."""
+    total, groups, dim = q.shape
+    dq = torch.empty_like(q) if need_q else None
+    dk = torch.empty_like(k) if need_k else None
+    if total and (dq is not None or dk is not None):
+        ds = grad_scores.to(torch.float32).contiguous()
+        if cu_blocks is None:
+            cu_blocks = torch.tensor(meta.cu_block_lens, dtype=torch.int32, device=q.device)
+        lib = _lib.lib()
+        ws_bytes = (lib.msa_score_bwd_workspace_bytes(total, groups, blocks, dim, meta.block_size,
+                                                     meta.total_blocks) if dk is not None else 0)
+        workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
+        with torch.cuda.device(q.device):
+            status = lib.msa_score_bwd(
+                q.data_ptr(), k.data_ptr(), _lib.DTYPE_CODE[q.dtype], cu.data_ptr(), cu_blocks.data_ptr(),
+                tie.data_ptr(), ds.data_ptr(), meta.num_seqs, total, groups, dim, blocks,
+                meta.block_size, meta.total_blocks, scale, _lib.ptr(dq), _lib.ptr(dk),
+                workspace.data_ptr(), _lib.stream_of(q.device),
+            )
+        _lib.check(status, "msa_score_bwd")
+    return dq, dk
+
+
 class _IndexScore(torch.autograd.Function):
     @staticmethod
     def forward(ctx, index_q, index_k, cu_seqlens, max_seqlen, block_size, scale, save_state, meta, cu_blocks):
         q = index_q.contiguous()
         k = index_k.contiguous()
         cu = cu_seqlens.contiguous()
-        total, groups, dim = q.shape
-        blocks = (max_seqlen + block_size - 1) // block_size
-        scores = torch.empty((total, groups, blocks), dtype=torch.float32, device=q.device)
-        tie = torch.empty((total, groups, blocks), dtype=torch.int32, device=q.device) if save_state else None
-        if total:
-            with torch.cuda.device(q.device):
-                status = _lib.lib().msa_score_fwd(
-                    q.data_ptr(), k.data_ptr(), _lib.DTYPE_CODE[q.dtype], cu.data_ptr(), meta.num_seqs,
-                    total, groups, dim, blocks, block_size, scale, scores.data_ptr(),
-                    None if tie is None else tie.data_ptr(), _lib.stream_of(q.device),
-                )
-            _lib.check(status, "msa_score_fwd")
+        scores, tie = _score_forward(q, k, cu, meta, max_seqlen, block_size, scale, save_state)
         if save_state:
             ctx.save_for_backward(q, k, cu, tie)
         ctx.meta = meta
         ctx.cu_blocks = cu_blocks  # prepared device copy of cu_block_lens, or None
         ctx.scale = scale
-        ctx.blocks = blocks
+        ctx.blocks = scores.shape[2]
         return scores
 
     @staticmethod
     def backward(ctx, grad_scores):
         q, k, cu, tie = ctx.saved_tensors
-        meta = ctx.meta
-        total, groups, dim = q.shape
-        dq = torch.empty_like(q) if ctx.needs_input_grad[0] else None
-        dk = torch.empty_like(k) if ctx.needs_input_grad[1] else None
-        if total and (dq is not None or dk is not None):
-            ds = grad_scores.to(torch.float32).contiguous()
-            cu_blocks = ctx.cu_blocks
-            if cu_blocks is None:
-                cu_blocks = torch.tensor(meta.cu_block_lens, dtype=torch.int32, device=q.device)
-            lib = _lib.lib()
-            ws_bytes = (lib.msa_score_bwd_workspace_bytes(total, groups, ctx.blocks, dim, meta.block_size,
-                                                         meta.total_blocks) if dk is not None else 0)
-            workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=q.device)
-            with torch.cuda.device(q.device):
-                status = lib.msa_score_bwd(
-                    q.data_ptr(), k.data_ptr(), _lib.DTYPE_CODE[q.dtype], cu.data_ptr(), cu_blocks.data_ptr(),
-                    tie.data_ptr(), ds.data_ptr(), meta.num_seqs, total, groups, dim, ctx.blocks,
-                    meta.block_size, meta.total_blocks, ctx.scale, _lib.ptr(dq), _lib.ptr(dk),
-                    workspace.data_ptr(), _lib.stream_of(q.device),
-                )
-            _lib.check(status, "msa_score_bwd")
+        dq, dk = _score_backward(q, k, cu, tie, grad_scores, ctx.meta, ctx.blocks, ctx.scale,
+                                 ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.cu_blocks)
         return dq, dk, None, None, None, None, None, None, None
 
 

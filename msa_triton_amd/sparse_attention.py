@@ -27,41 +27,91 @@ from . import k2q as _k2q
 from .layout import PackedSequences, prepared_for, sequence_lengths, sequence_meta
 
 
+def _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs):
+    """Forward launch on contiguous inputs: (out, lse, row_state, csr or None)."""
+    total, heads, dim = q.shape
+    groups = k.shape[1]
+    out = torch.empty_like(q)
+    lse = torch.empty((total, heads), device=q.device, dtype=torch.float32)
+    # Private fp64 per-row state shared by forward and backward: lse, mass, center, delta.
+    row_state = torch.empty((total, heads, 4), device=q.device, dtype=torch.float64)
+    csr = None
+    if total:
+        lib = _lib.lib()
+        dtype = _lib.DTYPE_CODE[q.dtype]
+        slots = indices.shape[2]
+        ws_bytes = lib.msa_attn_fwd_workspace_bytes(dtype, total, heads, groups, dim, slots,
+                                                    meta.total_blocks, block_size)
+        workspace = None
+        if ws_bytes > 0:
+            # The KV-major forward walks the block->query CSR of the selection.
+            csr = _k2q._build_device(indices, cu, meta, groups, slots, seqs)
+            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        with torch.cuda.device(q.device):
+            status = lib.msa_attn_fwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), dtype, indices.data_ptr(), cu.data_ptr(),
+                meta.num_seqs, total, heads, groups, dim, slots, block_size, scale,
+                _lib.ptr(None if csr is None else csr.cu_block_lens), meta.total_blocks,
+                _lib.ptr(None if csr is None else csr.row_ptr),
+                _lib.ptr(None if csr is None else csr.query_indices),
+                _lib.ptr(None if csr is None else csr.slot_indices), _lib.ptr(workspace), ws_bytes,
+                out.data_ptr(), lse.data_ptr(), row_state.data_ptr(), _lib.stream_of(q.device),
+            )
+        _lib.check(status, "msa_attn_fwd")
+    return out, lse, row_state, csr
+
+
+def _attn_backward(q, k, v, indices, cu, out, row_state, grad_output, meta, block_size, scale, seqs,
+                   need_q, need_k, need_v, csr=None):
+    """Backward launch: (dq, dk, dv), None where not needed. ``row_state`` gets the
+    backward's center; a backward that needs dK or dV builds the CSR through the
+    public builder (as the reference does), a dQ-only one reuses ``csr``."""
+    need_kv = need_k or need_v
+    dq = torch.empty_like(q) if need_q else None
+    dk = torch.empty_like(k) if need_k else None
+    dv = torch.empty_like(v) if need_v else None
+    total, heads, dim = q.shape
+    groups = k.shape[1]
+    slots = indices.shape[2]
+    if total and (need_q or need_kv):
+        lib = _lib.lib()
+        device = q.device
+        dtype = _lib.DTYPE_CODE[q.dtype]
+        if grad_output is None:
+            grad_output = torch.zeros_like(out)
+        dout = grad_output.to(q.dtype).contiguous()
+        ws_bytes = lib.msa_attn_bwd_workspace_bytes(dtype, total, heads, groups, dim, slots, meta.total_blocks,
+                                                    block_size)
+        if need_kv:
+            # Looked up through the module so the CSR build stays observable.
+            csr = _k2q.build_k2q_csr(indices, cu if seqs is None else seqs, block_size=block_size)
+        elif ws_bytes > 0:
+            csr = csr if csr is not None else _k2q._build_device(indices, cu, meta, groups, slots, seqs)
+        else:
+            csr = None
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
+        with torch.cuda.device(device):
+            status = lib.msa_attn_bwd(
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), dtype, out.data_ptr(), dout.data_ptr(),
+                row_state.data_ptr(), indices.data_ptr(), cu.data_ptr(), meta.num_seqs, total, heads, groups,
+                dim, slots, block_size, scale,
+                _lib.ptr(None if csr is None else csr.cu_block_lens), meta.total_blocks,
+                _lib.ptr(None if csr is None else csr.row_ptr),
+                _lib.ptr(None if csr is None else csr.query_indices),
+                _lib.ptr(None if csr is None else csr.slot_indices), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
+                _lib.ptr(workspace), ws_bytes, _lib.stream_of(device),
+            )
+        _lib.check(status, "msa_attn_bwd")
+    return dq, dk, dv
+
+
 class _SparseAttention(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, indices, cu_seqlens, block_size, scale, meta, seqs):
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         indices = indices.contiguous()
         cu = cu_seqlens.contiguous()
-        total, heads, dim = q.shape
-        groups = k.shape[1]
-        out = torch.empty_like(q)
-        lse = torch.empty((total, heads), device=q.device, dtype=torch.float32)
-        # Private fp64 per-row state shared by forward and backward: lse, mass, center, delta.
-        row_state = torch.empty((total, heads, 4), device=q.device, dtype=torch.float64)
-        csr = None
-        if total:
-            lib = _lib.lib()
-            dtype = _lib.DTYPE_CODE[q.dtype]
-            slots = indices.shape[2]
-            ws_bytes = lib.msa_attn_fwd_workspace_bytes(dtype, total, heads, groups, dim, slots,
-                                                        meta.total_blocks, block_size)
-            workspace = None
-            if ws_bytes > 0:
-                # The KV-major forward walks the block->query CSR of the selection.
-                csr = _k2q._build_device(indices, cu, meta, groups, slots, seqs)
-                workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-            with torch.cuda.device(q.device):
-                status = lib.msa_attn_fwd(
-                    q.data_ptr(), k.data_ptr(), v.data_ptr(), dtype, indices.data_ptr(), cu.data_ptr(),
-                    meta.num_seqs, total, heads, groups, dim, slots, block_size, scale,
-                    _lib.ptr(None if csr is None else csr.cu_block_lens), meta.total_blocks,
-                    _lib.ptr(None if csr is None else csr.row_ptr),
-                    _lib.ptr(None if csr is None else csr.query_indices),
-                    _lib.ptr(None if csr is None else csr.slot_indices), _lib.ptr(workspace), ws_bytes,
-                    out.data_ptr(), lse.data_ptr(), row_state.data_ptr(), _lib.stream_of(q.device),
-                )
-            _lib.check(status, "msa_attn_fwd")
+        out, lse, row_state, csr = _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs)
         ctx.save_for_backward(q, k, v, indices, cu, out, row_state)
         # A backward that needs dK or dV rebuilds the CSR through the public builder
         # (as the reference does); a dQ-only backward reuses the forward's.
@@ -77,45 +127,9 @@ class _SparseAttention(torch.autograd.Function):
     @staticmethod
     def backward(ctx, grad_output, grad_lse):
         q, k, v, indices, cu, out, row_state = ctx.saved_tensors
-        meta = ctx.meta
         need_q, need_k, need_v = ctx.needs_input_grad[:3]
-        need_kv = need_k or need_v
-        dq = torch.empty_like(q) if need_q else None
-        dk = torch.empty_like(k) if need_k else None
-        dv = torch.empty_like(v) if need_v else None
-        total, heads, dim = q.shape
-        groups = k.shape[1]
-        slots = indices.shape[2]
-        if total and (need_q or need_kv):
-            lib = _lib.lib()
-            device = q.device
-            dtype = _lib.DTYPE_CODE[q.dtype]
-            if grad_output is None:
-                grad_output = torch.zeros_like(out)
-            dout = grad_output.to(q.dtype).contiguous()
-            ws_bytes = lib.msa_attn_bwd_workspace_bytes(dtype, total, heads, groups, dim, slots, meta.total_blocks,
-                                                        ctx.block_size)
-            if need_kv:
-                # Looked up through the module so the CSR build stays observable.
-                csr = _k2q.build_k2q_csr(indices, cu if ctx.seqs is None else ctx.seqs, block_size=ctx.block_size)
-            elif ws_bytes > 0:
-                csr = ctx.csr if ctx.csr is not None else _k2q._build_device(indices, cu, meta, groups, slots,
-                                                                             ctx.seqs)
-            else:
-                csr = None
-            workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
-            with torch.cuda.device(device):
-                status = lib.msa_attn_bwd(
-                    q.data_ptr(), k.data_ptr(), v.data_ptr(), dtype, out.data_ptr(), dout.data_ptr(),
-                    row_state.data_ptr(), indices.data_ptr(), cu.data_ptr(), meta.num_seqs, total, heads, groups,
-                    dim, slots, ctx.block_size, ctx.scale,
-                    _lib.ptr(None if csr is None else csr.cu_block_lens), meta.total_blocks,
-                    _lib.ptr(None if csr is None else csr.row_ptr),
-                    _lib.ptr(None if csr is None else csr.query_indices),
-                    _lib.ptr(None if csr is None else csr.slot_indices), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv),
-                    _lib.ptr(workspace), ws_bytes, _lib.stream_of(device),
-                )
-            _lib.check(status, "msa_attn_bwd")
+        dq, dk, dv = _attn_backward(q, k, v, indices, cu, out, row_state, grad_output, ctx.meta, ctx.block_size,
+                                    ctx.scale, ctx.seqs, need_q, need_k, need_v, ctx.csr)
         ctx.csr = None
         return dq, dk, dv, None, None, None, None, None, None
 
