@@ -438,6 +438,16 @@ def main():
                 i2 = msa.m3_topk(s, cu, block_size=block, topk_blocks=topk, local_blocks=local)
                 msa.m3_sparse_attention(q, k, v, i2, cu, max_len, block_size=block)
 
+        def score_topk_fused():
+            with torch.no_grad():
+                msa.m3_index_score_topk(iq, ik, cu, max_len, block_size=block, topk_blocks=topk, local_blocks=local)
+
+        def pipeline_fwd_fused():
+            with torch.no_grad():
+                _, i2 = msa.m3_index_score_topk(iq, ik, cu, max_len, block_size=block, topk_blocks=topk,
+                                                local_blocks=local)
+                msa.m3_sparse_attention(q, k, v, i2, cu, max_len, block_size=block)
+
         iqg, ikg = iq.detach().clone().requires_grad_(), ik.detach().clone().requires_grad_()
         ones = torch.ones_like(scores)
 
@@ -448,7 +458,8 @@ def main():
         reps = max(3, args.repeats // 2)
         for name, fn in (("score_fwd_ms", score_fwd), ("topk_ms", sel), ("k2q_csr_ms", csr),
                          ("attention_fwd_ms", attn_fwd), ("pipeline_fwd_ms", pipeline_fwd),
-                         ("score_fwd_bwd_ms", score_fwd_bwd)):
+                         ("score_fwd_bwd_ms", score_fwd_bwd), ("score_topk_fused_ms", score_topk_fused),
+                         ("pipeline_fwd_fused_ms", pipeline_fwd_fused)):
             stages[name] = round(time_events(fn, reps)["median"], 4)
             log(f"{name}: {stages[name]:.3f}")
         stages["attention_fwd_bwd_ms"] = round(ms, 4)

@@ -58,6 +58,19 @@ int msa_score_fwd(const void* index_q, const void* index_k, int32_t dtype,
                   int64_t groups, int64_t index_dim, int64_t num_blocks, int64_t block_size,
                   double scale, float* scores, int32_t* tie_info, void* stream);
 
+/* Stage 1 forward fused with stage 2: the scores of msa_score_fwd and, from them,
+ * the causal top-k selection of msa_topk (int32 [T,G,K], same semantics and tie
+ * order). No counterpart entry point in the reference, which runs
+ * triton/index_score.py:298-357 and triton/topk.py:11-47 as two operators; this
+ * is the score -> top-k fusion the reference's survey lists as follow-on work,
+ * as one call: the selection is a second launch on the same stream (selecting
+ * inside the score kernel's tiles measured slower). */
+int msa_index_score_topk(const void* index_q, const void* index_k, int32_t dtype,
+                         const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
+                         int64_t groups, int64_t index_dim, int64_t num_blocks, int64_t block_size,
+                         double scale, int64_t topk_blocks, int64_t local_blocks, float* scores,
+                         int32_t* tie_info, int32_t* indices, void* stream);
+
 /* Score backward workspace in bytes (block-major tie/grad copies and the FP64
  * per-segment dk sums). */
 int64_t msa_score_bwd_workspace_bytes(int64_t total_tokens, int64_t groups, int64_t num_blocks,

@@ -12,6 +12,11 @@ not load the native library.
 All three run as hand-written gfx950 HIP kernels behind the C ABI declared in
 ``include/msa_mi355x.h``; there is no CPU or eager fallback.
 
+    m3_index_score_topk(index_q, index_k, cu_seqlens, max_seqlen, *, block_size=128, scale=1.0,
+                        topk_blocks=16, local_blocks=1) -> (scores, indices)
+
+is the first two stages in one call (score and selection kernels back to back);
+
     prepare_sequences(cu_seqlens, *, block_size=128) -> PackedSequences
 
 validates ``cu_seqlens`` once and returns immutable metadata with device copies;
@@ -48,10 +53,19 @@ def m3_sparse_attention(
     )
 
 
+def m3_index_score_topk(index_q, index_k, cu_seqlens, max_seqlen, *, block_size=128, scale=1.0, topk_blocks=16,
+                        local_blocks=1):
+    from .index_score import m3_index_score_topk as implementation
+
+    return implementation(index_q, index_k, cu_seqlens, max_seqlen, block_size=block_size, scale=scale,
+                          topk_blocks=topk_blocks, local_blocks=local_blocks)
+
+
 def prepare_sequences(cu_seqlens, *, block_size=128):
     from .layout import prepare_sequences as implementation
 
     return implementation(cu_seqlens, block_size=block_size)
 
 
-__all__ = ["m3_index_score", "m3_topk", "m3_sparse_attention", "prepare_sequences", "PackedSequences"]
+__all__ = ["m3_index_score", "m3_topk", "m3_sparse_attention", "m3_index_score_topk", "prepare_sequences",
+           "PackedSequences"]

@@ -19,6 +19,7 @@
 // order (no float atomics), then round to the input dtype.
 #include "common.hpp"
 #include "score_mfma.hpp"
+#include "topk_row.hpp"
 
 namespace msa {
 
@@ -621,14 +622,23 @@ static int64_t dk_nseg(int64_t rows) { return (rows + kDkSeg - 1) / kDkSeg; }
 
 template <int DT>
 int score_fwd_launch(const void* iq, const void* ik, const int32_t* cu, int nseq, int64_t rows, int G,
-                     int Di, int NB, int B, double scale, float* scores, int32_t* tie, hipStream_t st) {
+                     int Di, int NB, int B, double scale, float* scores, int32_t* tie, int K, int L, int32_t* sel,
+                     hipStream_t st) {
+  // sel != null: the top-k selection follows on the same stream (topk.hip). Selecting
+  // inside the MFMA kernel's tiles, from the scores just written, was measured slower
+  // at c4 (2.43-2.81 ms vs 2.27 ms for the two launches): the score kernel runs two
+  // workgroups per CU and the selection's registers cost its main loop.
   if (DT == kBF16 && score_mfma_supported(Di, B, scale)) {
-    return score_fwd_mfma_launch(iq, ik, cu, nseq, rows, G, Di, NB, B, scale, scores, tie, st);
+    const int rc = score_fwd_mfma_launch(iq, ik, cu, nseq, rows, G, Di, NB, B, scale, scores, tie, st);
+    if (rc != kOk || !sel) return rc;
+    return topk_launch(scores, cu, nseq, rows, G, NB, B, K, L, sel, st);
   }
   const int64_t waves = rows * NB;
   hipLaunchKernelGGL(score_fwd_exact<DT>, dim3(grid_1d(waves, 4)), dim3(256), 0, st, iq, ik, cu, nseq, rows,
                      G, Di, NB, B, scale, scores, tie);
-  return status_from(hipGetLastError());
+  const int rc = status_from(hipGetLastError());
+  if (rc != kOk || !sel) return rc;
+  return topk_launch(scores, cu, nseq, rows, G, NB, B, K, L, sel, st);
 }
 
 template <int DT>
@@ -690,9 +700,35 @@ extern "C" int msa_score_fwd(const void* index_q, const void* index_k, int32_t d
   const int Di = static_cast<int>(index_dim), NB = static_cast<int>(num_blocks);
   const int B = static_cast<int>(block_size);
   switch (dtype) {
-    case kF32: return score_fwd_launch<kF32>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, st);
-    case kF16: return score_fwd_launch<kF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, st);
-    case kBF16: return score_fwd_launch<kBF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, st);
+    case kF32: return score_fwd_launch<kF32>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, 0, 0, nullptr, st);
+    case kF16: return score_fwd_launch<kF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, 0, 0, nullptr, st);
+    case kBF16: return score_fwd_launch<kBF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, 0, 0, nullptr, st);
+    default: return kErrInvalidArgument;
+  }
+}
+
+extern "C" int msa_index_score_topk(const void* index_q, const void* index_k, int32_t dtype,
+                                    const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
+                                    int64_t groups, int64_t index_dim, int64_t num_blocks, int64_t block_size,
+                                    double scale, int64_t topk_blocks, int64_t local_blocks, float* scores,
+                                    int32_t* tie_info, int32_t* indices, void* stream) {
+  if (num_seqs <= 0 || total_tokens < 0 || groups <= 0 || index_dim <= 0 || num_blocks <= 0 ||
+      block_size <= 0 || topk_blocks < 0 || local_blocks < 0 || local_blocks > topk_blocks ||
+      (topk_blocks > 0 && !indices))
+    return kErrInvalidArgument;
+  const int64_t rows = total_tokens * groups;
+  if (rows == 0) return kOk;
+  if (index_dim > 512 || num_blocks > 16 * 256) return kErrUnsupported;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nseq = static_cast<int>(num_seqs), G = static_cast<int>(groups);
+  const int Di = static_cast<int>(index_dim), NB = static_cast<int>(num_blocks);
+  const int B = static_cast<int>(block_size), K = static_cast<int>(topk_blocks);
+  const int L = static_cast<int>(local_blocks);
+  int32_t* sel = K > 0 ? indices : nullptr;
+  switch (dtype) {
+    case kF32: return score_fwd_launch<kF32>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, K, L, sel, st);
+    case kF16: return score_fwd_launch<kF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, K, L, sel, st);
+    case kBF16: return score_fwd_launch<kBF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, K, L, sel, st);
     default: return kErrInvalidArgument;
   }
 }

@@ -13,98 +13,21 @@
 // registers (VPL values per lane). Selection is an iterated argmax on a 64-bit
 // key (ordered float bits << 32 | ~block) so that the comparison itself
 // implements "larger value, then smaller block id".
-#include "common.hpp"
+#include "topk_row.hpp"
 
 namespace msa {
 
-// Monotone map of float bits onto uint32 (+0 and -0 collapse to the same key).
-__device__ __forceinline__ uint32_t ordered_key(float f) {
-  uint32_t u = __float_as_uint(f);
-  if (u == 0x80000000u) u = 0u;
-  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-constexpr uint32_t kKeyNegInf = 0x007fffffu;  // ordered_key(-inf)
-constexpr uint32_t kKeyPosInf = 0xff800000u;  // ordered_key(+inf)
-
-// 64-bit max over the 16 lanes of a DPP row (every lane of the row receives it):
-// quad butterflies, then half-row and row mirrors pair disjoint groups.
-__device__ __forceinline__ uint64_t row16_max_u64(uint64_t v) {
-#define MSA_DPP_MAX(CTRL)                                                                         \
-  {                                                                                               \
-    const uint32_t lo = static_cast<uint32_t>(v), hi = static_cast<uint32_t>(v >> 32);            \
-    const uint32_t olo = __builtin_amdgcn_update_dpp(0u, lo, CTRL, 0xF, 0xF, false);              \
-    const uint32_t ohi = __builtin_amdgcn_update_dpp(0u, hi, CTRL, 0xF, 0xF, false);              \
-    const uint64_t o = (static_cast<uint64_t>(ohi) << 32) | olo;                                  \
-    v = o > v ? o : v;                                                                            \
-  }
-  MSA_DPP_MAX(0xB1)   // quad_perm [1, 0, 3, 2]
-  MSA_DPP_MAX(0x4E)   // quad_perm [2, 3, 0, 1]
-  MSA_DPP_MAX(0x141)  // row_half_mirror
-  MSA_DPP_MAX(0x140)  // row_mirror
-#undef MSA_DPP_MAX
-  return v;
-}
-
-// Sixteen lanes (one DPP row) per (token, group) row, four rows per wavefront: lane
-// j of a row holds blocks j, j + 16, ... (VPL values). Each pick is a 16-lane DPP
-// max of the lanes' running best keys; only the owner lane rescans its values.
+// Sixteen lanes per row, four rows per wavefront (topk_row16).
 template <int VPL>
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ scores,
                                                    const int32_t* __restrict__ cu, int nseq,
                                                    int64_t rows, int G, int NB, int B, int K, int L,
                                                    int32_t* __restrict__ out) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
-  const bool live = row < rows;  // rows past the end still run the (uniform) DPP steps
-  const int sub = threadIdx.x & 15;
-  const int64_t rr = live ? row : rows - 1;
-  const int64_t t = rr / G;
-  const int s = find_seq(cu, nseq, t);
-  const int64_t qb = (t - cu[s]) / B;
-  const int n = static_cast<int>(qb + 1 < NB ? qb + 1 : NB);
-  const int count = K < NB ? K : NB;
-  const int sel = live ? (count < n ? count : n) : 0;
-  const float* src = scores + rr * NB;
-  int32_t* dst = out + rr * K;
-
-  uint64_t key[VPL];
-#pragma unroll
-  for (int v = 0; v < VPL; ++v) {
-    const int b = v * 16 + sub;
-    uint32_t k = 0u;  // below every real key: never selected
-    if (b < n) {
-      k = (L > 0 && b > qb - L) ? kKeyPosInf : ordered_key(src[b]);
-    }
-    key[v] = (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(b));
-  }
-  uint64_t best = 0;
-#pragma unroll
-  for (int v = 0; v < VPL; ++v) best = key[v] > best ? key[v] : best;
-
-  // every row of the wave runs the same number of picks (the wave maximum)
-  int sel_w = sel;
-#pragma unroll
-  for (int o = 16; o < 64; o <<= 1) sel_w = max(sel_w, __shfl_xor(sel_w, o, kWave));
-  for (int it = 0; it < sel_w; ++it) {
-    const uint64_t win = row16_max_u64(best);
-    const int b = static_cast<int>(~static_cast<uint32_t>(win));
-    const uint32_t k = static_cast<uint32_t>(win >> 32);
-    if (sub == 0 && it < sel) dst[it] = (k == kKeyNegInf) ? -1 : b;
-    if ((b & 15) == sub && it < sel) {
-      best = 0;
-#pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        if (key[v] == win) key[v] = 0;
-        best = key[v] > best ? key[v] : best;
-      }
-    }
-  }
-  if (live)
-    for (int it = sel + sub; it < K; it += 16) dst[it] = -1;
+  topk_row16<VPL>(scores, cu, nseq, rows, G, NB, B, K, L, out,
+                  static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4), threadIdx.x & 15);
 }
 
-// One wavefront per row for long rows (more than 1024 blocks): lane j holds blocks
-// j, j + 64, ...; each pick is a 64-lane max.
+// One wavefront per row for long rows (more than 1024 blocks): topk_row64.
 template <int VPL>
 __global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict__ scores,
                                                         const int32_t* __restrict__ cu, int nseq,
@@ -112,62 +35,19 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict_
                                                         int32_t* __restrict__ out) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const int lane = threadIdx.x & 63;
-  const int64_t t = row / G;
-  const int s = find_seq(cu, nseq, t);
-  const int64_t qb = (t - cu[s]) / B;
-  const int n = static_cast<int>(qb + 1 < NB ? qb + 1 : NB);
-  const int count = K < NB ? K : NB;
-  const int sel = count < n ? count : n;
-  const float* src = scores + row * NB;
-  int32_t* dst = out + row * K;
-  uint64_t key[VPL];
-#pragma unroll
-  for (int v = 0; v < VPL; ++v) {
-    const int b = v * kWave + lane;
-    uint32_t k = 0u;
-    if (b < n) k = (L > 0 && b > qb - L) ? kKeyPosInf : ordered_key(src[b]);
-    key[v] = (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(b));
-  }
-  uint64_t best = 0;
-#pragma unroll
-  for (int v = 0; v < VPL; ++v) best = key[v] > best ? key[v] : best;
-  for (int it = 0; it < sel; ++it) {
-    const uint64_t win = wave_max_u64(best);
-    const int b = static_cast<int>(~static_cast<uint32_t>(win));
-    const uint32_t k = static_cast<uint32_t>(win >> 32);
-    if (lane == 0) dst[it] = (k == kKeyNegInf) ? -1 : b;
-    if ((b & 63) == lane) {
-      best = 0;
-#pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        if (key[v] == win) key[v] = 0;
-        best = key[v] > best ? key[v] : best;
-      }
-    }
-  }
-  for (int it = sel + lane; it < K; it += kWave) dst[it] = -1;
+  topk_row64<VPL>(scores, cu, nseq, G, NB, B, K, L, out, row, threadIdx.x & 63);
 }
 
 }  // namespace msa
 
 using namespace msa;
 
-extern "C" int msa_topk(const float* scores, const int32_t* cu_seqlens, int64_t num_seqs,
-                        int64_t total_tokens, int64_t groups, int64_t num_blocks, int64_t block_size,
-                        int64_t topk_blocks, int64_t local_blocks, int32_t* indices, void* stream) {
-  if (total_tokens < 0 || groups <= 0 || num_blocks <= 0 || block_size <= 0 || topk_blocks < 0 ||
-      local_blocks < 0 || local_blocks > topk_blocks || num_seqs <= 0)
-    return kErrInvalidArgument;
-  if (num_blocks > 16 * 256) return kErrUnsupported;
-  const int64_t rows = total_tokens * groups;
-  if (rows == 0 || topk_blocks == 0) return kOk;
-  hipStream_t st = static_cast<hipStream_t>(stream);
+namespace msa {
+
+int topk_launch(const float* scores, const int32_t* cu_seqlens, int nseq, int64_t rows, int G, int NB, int B, int K,
+                int L, int32_t* indices, hipStream_t st) {
+  if (rows == 0 || K == 0) return kOk;
   dim3 grid(grid_1d(rows, 16)), block(256);
-  const int nseq = static_cast<int>(num_seqs);
-  const int G = static_cast<int>(groups), NB = static_cast<int>(num_blocks);
-  const int B = static_cast<int>(block_size), K = static_cast<int>(topk_blocks);
-  const int L = static_cast<int>(local_blocks);
 #define MSA_TOPK_LAUNCH(V) \
   hipLaunchKernelGGL(topk_kernel<V>, grid, block, 0, st, scores, cu_seqlens, nseq, rows, G, NB, B, K, L, indices)
 #define MSA_TOPK_WAVE(V) \
@@ -184,4 +64,18 @@ extern "C" int msa_topk(const float* scores, const int32_t* cu_seqlens, int64_t 
 #undef MSA_TOPK_LAUNCH
 #undef MSA_TOPK_WAVE
   return status_from(hipGetLastError());
+}
+
+}  // namespace msa
+
+extern "C" int msa_topk(const float* scores, const int32_t* cu_seqlens, int64_t num_seqs,
+                        int64_t total_tokens, int64_t groups, int64_t num_blocks, int64_t block_size,
+                        int64_t topk_blocks, int64_t local_blocks, int32_t* indices, void* stream) {
+  if (total_tokens < 0 || groups <= 0 || num_blocks <= 0 || block_size <= 0 || topk_blocks < 0 ||
+      local_blocks < 0 || local_blocks > topk_blocks || num_seqs <= 0)
+    return kErrInvalidArgument;
+  if (num_blocks > 16 * 256) return kErrUnsupported;
+  return topk_launch(scores, cu_seqlens, static_cast<int>(num_seqs), total_tokens * groups, static_cast<int>(groups),
+                     static_cast<int>(num_blocks), static_cast<int>(block_size), static_cast<int>(topk_blocks),
+                     static_cast<int>(local_blocks), indices, static_cast<hipStream_t>(stream));
 }

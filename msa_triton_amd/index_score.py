@@ -86,23 +86,8 @@ class _IndexScore(torch.autograd.Function):
         return dq, dk, None, None, None, None, None, None, None
 
 
-def m3_index_score(
-    index_q: torch.Tensor,
-    index_k: torch.Tensor,
-    cu_seqlens: torch.Tensor,
-    max_seqlen: int,
-    *,
-    block_size: int = 128,
-    scale: float = 1.0,
-) -> torch.Tensor:
-    """Return per-group causal block maxima as FP32 ``[T, G, Bmax]``.
-
-    ``index_q`` is ``[T,G,Di]`` and ``index_k`` is ``[T,1,Di]``. Blocks are
-    relative to the start of each packed sequence. Future and out-of-sequence
-    blocks return ``-inf`` and have zero derivative. Exact max ties share the
-    gradient equally, matching ``torch.amax``. Inputs must be finite.
-    Metadata validation reads ``cu_seqlens`` on the host.
-    """
+def _validate(index_q, index_k, cu_seqlens, max_seqlen, block_size, scale):
+    """m3_index_score's checks, in the reference's order; returns (cu, meta, seqs, save_state)."""
     if index_q.ndim != 3 or index_k.ndim != 3:
         raise ValueError("index_q and index_k must be rank-3 TND tensors")
     total, groups, dim = index_q.shape
@@ -141,5 +126,85 @@ def m3_index_score(
         raise ValueError("max_seqlen is smaller than a packed sequence")
     _lib.require_gpu(index_q, "m3_index_score")
     save_state = torch.is_grad_enabled() and (index_q.requires_grad or index_k.requires_grad)
+    return cu, meta, seqs, save_state
+
+
+def m3_index_score(
+    index_q: torch.Tensor,
+    index_k: torch.Tensor,
+    cu_seqlens: torch.Tensor,
+    max_seqlen: int,
+    *,
+    block_size: int = 128,
+    scale: float = 1.0,
+) -> torch.Tensor:
+    """Return per-group causal block maxima as FP32 ``[T, G, Bmax]``.
+
+    ``index_q`` is ``[T,G,Di]`` and ``index_k`` is ``[T,1,Di]``. Blocks are
+    relative to the start of each packed sequence. Future and out-of-sequence
+    blocks return ``-inf`` and have zero derivative. Exact max ties share the
+    gradient equally, matching ``torch.amax``. Inputs must be finite.
+    Metadata validation reads ``cu_seqlens`` on the host.
+    """
+    cu, meta, seqs, save_state = _validate(index_q, index_k, cu_seqlens, max_seqlen, block_size, scale)
     return _IndexScore.apply(index_q, index_k, cu, max_seqlen, block_size, float(scale), save_state, meta,
                              None if seqs is None else seqs.cu_block_lens)
+
+
+
+class _IndexScoreTopk(torch.autograd.Function):
+    """Scores with the top-k selection from the same launch; indices carry no gradient."""
+
+    @staticmethod
+    def forward(ctx, index_q, index_k, cu_seqlens, max_seqlen, block_size, scale, save_state, meta, cu_blocks,
+                topk_blocks, local_blocks):
+        q = index_q.contiguous()
+        k = index_k.contiguous()
+        cu = cu_seqlens.contiguous()
+        total, groups, dim = q.shape
+        blocks = (max_seqlen + block_size - 1) // block_size
+        scores = torch.empty((total, groups, blocks), dtype=torch.float32, device=q.device)
+        tie = torch.empty((total, groups, blocks), dtype=torch.int32, device=q.device) if save_state else None
+        indices = torch.empty((total, groups, topk_blocks), dtype=torch.int32, device=q.device)
+        if total:
+            with torch.cuda.device(q.device):
+                status = _lib.lib().msa_index_score_topk(
+                    q.data_ptr(), k.data_ptr(), _lib.DTYPE_CODE[q.dtype], cu.data_ptr(), meta.num_seqs,
+                    total, groups, dim, blocks, block_size, scale, topk_blocks, local_blocks, scores.data_ptr(),
+                    None if tie is None else tie.data_ptr(), indices.data_ptr(), _lib.stream_of(q.device),
+                )
+            _lib.check(status, "msa_index_score_topk")
+        if save_state:
+            ctx.save_for_backward(q, k, cu, tie)
+        ctx.meta = meta
+        ctx.cu_blocks = cu_blocks
+        ctx.scale = scale
+        ctx.blocks = blocks
+        ctx.mark_non_differentiable(indices)
+        return scores, indices
+
+    @staticmethod
+    def backward(ctx, grad_scores, grad_indices):
+        q, k, cu, tie = ctx.saved_tensors
+        dq, dk = _score_backward(q, k, cu, tie, grad_scores, ctx.meta, ctx.blocks, ctx.scale,
+                                 ctx.needs_input_grad[0], ctx.needs_input_grad[1], ctx.cu_blocks)
+        return dq, dk, None, None, None, None, None, None, None, None, None
+
+
+def m3_index_score_topk(index_q, index_k, cu_seqlens, max_seqlen, *, block_size=128, scale=1.0, topk_blocks=16,
+                        local_blocks=1):
+    """``m3_index_score`` and ``m3_topk`` of its scores in one call: ``(scores, indices)``.
+
+    Equal, bit for bit, to ``m3_topk(m3_index_score(...), ...)`` with the same
+    arguments; the scores keep their gradient, the indices have none. One C call
+    (``msa_index_score_topk``) launches both kernels back to back.
+    """
+    if not isinstance(topk_blocks, int) or topk_blocks < 0:
+        raise ValueError("topk_blocks must be a nonnegative integer")
+    if not isinstance(local_blocks, int) or not 0 <= local_blocks <= topk_blocks:
+        raise ValueError("local_blocks must satisfy 0 <= local_blocks <= topk_blocks")
+    cu, meta, seqs, save_state = _validate(index_q, index_k, cu_seqlens, max_seqlen, block_size, scale)
+    if (max_seqlen + block_size - 1) // block_size > 4096:
+        raise NotImplementedError("m3_topk supports at most 4096 block columns")
+    return _IndexScoreTopk.apply(index_q, index_k, cu, max_seqlen, block_size, float(scale), save_state, meta,
+                                 None if seqs is None else seqs.cu_block_lens, topk_blocks, local_blocks)

@@ -132,3 +132,15 @@ def test_attention_validation_messages():
         msa.m3_sparse_attention(q, k, k, ids.long(), cu, 2)
     with pytest.raises(RuntimeError, match="ROCm device"):
         msa.m3_sparse_attention(q, k, k, ids, cu, 2, block_size=2)
+
+
+def test_fused_score_topk_validation_messages():
+    iq = torch.zeros(4, 1, 8, dtype=torch.bfloat16)
+    ik = torch.zeros(4, 1, 8, dtype=torch.bfloat16)
+    cu = torch.tensor([0, 4], dtype=torch.int32)
+    with pytest.raises(ValueError, match="max_seqlen"):
+        msa.m3_index_score_topk(iq, ik, cu, 3, block_size=2, topk_blocks=1)
+    with pytest.raises(ValueError, match="local_blocks"):
+        msa.m3_index_score_topk(iq, ik, cu, 4, block_size=2, topk_blocks=1, local_blocks=2)
+    with pytest.raises(ValueError, match="topk_blocks"):
+        msa.m3_index_score_topk(iq, ik, cu, 4, block_size=2, topk_blocks=-1)
