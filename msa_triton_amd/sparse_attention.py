@@ -27,8 +27,9 @@ from . import k2q as _k2q
 from .layout import PackedSequences, prepared_for, sequence_lengths, sequence_meta
 
 
-def _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs):
-    """Forward launch on contiguous inputs: (out, lse, row_state, csr or None)."""
+def _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs, public_csr=False):
+    """Forward launch on contiguous inputs: (out, lse, row_state, csr or None). With
+    ``public_csr`` the KV-major path builds its CSR through the public builder."""
     total, heads, dim = q.shape
     groups = k.shape[1]
     out = torch.empty_like(q)
@@ -45,7 +46,10 @@ def _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs):
         workspace = None
         if ws_bytes > 0:
             # The KV-major forward walks the block->query CSR of the selection.
-            csr = _k2q._build_device(indices, cu, meta, groups, slots, seqs)
+            if public_csr:  # looked up through the module so the build stays observable
+                csr = _k2q.build_k2q_csr(indices, cu if seqs is None else seqs, block_size=block_size)
+            else:
+                csr = _k2q._build_device(indices, cu, meta, groups, slots, seqs)
             workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
         with torch.cuda.device(q.device):
             status = lib.msa_attn_fwd(
@@ -64,8 +68,9 @@ def _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs):
 def _attn_backward(q, k, v, indices, cu, out, row_state, grad_output, meta, block_size, scale, seqs,
                    need_q, need_k, need_v, csr=None):
     """Backward launch: (dq, dk, dv), None where not needed. ``row_state`` gets the
-    backward's center; a backward that needs dK or dV builds the CSR through the
-    public builder (as the reference does), a dQ-only one reuses ``csr``."""
+    backward's center. ``csr`` (the forward's) is reused when given; otherwise a
+    backward that needs dK or dV builds it through the public builder (as the
+    reference does) and a dQ-only one privately."""
     need_kv = need_k or need_v
     dq = torch.empty_like(q) if need_q else None
     dk = torch.empty_like(k) if need_k else None
@@ -82,13 +87,13 @@ def _attn_backward(q, k, v, indices, cu, out, row_state, grad_output, meta, bloc
         dout = grad_output.to(q.dtype).contiguous()
         ws_bytes = lib.msa_attn_bwd_workspace_bytes(dtype, total, heads, groups, dim, slots, meta.total_blocks,
                                                     block_size)
-        if need_kv:
+        if csr is not None:
+            pass
+        elif need_kv:
             # Looked up through the module so the CSR build stays observable.
             csr = _k2q.build_k2q_csr(indices, cu if seqs is None else seqs, block_size=block_size)
         elif ws_bytes > 0:
-            csr = csr if csr is not None else _k2q._build_device(indices, cu, meta, groups, slots, seqs)
-        else:
-            csr = None
+            csr = _k2q._build_device(indices, cu, meta, groups, slots, seqs)
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes > 0 else None
         with torch.cuda.device(device):
             status = lib.msa_attn_bwd(
@@ -111,12 +116,14 @@ class _SparseAttention(torch.autograd.Function):
         q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
         indices = indices.contiguous()
         cu = cu_seqlens.contiguous()
-        out, lse, row_state, csr = _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs)
-        ctx.save_for_backward(q, k, v, indices, cu, out, row_state)
-        # A backward that needs dK or dV rebuilds the CSR through the public builder
-        # (as the reference does); a dQ-only backward reuses the forward's.
+        # The KV-major forward needs the CSR anyway: when dK or dV will be needed it is
+        # built through the public builder (the one build the reference makes, in its
+        # backward) and the backward reuses it; a dQ-only backward reuses a private one.
         need_kv = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
-        ctx.csr = None if need_kv else csr
+        out, lse, row_state, csr = _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs,
+                                                 public_csr=need_kv)
+        ctx.save_for_backward(q, k, v, indices, cu, out, row_state)
+        ctx.csr = csr
         ctx.meta = meta
         ctx.seqs = seqs
         ctx.scale = scale
