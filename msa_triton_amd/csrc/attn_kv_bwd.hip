@@ -32,8 +32,14 @@ namespace msa {
 
 namespace {
 
-constexpr int kStatRowsPerTile = 128;  // B1: (edge, head) rows per tile (4 waves x 32)
-constexpr int kStatTilesPerItem = 4;
+// B1: 8 waves per workgroup, one 16-row group per wave and tile (102 VGPRs, so two
+// workgroups give 4 waves per SIMD to hide the Q/dO fragment loads; 4 waves x 2 groups
+// and 8 waves x 2 groups measured slower)
+constexpr int kStatWaves = 8;
+constexpr int kStatRT = 1;
+constexpr int kStatThreads = 64 * kStatWaves;
+constexpr int kStatRowsPerTile = 16 * kStatRT * kStatWaves;  // (edge, head) rows per tile
+constexpr int kStatTilesPerItem = 512 / kStatRowsPerTile;
 constexpr int kStatItemRows = kStatRowsPerTile * kStatTilesPerItem;
 constexpr int kMainEdges = 512;        // B2: CSR edges per work item
 constexpr int kMainThreads = 512;      // B2: 8 waves, 16 keys each (S, dP, dV, dK), 16 rows x 32 dims each (dQ)
@@ -106,9 +112,9 @@ __global__ __launch_bounds__(256) void kv_bwd_center(const uint16_t* __restrict_
 
 // B1: per (edge, head) row and key block, sum_j p_j and sum_j p_j (dp_j - c).
 // Structure of the forward partial kernel: K and V blocks row-major in LDS,
-// 4 waves x 32 rows per tile; S^T = K Q^T and dP^T = V dO^T (lane: row c, keys 4*q4 + i).
+// kStatWaves waves x 16 kStatRT rows per tile; S^T = K Q^T and dP^T = V dO^T (lane: row c, keys 4*q4 + i).
 template <int NK, bool FULLD>
-__global__ __launch_bounds__(256, 2) void kv_bwd_stats_kernel(
+__global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx, const int32_t* __restrict__ sidx,
@@ -126,29 +132,29 @@ __global__ __launch_bounds__(256, 2) void kv_bwd_stats_kernel(
   const int e_end = e_begin + epi < e_hi[row] ? e_begin + epi : e_hi[row];
   const int nrows = (e_end - e_begin) * R;  // 1 <= nrows <= kStatItemRows
 
-  constexpr int KVI = 128 * (DP / 8) / 256;
+  constexpr int KVI = 128 * (DP / 8) / kStatThreads;
   uint4 kw[KVI], vw[KVI];
 #pragma unroll
   for (int i = 0; i < KVI; ++i) {
-    const int e = tid + 256 * i;
+    const int e = tid + kStatThreads * i;
     const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));
     const int klc = kl < rg.nk ? kl : rg.nk - 1, d0c = (FULLD || d0 < D) ? d0 : D - 8;
     const int64_t off = ((rg.kb + klc) * G + rg.g) * D + d0c;
     kw[i] = *reinterpret_cast<const uint4*>(k + off);
     vw[i] = *reinterpret_cast<const uint4*>(v + off);
   }
-  constexpr int MI = kStatItemRows / 256;
+  constexpr int MI = kStatItemRows / kStatThreads;
   int32_t mtok[MI], mslot[MI];
 #pragma unroll
   for (int j = 0; j < MI; ++j) {
-    const int rho = tid + 256 * j;
+    const int rho = tid + kStatThreads * j;
     const int eo = (rho < nrows ? rho : nrows - 1) / R;
     mtok[j] = qidx[e_begin + eo];
     mslot[j] = sidx[e_begin + eo];
   }
 #pragma unroll
   for (int i = 0; i < KVI; ++i) {
-    const int e = tid + 256 * i;
+    const int e = tid + kStatThreads * i;
     const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));
     const bool ok = kl < rg.nk && (FULLD || d0 < D);
     *reinterpret_cast<uint4*>(sm.k + kl * KS + d0) = ok ? kw[i] : make_uint4(0u, 0u, 0u, 0u);
@@ -156,7 +162,7 @@ __global__ __launch_bounds__(256, 2) void kv_bwd_stats_kernel(
   }
 #pragma unroll
   for (int j = 0; j < MI; ++j) {
-    const int rho = tid + 256 * j;
+    const int rho = tid + kStatThreads * j;
     if (rho < nrows) {
       const int eo = rho / R;
       const int h = rg.g * R + (rho - eo * R);
@@ -171,13 +177,13 @@ __global__ __launch_bounds__(256, 2) void kv_bwd_stats_kernel(
 
   const int ntiles = (nrows + kStatRowsPerTile - 1) / kStatRowsPerTile;
   for (int tile = 0; tile < ntiles; ++tile) {
-    const int rbase = tile * kStatRowsPerTile + 32 * wid;
+    const int rbase = tile * kStatRowsPerTile + 16 * kStatRT * wid;
     if (rbase >= nrows) break;  // wave-uniform
-    bf16x8 qf[2][NK], gf[2][NK];
-    int lim[2];
-    float lse2[2], cen[2];
+    bf16x8 qf[kStatRT][NK], gf[kStatRT][NK];
+    int lim[kStatRT];
+    float lse2[kStatRT], cen[kStatRT];
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < kStatRT; ++rt) {
       const int rho = rbase + 16 * rt + c;
       const bool ok = rho < nrows;
       const int64_t th = ok ? static_cast<int64_t>(sm.tok[rho]) * Hq + rg.g * R + rho % R : 0;
@@ -193,9 +199,14 @@ __global__ __launch_bounds__(256, 2) void kv_bwd_stats_kernel(
         gf[rt][kk] = dok ? load_frag(dout + th * D + d0) : zero_frag();
       }
     }
-    float psum[2] = {0.f, 0.f}, usum[2] = {0.f, 0.f};
+    float psum[kStatRT], usum[kStatRT];
+#pragma unroll
+    for (int rt = 0; rt < kStatRT; ++rt) psum[rt] = usum[rt] = 0.f;
     // rows are in token order: when every row of the wave sees all 128 keys, no masks
-    const bool full = __all(lim[0] >= 128 && lim[1] >= 128);
+    bool fl = true;
+#pragma unroll
+    for (int rt = 0; rt < kStatRT; ++rt) fl = fl && lim[rt] >= 128;
+    const bool full = __all(fl);
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
       bf16x8 kf[NK], vf[NK];
@@ -205,7 +216,7 @@ __global__ __launch_bounds__(256, 2) void kv_bwd_stats_kernel(
         vf[kk] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(sm.v + (16 * kt + c) * KS + 32 * kk + 8 * q4));
       }
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
+      for (int rt = 0; rt < kStatRT; ++rt) {
         f32x4 sa = {0.f, 0.f, 0.f, 0.f}, da = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk) {
@@ -231,7 +242,7 @@ __global__ __launch_bounds__(256, 2) void kv_bwd_stats_kernel(
       }
     }
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < kStatRT; ++rt) {
       float a = psum[rt], b = usum[rt];
       a += __shfl_xor(a, 16, kWave);
       b += __shfl_xor(b, 16, kWave);
@@ -740,7 +751,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       const int32_t* nit = kv_plan_count(sp, sbase, c);
       const int2* its = kv_plan_items(sp, sbase, c);
       const int sepi = static_cast<int>(sp.epi);
-      const dim3 grid(static_cast<unsigned>(sp.max_items)), block(256);
+      const dim3 grid(static_cast<unsigned>(sp.max_items)), block(kStatThreads);
 #define MSA_BWD_STATS(NKV, FD) hipLaunchKernelGGL((kv_bwd_stats_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, sepi, it0, spart)
       if (nk == 1) { if (fd) MSA_BWD_STATS(1, true); else MSA_BWD_STATS(1, false); }
       else if (nk == 2) { if (fd) MSA_BWD_STATS(2, true); else MSA_BWD_STATS(2, false); }
