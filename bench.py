@@ -199,6 +199,9 @@ class Harness:
         self.out = torch.empty_like(q)
         self.lse = torch.empty(q.shape[:2], dtype=torch.float32, device=device)
         self.rs = torch.empty((*q.shape[:2], 4), dtype=torch.float64, device=device)
+        # the forward's fp32 output, which lets the backward skip its statistics pass
+        self.o32 = torch.empty(q.shape, dtype=torch.float32, device=device)
+        self.use_f32 = True
         self.dq = torch.empty_like(q)
         self.dk = torch.empty_like(k)
         self.dv = torch.empty_like(v)
@@ -219,14 +222,15 @@ class Harness:
                                    c["block"], self.scale, csr.cu_block_lens.data_ptr(), self.meta.total_blocks,
                                    csr.row_ptr.data_ptr(), csr.query_indices.data_ptr(), csr.slot_indices.data_ptr(),
                                    self.fws.data_ptr(), self.fws_bytes, self.out.data_ptr(), self.lse.data_ptr(),
-                                   self.rs.data_ptr(), self.stream)
+                                   self.rs.data_ptr(), self.o32.data_ptr(), self.stream)
         assert st == 0
 
     def bwd(self):
         c = self.cfg
         csr = self.csr
         st = self.lib.msa_attn_bwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), 2, self.out.data_ptr(),
-                                   self.dout.data_ptr(), self.rs.data_ptr(), self.ids.data_ptr(), self.cu.data_ptr(),
+                                   self.dout.data_ptr(), self.rs.data_ptr(),
+                                   self.o32.data_ptr() if self.use_f32 else None, self.ids.data_ptr(), self.cu.data_ptr(),
                                    self.meta.num_seqs, self.T, c["hq"], c["g"], c["d"], c["topk"], c["block"],
                                    self.scale, csr.cu_block_lens.data_ptr(), self.meta.total_blocks,
                                    csr.row_ptr.data_ptr(), csr.query_indices.data_ptr(), csr.slot_indices.data_ptr(),

@@ -102,16 +102,19 @@ int64_t msa_attn_fwd_workspace_bytes(int32_t dtype, int64_t total_tokens, int64_
  * (msa_k2q_build: cu_block_lens, row_ptr, query_indices, slot_indices) and a
  * workspace of msa_attn_fwd_workspace_bytes(...) bytes; these may be NULL / 0
  * when that query returns 0.
- * row_state (nullable): private fp64 [T,Hq,4] consumed by msa_attn_bwd; slot 0
- * receives the full-precision lse in the path's own convention (the reference
- * keeps (max, denominator), sparse_attention.py:83-84); treat it as opaque. */
+ * row_state (nullable): private fp64 [T,Hq,4] consumed by msa_attn_bwd; slots 0
+ * and 1 receive the full-precision lse in the path's own convention and its
+ * normalisation (the reference keeps (max, denominator), sparse_attention.py:83-84);
+ * treat it as opaque. out_f32 (nullable): fp32 [T,Hq,D], the output before its
+ * rounding to the input dtype; handed to msa_attn_bwd it replaces the backward's
+ * per-slot statistics pass (no reference counterpart: the reference recomputes). */
 int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t dtype, const int32_t* indices,
                  const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
                  int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
                  int64_t block_size, double scale, const int32_t* cu_block_lens,
                  int64_t total_blocks, const int32_t* row_ptr, const int32_t* query_indices,
                  const int32_t* slot_indices, void* workspace, int64_t workspace_bytes, void* out,
-                 float* lse, double* row_state, void* stream);
+                 float* lse, double* row_state, float* out_f32, void* stream);
 
 /* Stage 3 backward workspace in bytes; 0 means this configuration runs the VALU
  * kernels, which need no workspace. */
@@ -123,15 +126,18 @@ int64_t msa_attn_bwd_workspace_bytes(int32_t dtype, int64_t total_tokens, int64_
  * attention computed by msa_attn_fwd with the same row_state. Replaces the
  * autograd backward of triton/sparse_attention.py:361-394 (_backward_kernel,
  * :87-198, with the dK/dV pass _backward_kv_kernel, :223-295, over
- * build_k2q_csr). Softmax derivative centred as in the reference
- * (:119-158): delta = sum p (dp - c) / mass from the same p and dp as dS.
+ * build_k2q_csr). Without out_f32 the softmax derivative is centred as in the
+ * reference (:119-158): delta = sum p (dp - c) / mass from the same p and dp as
+ * dS, one extra pass over every (row, slot). With out_f32 (the forward's, for the
+ * same row_state) the bf16 path takes delta = out_f32 . dO in fp64 and the
+ * forward's exact mass instead, and skips that pass; other paths ignore it.
  * The bf16 path is KV-major and needs the k2q CSR (cu_block_lens, row_ptr,
  * query_indices, slot_indices) and msa_attn_bwd_workspace_bytes(...) bytes of
  * workspace for every gradient set; the VALU path needs the CSR only when
  * grad_k or grad_v is requested. row_state slots 1..3 are (re)written.
  * Deterministic: no floating-point atomics. */
 int msa_attn_bwd(const void* q, const void* k, const void* v, int32_t dtype, const void* out,
-                 const void* grad_out, double* row_state, const int32_t* indices,
+                 const void* grad_out, double* row_state, const float* out_f32, const int32_t* indices,
                  const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
                  int64_t q_heads, int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
                  int64_t block_size, double scale, const int32_t* cu_block_lens,

@@ -41,9 +41,9 @@ SIGNATURES = {
     "msa_score_bwd_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64]),
     "msa_attn_fwd_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "msa_attn_fwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64,
-                            _i64, _f64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp]),
+                            _i64, _f64, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _vp]),
     "msa_attn_bwd_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
-    "msa_attn_bwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+    "msa_attn_bwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _f64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
 }
 

@@ -9,7 +9,7 @@ namespace msa {
 
 template <int DT>
 int attn_fwd_valu_dispatch(const void*, const void*, const void*, const int32_t*, const int32_t*, int, int64_t, int,
-                           int, int, int, int, double, void*, float*, double*, hipStream_t);
+                           int, int, int, int, double, void*, float*, double*, float*, hipStream_t);
 template <int DT>
 int attn_dq_valu_dispatch(const void*, const void*, const void*, const void*, const void*, double*, const int32_t*,
                           const int32_t*, int, int64_t, int, int, int, int, int, double, void*, hipStream_t);
@@ -39,7 +39,8 @@ extern "C" int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t
                             int64_t kv_groups, int64_t head_dim, int64_t topk_slots, int64_t block_size,
                             double scale, const int32_t* cu_block_lens, int64_t total_blocks, const int32_t* row_ptr,
                             const int32_t* query_indices, const int32_t* slot_indices, void* workspace,
-                            int64_t workspace_bytes, void* out, float* lse, double* row_state, void* stream) {
+                            int64_t workspace_bytes, void* out, float* lse, double* row_state, float* out_f32,
+                            void* stream) {
   if (!valid_common(num_seqs, total_tokens, q_heads, kv_groups, head_dim, block_size) || topk_slots < 0)
     return kErrInvalidArgument;
   if (total_tokens == 0) return kOk;
@@ -53,12 +54,12 @@ extern "C" int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t
       return kErrInvalidArgument;
     return attn_fwd_kv(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, static_cast<float>(scale),
                        cu_block_lens, total_blocks, row_ptr, query_indices, slot_indices, workspace, workspace_bytes,
-                       out, lse, row_state, st);
+                       out, lse, row_state, out_f32, st);
   }
   switch (dtype) {
-    case kF32: return attn_fwd_valu_dispatch<kF32>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, row_state, st);
-    case kF16: return attn_fwd_valu_dispatch<kF16>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, row_state, st);
-    case kBF16: return attn_fwd_valu_dispatch<kBF16>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, row_state, st);
+    case kF32: return attn_fwd_valu_dispatch<kF32>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, row_state, out_f32, st);
+    case kF16: return attn_fwd_valu_dispatch<kF16>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, row_state, out_f32, st);
+    case kBF16: return attn_fwd_valu_dispatch<kBF16>(q, k, v, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B, scale, out, lse, row_state, out_f32, st);
     default: return kErrInvalidArgument;
   }
 }
@@ -72,7 +73,7 @@ extern "C" int64_t msa_attn_bwd_workspace_bytes(int32_t dtype, int64_t total_tok
 }
 
 extern "C" int msa_attn_bwd(const void* q, const void* k, const void* v, int32_t dtype, const void* out,
-                            const void* grad_out, double* row_state, const int32_t* indices,
+                            const void* grad_out, double* row_state, const float* out_f32, const int32_t* indices,
                             const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens, int64_t q_heads,
                             int64_t kv_groups, int64_t head_dim, int64_t topk_slots, int64_t block_size,
                             double scale, const int32_t* cu_block_lens, int64_t total_blocks, const int32_t* row_ptr,
@@ -92,7 +93,7 @@ extern "C" int msa_attn_bwd(const void* q, const void* k, const void* v, int32_t
       return kErrInvalidArgument;
     return attn_bwd_kv(q, k, v, out, grad_out, row_state, indices, cu_seqlens, nseq, total_tokens, Hq, G, D, K, B,
                        static_cast<float>(scale), cu_block_lens, total_blocks, row_ptr, query_indices, slot_indices,
-                       grad_q, grad_k, grad_v, workspace, workspace_bytes, st);
+                       grad_q, grad_k, grad_v, workspace, workspace_bytes, out_f32, st);
   }
   if (need_kv && (!cu_block_lens || !row_ptr || (K > 0 && !query_indices))) return kErrInvalidArgument;
   // VALU path: the query pass (dQ and the row statistics), then the KV pass.

@@ -63,7 +63,7 @@ struct StatSmem {
   static constexpr int KS = lds_row_stride<DP>();
   alignas(16) uint16_t k[128 * KS];
   alignas(16) uint16_t v[128 * KS];
-  int32_t tok[kStatItemRows];
+  int32_t th[kStatItemRows];   // token * Hq + head of each (compacted) row
   int32_t rec[kStatItemRows];
   float lse2[kStatItemRows];
   float cen[kStatItemRows];
@@ -89,28 +89,50 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 
 }  // namespace
 
-// c = O . dO per (token, head) in FP64 (exact products of bf16 values); 32 lanes per row.
-__global__ __launch_bounds__(256) void kv_bwd_center(const uint16_t* __restrict__ out,
+// O . dO per (token, head) in FP64 (exact products); 32 lanes per row.
+// Rows that take the statistics pass (all rows without o32; with o32 those the
+// forward marked peaked, slot 1 < 0): c = O . dO of the rounded output, the
+// center that pass refines. Other rows (flat, with o32, the forward's FP32
+// output): delta = O . dO itself, kept as c = float(delta) plus the residual
+// delta - c (slots 2 and 3).
+__global__ __launch_bounds__(256) void kv_bwd_center(const uint16_t* __restrict__ out, const float* __restrict__ o32,
                                                      const uint16_t* __restrict__ dout, int64_t rows_th, int D,
                                                      double* __restrict__ row_state) {
   const int sub = threadIdx.x & 31;
   const int64_t th = static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
   if (th >= rows_th) return;
+  const bool flat = o32 && row_state[th * 4 + 1] > 0.0;  // uniform over the row's 32 lanes
   double acc = 0.0;
   for (int d0 = 4 * sub; d0 < D; d0 += 128) {
-    const uint2 o = *reinterpret_cast<const uint2*>(out + th * D + d0);
     const uint2 g = *reinterpret_cast<const uint2*>(dout + th * D + d0);
-    acc = fma(static_cast<double>(bf16_lo(o.x)), static_cast<double>(bf16_lo(g.x)), acc);
-    acc = fma(static_cast<double>(bf16_hi(o.x)), static_cast<double>(bf16_hi(g.x)), acc);
-    acc = fma(static_cast<double>(bf16_lo(o.y)), static_cast<double>(bf16_lo(g.y)), acc);
-    acc = fma(static_cast<double>(bf16_hi(o.y)), static_cast<double>(bf16_hi(g.y)), acc);
+    float o[4];
+    if (flat) {
+      const float4 x = *reinterpret_cast<const float4*>(o32 + th * D + d0);
+      o[0] = x.x, o[1] = x.y, o[2] = x.z, o[3] = x.w;
+    } else {
+      const uint2 x = *reinterpret_cast<const uint2*>(out + th * D + d0);
+      o[0] = bf16_lo(x.x), o[1] = bf16_hi(x.x), o[2] = bf16_lo(x.y), o[3] = bf16_hi(x.y);
+    }
+    acc = fma(static_cast<double>(o[0]), static_cast<double>(bf16_lo(g.x)), acc);
+    acc = fma(static_cast<double>(o[1]), static_cast<double>(bf16_hi(g.x)), acc);
+    acc = fma(static_cast<double>(o[2]), static_cast<double>(bf16_lo(g.y)), acc);
+    acc = fma(static_cast<double>(o[3]), static_cast<double>(bf16_hi(g.y)), acc);
   }
 #pragma unroll
   for (int o = 16; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 32);
-  if (sub == 0) row_state[th * 4 + 2] = acc;
+  if (sub == 0) {
+    if (flat) {
+      const double c = static_cast<double>(static_cast<float>(acc));
+      row_state[th * 4 + 2] = c;
+      row_state[th * 4 + 3] = acc - c;
+    } else {
+      row_state[th * 4 + 2] = acc;
+    }
+  }
 }
 
-// B1: per (edge, head) row and key block, sum_j p_j and sum_j p_j (dp_j - c).
+// B1: per (edge, head) row and key block, sum_j p_j and sum_j p_j (dp_j - c), for every
+// row (all_rows) or for the rows the forward marked peaked (row_state slot 1 < 0).
 // Structure of the forward partial kernel: K and V blocks row-major in LDS,
 // kStatWaves waves x 16 kStatRT rows per tile; S^T = K Q^T and dP^T = V dO^T (lane: row c, keys 4*q4 + i).
 template <int NK, bool FULLD>
@@ -119,7 +141,7 @@ __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
     const uint16_t* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx, const int32_t* __restrict__ sidx,
     const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items, const int2* __restrict__ items, int nseq,
-    int Hq, int G, int D, int K, int B, float scale2, int epi, int t0, float2* __restrict__ spart) {
+    int Hq, int G, int D, int K, int B, float scale2, int epi, int t0, int all_rows, float2* __restrict__ spart) {
   constexpr int DP = 32 * NK, KS = StatSmem<NK>::KS;
   __shared__ StatSmem<NK> sm;
   const int item = blockIdx.x;
@@ -132,6 +154,51 @@ __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
   const int e_end = e_begin + epi < e_hi[row] ? e_begin + epi : e_hi[row];
   const int nrows = (e_end - e_begin) * R;  // 1 <= nrows <= kStatItemRows
 
+  // The rows that take the pass, compacted in (edge, head) order (so still in token
+  // order); the per-wave counts borrow the K block's LDS before it is filled.
+  constexpr int MI = kStatItemRows / kStatThreads;
+  int32_t* wcnt = reinterpret_cast<int32_t*>(sm.k);
+  int nsel = 0;
+#pragma unroll
+  for (int j = 0; j < MI; ++j) {
+    const int rho = tid + kStatThreads * j;
+    bool take = false;
+    int th = 0, rec = 0;
+    float l2 = 0.f, ce = 0.f;
+    if (rho < nrows) {
+      const int eo = rho / R;
+      const int h = rg.g * R + (rho - eo * R);
+      const int tok = qidx[e_begin + eo];
+      th = tok * Hq + h;  // < 2^31: token-head products are checked on the host
+      const double* rs = row_state + static_cast<int64_t>(th) * 4;
+      const double2 lm = *reinterpret_cast<const double2*>(rs);
+      take = all_rows || lm.y < 0.0;
+      rec = ((tok - t0) * Hq + h) * K + sidx[e_begin + eo];
+      l2 = static_cast<float>(lm.x);
+      ce = static_cast<float>(rs[2]);
+    }
+    const uint64_t bal = __ballot(take);
+    if (lane == 0) wcnt[wid] = __popcll(bal);
+    __syncthreads();
+    int before = nsel, total = 0;
+#pragma unroll
+    for (int w = 0; w < kStatWaves; ++w) {
+      const int n = wcnt[w];
+      before += w < wid ? n : 0;
+      total += n;
+    }
+    if (take) {
+      const int pos = before + __popcll(bal & ((uint64_t(1) << lane) - 1));
+      sm.th[pos] = th;
+      sm.rec[pos] = rec;
+      sm.lse2[pos] = l2;
+      sm.cen[pos] = ce;
+    }
+    nsel += total;
+    __syncthreads();  // counts read before the K block overwrites them
+  }
+  if (nsel == 0) return;  // workgroup-uniform
+
   constexpr int KVI = 128 * (DP / 8) / kStatThreads;
   uint4 kw[KVI], vw[KVI];
 #pragma unroll
@@ -143,15 +210,6 @@ __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
     kw[i] = *reinterpret_cast<const uint4*>(k + off);
     vw[i] = *reinterpret_cast<const uint4*>(v + off);
   }
-  constexpr int MI = kStatItemRows / kStatThreads;
-  int32_t mtok[MI], mslot[MI];
-#pragma unroll
-  for (int j = 0; j < MI; ++j) {
-    const int rho = tid + kStatThreads * j;
-    const int eo = (rho < nrows ? rho : nrows - 1) / R;
-    mtok[j] = qidx[e_begin + eo];
-    mslot[j] = sidx[e_begin + eo];
-  }
 #pragma unroll
   for (int i = 0; i < KVI; ++i) {
     const int e = tid + kStatThreads * i;
@@ -160,34 +218,21 @@ __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
     *reinterpret_cast<uint4*>(sm.k + kl * KS + d0) = ok ? kw[i] : make_uint4(0u, 0u, 0u, 0u);
     *reinterpret_cast<uint4*>(sm.v + kl * KS + d0) = ok ? vw[i] : make_uint4(0u, 0u, 0u, 0u);
   }
-#pragma unroll
-  for (int j = 0; j < MI; ++j) {
-    const int rho = tid + kStatThreads * j;
-    if (rho < nrows) {
-      const int eo = rho / R;
-      const int h = rg.g * R + (rho - eo * R);
-      const int th = mtok[j] * Hq + h;
-      sm.tok[rho] = mtok[j];
-      sm.rec[rho] = ((mtok[j] - t0) * Hq + h) * K + mslot[j];
-      sm.lse2[rho] = static_cast<float>(row_state[static_cast<int64_t>(th) * 4]);
-      sm.cen[rho] = static_cast<float>(row_state[static_cast<int64_t>(th) * 4 + 2]);
-    }
-  }
   __syncthreads();
 
-  const int ntiles = (nrows + kStatRowsPerTile - 1) / kStatRowsPerTile;
+  const int ntiles = (nsel + kStatRowsPerTile - 1) / kStatRowsPerTile;
   for (int tile = 0; tile < ntiles; ++tile) {
     const int rbase = tile * kStatRowsPerTile + 16 * kStatRT * wid;
-    if (rbase >= nrows) break;  // wave-uniform
+    if (rbase >= nsel) break;  // wave-uniform
     bf16x8 qf[kStatRT][NK], gf[kStatRT][NK];
     int lim[kStatRT];
     float lse2[kStatRT], cen[kStatRT];
 #pragma unroll
     for (int rt = 0; rt < kStatRT; ++rt) {
       const int rho = rbase + 16 * rt + c;
-      const bool ok = rho < nrows;
-      const int64_t th = ok ? static_cast<int64_t>(sm.tok[rho]) * Hq + rg.g * R + rho % R : 0;
-      const int64_t vis = ok ? static_cast<int64_t>(sm.tok[rho]) - rg.kb + 1 : 0;
+      const bool ok = rho < nsel;
+      const int64_t th = ok ? sm.th[rho] : 0;
+      const int64_t vis = ok ? static_cast<int64_t>(sm.th[rho] / Hq) - rg.kb + 1 : 0;
       lim[rt] = vis < rg.nk ? static_cast<int>(vis) : rg.nk;
       lse2[rt] = ok ? sm.lse2[rho] : 0.f;
       cen[rt] = ok ? sm.cen[rho] : 0.f;
@@ -249,21 +294,25 @@ __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
       a += __shfl_xor(a, 32, kWave);
       b += __shfl_xor(b, 32, kWave);
       const int rho = rbase + 16 * rt + c;
-      if (q4 == 0 && rho < nrows) spart[sm.rec[rho]] = make_float2(a, b);
+      if (q4 == 0 && rho < nsel) spart[sm.rec[rho]] = make_float2(a, b);
     }
   }
 }
 
 // mass = sum_s A_s, delta = sum_s B_s / mass over the row's valid slots (FP64);
-// 32 lanes per (token, head), slots lane-parallel then a fixed shuffle tree.
+// 32 lanes per (token, head), slots lane-parallel then a fixed shuffle tree. Rows
+// outside the pass (flat rows, unless all_rows) keep the forward's mass. The mass
+// keeps the sign of the forward's mark, so a repeated backward selects the same rows.
 __global__ __launch_bounds__(256) void kv_bwd_stats_combine(const int32_t* __restrict__ indices,
                                                             const int32_t* __restrict__ cu, int nseq, int64_t t0,
-                                                            int64_t t1, int Hq, int G, int K, int B,
+                                                            int64_t t1, int Hq, int G, int K, int B, int all_rows,
                                                             const float2* __restrict__ spart,
                                                             double* __restrict__ row_state) {
   const int sub = threadIdx.x & 31;
   const int64_t th = t0 * Hq + static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
   if (th >= t1 * Hq) return;
+  const double mark = row_state[th * 4 + 1];
+  if (!all_rows && mark > 0.0) return;  // uniform over the row's 32 lanes
   const int64_t t = th / Hq;
   const int h = static_cast<int>(th % Hq);
   const int g = h / (Hq / G);
@@ -287,7 +336,7 @@ __global__ __launch_bounds__(256) void kv_bwd_stats_combine(const int32_t* __res
   }
   if (sub == 0) {
     const bool has = a > 0.0;
-    row_state[th * 4 + 1] = has ? a : 1.0;
+    row_state[th * 4 + 1] = copysign(has ? a : 1.0, mark);
     row_state[th * 4 + 3] = has ? b / a : 0.0;
   }
 }
@@ -432,7 +481,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       }                                                                                                     \
     }                                                                                                       \
     if (tid < 32) {                                                                                         \
-      sm.st[BUF][tid] = make_float4(static_cast<float>(pst.x), static_cast<float>(1.0 / pst.y),              \
+      sm.st[BUF][tid] = make_float4(static_cast<float>(pst.x), static_cast<float>(1.0 / fabs(pst.y)),        \
                                     static_cast<float>(pst.z), static_cast<float>(pst.w));                   \
       sm.vis[BUF][tid] = pvis;                                                                              \
       sm.rec[BUF][tid] = prec;                                                                              \
@@ -713,7 +762,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
                 const int32_t* indices, const int32_t* cu, int nseq, int64_t T, int Hq, int G, int D, int K, int B,
                 float scale, const int32_t* cu_blocks, int64_t total_blocks, const int32_t* row_ptr,
                 const int32_t* qidx, const int32_t* sidx, void* dq, void* dk, void* dv, void* ws, int64_t ws_bytes,
-                hipStream_t st) {
+                const float* o32, hipStream_t st) {
   const int64_t rows = total_blocks * G;
   const BwdLayout L = bwd_layout(T, Hq, G, D, K, total_blocks);
   if (ws_bytes < L.total) return kErrInvalidArgument;
@@ -737,7 +786,11 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   const int64_t nacc = T * G * D;
   const bool need_kv = dk != nullptr || dv != nullptr;
 
-  hipLaunchKernelGGL(kv_bwd_center, dim3(grid_1d(T * Hq, 8)), dim3(256), 0, st, ob, gb, T * Hq, D, rs);
+  // With the forward's FP32 output, flat rows take delta = O . dO and the forward's
+  // mass, and only the rows it marked peaked take the statistics pass; without it,
+  // every row does.
+  const int all_rows = o32 == nullptr;
+  hipLaunchKernelGGL(kv_bwd_center, dim3(grid_1d(T * Hq, 8)), dim3(256), 0, st, ob, o32, gb, T * Hq, D, rs);
   if (need_kv) hipLaunchKernelGGL(kv_bwd_zero, dim3(grid_1d(2 * nacc, 256)), dim3(256), 0, st, acc, 2 * nacc);
   kv_plan_launch(L.stat_plan, row_ptr, qidx, T, sbase, st);
   kv_plan_launch(L.main_plan, row_ptr, qidx, T, mbase, st);
@@ -752,14 +805,14 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       const int2* its = kv_plan_items(sp, sbase, c);
       const int sepi = static_cast<int>(sp.epi);
       const dim3 grid(static_cast<unsigned>(sp.max_items)), block(kStatThreads);
-#define MSA_BWD_STATS(NKV, FD) hipLaunchKernelGGL((kv_bwd_stats_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, sepi, it0, spart)
+#define MSA_BWD_STATS(NKV, FD) hipLaunchKernelGGL((kv_bwd_stats_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, sepi, it0, all_rows, spart)
       if (nk == 1) { if (fd) MSA_BWD_STATS(1, true); else MSA_BWD_STATS(1, false); }
       else if (nk == 2) { if (fd) MSA_BWD_STATS(2, true); else MSA_BWD_STATS(2, false); }
       else { if (fd) MSA_BWD_STATS(4, true); else MSA_BWD_STATS(4, false); }
 #undef MSA_BWD_STATS
     }
     hipLaunchKernelGGL(kv_bwd_stats_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu, nseq,
-                       t0, t1, Hq, G, K, B, spart, rs);
+                       t0, t1, Hq, G, K, B, all_rows, spart, rs);
     if (rows > 0) {
       const int32_t* hi = kv_plan_hi(mp, mbase, c);
       const int32_t* nit = kv_plan_count(mp, mbase, c);

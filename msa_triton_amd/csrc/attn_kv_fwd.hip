@@ -316,13 +316,20 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
 // all of their partial loads issued before any arithmetic (records are in bounds
 // for every slot, valid or not; invalid slots are masked, never multiplied).
 constexpr int kCombineBatch = 8;
+// A row is flat when sum_j 2^(x_j - max x) >= kFlatRowMass, i.e. no key has probability
+// above 5 %; then sum_j p_j^2 <= 0.05 and the delta = O . dO shortcut's extra dQ / dK
+// error term (~ sqrt(sum p^2) times the statistics pass's error) stays below ~22 % of
+// it, ~2.5 % in quadrature. Measured: the same count of one-ulp bf16 flips against the
+// FP64 oracle as the statistics pass for every row, at logit scales 0.3x to 16x.
+constexpr double kFlatRowMass = 20.0;
 
 __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restrict__ indices,
                                                         const int32_t* __restrict__ cu, int nseq, int64_t t0,
                                                         int64_t t1, int Hq, int G, int D, int K, int B,
                                                         const float* __restrict__ opart,
                                                         const float2* __restrict__ mlpart, uint16_t* __restrict__ out,
-                                                        float* __restrict__ lse, double* __restrict__ row_state) {
+                                                        float* __restrict__ lse, double* __restrict__ row_state,
+                                                        float* __restrict__ o32) {
   const int sub = threadIdx.x & 31;
   const int64_t th = t0 * Hq + static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
   if (th >= t1 * Hq) return;  // whole 32-lane segments exit together
@@ -397,21 +404,31 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
   for (int o = 16; o > 0; o >>= 1) L += __shfl_xor(L, o, 32);
   const bool has = L > 0.0;
   if (has_dims) {
-    uint32_t w2[2];
+    float r[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t a = f32_to_bf16_bits(has ? static_cast<float>(acc[2 * i] / L) : 0.f);
-      const uint32_t b = f32_to_bf16_bits(has ? static_cast<float>(acc[2 * i + 1] / L) : 0.f);
-      w2[i] = a | (b << 16);
-    }
-    *reinterpret_cast<uint2*>(out + th * D + 4 * sub) = make_uint2(w2[0], w2[1]);
+    for (int i = 0; i < 4; ++i) r[i] = has ? static_cast<float>(acc[i] / L) : 0.f;
+    const uint32_t w0 = f32_to_bf16_bits(r[0]) | (f32_to_bf16_bits(r[1]) << 16);
+    const uint32_t w1 = f32_to_bf16_bits(r[2]) | (f32_to_bf16_bits(r[3]) << 16);
+    *reinterpret_cast<uint2*>(out + th * D + 4 * sub) = make_uint2(w0, w1);
+    if (o32) *reinterpret_cast<float4*>(o32 + th * D + 4 * sub) = make_float4(r[0], r[1], r[2], r[3]);
   }
   if (sub == 0) {
     // row_state keeps the base-2 lse (the backward's p = 2^(x - lse2) is then exactly
     // 1 for a row whose only visible key attains it); the public lse is natural.
     const double lse2 = has ? static_cast<double>(M) + log2(L) : -__builtin_inf();
     lse[th] = static_cast<float>(lse2 * kLn2);
-    if (row_state) row_state[th * 4] = lse2;
+    if (row_state) {
+      // slot 1: the mass sum_j 2^(x_j - float(lse2)) in closed form, 2^(lse2 - float(lse2)),
+      // so that the backward's p = 2^(x - float(lse2)) / mass is normalised exactly; its
+      // sign marks the row: negative when its largest probability 1 / L exceeds
+      // 1 / kFlatRowMass (peaked). The backward takes delta = O . dO (FP32 output) for the
+      // positive (flat) rows; the peaked ones take the reference's centred statistics
+      // pass, whose delta shares the rounding of the dP values of dS (the error of the
+      // dominant key's dP then cancels in dS).
+      row_state[th * 4] = lse2;
+      const double mass = has ? exp2(lse2 - static_cast<double>(static_cast<float>(lse2))) : 1.0;
+      row_state[th * 4 + 1] = has && L < kFlatRowMass ? -mass : mass;
+    }
   }
 }
 
@@ -487,7 +504,7 @@ int64_t attn_fwd_kv_workspace_bytes(int64_t T, int64_t Hq, int64_t G, int64_t D,
 int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indices, const int32_t* cu, int nseq,
                 int64_t T, int Hq, int G, int D, int K, int B, float scale, const int32_t* cu_blocks,
                 int64_t total_blocks, const int32_t* row_ptr, const int32_t* qidx, const int32_t* sidx, void* ws,
-                int64_t ws_bytes, void* out, float* lse, double* rs, hipStream_t st) {
+                int64_t ws_bytes, void* out, float* lse, double* rs, float* o32, hipStream_t st) {
   const int64_t rows = total_blocks * G;
   const FwdLayout f = fwd_layout(T, Hq, G, D, K, total_blocks);
   if (ws_bytes < f.total) return kErrInvalidArgument;
@@ -522,7 +539,7 @@ int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indi
 #undef MSA_FWD_PARTIAL
     }
     hipLaunchKernelGGL(attn_fwd_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu, nseq, t0, t1,
-                       Hq, G, D, K, B, opart, ml, ob, lse, rs);
+                       Hq, G, D, K, B, opart, ml, ob, lse, rs, o32);
   }
   return status_from(hipGetLastError());
 }

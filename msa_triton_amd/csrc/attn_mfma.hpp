@@ -17,11 +17,11 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
                 const int32_t* indices, const int32_t* cu, int nseq, int64_t T, int Hq, int G, int D, int K, int B,
                 float scale, const int32_t* cu_blocks, int64_t total_blocks, const int32_t* row_ptr,
                 const int32_t* qidx, const int32_t* sidx, void* dq, void* dk, void* dv, void* ws, int64_t ws_bytes,
-                hipStream_t st);
+                const float* o32, hipStream_t st);
 
 int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indices, const int32_t* cu, int nseq,
                 int64_t T, int Hq, int G, int D, int K, int B, float scale, const int32_t* cu_blocks,
                 int64_t total_blocks, const int32_t* row_ptr, const int32_t* qidx, const int32_t* sidx, void* ws,
-                int64_t ws_bytes, void* out, float* lse, double* rs, hipStream_t st);
+                int64_t ws_bytes, void* out, float* lse, double* rs, float* o32, hipStream_t st);
 
 }  // namespace msa

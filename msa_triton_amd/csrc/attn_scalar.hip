@@ -43,7 +43,7 @@ __global__ __launch_bounds__(256) void attn_fwd_valu(const void* __restrict__ q,
                                                      const int32_t* __restrict__ cu, int nseq, int64_t T,
                                                      int Hq, int G, int D, int K, int B, double scale,
                                                      void* __restrict__ out, float* __restrict__ lse,
-                                                     double* __restrict__ row_state) {
+                                                     double* __restrict__ row_state, float* __restrict__ o32) {
   extern __shared__ float smem[];
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t th = static_cast<int64_t>(blockIdx.x) * 4 + wid;
@@ -99,12 +99,19 @@ __global__ __launch_bounds__(256) void attn_fwd_valu(const void* __restrict__ q,
 #pragma unroll
   for (int j = 0; j < DPL; ++j) {
     const int d = lane + j * kWave;
-    if (d < D) store_from_f32<DT>(out, th * D + d, l > 0.0 ? static_cast<float>(o[j] / l) : 0.f);
+    if (d < D) {
+      const float r = l > 0.0 ? static_cast<float>(o[j] / l) : 0.f;
+      store_from_f32<DT>(out, th * D + d, r);
+      if (o32) o32[th * D + d] = r;
+    }
   }
   if (lane == 0) {
     const double full = l > 0.0 ? m + log(l) : -__builtin_inf();
     lse[th] = static_cast<float>(full);
-    if (row_state) row_state[th * 4] = full;
+    if (row_state) {
+      row_state[th * 4] = full;
+      row_state[th * 4 + 1] = 1.0;  // FP64 lse: p = exp(x - lse) needs no mass correction
+    }
   }
 }
 
@@ -271,9 +278,9 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_valu(
 template <int DT, int DPL>
 int attn_valu_launch_fwd(const void* q, const void* k, const void* v, const int32_t* idx, const int32_t* cu,
                          int nseq, int64_t T, int Hq, int G, int D, int K, int B, double scale, void* out,
-                         float* lse, double* rs, hipStream_t st) {
+                         float* lse, double* rs, float* o32, hipStream_t st) {
   hipLaunchKernelGGL((attn_fwd_valu<DT, DPL>), dim3(grid_1d(T * Hq, 4)), dim3(256), 4 * D * sizeof(float), st, q,
-                     k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse, rs);
+                     k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse, rs, o32);
   return status_from(hipGetLastError());
 }
 
@@ -305,9 +312,9 @@ int attn_valu_launch_dkdv(const void* q, const void* k, const void* v, const voi
 template <int DT>
 int attn_fwd_valu_dispatch(const void* q, const void* k, const void* v, const int32_t* idx, const int32_t* cu,
                            int nseq, int64_t T, int Hq, int G, int D, int K, int B, double scale, void* out,
-                           float* lse, double* rs, hipStream_t st) {
+                           float* lse, double* rs, float* o32, hipStream_t st) {
   return MSA_DPL_DISPATCH(D, attn_valu_launch_fwd, q, k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse, rs,
-                          st);
+                          o32, st);
 }
 
 template <int DT>
@@ -329,7 +336,7 @@ int attn_dkdv_valu_dispatch(const void* q, const void* k, const void* v, const v
 
 #define MSA_INSTANTIATE_VALU(DT)                                                                                    \
   template int attn_fwd_valu_dispatch<DT>(const void*, const void*, const void*, const int32_t*, const int32_t*, int, \
-                                          int64_t, int, int, int, int, int, double, void*, float*, double*,          \
+                                          int64_t, int, int, int, int, int, double, void*, float*, double*, float*,  \
                                           hipStream_t);                                                              \
   template int attn_dq_valu_dispatch<DT>(const void*, const void*, const void*, const void*, const void*, double*,   \
                                          const int32_t*, const int32_t*, int, int64_t, int, int, int, int, int,      \

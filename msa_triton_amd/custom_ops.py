@@ -12,9 +12,10 @@ graph breaks and AOTAutograd differentiates it:
     msa_mi355x::index_score_backward(index_q, index_k, cu_seqlens, tie, grad_scores, max_seqlen,
                                      block_size, scale, need_q, need_k) -> (dq, dk)
     msa_mi355x::topk(scores, cu_seqlens, block_size, topk_blocks, local_blocks) -> indices
-    msa_mi355x::sparse_attention(q, k, v, indices, cu_seqlens, max_seqlen, block_size, scale)
-        -> (out, lse, row_state)   row_state: the fp64 per-row state the backward reads
-    msa_mi355x::sparse_attention_backward(q, k, v, indices, cu_seqlens, out, row_state, grad_out,
+    msa_mi355x::sparse_attention(q, k, v, indices, cu_seqlens, max_seqlen, block_size, scale, save_state)
+        -> (out, lse, row_state, out_f32)   row_state: the fp64 per-row state the backward reads;
+                                            out_f32: the fp32 output, or an empty tensor when not saved
+    msa_mi355x::sparse_attention_backward(q, k, v, indices, cu_seqlens, out, row_state, out_f32, grad_out,
                                           block_size, scale, need_q, need_k, need_v) -> (dq, dk, dv)
 
 A gradient that is not needed comes back as an empty tensor. ``m3_index_score``,
@@ -135,59 +136,63 @@ def _(scores, cu_seqlens, block_size, topk_blocks, local_blocks):
 
 @torch.library.custom_op(f"{_NS}::sparse_attention", mutates_args=())
 def _sparse_attention(q: Tensor, k: Tensor, v: Tensor, indices: Tensor, cu_seqlens: Tensor, max_seqlen: int,
-                      block_size: int, scale: float) -> tuple[Tensor, Tensor, Tensor]:
+                      block_size: int, scale: float, save_state: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     _lib.require_gpu(q, "m3_sparse_attention")
     cu = cu_seqlens.contiguous()
     meta = _attention_meta(cu, q.shape[0], max_seqlen, block_size)
-    out, lse, row_state, _ = _attn_forward(q.contiguous(), k.contiguous(), v.contiguous(), indices.contiguous(),
-                                           cu, meta, block_size, scale, None)
-    row_state[..., 1:].zero_()  # only the lse entry is forward state; the rest is the backward's scratch
-    return out, lse, row_state
+    out, lse, row_state, out_f32, _ = _attn_forward(q.contiguous(), k.contiguous(), v.contiguous(),
+                                                    indices.contiguous(), cu, meta, block_size, scale, None,
+                                                    save_f32=save_state)
+    row_state[..., 2:].zero_()  # lse and mass are forward state; the rest is the backward's scratch
+    return out, lse, row_state, (out_f32 if out_f32 is not None else q.new_empty(0, dtype=torch.float32))
 
 
 @_sparse_attention.register_fake
-def _(q, k, v, indices, cu_seqlens, max_seqlen, block_size, scale):
-    total, heads, _ = q.shape
+def _(q, k, v, indices, cu_seqlens, max_seqlen, block_size, scale, save_state):
+    total, heads, dim = q.shape
     return (q.new_empty(q.shape), q.new_empty((total, heads), dtype=torch.float32),
-            q.new_empty((total, heads, 4), dtype=torch.float64))
+            q.new_empty((total, heads, 4), dtype=torch.float64),
+            q.new_empty((total, heads, dim) if save_state else (0,), dtype=torch.float32))
 
 
 @torch.library.custom_op(f"{_NS}::sparse_attention_backward", mutates_args=())
 def _sparse_attention_backward(q: Tensor, k: Tensor, v: Tensor, indices: Tensor, cu_seqlens: Tensor, out: Tensor,
-                               row_state: Tensor, grad_out: Tensor, block_size: int, scale: float, need_q: bool,
-                               need_k: bool, need_v: bool) -> tuple[Tensor, Tensor, Tensor]:
+                               row_state: Tensor, out_f32: Tensor, grad_out: Tensor, block_size: int, scale: float,
+                               need_q: bool, need_k: bool, need_v: bool) -> tuple[Tensor, Tensor, Tensor]:
     cu = cu_seqlens.contiguous()
     meta = _attention_meta(cu, q.shape[0], max(1, q.shape[0]), block_size)
     # the backward writes its center into the row state: work on a copy (inputs are not mutated)
     dq, dk, dv = _attn_backward(q.contiguous(), k.contiguous(), v.contiguous(), indices.contiguous(), cu,
                                 out.contiguous(), row_state.clone(), grad_out, meta, block_size, scale, None,
-                                need_q, need_k, need_v)
+                                need_q, need_k, need_v,
+                                out_f32=out_f32.contiguous() if out_f32.numel() else None)
     empty = q.new_empty(0)
     return (dq if dq is not None else empty, dk if dk is not None else empty, dv if dv is not None else empty)
 
 
 @_sparse_attention_backward.register_fake
-def _(q, k, v, indices, cu_seqlens, out, row_state, grad_out, block_size, scale, need_q, need_k, need_v):
+def _(q, k, v, indices, cu_seqlens, out, row_state, out_f32, grad_out, block_size, scale, need_q, need_k, need_v):
     return (q.new_empty(q.shape if need_q else (0,)), k.new_empty(k.shape if need_k else (0,)),
             v.new_empty(v.shape if need_v else (0,)))
 
 
 def _attention_setup(ctx, inputs, output):
-    q, k, v, indices, cu_seqlens, max_seqlen, block_size, scale = inputs
-    out, lse, row_state = output
-    ctx.save_for_backward(q, k, v, indices, cu_seqlens, out, row_state)
+    q, k, v, indices, cu_seqlens, max_seqlen, block_size, scale, save_state = inputs
+    out, lse, row_state, out_f32 = output
+    ctx.save_for_backward(q, k, v, indices, cu_seqlens, out, row_state, out_f32)
     ctx.args = (block_size, scale)
-    ctx.mark_non_differentiable(lse, row_state)
+    ctx.mark_non_differentiable(lse, row_state, out_f32)
 
 
-def _attention_grad(ctx, grad_out, grad_lse, grad_row_state):
-    q, k, v, indices, cu_seqlens, out, row_state = ctx.saved_tensors
+def _attention_grad(ctx, grad_out, grad_lse, grad_row_state, grad_out_f32):
+    q, k, v, indices, cu_seqlens, out, row_state, out_f32 = ctx.saved_tensors
     need = [bool(x) for x in ctx.needs_input_grad[:3]]
     if grad_out is None:
         grad_out = torch.zeros_like(out)
     dq, dk, dv = torch.ops.msa_mi355x.sparse_attention_backward(q, k, v, indices, cu_seqlens, out, row_state,
-                                                                grad_out, *ctx.args, *need)
-    return (dq if need[0] else None, dk if need[1] else None, dv if need[2] else None, None, None, None, None, None)
+                                                                out_f32, grad_out, *ctx.args, *need)
+    return (dq if need[0] else None, dk if need[1] else None, dv if need[2] else None, None, None, None, None, None,
+            None)
 
 
 torch.library.register_autograd(f"{_NS}::sparse_attention", _attention_grad, setup_context=_attention_setup)
@@ -258,6 +263,7 @@ def m3_sparse_attention(q, k, v, indices, cu_seqlens, max_seqlen, *, block_size=
     effective_scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
     if not math.isfinite(effective_scale):
         raise ValueError("scale must be finite.")
-    out, lse, _ = torch.ops.msa_mi355x.sparse_attention(q, k, v, indices, cu_seqlens, max_seqlen, block_size,
-                                                        effective_scale)
+    save_state = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
+    out, lse, _, _ = torch.ops.msa_mi355x.sparse_attention(q, k, v, indices, cu_seqlens, max_seqlen, block_size,
+                                                           effective_scale, save_state)
     return (out, lse) if return_lse else out

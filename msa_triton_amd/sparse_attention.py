@@ -12,8 +12,11 @@ owned per key block, no floating-point atomics); the forward builds the CSR
 itself and keeps it for a backward that needs only dQ. ``cu_seqlens`` may be a
 ``PackedSequences`` (``prepare_sequences``): then neither pass reads metadata
 back from the device. Saved state is q, k, v,
-out in the input dtype plus an fp64 [T,Hq,4] per-row state (full-precision
-lse, then the backward's mass / center / delta); no fp32 staging copies.
+out in the input dtype, an fp64 [T,Hq,4] per-row state (full-precision lse
+and its normalisation, then the backward's center / delta) and the output in
+fp32, from which the backward takes delta = O . dO directly instead of
+recomputing the softmax statistics over every selected block (the reference's
+centred recomputation, :119-158, remains the C path without the fp32 output).
 """
 
 from __future__ import annotations
@@ -27,15 +30,17 @@ from . import k2q as _k2q
 from .layout import PackedSequences, prepared_for, sequence_lengths, sequence_meta
 
 
-def _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs, public_csr=False):
-    """Forward launch on contiguous inputs: (out, lse, row_state, csr or None). With
-    ``public_csr`` the KV-major path builds its CSR through the public builder."""
+def _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs, public_csr=False, save_f32=False):
+    """Forward launch on contiguous inputs: (out, lse, row_state, out_f32 or None,
+    csr or None). With ``public_csr`` the KV-major path builds its CSR through the
+    public builder; with ``save_f32`` it also returns the fp32 output for the backward."""
     total, heads, dim = q.shape
     groups = k.shape[1]
     out = torch.empty_like(q)
     lse = torch.empty((total, heads), device=q.device, dtype=torch.float32)
     # Private fp64 per-row state shared by forward and backward: lse, mass, center, delta.
     row_state = torch.empty((total, heads, 4), device=q.device, dtype=torch.float64)
+    out_f32 = torch.empty((total, heads, dim), device=q.device, dtype=torch.float32) if save_f32 else None
     csr = None
     if total:
         lib = _lib.lib()
@@ -59,16 +64,17 @@ def _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs, public_cs
                 _lib.ptr(None if csr is None else csr.row_ptr),
                 _lib.ptr(None if csr is None else csr.query_indices),
                 _lib.ptr(None if csr is None else csr.slot_indices), _lib.ptr(workspace), ws_bytes,
-                out.data_ptr(), lse.data_ptr(), row_state.data_ptr(), _lib.stream_of(q.device),
+                out.data_ptr(), lse.data_ptr(), row_state.data_ptr(), _lib.ptr(out_f32), _lib.stream_of(q.device),
             )
         _lib.check(status, "msa_attn_fwd")
-    return out, lse, row_state, csr
+    return out, lse, row_state, out_f32, csr
 
 
 def _attn_backward(q, k, v, indices, cu, out, row_state, grad_output, meta, block_size, scale, seqs,
-                   need_q, need_k, need_v, csr=None):
+                   need_q, need_k, need_v, csr=None, out_f32=None):
     """Backward launch: (dq, dk, dv), None where not needed. ``row_state`` gets the
-    backward's center. ``csr`` (the forward's) is reused when given; otherwise a
+    backward's center; ``out_f32`` is the forward's fp32 output (None: the backward
+    recomputes the statistics). ``csr`` (the forward's) is reused when given; otherwise a
     backward that needs dK or dV builds it through the public builder (as the
     reference does) and a dQ-only one privately."""
     need_kv = need_k or need_v
@@ -98,7 +104,8 @@ def _attn_backward(q, k, v, indices, cu, out, row_state, grad_output, meta, bloc
         with torch.cuda.device(device):
             status = lib.msa_attn_bwd(
                 q.data_ptr(), k.data_ptr(), v.data_ptr(), dtype, out.data_ptr(), dout.data_ptr(),
-                row_state.data_ptr(), indices.data_ptr(), cu.data_ptr(), meta.num_seqs, total, heads, groups,
+                row_state.data_ptr(), _lib.ptr(out_f32), indices.data_ptr(), cu.data_ptr(), meta.num_seqs, total,
+                heads, groups,
                 dim, slots, block_size, scale,
                 _lib.ptr(None if csr is None else csr.cu_block_lens), meta.total_blocks,
                 _lib.ptr(None if csr is None else csr.row_ptr),
@@ -120,9 +127,10 @@ class _SparseAttention(torch.autograd.Function):
         # built through the public builder (the one build the reference makes, in its
         # backward) and the backward reuses it; a dQ-only backward reuses a private one.
         need_kv = ctx.needs_input_grad[1] or ctx.needs_input_grad[2]
-        out, lse, row_state, csr = _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs,
-                                                 public_csr=need_kv)
-        ctx.save_for_backward(q, k, v, indices, cu, out, row_state)
+        need_any = need_kv or ctx.needs_input_grad[0]
+        out, lse, row_state, out_f32, csr = _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs,
+                                                          public_csr=need_kv, save_f32=need_any)
+        ctx.save_for_backward(q, k, v, indices, cu, out, row_state, out_f32)
         ctx.csr = csr
         ctx.meta = meta
         ctx.seqs = seqs
@@ -133,10 +141,10 @@ class _SparseAttention(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_output, grad_lse):
-        q, k, v, indices, cu, out, row_state = ctx.saved_tensors
+        q, k, v, indices, cu, out, row_state, out_f32 = ctx.saved_tensors
         need_q, need_k, need_v = ctx.needs_input_grad[:3]
         dq, dk, dv = _attn_backward(q, k, v, indices, cu, out, row_state, grad_output, ctx.meta, ctx.block_size,
-                                    ctx.scale, ctx.seqs, need_q, need_k, need_v, ctx.csr)
+                                    ctx.scale, ctx.seqs, need_q, need_k, need_v, ctx.csr, out_f32)
         ctx.csr = None
         return dq, dk, dv, None, None, None, None, None, None
 

@@ -32,10 +32,12 @@ def test_fake_kernels_shapes_and_dtypes():
         assert ids.shape == (37, 3, 5) and ids.dtype == torch.int32
         q = torch.empty(37, 6, 32, dtype=torch.bfloat16, device="cuda")
         kv = torch.empty(37, 3, 32, dtype=torch.bfloat16, device="cuda")
-        out, lse, rs = torch.ops.msa_mi355x.sparse_attention(q, kv, kv, ids, cu, 30, 8, 0.25)
+        out, lse, rs, o32 = torch.ops.msa_mi355x.sparse_attention(q, kv, kv, ids, cu, 30, 8, 0.25, True)
         assert out.shape == q.shape and out.dtype == q.dtype
         assert lse.shape == (37, 6) and lse.dtype == torch.float32 and rs.shape == (37, 6, 4) and rs.dtype == torch.float64
-        dq, dk, dv = torch.ops.msa_mi355x.sparse_attention_backward(q, kv, kv, ids, cu, out, rs, out, 8, 0.25,
+        assert o32.shape == q.shape and o32.dtype == torch.float32
+        assert torch.ops.msa_mi355x.sparse_attention(q, kv, kv, ids, cu, 30, 8, 0.25, False)[3].shape == (0,)
+        dq, dk, dv = torch.ops.msa_mi355x.sparse_attention_backward(q, kv, kv, ids, cu, out, rs, o32, out, 8, 0.25,
                                                                     False, True, True)
         assert dq.shape == (0,) and dk.shape == kv.shape and dv.shape == kv.shape
 

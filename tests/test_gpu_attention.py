@@ -18,7 +18,7 @@ import torch
 
 import msa_triton_amd as msa
 from oracle import msa_oracle as O
-from tests.helpers import attention_inputs, np64
+from tests.helpers import attention_inputs, check_bf16_stated, np64
 
 pytestmark = pytest.mark.gpu
 
@@ -249,3 +249,48 @@ def test_dtype_and_gqa16_forward_backward_against_fp64(dtype, device):
     actual.backward(grad.to(device))
     for tensor, ref in zip(tensors, (dq, dk, dv)):
         _close(tensor.grad, ref, dtype)
+
+
+@pytest.mark.parametrize("lengths,groups,ratio,dimension,block_size,topk,scale,stated", [
+    ([5, 1, 9], 2, 4, 32, 4, 4, None, False),
+    ([300, 45], 2, 4, 64, 16, 5, 0.02, True),
+    ([127, 128, 257], 1, 8, 128, 128, 3, 0.02, True),
+    ([127, 128, 257], 1, 8, 128, 128, 3, 0.5, True),
+])
+def test_backward_with_and_without_fp32_output(lengths, groups, ratio, dimension, block_size, topk, scale, stated,
+                                               device):
+    """The C-ABI backward both ways, each against the FP64 oracle: with the forward's
+    fp32 output (flat rows take delta = O . dO, rows the forward marked peaked take
+    the statistics pass; the autograd function's path) and without it (the
+    reference's centred statistics pass for every row). With the small scale about
+    a quarter to a half of the rows are flat (rows with few visible keys stay
+    peaked); the large scale peaks them all. These use the stated tolerance; the
+    small case meets the reference's gate."""
+    from msa_triton_amd.layout import sequence_meta
+    from msa_triton_amd.sparse_attention import _attn_backward, _attn_forward
+
+    cpu, indices, cu = attention_inputs(lengths, groups, ratio, dimension, block_size, topk)
+    grad = torch.randn(cpu[0].shape, generator=torch.Generator().manual_seed(4321)).bfloat16()
+    out_ref, _, dq, dk, dv = _oracle(cpu, indices, cu, block_size, scale, grad)
+    q, k, v = (x.to(device).contiguous() for x in cpu)
+    ids, cu_d = indices.to(device), cu.to(device)
+    meta = sequence_meta(cu.tolist(), block_size)
+    sc = dimension ** -0.5 if scale is None else scale
+    out, _, row_state, out_f32, _ = _attn_forward(q, k, v, ids, cu_d, meta, block_size, sc, None, save_f32=True)
+    torch.testing.assert_close(out_f32.to(torch.bfloat16), out, atol=0, rtol=0)
+    peaked = row_state[..., 1] < 0
+    assert bool(peaked.any())
+    if scale is not None and scale < 0.1:
+        assert not bool(peaked.all())
+    runs = {}
+    for name, saved in (("fp32", out_f32), ("stats", None)):
+        grads = _attn_backward(q, k, v, ids, cu_d, out, row_state.clone(), grad.to(device), meta, block_size, sc,
+                               None, True, True, True, out_f32=saved)
+        runs[name] = grads
+        for actual, ref, what in zip(grads, (dq, dk, dv), ("dq", "dk", "dv")):
+            if stated:
+                check_bf16_stated(actual, ref, f"{name} {what}")
+            else:
+                _close(actual, ref)
+    # rows that take the statistics pass either way get the same dQ bit for bit
+    torch.testing.assert_close(runs["fp32"][0][peaked], runs["stats"][0][peaked], atol=0, rtol=0)

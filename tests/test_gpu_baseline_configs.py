@@ -33,6 +33,7 @@ import bench
 import msa_triton_amd as msa
 from msa_triton_amd.k2q import build_k2q_csr
 from oracle import msa_oracle as O
+from tests.helpers import check_bf16_stated as _check_bf16
 
 pytestmark = [pytest.mark.gpu, pytest.mark.timeout(600)]  # c5 oracle work takes ~1 min on the host
 
@@ -68,22 +69,6 @@ def _sample_keys(lengths, block, name):
     if name in ("c1", "c2", "c3"):
         keys.update({a, a + block // 2, a + n // 2})
     return np.array(sorted(keys), dtype=np.int64)
-
-
-def _check_bf16(actual, expected, what):
-    act = actual.detach().float().cpu().numpy().astype(np.float64).ravel()
-    exp = np.asarray(expected, dtype=np.float64).ravel()
-    ref_r = torch.from_numpy(exp).to(torch.bfloat16).double().numpy()
-    gate = np.abs(act - ref_r) <= 1e-4 + 1e-4 * np.abs(ref_r)
-    bad = int((~gate).sum())
-    err = np.abs(act - exp)
-    bound = 1e-4 + 2.0 ** -8 * np.abs(exp)
-    worst = np.argsort(-(err / bound))[:5]
-    detail = ", ".join(f"(got {act[i]:.6g}, fp64 {exp[i]:.6g})" for i in worst)
-    print(f"{what}: {bad} of {gate.size} outside the 1e-4 gate; worst err/bound {float((err / bound).max()):.3f}: "
-          f"{detail}", flush=True)
-    assert bad <= max(1, gate.size // 1000), f"{what}: {bad} of {gate.size} elements outside the gate; {detail}"
-    assert np.all(err <= bound), f"{what}: error above 1e-4 + 2^-8 |x|; {detail}"
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])

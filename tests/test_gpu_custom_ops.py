@@ -33,7 +33,7 @@ def test_opcheck_each_op(device):
     torch.library.opcheck(torch.ops.msa_mi355x.topk.default, (scores, cu, block, 3, 1))
     ids = msa.m3_topk(scores, cu, block_size=block, topk_blocks=3, local_blocks=1)
     q, k, v = (x.clone().requires_grad_() for x in (q, k, v))
-    torch.library.opcheck(torch.ops.msa_mi355x.sparse_attention.default, (q, k, v, ids, cu, maxlen, block, 0.125))
+    torch.library.opcheck(torch.ops.msa_mi355x.sparse_attention.default, (q, k, v, ids, cu, maxlen, block, 0.125, True))
 
 
 def _forward(ops, iq, ik, q, k, v, g, cu, maxlen, block, topk):
