@@ -18,6 +18,11 @@ Functions and the reference code they restate:
                        for parity at sizes where the dense form does not fit.
   index_score_rows / topk_rows   index_score / topk for a subset of query
                        rows (pinned against the full restatements).
+  indexer_kl (+ _rows, _key_rows)   the indexer KL branch, not implemented
+                       upstream: restated from docs/msa_training_flow.md:92-138
+                       and docs/implementation_plan.md:66-69 (pinned by closed
+                       forms, finite differences and torch float64 autograd of an
+                       independent dense formulation, tests/test_oracle_kl.py).
 
 Pinning (see tests/test_oracle_*.py): every function is checked against the
 reference's known-answer cases (tests/test_eager.py:143-170,
@@ -387,3 +392,120 @@ def attention_kv_rows(q, k, v, indices, cu, dout, keys, *, block_size=128, scale
                 dk[i, g] += scale * (p * (dp - delta_t[hs])) @ q[t, hs]
                 dv[i, g] += p @ do[t, hs]
     return dk, dv
+
+
+# ---------------------------------------------------------------------------- indexer KL
+#
+# Not implemented upstream. The definition restated here is the reference's
+# training-flow description (docs/msa_training_flow.md:92-138, docs/implementation_plan.md:66-69):
+# over the causal tokens of each (token, group)'s selected blocks, the student is
+# softmax of the index token logits z_j = index_scale * iq[t,g] . ik[j] (token
+# logits, not block maxima, and no local +inf boost), the teacher is the mean over
+# the group's query heads of softmax(a_hj), a_hj = scale * q[t,h] . k[j,g] (the
+# main attention's probabilities, detached), and the loss is
+# KL(teacher || student) = sum_j T_j (log T_j - log S_j), averaged over all
+# (token, group) pairs (a pair without visible keys contributes 0). Only index_q
+# and index_k receive gradients: dLoss/dz_j = (S_j - T_j) / (T * G).
+
+
+def _kl_row(iq_row, ik_keys, q_rows, k_keys, index_scale, scale):
+    """(KL, dz [n]) of one (token, group) over its visible keys, in float64."""
+    z = index_scale * (ik_keys @ iq_row)
+    zs = z - z.max()
+    log_s = zs - np.log(np.exp(zs).sum())
+    a = scale * (q_rows @ k_keys.T)  # [R, n]
+    a = a - a.max(-1, keepdims=True)
+    p = np.exp(a)
+    p /= p.sum(-1, keepdims=True)
+    t = p.mean(0)
+    with np.errstate(divide="ignore"):
+        log_t = np.where(t > 0, np.log(np.where(t > 0, t, 1.0)), 0.0)
+    kl = float(np.sum(np.where(t > 0, t * (log_t - log_s), 0.0)))
+    return kl, np.exp(log_s) - t
+
+
+def indexer_kl(iq, ik, q, k, indices, cu, *, block_size=128, index_scale=1.0, scale=None):
+    """Loss, per-row KL [T,G] and the loss gradients d_iq [T,G,Di], d_ik [T,1,Di]."""
+    iq = np.asarray(iq, dtype=np.float64)
+    ik = np.asarray(ik, dtype=np.float64)
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    ids = np.asarray(indices)
+    total, groups, _ = iq.shape
+    ratio = q.shape[1] // groups
+    scale = q.shape[2] ** -0.5 if scale is None else float(scale)
+    _, start = _token_positions(bounds_of(cu))
+    row_kl = np.zeros((total, groups))
+    d_iq = np.zeros_like(iq)
+    d_ik = np.zeros_like(ik)
+    rows = max(total * groups, 1)
+    for t in range(total):
+        for g in range(groups):
+            keys = _row_keys(t, g, ids, int(start[t]), block_size)
+            if keys.size == 0:
+                continue
+            hs = slice(g * ratio, (g + 1) * ratio)
+            kl, dz = _kl_row(iq[t, g], ik[keys, 0], q[t, hs], k[keys, g], index_scale, scale)
+            row_kl[t, g] = kl
+            dz = dz * (index_scale / rows)
+            d_iq[t, g] = dz @ ik[keys, 0]
+            d_ik[keys, 0] += dz[:, None] * iq[t, g][None, :]
+    return {"loss": float(row_kl.sum() / rows), "row_kl": row_kl, "d_iq": d_iq, "d_ik": d_ik}
+
+
+def indexer_kl_rows(iq, ik, q, k, indices, cu, tokens, *, block_size=128, index_scale=1.0, scale=None):
+    """``indexer_kl``'s row KL [n,G] and d_iq [n,G,Di] for the given query tokens only."""
+    iq = np.asarray(iq, dtype=np.float64)
+    ik = np.asarray(ik, dtype=np.float64)
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    ids = np.asarray(indices)
+    total, groups, dim_i = iq.shape
+    ratio = q.shape[1] // groups
+    scale = q.shape[2] ** -0.5 if scale is None else float(scale)
+    _, start = _token_positions(bounds_of(cu))
+    tokens = np.asarray(tokens, dtype=np.int64)
+    row_kl = np.zeros((len(tokens), groups))
+    d_iq = np.zeros((len(tokens), groups, dim_i))
+    rows = max(total * groups, 1)
+    for i, t in enumerate(tokens):
+        t = int(t)
+        for g in range(groups):
+            keys = _row_keys(t, g, ids, int(start[t]), block_size)
+            if keys.size == 0:
+                continue
+            hs = slice(g * ratio, (g + 1) * ratio)
+            kl, dz = _kl_row(iq[t, g], ik[keys, 0], q[t, hs], k[keys, g], index_scale, scale)
+            row_kl[i, g] = kl
+            d_iq[i, g] = (dz * (index_scale / rows)) @ ik[keys, 0]
+    return {"row_kl": row_kl, "d_iq": d_iq}
+
+
+def indexer_kl_key_rows(iq, ik, q, k, indices, cu, keys, *, block_size=128, index_scale=1.0, scale=None):
+    """``indexer_kl``'s d_ik [n,Di] for the given key tokens only (all rows that see them)."""
+    iq = np.asarray(iq, dtype=np.float64)
+    ik = np.asarray(ik, dtype=np.float64)
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    ids = np.asarray(indices)
+    total, groups, dim_i = iq.shape
+    ratio = q.shape[1] // groups
+    scale = q.shape[2] ** -0.5 if scale is None else float(scale)
+    bounds = bounds_of(cu)
+    seq, start = _token_positions(bounds)
+    rows = max(total * groups, 1)
+    keys = np.asarray(keys, dtype=np.int64)
+    out = np.zeros((len(keys), dim_i))
+    for i, j in enumerate(keys):
+        j = int(j)
+        s = int(seq[j])
+        b = bounds[s + 1]
+        blk = (j - bounds[s]) // block_size
+        for g in range(groups):
+            hs = slice(g * ratio, (g + 1) * ratio)
+            for t in np.nonzero((ids[j:b, g, :] == blk).any(-1))[0] + j:
+                t = int(t)
+                row_keys = _row_keys(t, g, ids, int(start[t]), block_size)
+                _, dz = _kl_row(iq[t, g], ik[row_keys, 0], q[t, hs], k[row_keys, g], index_scale, scale)
+                out[i] += dz[np.searchsorted(row_keys, j)] * (index_scale / rows) * iq[t, g]
+    return out
