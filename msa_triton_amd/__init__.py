@@ -17,6 +17,12 @@ All three run as hand-written gfx950 HIP kernels behind the C ABI declared in
 
 is the first two stages in one call (score and selection kernels back to back);
 
+    m3_indexer_kl(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, *, block_size=128,
+                  index_scale=1.0, scale=None, return_rows=False) -> loss
+
+is the indexer's KL training loss over the selected tokens (teacher: the detached
+attention probabilities; student: the index token logits);
+
     prepare_sequences(cu_seqlens, *, block_size=128) -> PackedSequences
 
 validates ``cu_seqlens`` once and returns immutable metadata with device copies;
@@ -61,11 +67,19 @@ def m3_index_score_topk(index_q, index_k, cu_seqlens, max_seqlen, *, block_size=
                           topk_blocks=topk_blocks, local_blocks=local_blocks)
 
 
+def m3_indexer_kl(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, *, block_size=128, index_scale=1.0,
+                  scale=None, return_rows=False):
+    from .indexer_kl import m3_indexer_kl as implementation
+
+    return implementation(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, block_size=block_size,
+                          index_scale=index_scale, scale=scale, return_rows=return_rows)
+
+
 def prepare_sequences(cu_seqlens, *, block_size=128):
     from .layout import prepare_sequences as implementation
 
     return implementation(cu_seqlens, block_size=block_size)
 
 
-__all__ = ["m3_index_score", "m3_topk", "m3_sparse_attention", "m3_index_score_topk", "prepare_sequences",
-           "PackedSequences"]
+__all__ = ["m3_index_score", "m3_topk", "m3_sparse_attention", "m3_index_score_topk", "m3_indexer_kl",
+           "prepare_sequences", "PackedSequences"]

@@ -45,6 +45,9 @@ SIGNATURES = {
     "msa_attn_bwd_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "msa_attn_bwd": (_i32, [_vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _f64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
+    "msa_indexer_kl_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
+    "msa_indexer_kl": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+                              _f64, _f64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
 }
 
 STATUS_TEXT = {1: "invalid argument", 2: "unsupported configuration", 3: "HIP launch failure"}
