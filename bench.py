@@ -459,11 +459,18 @@ def main():
             iqg.grad = ikg.grad = None
             msa.m3_index_score(iqg, ikg, cu, max_len, block_size=block).backward(ones)
 
+        iqk, ikk = iq.detach().clone().requires_grad_(), ik.detach().clone().requires_grad_()
+
+        def indexer_kl():
+            # the KL training branch: loss with index_q / index_k gradients (teacher from q, k)
+            iqk.grad = ikk.grad = None
+            msa.m3_indexer_kl(iqk, ikk, q, k, ids, cu, max_len, block_size=block).backward()
+
         reps = max(3, args.repeats // 2)
         for name, fn in (("score_fwd_ms", score_fwd), ("topk_ms", sel), ("k2q_csr_ms", csr),
                          ("attention_fwd_ms", attn_fwd), ("pipeline_fwd_ms", pipeline_fwd),
                          ("score_fwd_bwd_ms", score_fwd_bwd), ("score_topk_fused_ms", score_topk_fused),
-                         ("pipeline_fwd_fused_ms", pipeline_fwd_fused)):
+                         ("pipeline_fwd_fused_ms", pipeline_fwd_fused), ("indexer_kl_fwd_bwd_ms", indexer_kl)):
             stages[name] = round(time_events(fn, reps)["median"], 4)
             log(f"{name}: {stages[name]:.3f}")
         stages["attention_fwd_bwd_ms"] = round(ms, 4)
@@ -510,6 +517,11 @@ def main():
             "attention_bwd": {"bound": "mfma", "unit": "TFLOP/s",
                               **frac(2.5 * fwd_flops, stages["attention_bwd_kernel_ms"], MFMA_BF16_PEAK_TFLOPS,
                                      1e12)},
+            # per visible (token, group, key): teacher logits 2 D R, student logits 2 Di,
+            # d_iq and d_ik 2 Di each
+            "indexer_kl": {"bound": "mfma", "unit": "TFLOP/s",
+                           **frac(keys * (2.0 * cfg["d"] * (cfg["hq"] // cfg["g"]) + 6.0 * cfg["di"]),
+                                  stages["indexer_kl_fwd_bwd_ms"], MFMA_BF16_PEAK_TFLOPS, 1e12)},
         }
 
     baseline = None

@@ -220,11 +220,11 @@ namespace {
 template <int NK, int NKI>
 struct KlMainSmem {
   static constexpr int KS = kl_stride<32 * NK>(), KSI = kl_stride<32 * NKI>();
-  alignas(16) uint16_t qs[2][16 * kKlMaxRatio * KS];  // q rows of a tile [edge * R + head][dim]
+  alignas(16) uint16_t qs[2][16 * kKlMaxRatio * KS];  // q rows of a tile [head * 16 + edge][dim]
   alignas(16) uint16_t iqs[2][16 * KSI];              // index_q rows of a tile [edge][dim]
   alignas(16) uint16_t ikb[128 * KSI];                // the index_k block [key][dim]
   alignas(16) uint16_t dz[2][3][128 * 16];            // dz split planes (hi, mid, lo) [key][edge]
-  alignas(16) float4 tst[2][16 * kKlMaxRatio];        // teacher normalisers per tile row
+  alignas(16) float2 tst[2][16 * kKlMaxRatio];        // teacher (lse2, 1 / mass) per tile row
   alignas(16) float4 sst[2][16];                      // student normalisers per tile edge
   alignas(16) int32_t vis[2][16];                     // visible keys per tile edge (0 past the end)
   alignas(16) int32_t rec[2][16];                     // (token, group, slot) record per tile edge (-1 past the end)
@@ -354,9 +354,12 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
     for (int i = 0; i < QI; ++i) {
       const int idx = tid + kKlThreads * i;
       if (idx < 16 * R * QV) {
+        // head-major rows: the A-operand reads of one head (lane c -> edge c) hit
+        // consecutive rows, conflict-free with the padded stride
         const int rr = idx / QV, d0 = 8 * (idx % QV);
-        const bool ok = e0 + rr / R < ne;
-        *reinterpret_cast<uint4*>(sm.qs[buf] + rr * KS + d0) = ok ? pf[i] : make_uint4(0u, 0u, 0u, 0u);
+        const int el = rr / R, h = rr - el * R;
+        const bool ok = e0 + el < ne;
+        *reinterpret_cast<uint4*>(sm.qs[buf] + (h * 16 + el) * KS + d0) = ok ? pf[i] : make_uint4(0u, 0u, 0u, 0u);
       }
     }
     if (tid < 16 * IV) {
@@ -364,7 +367,7 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
       *reinterpret_cast<uint4*>(sm.iqs[buf] + el * KSI + d0) = e0 + el < ne ? pfi : make_uint4(0u, 0u, 0u, 0u);
     }
     if (tid < 16 * R) {
-      sm.tst[buf][tid] = pst;
+      sm.tst[buf][tid] = make_float2(pst.x, pst.y);
     } else if (tid >= 256 && tid < 256 + 16) {
       sm.sst[buf][tid - 256] = pst;
       sm.vis[buf][tid - 256] = pvis;
@@ -388,15 +391,18 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
     const int vv[4] = {vis4.x, vis4.y, vis4.z, vis4.w};
     // ---- teacher: T[edge 4 q4 + i][key] = mean_h 2^(a_h * as2 - lse2_h) / mass_h
     float tsum[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int h = 0; h < R; ++h) {
-      f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < NK; ++kk) a = mfma(load_frag(sm.qs[b] + (c * R + h) * KS + 32 * kk + 8 * q4), kf[kk], a);
+    for (int h = 0; h < kKlMaxRatio; ++h) {
+      if (h < R) {  // wave-uniform; unrolled so that heads interleave
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float4 st = sm.tst[b][(4 * q4 + i) * R + h];
-        const float p = __builtin_amdgcn_exp2f(a[i] * as2 - st.x) * st.y;
-        tsum[i] += key < vv[i] ? p : 0.f;
+        for (int kk = 0; kk < NK; ++kk) a = mfma(load_frag(sm.qs[b] + (h * 16 + c) * KS + 32 * kk + 8 * q4), kf[kk], a);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float2 st = sm.tst[b][(4 * q4 + i) * R + h];
+          const float p = __builtin_amdgcn_exp2f(a[i] * as2 - st.x) * st.y;
+          tsum[i] += key < vv[i] ? p : 0.f;
+        }
       }
     }
     // ---- student, KL terms and dz
