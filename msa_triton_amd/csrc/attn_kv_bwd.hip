@@ -361,7 +361,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     const uint16_t* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx, const int32_t* __restrict__ sidx,
     const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items, const int2* __restrict__ items, int nseq,
-    int Hq, int G, int D, int K, int B, float scale2, int epi, int t0, float* __restrict__ dqpart,
+    int Hq, int G, int D, int K, int B, float scale2, int epi, int t0, uint32_t rmagic, float* __restrict__ dqpart,
     float* __restrict__ kvpart) {
   constexpr int DP = 32 * NK, NDT = DP / 16, KS = MainSmem<NK>::KS;
   constexpr int RV = DP / 8;             // 16-byte chunks per row
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       if (TV % 256 == 0 || idx < TV) {                                                                      \
         const int rr = idx / RV, d0 = 8 * (idx % RV);                                                       \
         const int rho = (R0) + rr < nrows ? (R0) + rr : nrows - 1;                                          \
-        const int eo = rho / R;                                                                             \
+        const int eo = div_by_ratio(rho, rmagic);                                                           \
         const int64_t th = static_cast<int64_t>(sm.etok[eo]) * Hq + rg.g * R + (rho - eo * R);              \
         const int d0c = (FULLD || d0 < D) ? d0 : D - 8;                                                     \
         pf[i] = *reinterpret_cast<const uint4*>(src + th * D + d0c);                                        \
@@ -455,7 +455,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     if (tid < 32) {                                                                                         \
       const int rho = (R0) + tid;                                                                           \
       if (rho < nrows) {                                                                                    \
-        const int eo = rho / R;                                                                             \
+        const int eo = div_by_ratio(rho, rmagic);                                                           \
         const int h = rg.g * R + (rho - eo * R);                                                            \
         const int tk = sm.etok[eo];                                                                         \
         pst = *reinterpret_cast<const double4*>(row_state + (static_cast<int64_t>(tk) * Hq + h) * 4);       \
@@ -790,6 +790,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   // mass, and only the rows it marked peaked take the statistics pass; without it,
   // every row does.
   const int all_rows = o32 == nullptr;
+  const uint32_t rmagic = ratio_magic(Hq / G);  // rows x ratio < 512 * 512^2 < 2^32
   hipLaunchKernelGGL(kv_bwd_center, dim3(grid_1d(T * Hq, 8)), dim3(256), 0, st, ob, o32, gb, T * Hq, D, rs);
   if (need_kv) hipLaunchKernelGGL(kv_bwd_zero, dim3(grid_1d(2 * nacc, 256)), dim3(256), 0, st, acc, 2 * nacc);
   kv_plan_launch(L.stat_plan, row_ptr, qidx, T, sbase, st);
@@ -819,7 +820,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       const int2* its = kv_plan_items(mp, mbase, c);
       const int mepi = static_cast<int>(mp.epi);
       const dim3 grid(static_cast<unsigned>(mp.max_items)), block(kMainThreads);
-#define MSA_BWD_MAIN(NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, mepi, it0, dqpart, kvpart)
+#define MSA_BWD_MAIN(NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, dqpart, kvpart)
       if (nk == 1) { if (fd) MSA_BWD_MAIN(1, true); else MSA_BWD_MAIN(1, false); }
       else if (nk == 2) { if (fd) MSA_BWD_MAIN(2, true); else MSA_BWD_MAIN(2, false); }
       else { if (fd) MSA_BWD_MAIN(4, true); else MSA_BWD_MAIN(4, false); }

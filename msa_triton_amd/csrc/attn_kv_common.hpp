@@ -46,6 +46,17 @@ __device__ __forceinline__ RowGeom row_geom(const int32_t* __restrict__ cu, cons
 
 inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
+// x / r for 0 <= x with x * r < 2^32 (the row -> edge split inside a work item) as a
+// multiply-high by magic = ceil(2^32 / r): with 2^32 = magic * r - e, 0 <= e < r, the
+// error term x * e / (r * 2^32) stays below 1 / r, so the floor is exact. r == 1 is
+// passed as magic 0.
+__device__ __forceinline__ int div_by_ratio(int x, uint32_t magic) {
+  return magic ? static_cast<int>(__umulhi(static_cast<uint32_t>(x), magic)) : x;
+}
+inline uint32_t ratio_magic(int64_t r) {
+  return r <= 1 ? 0u : static_cast<uint32_t>(((int64_t(1) << 32) + r - 1) / r);
+}
+
 // Query tokens per chunk: per-(token, head, slot) records of `record_bytes` each
 // within `budget` bytes, chunks of equal size. The forward partial pass runs
 // best with ~1 GiB chunks (its gathered query rows stay cache-resident), the

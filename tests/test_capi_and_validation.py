@@ -144,3 +144,15 @@ def test_fused_score_topk_validation_messages():
         msa.m3_index_score_topk(iq, ik, cu, 4, block_size=2, topk_blocks=1, local_blocks=2)
     with pytest.raises(ValueError, match="topk_blocks"):
         msa.m3_index_score_topk(iq, ik, cu, 4, block_size=2, topk_blocks=-1)
+
+
+def test_ratio_magic_division_is_exact_in_its_range():
+    """The kernels split a work item's row index x into (edge, head) with
+    x / r = umulhi(x, ceil(2^32 / r)) for x * r < 2^32 (attn_kv_common.hpp
+    div_by_ratio); exhaustive over the ranges the kernels use (r <= 512, x < 512 r)."""
+    import numpy as np
+
+    for r in range(2, 513):
+        magic = ((1 << 32) + r - 1) // r
+        x = np.arange(512 * r, dtype=np.uint64)
+        assert np.array_equal((x * np.uint64(magic)) >> np.uint64(32), x // np.uint64(r)), r
