@@ -17,6 +17,9 @@ graph breaks and AOTAutograd differentiates it:
                                             out_f32: the fp32 output, or an empty tensor when not saved
     msa_mi355x::sparse_attention_backward(q, k, v, indices, cu_seqlens, out, row_state, out_f32, grad_out,
                                           block_size, scale, need_q, need_k, need_v) -> (dq, dk, dv)
+    msa_mi355x::indexer_kl(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, block_size, index_scale,
+                           scale, need_q, need_k) -> (loss, row_kl, d_iq, d_ik)
+                                               d_iq / d_ik: fp32 gradients of loss, empty when not wanted
 
 A gradient that is not needed comes back as an empty tensor. ``m3_index_score``,
 ``m3_topk`` and ``m3_sparse_attention`` below keep the public signatures: their
@@ -34,6 +37,7 @@ from torch import Tensor
 
 from . import _lib
 from .index_score import _score_backward, _score_forward
+from .indexer_kl import _launch as _kl_launch
 from .layout import sequence_lengths, sequence_meta
 from .sparse_attention import _attn_backward, _attn_forward
 from .topk import m3_topk as _eager_topk
@@ -198,6 +202,48 @@ def _attention_grad(ctx, grad_out, grad_lse, grad_row_state, grad_out_f32):
 torch.library.register_autograd(f"{_NS}::sparse_attention", _attention_grad, setup_context=_attention_setup)
 
 
+# ---------------------------------------------------------------------------- indexer KL
+
+@torch.library.custom_op(f"{_NS}::indexer_kl", mutates_args=())
+def _indexer_kl(index_q: Tensor, index_k: Tensor, q: Tensor, k: Tensor, indices: Tensor, cu_seqlens: Tensor,
+                max_seqlen: int, block_size: int, index_scale: float, scale: float, need_q: bool,
+                need_k: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    _lib.require_gpu(index_q, "m3_indexer_kl")
+    cu = cu_seqlens.contiguous()
+    meta = _attention_meta(cu, index_q.shape[0], max_seqlen, block_size)
+    loss, rows, d_iq, d_ik = _kl_launch(index_q.contiguous(), index_k.contiguous(), q.contiguous(), k.contiguous(),
+                                        indices.contiguous(), cu, meta, None, block_size, index_scale, scale, True,
+                                        need_q, need_k)
+    empty = loss.new_empty(0)
+    return loss.clone(), rows, d_iq if d_iq is not None else empty, d_ik if d_ik is not None else empty
+
+
+@_indexer_kl.register_fake
+def _(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, block_size, index_scale, scale, need_q, need_k):
+    total, groups, dim_i = index_q.shape
+    f32 = torch.float32
+    return (index_q.new_empty((), dtype=f32), index_q.new_empty((total, groups), dtype=f32),
+            index_q.new_empty((total, groups, dim_i) if need_q else (0,), dtype=f32),
+            index_k.new_empty((total, 1, dim_i) if need_k else (0,), dtype=f32))
+
+
+def _kl_setup(ctx, inputs, output):
+    ctx.save_for_backward(output[2], output[3])
+    ctx.dtypes = (inputs[0].dtype, inputs[1].dtype)
+    ctx.mark_non_differentiable(output[1], output[2], output[3])
+
+
+def _kl_grad(ctx, grad_loss, grad_rows, grad_diq, grad_dik):
+    d_iq, d_ik = ctx.saved_tensors
+    need_q, need_k = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+    g = grad_loss.to(torch.float32)
+    return ((d_iq * g).to(ctx.dtypes[0]) if need_q else None, (d_ik * g).to(ctx.dtypes[1]) if need_k else None,
+            None, None, None, None, None, None, None, None, None, None)
+
+
+torch.library.register_autograd(f"{_NS}::indexer_kl", _kl_grad, setup_context=_kl_setup)
+
+
 # ---------------------------------------------------------------------------- public wrappers
 
 def m3_index_score(index_q, index_k, cu_seqlens, max_seqlen, *, block_size=128, scale=1.0):
@@ -267,3 +313,33 @@ def m3_sparse_attention(q, k, v, indices, cu_seqlens, max_seqlen, *, block_size=
     out, lse, _, _ = torch.ops.msa_mi355x.sparse_attention(q, k, v, indices, cu_seqlens, max_seqlen, block_size,
                                                            effective_scale, save_state)
     return (out, lse) if return_lse else out
+
+
+def m3_indexer_kl(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, *, block_size=128, index_scale=1.0,
+                  scale=None, return_rows=False):
+    """``msa_triton_amd.m3_indexer_kl`` through the registered op (same arguments and static checks)."""
+    if index_q.ndim != 3 or index_k.ndim != 3 or q.ndim != 3 or k.ndim != 3:
+        raise ValueError("expected index_q[T,G,Di], index_k[T,1,Di], q[T,Hq,D] and k[T,G,D]")
+    total, groups, dim_i = index_q.shape
+    if groups < 1 or dim_i < 1 or index_k.shape != (total, 1, dim_i):
+        raise ValueError("expected index_q[T,G,Di] and index_k[T,1,Di] with G, Di > 0")
+    if k.shape[:2] != (total, groups) or q.shape[0] != total or q.shape[2] != k.shape[2] or k.shape[2] < 1:
+        raise ValueError("expected q[T,Hq,D] and k[T,G,D] matching index_q's tokens and groups")
+    if q.shape[1] % groups or q.shape[1] == 0:
+        raise ValueError("Hq must be a positive multiple of G")
+    if indices.ndim != 3 or indices.shape[:2] != (total, groups) or indices.dtype != torch.int32:
+        raise ValueError("indices must be int32 [T,G,K]")
+    if cu_seqlens.ndim != 1 or cu_seqlens.numel() < 2 or cu_seqlens.dtype != torch.int32:
+        raise ValueError("cu_seqlens must be int32 [num_sequences + 1]")
+    if not isinstance(block_size, int) or block_size <= 0:
+        raise ValueError("block_size must be a positive integer")
+    if not isinstance(max_seqlen, int) or max_seqlen <= 0:
+        raise ValueError("max_seqlen must be a positive integer")
+    effective_scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
+    if not math.isfinite(effective_scale) or not math.isfinite(index_scale):
+        raise ValueError("scale and index_scale must be finite")
+    grad = torch.is_grad_enabled()
+    loss, rows, _, _ = torch.ops.msa_mi355x.indexer_kl(index_q, index_k, q.detach(), k.detach(), indices, cu_seqlens,
+                                                       max_seqlen, block_size, float(index_scale), effective_scale,
+                                                       grad and index_q.requires_grad, grad and index_k.requires_grad)
+    return (loss, rows) if return_rows else loss

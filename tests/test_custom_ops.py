@@ -12,7 +12,8 @@ from msa_triton_amd import custom_ops as C
 
 
 def test_ops_are_registered():
-    for name in ("index_score", "index_score_backward", "topk", "sparse_attention", "sparse_attention_backward"):
+    for name in ("index_score", "index_score_backward", "topk", "sparse_attention", "sparse_attention_backward",
+                 "indexer_kl"):
         assert hasattr(torch.ops.msa_mi355x, name)
 
 
@@ -40,6 +41,10 @@ def test_fake_kernels_shapes_and_dtypes():
         dq, dk, dv = torch.ops.msa_mi355x.sparse_attention_backward(q, kv, kv, ids, cu, out, rs, o32, out, 8, 0.25,
                                                                     False, True, True)
         assert dq.shape == (0,) and dk.shape == kv.shape and dv.shape == kv.shape
+        loss, rows, d_iq, d_ik = torch.ops.msa_mi355x.indexer_kl(iq, ik, q, kv, ids, cu, 30, 8, 1.0, 0.25, True,
+                                                                 False)
+        assert loss.shape == () and loss.dtype == torch.float32 and rows.shape == (37, 3)
+        assert d_iq.shape == iq.shape and d_iq.dtype == torch.float32 and d_ik.shape == (0,)
 
 
 def test_wrappers_keep_static_checks():

@@ -34,13 +34,16 @@ def test_opcheck_each_op(device):
     ids = msa.m3_topk(scores, cu, block_size=block, topk_blocks=3, local_blocks=1)
     q, k, v = (x.clone().requires_grad_() for x in (q, k, v))
     torch.library.opcheck(torch.ops.msa_mi355x.sparse_attention.default, (q, k, v, ids, cu, maxlen, block, 0.125, True))
+    torch.library.opcheck(torch.ops.msa_mi355x.indexer_kl.default,
+                          (iq, ik, q.detach(), k.detach(), ids, cu, maxlen, block, 1.0, 0.125, True, True))
 
 
 def _forward(ops, iq, ik, q, k, v, g, cu, maxlen, block, topk):
     scores = ops.m3_index_score(iq, ik, cu, maxlen, block_size=block)
     ids = ops.m3_topk(scores.detach(), cu, block_size=block, topk_blocks=topk, local_blocks=1)
     out, lse = ops.m3_sparse_attention(q, k, v, ids, cu, maxlen, block_size=block, return_lse=True)
-    loss = (out.float() * g.float()).sum() + torch.where(torch.isinf(scores), 0.0, scores).sum()
+    kl = ops.m3_indexer_kl(iq, ik, q, k, ids, cu, maxlen, block_size=block)
+    loss = (out.float() * g.float()).sum() + torch.where(torch.isinf(scores), 0.0, scores).sum() + kl
     return loss, scores, ids, out, lse
 
 
