@@ -162,16 +162,16 @@ __global__ __launch_bounds__(kKlThreads, 2) void kl_stats_kernel(
 // valid slots' (max, sum) in FP64 into lse2 = log2 sum_j 2^x_j, kept as
 // (float(lse2), 2^(float(lse2) - lse2), float(lse2) - lse2): with them
 // 2^(x - float(lse2)) * the second value is the normalised probability, and
-// log2 p = (x - float(lse2)) + the third. 32 lanes per row.
+// log2 p = (x - float(lse2)) + the third. 16 lanes per row (slots lane-parallel).
 __global__ __launch_bounds__(256) void kl_stats_combine(const int32_t* __restrict__ indices,
                                                         const int32_t* __restrict__ cu, int nseq, int64_t t0,
                                                         int64_t t1, int Hq, int G, int K, int B,
                                                         const float2* __restrict__ tpart,
                                                         const float2* __restrict__ spart, float4* __restrict__ tstate,
                                                         float4* __restrict__ sstate) {
-  const int sub = threadIdx.x & 31;
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
-  if (r >= (t1 - t0) * (Hq + G)) return;
+  const int sub = threadIdx.x & 15;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
+  if (r >= (t1 - t0) * (Hq + G)) return;  // whole 16-lane segments exit together
   const int64_t tl = r / (Hq + G);
   const int j = static_cast<int>(r % (Hq + G));
   const int64_t t = t0 + tl;
@@ -182,15 +182,15 @@ __global__ __launch_bounds__(256) void kl_stats_combine(const int32_t* __restric
   const int64_t qb = (t - cu[s]) / B;
   const int32_t* sel = indices + (t * G + g) * K;
   float M = -__builtin_inff();
-  for (int slot = sub; slot < K; slot += 32) {
+  for (int slot = sub; slot < K; slot += 16) {
     const int id = sel[slot];
     if (id >= 0 && id <= qb) M = fmaxf(M, part[slot].x);
   }
 #pragma unroll
-  for (int o = 16; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 32));
+  for (int o = 8; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 16));
   double L = 0.0;
   if (M != -__builtin_inff()) {
-    for (int slot = sub; slot < K; slot += 32) {
+    for (int slot = sub; slot < K; slot += 16) {
       const int id = sel[slot];
       if (id >= 0 && id <= qb) {
         const float2 ml = part[slot];
@@ -199,7 +199,7 @@ __global__ __launch_bounds__(256) void kl_stats_combine(const int32_t* __restric
     }
   }
 #pragma unroll
-  for (int o = 16; o > 0; o >>= 1) L += __shfl_xor(L, o, 32);
+  for (int o = 8; o > 0; o >>= 1) L += __shfl_xor(L, o, 16);
   if (sub == 0) {
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
     if (L > 0.0) {
@@ -735,7 +735,7 @@ extern "C" int msa_indexer_kl(const void* index_q, const void* index_k, const vo
       MSA_KL_DISPATCH(MSA_KL_STATS)
 #undef MSA_KL_STATS
     }
-    hipLaunchKernelGGL(kl_stats_combine, dim3(grid_1d((t1 - t0) * (Hq + G), 8)), dim3(256), 0, st, indices,
+    hipLaunchKernelGGL(kl_stats_combine, dim3(grid_1d((t1 - t0) * (Hq + G), 16)), dim3(256), 0, st, indices,
                        cu_seqlens, nseq, t0, t1, iHq, iG, iK, iB, tpart, spart, tstate, sstate);
     if (rows > 0 && pl.max_items > 0) {
 #define MSA_KL_MAIN(A, C) hipLaunchKernelGGL((kl_main_kernel<A, C>), grid, block, 0, st, iqb, ikb, qb, kb, tstate, sstate, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, need_diq, need_dik, klpart, diqpart, ikpart)
