@@ -312,16 +312,24 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
   uint4 pf[QI], pfi = make_uint4(0u, 0u, 0u, 0u);
   float4 pst = make_float4(0.f, 0.f, 0.f, 0.f);
   int pvis = 0, prec = -1;
+  // the thread -> (tile edge, head, dims) split of the q rows is the same for every tile
+  int qel[QI], qsrc[QI], qdst[QI];
+#pragma unroll
+  for (int i = 0; i < QI; ++i) {
+    const int idx = tid + kKlThreads * i;
+    const int rr = idx / QV, d0 = 8 * (idx % QV);
+    const int el = rr / R, h = rr - el * R;
+    qel[i] = idx < 16 * R * QV ? el : -1;  // -1: no chunk for this thread
+    qsrc[i] = (rg.g * R + h) * D + d0;
+    qdst[i] = (h * 16 + el) * KS + d0;
+  }
+  const int64_t qrow = static_cast<int64_t>(Hq) * D;
   auto issue = [&](int e0) {
 #pragma unroll
     for (int i = 0; i < QI; ++i) {
-      const int idx = tid + kKlThreads * i;
-      if (idx < 16 * R * QV) {
-        const int rr = idx / QV, d0 = 8 * (idx % QV);
-        const int el = rr / R, h = rr - el * R;
-        const int e = e0 + el < ne ? e0 + el : ne - 1;
-        const int64_t th = static_cast<int64_t>(sm.etok[e]) * Hq + rg.g * R + h;
-        pf[i] = *reinterpret_cast<const uint4*>(q + th * D + d0);
+      if (qel[i] >= 0) {
+        const int e = e0 + qel[i] < ne ? e0 + qel[i] : ne - 1;
+        pf[i] = *reinterpret_cast<const uint4*>(q + sm.etok[e] * qrow + qsrc[i]);
       }
     }
     if (tid < 16 * IV) {
@@ -352,15 +360,10 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
   auto commit = [&](int e0, int buf) {
 #pragma unroll
     for (int i = 0; i < QI; ++i) {
-      const int idx = tid + kKlThreads * i;
-      if (idx < 16 * R * QV) {
-        // head-major rows: the A-operand reads of one head (lane c -> edge c) hit
-        // consecutive rows, conflict-free with the padded stride
-        const int rr = idx / QV, d0 = 8 * (idx % QV);
-        const int el = rr / R, h = rr - el * R;
-        const bool ok = e0 + el < ne;
-        *reinterpret_cast<uint4*>(sm.qs[buf] + (h * 16 + el) * KS + d0) = ok ? pf[i] : make_uint4(0u, 0u, 0u, 0u);
-      }
+      // head-major rows: the A-operand reads of one head (lane c -> edge c) hit
+      // consecutive rows, conflict-free with the padded stride
+      if (qel[i] >= 0)
+        *reinterpret_cast<uint4*>(sm.qs[buf] + qdst[i]) = e0 + qel[i] < ne ? pf[i] : make_uint4(0u, 0u, 0u, 0u);
     }
     if (tid < 16 * IV) {
       const int el = tid / IV, d0 = 8 * (tid % IV);
