@@ -156,3 +156,30 @@ def test_ratio_magic_division_is_exact_in_its_range():
         magic = ((1 << 32) + r - 1) // r
         x = np.arange(512 * r, dtype=np.uint64)
         assert np.array_equal((x * np.uint64(magic)) >> np.uint64(32), x // np.uint64(r)), r
+
+
+def test_indexer_kl_validation_messages():
+    iq = torch.zeros(6, 2, 32, dtype=torch.bfloat16)
+    ik = torch.zeros(6, 1, 32, dtype=torch.bfloat16)
+    q = torch.zeros(6, 4, 32, dtype=torch.bfloat16)
+    k = torch.zeros(6, 2, 32, dtype=torch.bfloat16)
+    ids = torch.zeros(6, 2, 1, dtype=torch.int32)
+    cu = torch.tensor([0, 6], dtype=torch.int32)
+    with pytest.raises(ValueError, match="index_k"):
+        msa.m3_indexer_kl(iq, ik[:, :, :16], q, k, ids, cu, 6)
+    with pytest.raises(ValueError, match="matching index_q"):
+        msa.m3_indexer_kl(iq, ik, q, k[:, :1], ids, cu, 6)
+    with pytest.raises(ValueError, match="multiple of G"):
+        msa.m3_indexer_kl(iq, ik, q[:, :3], k, ids, cu, 6)
+    with pytest.raises(ValueError, match="indices"):
+        msa.m3_indexer_kl(iq, ik, q, k, ids.long(), cu, 6)
+    with pytest.raises(TypeError, match="dtype"):
+        msa.m3_indexer_kl(iq, ik, q.half(), k, ids, cu, 6)
+    with pytest.raises(ValueError, match="block_size"):
+        msa.m3_indexer_kl(iq, ik, q, k, ids, cu, 6, block_size=0)
+    with pytest.raises(ValueError, match="finite"):
+        msa.m3_indexer_kl(iq, ik, q, k, ids, cu, 6, scale=float("nan"))
+    with pytest.raises(ValueError, match="max_seqlen"):
+        msa.m3_indexer_kl(iq, ik, q, k, ids, cu, 5)
+    with pytest.raises(RuntimeError):  # valid CPU tensors: no CPU execution path
+        msa.m3_indexer_kl(iq, ik, q, k, ids, cu, 6)
