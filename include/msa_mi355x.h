@@ -160,17 +160,19 @@ int64_t msa_indexer_kl_workspace_bytes(int32_t dtype, int64_t total_tokens, int6
  * group's query heads of softmax(scale * q . k); loss [1] = mean over the T x G
  * (token, group) pairs (pairs without visible keys count as 0). row_kl [T,G]
  * (nullable) receives the per-pair KL; grad_index_q [T,G,Di] and grad_index_k
- * [T,1,Di] (fp32, each nullable) the gradients of loss. Uses the k2q CSR of
- * `indices` (msa_k2q_build) and msa_indexer_kl_workspace_bytes(...) bytes.
- * Deterministic: no floating-point atomics. */
+ * [T,1,Di] (fp32, each nullable) the gradients of loss. teacher_lse (nullable):
+ * msa_attn_fwd's lse [T,Hq] for the same q, k, indices and scale; when given, the
+ * teacher's normalisers are taken from it instead of being recomputed. Uses the
+ * k2q CSR of `indices` (msa_k2q_build) and msa_indexer_kl_workspace_bytes(...)
+ * bytes. Deterministic: no floating-point atomics. */
 int msa_indexer_kl(const void* index_q, const void* index_k, const void* q, const void* k, int32_t dtype,
                    const int32_t* indices, const int32_t* cu_seqlens, int64_t num_seqs,
                    int64_t total_tokens, int64_t q_heads, int64_t kv_groups, int64_t head_dim,
                    int64_t index_dim, int64_t topk_slots, int64_t block_size, double index_scale,
                    double scale, const int32_t* cu_block_lens, int64_t total_blocks,
                    const int32_t* row_ptr, const int32_t* query_indices, const int32_t* slot_indices,
-                   float* loss, float* row_kl, float* grad_index_q, float* grad_index_k, void* workspace,
-                   int64_t workspace_bytes, void* stream);
+                   const float* teacher_lse, float* loss, float* row_kl, float* grad_index_q,
+                   float* grad_index_k, void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

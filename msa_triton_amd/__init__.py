@@ -68,11 +68,11 @@ def m3_index_score_topk(index_q, index_k, cu_seqlens, max_seqlen, *, block_size=
 
 
 def m3_indexer_kl(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, *, block_size=128, index_scale=1.0,
-                  scale=None, return_rows=False):
+                  scale=None, return_rows=False, teacher_lse=None):
     from .indexer_kl import m3_indexer_kl as implementation
 
     return implementation(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, block_size=block_size,
-                          index_scale=index_scale, scale=scale, return_rows=return_rows)
+                          index_scale=index_scale, scale=scale, return_rows=return_rows, teacher_lse=teacher_lse)
 
 
 def prepare_sequences(cu_seqlens, *, block_size=128):

@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kKlThreads, 2) void kl_stats_kernel(
     const uint16_t* __restrict__ k, const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks,
     const int32_t* __restrict__ qidx, const int32_t* __restrict__ sidx, const int32_t* __restrict__ e_hi,
     const int32_t* __restrict__ n_items, const int2* __restrict__ items, int nseq, int Hq, int G, int K, int B,
-    float zs2, float as2, int epi, int t0, float2* __restrict__ tpart, float2* __restrict__ spart) {
+    float zs2, float as2, int epi, int t0, int teacher, float2* __restrict__ tpart, float2* __restrict__ spart) {
   constexpr int D = 32 * NK, Di = 32 * NKI;
   constexpr int KS = KlStatSmem<NK, NKI>::KS, KSI = KlStatSmem<NK, NKI>::KSI;
   __shared__ KlStatSmem<NK, NKI> sm;
@@ -137,8 +137,9 @@ __global__ __launch_bounds__(kKlThreads, 2) void kl_stats_kernel(
       const float2 ml = lane_max_sum(x);
       if (q4 == 0 && ok) spart[((static_cast<int64_t>(tok) - t0) * G + rg.g) * K + slot] = ml;
     }
-    // ---- teacher, head by head: a^T = K_block . q_h^T
-    for (int h = 0; h < R; ++h) {
+    // ---- teacher, head by head: a^T = K_block . q_h^T (skipped when the caller supplies
+    // the attention's lse, which is the teacher's normaliser)
+    for (int h = 0; h < (teacher ? R : 0); ++h) {
       const int hq = rg.g * R + h;
       bf16x8 bq[NK];
 #pragma unroll
@@ -163,12 +164,14 @@ __global__ __launch_bounds__(kKlThreads, 2) void kl_stats_kernel(
 // (float(lse2), 2^(float(lse2) - lse2), float(lse2) - lse2): with them
 // 2^(x - float(lse2)) * the second value is the normalised probability, and
 // log2 p = (x - float(lse2)) + the third. 16 lanes per row (slots lane-parallel).
+// With tlse (the attention's natural-log lse [T, Hq] for the same q, k, selection and
+// scale), a teacher row takes (float(lse * log2 e), 1, 0) instead.
 __global__ __launch_bounds__(256) void kl_stats_combine(const int32_t* __restrict__ indices,
                                                         const int32_t* __restrict__ cu, int nseq, int64_t t0,
                                                         int64_t t1, int Hq, int G, int K, int B,
                                                         const float2* __restrict__ tpart,
-                                                        const float2* __restrict__ spart, float4* __restrict__ tstate,
-                                                        float4* __restrict__ sstate) {
+                                                        const float2* __restrict__ spart, const float* __restrict__ tlse,
+                                                        float4* __restrict__ tstate, float4* __restrict__ sstate) {
   const int sub = threadIdx.x & 15;
   const int64_t r = static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4);
   if (r >= (t1 - t0) * (Hq + G)) return;  // whole 16-lane segments exit together
@@ -177,6 +180,15 @@ __global__ __launch_bounds__(256) void kl_stats_combine(const int32_t* __restric
   const int64_t t = t0 + tl;
   const bool student = j >= Hq;
   const int g = student ? j - Hq : j / (Hq / G);
+  if (!student && tlse) {
+    if (sub == 0) {
+      const float l = tlse[t * Hq + j];
+      tstate[t * Hq + j] = l == -__builtin_inff() ? make_float4(0.f, 0.f, 0.f, 0.f)
+                                                  : make_float4(static_cast<float>(static_cast<double>(l) * 1.4426950408889634),
+                                                                1.f, 0.f, 0.f);
+    }
+    return;
+  }
   const float2* part = student ? spart + (tl * G + g) * K : tpart + (tl * Hq + j) * K;
   const int s = find_seq(cu, nseq, t);
   const int64_t qb = (t - cu[s]) / B;
@@ -678,8 +690,8 @@ extern "C" int msa_indexer_kl(const void* index_q, const void* index_k, const vo
                               int64_t index_dim, int64_t topk_slots, int64_t block_size, double index_scale,
                               double scale, const int32_t* cu_block_lens, int64_t total_blocks,
                               const int32_t* row_ptr, const int32_t* query_indices, const int32_t* slot_indices,
-                              float* loss, float* row_kl, float* grad_index_q, float* grad_index_k, void* workspace,
-                              int64_t workspace_bytes, void* stream) {
+                              const float* teacher_lse, float* loss, float* row_kl, float* grad_index_q,
+                              float* grad_index_k, void* workspace, int64_t workspace_bytes, void* stream) {
   if (num_seqs <= 0 || total_tokens < 0 || topk_slots < 0 || total_blocks < 0 || !loss || q_heads <= 0 ||
       kv_groups <= 0 || q_heads % kv_groups)
     return kErrInvalidArgument;
@@ -730,7 +742,7 @@ extern "C" int msa_indexer_kl(const void* index_q, const void* index_k, const vo
     const int epi = static_cast<int>(pl.epi);
     const dim3 grid(static_cast<unsigned>(pl.max_items > 0 ? pl.max_items : 1)), block(kKlThreads);
     if (rows > 0 && pl.max_items > 0) {
-#define MSA_KL_STATS(A, C) hipLaunchKernelGGL((kl_stats_kernel<A, C>), grid, block, 0, st, iqb, ikb, qb, kb, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, tpart, spart)
+#define MSA_KL_STATS(A, C) hipLaunchKernelGGL((kl_stats_kernel<A, C>), grid, block, 0, st, iqb, ikb, qb, kb, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, teacher_lse ? 0 : 1, tpart, spart)
 #define MSA_KL_DISPATCH(M)                                   \
   if (nk == 1) { if (nki == 1) M(1, 1); else if (nki == 2) M(1, 2); else M(1, 4); } \
   else if (nk == 2) { if (nki == 1) M(2, 1); else if (nki == 2) M(2, 2); else M(2, 4); } \
@@ -739,7 +751,7 @@ extern "C" int msa_indexer_kl(const void* index_q, const void* index_k, const vo
 #undef MSA_KL_STATS
     }
     hipLaunchKernelGGL(kl_stats_combine, dim3(grid_1d((t1 - t0) * (Hq + G), 16)), dim3(256), 0, st, indices,
-                       cu_seqlens, nseq, t0, t1, iHq, iG, iK, iB, tpart, spart, tstate, sstate);
+                       cu_seqlens, nseq, t0, t1, iHq, iG, iK, iB, tpart, spart, teacher_lse, tstate, sstate);
     if (rows > 0 && pl.max_items > 0) {
 #define MSA_KL_MAIN(A, C) hipLaunchKernelGGL((kl_main_kernel<A, C>), grid, block, 0, st, iqb, ikb, qb, kb, tstate, sstate, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, need_diq, need_dik, klpart, diqpart, ikpart)
       MSA_KL_DISPATCH(MSA_KL_MAIN)

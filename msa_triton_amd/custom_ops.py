@@ -18,7 +18,7 @@ graph breaks and AOTAutograd differentiates it:
     msa_mi355x::sparse_attention_backward(q, k, v, indices, cu_seqlens, out, row_state, out_f32, grad_out,
                                           block_size, scale, need_q, need_k, need_v) -> (dq, dk, dv)
     msa_mi355x::indexer_kl(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, block_size, index_scale,
-                           scale, need_q, need_k) -> (loss, row_kl, d_iq, d_ik)
+                           scale, need_q, need_k, teacher_lse) -> (loss, row_kl, d_iq, d_ik)
                                                d_iq / d_ik: fp32 gradients of loss, empty when not wanted
 
 A gradient that is not needed comes back as an empty tensor. ``m3_index_score``,
@@ -31,6 +31,7 @@ Importing this module registers the ops; it does not load the HIP library.
 from __future__ import annotations
 
 import math
+from typing import Optional
 
 import torch
 from torch import Tensor
@@ -206,20 +207,22 @@ torch.library.register_autograd(f"{_NS}::sparse_attention", _attention_grad, set
 
 @torch.library.custom_op(f"{_NS}::indexer_kl", mutates_args=())
 def _indexer_kl(index_q: Tensor, index_k: Tensor, q: Tensor, k: Tensor, indices: Tensor, cu_seqlens: Tensor,
-                max_seqlen: int, block_size: int, index_scale: float, scale: float, need_q: bool,
-                need_k: bool) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+                max_seqlen: int, block_size: int, index_scale: float, scale: float, need_q: bool, need_k: bool,
+                teacher_lse: Optional[Tensor]) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     _lib.require_gpu(index_q, "m3_indexer_kl")
     cu = cu_seqlens.contiguous()
     meta = _attention_meta(cu, index_q.shape[0], max_seqlen, block_size)
     loss, rows, d_iq, d_ik = _kl_launch(index_q.contiguous(), index_k.contiguous(), q.contiguous(), k.contiguous(),
                                         indices.contiguous(), cu, meta, None, block_size, index_scale, scale, True,
-                                        need_q, need_k)
+                                        need_q, need_k,
+                                        teacher_lse.contiguous() if teacher_lse is not None else None)
     empty = loss.new_empty(0)
     return loss.clone(), rows, d_iq if d_iq is not None else empty, d_ik if d_ik is not None else empty
 
 
 @_indexer_kl.register_fake
-def _(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, block_size, index_scale, scale, need_q, need_k):
+def _(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, block_size, index_scale, scale, need_q, need_k,
+      teacher_lse):
     total, groups, dim_i = index_q.shape
     f32 = torch.float32
     return (index_q.new_empty((), dtype=f32), index_q.new_empty((total, groups), dtype=f32),
@@ -238,7 +241,7 @@ def _kl_grad(ctx, grad_loss, grad_rows, grad_diq, grad_dik):
     need_q, need_k = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
     g = grad_loss.to(torch.float32)
     return ((d_iq * g).to(ctx.dtypes[0]) if need_q else None, (d_ik * g).to(ctx.dtypes[1]) if need_k else None,
-            None, None, None, None, None, None, None, None, None, None)
+            None, None, None, None, None, None, None, None, None, None, None)
 
 
 torch.library.register_autograd(f"{_NS}::indexer_kl", _kl_grad, setup_context=_kl_setup)
@@ -316,7 +319,7 @@ def m3_sparse_attention(q, k, v, indices, cu_seqlens, max_seqlen, *, block_size=
 
 
 def m3_indexer_kl(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, *, block_size=128, index_scale=1.0,
-                  scale=None, return_rows=False):
+                  scale=None, return_rows=False, teacher_lse=None):
     """``msa_triton_amd.m3_indexer_kl`` through the registered op (same arguments and static checks)."""
     if index_q.ndim != 3 or index_k.ndim != 3 or q.ndim != 3 or k.ndim != 3:
         raise ValueError("expected index_q[T,G,Di], index_k[T,1,Di], q[T,Hq,D] and k[T,G,D]")
@@ -341,5 +344,6 @@ def m3_indexer_kl(index_q, index_k, q, k, indices, cu_seqlens, max_seqlen, *, bl
     grad = torch.is_grad_enabled()
     loss, rows, _, _ = torch.ops.msa_mi355x.indexer_kl(index_q, index_k, q.detach(), k.detach(), indices, cu_seqlens,
                                                        max_seqlen, block_size, float(index_scale), effective_scale,
-                                                       grad and index_q.requires_grad, grad and index_k.requires_grad)
+                                                       grad and index_q.requires_grad, grad and index_k.requires_grad,
+                                                       None if teacher_lse is None else teacher_lse.detach())
     return (loss, rows) if return_rows else loss

@@ -34,7 +34,8 @@ from . import k2q as _k2q
 from .layout import PackedSequences, prepared_for, sequence_lengths, sequence_meta
 
 
-def _launch(iq, ik, q, k, indices, cu, meta, seqs, block_size, index_scale, scale, want_rows, need_q, need_k):
+def _launch(iq, ik, q, k, indices, cu, meta, seqs, block_size, index_scale, scale, want_rows, need_q, need_k,
+            teacher_lse=None):
     total, groups, dim_i = iq.shape
     heads, dim = q.shape[1], q.shape[2]
     slots = indices.shape[2]
@@ -58,7 +59,8 @@ def _launch(iq, ik, q, k, indices, cu, meta, seqs, block_size, index_scale, scal
                 iq.data_ptr(), ik.data_ptr(), q.data_ptr(), k.data_ptr(), _lib.DTYPE_CODE[iq.dtype],
                 indices.data_ptr(), cu.data_ptr(), meta.num_seqs, total, heads, groups, dim, dim_i, slots,
                 block_size, index_scale, scale, csr.cu_block_lens.data_ptr(), meta.total_blocks,
-                csr.row_ptr.data_ptr(), _lib.ptr(csr.query_indices), _lib.ptr(csr.slot_indices), loss.data_ptr(),
+                csr.row_ptr.data_ptr(), _lib.ptr(csr.query_indices), _lib.ptr(csr.slot_indices),
+                _lib.ptr(teacher_lse), loss.data_ptr(),
                 _lib.ptr(row_kl), _lib.ptr(d_iq), _lib.ptr(d_ik), workspace.data_ptr(), ws_bytes,
                 _lib.stream_of(device))
         _lib.check(status, "msa_indexer_kl")
@@ -67,11 +69,11 @@ def _launch(iq, ik, q, k, indices, cu, meta, seqs, block_size, index_scale, scal
 
 class _IndexerKL(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, iq, ik, q, k, indices, cu, meta, seqs, block_size, index_scale, scale, want_rows):
+    def forward(ctx, iq, ik, q, k, indices, cu, meta, seqs, block_size, index_scale, scale, want_rows, teacher_lse):
         need_q, need_k = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         loss, row_kl, d_iq, d_ik = _launch(iq.contiguous(), ik.contiguous(), q.detach().contiguous(),
                                            k.detach().contiguous(), indices.contiguous(), cu, meta, seqs, block_size,
-                                           index_scale, scale, want_rows, need_q, need_k)
+                                           index_scale, scale, want_rows, need_q, need_k, teacher_lse)
         ctx.save_for_backward(d_iq, d_ik)
         ctx.dtypes = (iq.dtype, ik.dtype)
         if row_kl is None:
@@ -85,7 +87,7 @@ class _IndexerKL(torch.autograd.Function):
         g = grad_loss.to(torch.float32)
         diq = (d_iq * g).to(ctx.dtypes[0]) if d_iq is not None else None
         dik = (d_ik * g).to(ctx.dtypes[1]) if d_ik is not None else None
-        return diq, dik, None, None, None, None, None, None, None, None, None, None
+        return diq, dik, None, None, None, None, None, None, None, None, None, None, None
 
 
 def m3_indexer_kl(
@@ -101,11 +103,15 @@ def m3_indexer_kl(
     index_scale: float = 1.0,
     scale: float | None = None,
     return_rows: bool = False,
+    teacher_lse: torch.Tensor | None = None,
 ):
     """KL(stopgrad(teacher) || student) over the selected causal tokens, averaged over
     (token, group) pairs: a differentiable fp32 scalar (gradients reach ``index_q`` and
     ``index_k`` only). With ``return_rows`` also the per-pair KL ``[T, G]`` (fp32,
-    non-differentiable)."""
+    non-differentiable). ``teacher_lse``: the lse ``m3_sparse_attention(...,
+    return_lse=True)`` returned for the same ``q``, ``k``, ``indices``, ``block_size``
+    and ``scale`` (fp32 ``[T, Hq]``); the teacher's normalisers are then taken from it
+    instead of being recomputed (about a quarter of the work)."""
     if index_q.ndim != 3 or index_k.ndim != 3 or q.ndim != 3 or k.ndim != 3:
         raise ValueError("expected index_q[T,G,Di], index_k[T,1,Di], q[T,Hq,D] and k[T,G,D]")
     total, groups, dim_i = index_q.shape
@@ -135,6 +141,12 @@ def m3_indexer_kl(
     effective_scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
     if not math.isfinite(effective_scale) or not math.isfinite(index_scale):
         raise ValueError("scale and index_scale must be finite")
+    if teacher_lse is not None:
+        if teacher_lse.shape != q.shape[:2] or teacher_lse.dtype != torch.float32:
+            raise ValueError("teacher_lse must be the fp32 [T, Hq] lse of the attention")
+        if teacher_lse.device != index_q.device:
+            raise ValueError("all inputs must reside on the same device")
+        teacher_lse = teacher_lse.detach().contiguous()
     if seqs is None:
         lengths = sequence_lengths(cu, total)
     else:  # prepared: no host read
@@ -150,5 +162,5 @@ def m3_indexer_kl(
     else:
         meta = seqs.meta
     loss, rows = _IndexerKL.apply(index_q, index_k, q, k, indices, cu, meta, seqs, block_size, float(index_scale),
-                                  effective_scale, return_rows)
+                                  effective_scale, return_rows, teacher_lse)
     return (loss, rows) if return_rows else loss

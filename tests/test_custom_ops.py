@@ -42,7 +42,7 @@ def test_fake_kernels_shapes_and_dtypes():
                                                                     False, True, True)
         assert dq.shape == (0,) and dk.shape == kv.shape and dv.shape == kv.shape
         loss, rows, d_iq, d_ik = torch.ops.msa_mi355x.indexer_kl(iq, ik, q, kv, ids, cu, 30, 8, 1.0, 0.25, True,
-                                                                 False)
+                                                                 False, None)
         assert loss.shape == () and loss.dtype == torch.float32 and rows.shape == (37, 3)
         assert d_iq.shape == iq.shape and d_iq.dtype == torch.float32 and d_ik.shape == (0,)
 

@@ -35,7 +35,7 @@ def test_opcheck_each_op(device):
     q, k, v = (x.clone().requires_grad_() for x in (q, k, v))
     torch.library.opcheck(torch.ops.msa_mi355x.sparse_attention.default, (q, k, v, ids, cu, maxlen, block, 0.125, True))
     torch.library.opcheck(torch.ops.msa_mi355x.indexer_kl.default,
-                          (iq, ik, q.detach(), k.detach(), ids, cu, maxlen, block, 1.0, 0.125, True, True))
+                          (iq, ik, q.detach(), k.detach(), ids, cu, maxlen, block, 1.0, 0.125, True, True, None))
 
 
 def _forward(ops, iq, ik, q, k, v, g, cu, maxlen, block, topk):

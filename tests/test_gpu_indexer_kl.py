@@ -136,3 +136,30 @@ def test_unsupported_configurations_raise(device):
     with pytest.raises(NotImplementedError):
         q16 = torch.randn(20, 16, 32, device=device).bfloat16()
         msa.m3_indexer_kl(d[0], d[1], q16, d[3], d[4], d[5], 20, block_size=8)
+
+
+def test_teacher_lse_from_the_attention(device):
+    """The attention's lse as the teacher's normalisers (the teacher half of the
+    statistics pass is skipped): the same oracle tolerances as the full pass."""
+    lengths, groups, ratio, dim, block = [300, 0, 200], 2, 4, 64, 32
+    iq, ik, q, k, ids, cu = _inputs(lengths, groups, ratio, dim, 64, block, 4, 31)
+    ids[5, 1] = -1  # a pair with no visible key: lse -inf, KL 0
+    d = [x.to(device) for x in (iq, ik, q, k, ids, cu)]
+    v = torch.randn(k.shape, generator=torch.Generator().manual_seed(2)).bfloat16().to(device)
+    _, lse = msa.m3_sparse_attention(d[2], d[3], v, d[4], d[5], 300, block_size=block, return_lse=True)
+    sc = dim ** -0.5
+    ref = _oracle(iq, ik, q, k, ids, cu, block, 1.0, sc)
+    meta = sequence_meta(cu.tolist(), block)
+    loss, rows, d_iq, d_ik = _launch(*d[:6], meta, None, block, 1.0, sc, True, True, True, teacher_lse=lse)
+    assert float(loss) == pytest.approx(ref["loss"], rel=1e-5, abs=1e-6)
+    np.testing.assert_allclose(rows.cpu().double().numpy(), ref["row_kl"], rtol=1e-5, atol=1e-6)
+    assert float(rows[5, 1]) == 0.0
+    _close32(d_iq, ref["d_iq"], "d_iq")
+    _close32(d_ik, ref["d_ik"], "d_ik")
+    a = d[0].clone().requires_grad_()
+    out = msa.m3_indexer_kl(a, d[1], d[2], d[3], d[4], d[5], 300, block_size=block, teacher_lse=lse)
+    assert float(out.detach()) == float(loss)
+    out.backward()
+    assert torch.equal(a.grad, d_iq.to(torch.bfloat16))
+    with pytest.raises(ValueError, match="teacher_lse"):
+        msa.m3_indexer_kl(a, d[1], d[2], d[3], d[4], d[5], 300, block_size=block, teacher_lse=lse[:, :1])
