@@ -466,11 +466,20 @@ def main():
             iqk.grad = ikk.grad = None
             msa.m3_indexer_kl(iqk, ikk, q, k, ids, cu, max_len, block_size=block).backward()
 
+        with torch.no_grad():
+            _, attn_lse = msa.m3_sparse_attention(q, k, v, ids, cu, max_len, block_size=block, return_lse=True)
+
+        def indexer_kl_lse():
+            # the same, with the teacher normalisers taken from the attention forward's lse
+            iqk.grad = ikk.grad = None
+            msa.m3_indexer_kl(iqk, ikk, q, k, ids, cu, max_len, block_size=block, teacher_lse=attn_lse).backward()
+
         reps = max(3, args.repeats // 2)
         for name, fn in (("score_fwd_ms", score_fwd), ("topk_ms", sel), ("k2q_csr_ms", csr),
                          ("attention_fwd_ms", attn_fwd), ("pipeline_fwd_ms", pipeline_fwd),
                          ("score_fwd_bwd_ms", score_fwd_bwd), ("score_topk_fused_ms", score_topk_fused),
-                         ("pipeline_fwd_fused_ms", pipeline_fwd_fused), ("indexer_kl_fwd_bwd_ms", indexer_kl)):
+                         ("pipeline_fwd_fused_ms", pipeline_fwd_fused), ("indexer_kl_fwd_bwd_ms", indexer_kl),
+                         ("indexer_kl_teacher_lse_fwd_bwd_ms", indexer_kl_lse)):
             stages[name] = round(time_events(fn, reps)["median"], 4)
             log(f"{name}: {stages[name]:.3f}")
         stages["attention_fwd_bwd_ms"] = round(ms, 4)
