@@ -10,9 +10,11 @@
 // sort whose tiles are the query blocks themselves: every token of query block
 // qb can only reach rows with block id <= qb, so tile (seq, qb) owns a compact
 // counter range of (qb+1)*G entries.
-//   1. k2q_count   : per-tile histogram of its edges (integer atomics -> exact).
+//   1. k2q_count   : per-tile histogram of its edges (integer atomics -> exact),
+//                    in LDS when the tile's counters fit.
 //   2. k2q_rowscan : per row, exclusive prefix of the counts over the tiles
-//                    qb >= b (in qb order), giving the tile's start inside the row.
+//                    qb >= b (in qb order), giving the tile's start inside the row;
+//                    one wavefront per row, 64 tiles per step.
 //   3. k2q_ptrscan : exclusive scan of row totals -> row_ptr (one workgroup).
 //   4. k2q_scatter_par : per (tile, group), a stable counting sort of the tile's
 //                    edges on their block id places each edge at row_ptr[row] +
@@ -48,49 +50,76 @@ __device__ __forceinline__ TileInfo tile_info(int64_t tile, const int32_t* __res
   return ti;
 }
 
+// Tiles with at most this many counters ((qb + 1) * G) count in LDS.
+constexpr int kCountLds = 8192;
+
 __global__ __launch_bounds__(256) void k2q_count(const int32_t* __restrict__ indices,
                                                  const int32_t* __restrict__ cu,
                                                  const int32_t* __restrict__ cu_blocks,
                                                  const int64_t* __restrict__ tri_prefix, int nseq,
                                                  int G, int K, int B, int32_t* __restrict__ counters) {
+  __shared__ int32_t hist[kCountLds];
   const TileInfo ti = tile_info(blockIdx.x, cu, cu_blocks, tri_prefix, nseq, G, B);
   const int64_t ncnt = static_cast<int64_t>(ti.qb + 1) * G;
+  const bool in_lds = ncnt <= kCountLds;  // uniform over the workgroup
   int32_t* cnt = counters + ti.counter_base;
-  for (int64_t i = threadIdx.x; i < ncnt; i += blockDim.x) cnt[i] = 0;
+  int32_t* h = in_lds ? hist : cnt;
+  for (int64_t i = threadIdx.x; i < ncnt; i += blockDim.x) h[i] = 0;
   __syncthreads();
   const int nb = cu_blocks[ti.seq + 1] - cu_blocks[ti.seq];
-  const int64_t edges = (ti.tok_end - ti.tok_begin) * G * K;
+  // a tile holds at most B tokens: its edge count fits in 32 bits (B * G * K < 2^31 checked on the host)
+  const int edges = static_cast<int>((ti.tok_end - ti.tok_begin) * G * K);
   const int32_t* src = indices + ti.tok_begin * G * K;
-  for (int64_t e = threadIdx.x; e < edges; e += blockDim.x) {
+  for (int e = threadIdx.x; e < edges; e += blockDim.x) {
     const int id = src[e];
-    const int g = static_cast<int>((e / K) % G);
-    if (id >= 0 && id < nb && id <= ti.qb) atomicAdd(&cnt[static_cast<int64_t>(id) * G + g], 1);
+    const int g = (e / K) % G;
+    if (id >= 0 && id < nb && id <= ti.qb) {
+      if (in_lds)
+        atomicAdd(&hist[id * G + g], 1);
+      else
+        atomicAdd(&cnt[static_cast<int64_t>(id) * G + g], 1);
+    }
+  }
+  if (in_lds) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < static_cast<int>(ncnt); i += blockDim.x) cnt[i] = hist[i];
   }
 }
 
-// One thread per row: rewrite the row's per-tile counts into exclusive
-// offsets (in tile order) and emit the row total.
+// One wavefront per row: rewrite the row's per-tile counts into exclusive offsets
+// (in tile order, 64 tiles per step with a wave prefix sum) and emit the row total.
 __global__ __launch_bounds__(256) void k2q_rowscan(const int32_t* __restrict__ cu_blocks,
                                                    const int64_t* __restrict__ tri_prefix, int nseq,
                                                    int G, int64_t rows, int32_t* __restrict__ counters,
                                                    int32_t* __restrict__ totals) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (r >= rows) return;  // whole wavefronts
   const int64_t gb = r / G;
   const int g = static_cast<int>(r % G);
   int s = upper_index(cu_blocks, nseq + 1, gb);
   while (s < nseq && cu_blocks[s + 1] <= gb) ++s;
   const int b = static_cast<int>(gb - cu_blocks[s]);
   const int nb = cu_blocks[s + 1] - cu_blocks[s];
-  int32_t running = 0;
-  for (int qb = b; qb < nb; ++qb) {
-    const int64_t idx = tri_prefix[s] + static_cast<int64_t>(G) * qb * (qb + 1) / 2 +
-                        static_cast<int64_t>(b) * G + g;
-    const int32_t c = counters[idx];
-    counters[idx] = running;
-    running += c;
+  int32_t carry = 0;
+  for (int q0 = b; q0 < nb; q0 += kWave) {  // trip count uniform over the wavefront
+    const int qb = q0 + lane;
+    int64_t idx = 0;
+    int32_t c = 0;
+    if (qb < nb) {
+      idx = tri_prefix[s] + static_cast<int64_t>(G) * qb * (qb + 1) / 2 + static_cast<int64_t>(b) * G + g;
+      c = counters[idx];
+    }
+    int32_t x = c;  // inclusive prefix over the lanes
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int32_t y = __shfl_up(x, o, kWave);
+      if (lane >= o) x += y;
+    }
+    if (qb < nb) counters[idx] = carry + x - c;
+    carry += __shfl(x, kWave - 1, kWave);
   }
-  totals[r] = running;
+  if (lane == 0) totals[r] = carry;
 }
 
 // Exclusive scan of totals[0..rows) into row_ptr[0..rows], one workgroup of 1024.
@@ -273,6 +302,7 @@ extern "C" int msa_k2q_build(const int32_t* indices, const int32_t* cu_seqlens,
   if (num_seqs <= 0 || total_tokens < 0 || groups <= 0 || topk_slots < 0 || block_size <= 0 ||
       total_blocks < 0 || counter_elems < 0)
     return kErrInvalidArgument;
+  if (block_size * groups * topk_slots >= (int64_t(1) << 31)) return kErrUnsupported;  // edges per tile in int32
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t rows = total_blocks * groups;
   const int64_t capacity = total_tokens * groups * topk_slots;
@@ -286,7 +316,7 @@ extern "C" int msa_k2q_build(const int32_t* indices, const int32_t* cu_seqlens,
   const int K = static_cast<int>(topk_slots), B = static_cast<int>(block_size);
   hipLaunchKernelGGL(k2q_count, dim3(static_cast<unsigned>(total_blocks)), dim3(256), 0, st, indices,
                      cu_seqlens, cu_block_lens, tri_prefix, nseq, G, K, B, counters);
-  hipLaunchKernelGGL(k2q_rowscan, dim3(grid_1d(rows, 256)), dim3(256), 0, st, cu_block_lens, tri_prefix,
+  hipLaunchKernelGGL(k2q_rowscan, dim3(grid_1d(rows, 4)), dim3(256), 0, st, cu_block_lens, tri_prefix,
                      nseq, G, rows, counters, totals);
   hipLaunchKernelGGL(k2q_ptrscan, dim3(1), dim3(1024), 0, st, totals, rows, row_ptr);
   hipLaunchKernelGGL(k2q_scatter_par, dim3(static_cast<unsigned>(total_blocks), static_cast<unsigned>(G)),
