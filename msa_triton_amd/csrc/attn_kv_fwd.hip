@@ -50,17 +50,17 @@ struct FwdSmem {
 }  // namespace
 
 // Per row, the first edge whose query token is >= c * tc, for c = 0..nch
-// (bounds[c * rows + row]); bound nch is the row end.
+// (bounds[c * rows + row]); bound nch is the row end. One wavefront per row, one
+// lane per chunk boundary (independent binary searches over the row's edges).
 __global__ __launch_bounds__(256) void kv_chunk_bounds(const int32_t* __restrict__ row_ptr,
                                                        const int32_t* __restrict__ qidx, int64_t rows, int64_t T,
                                                        int64_t tc, int nch, int32_t* __restrict__ bounds) {
-  const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t r = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (r >= rows) return;
   const int32_t a = row_ptr[r], b = row_ptr[r + 1];
-  int32_t lo = a;
-  for (int c = 0; c <= nch; ++c) {
+  for (int c = threadIdx.x & 63; c <= nch; c += kWave) {
     const int64_t t = c * tc < T ? c * tc : T;
-    int32_t hi = b;
+    int32_t lo = a, hi = b;
     while (lo < hi) {
       const int32_t mid = (lo + hi) >> 1;
       if (qidx[mid] < t) lo = mid + 1; else hi = mid;
@@ -475,7 +475,7 @@ void kv_plan_launch(const KvPlan& p, const int32_t* row_ptr, const int32_t* qidx
   if (p.rows <= 0) return;
   char* b = static_cast<char*>(base);
   int32_t* bounds = reinterpret_cast<int32_t*>(b + p.bounds);
-  hipLaunchKernelGGL(kv_chunk_bounds, dim3(grid_1d(p.rows, 256)), dim3(256), 0, st, row_ptr, qidx, p.rows, T, p.tc,
+  hipLaunchKernelGGL(kv_chunk_bounds, dim3(grid_1d(p.rows, 4)), dim3(256), 0, st, row_ptr, qidx, p.rows, T, p.tc,
                      static_cast<int>(p.nch), bounds);
   hipLaunchKernelGGL(kv_item_scan, dim3(static_cast<unsigned>(p.nch)), dim3(1024), 0, st, bounds, p.rows,
                      static_cast<int>(p.epi), p.max_items, reinterpret_cast<int32_t*>(b + p.starts),
