@@ -16,9 +16,9 @@
 //   combine       mass, delta per row (FP64, slot order)
 //   main    (B2)  dK, dV per key block (registers) and dQ per (row, block)
 //                 partials                                  KV-major, 16 keys per wave
-//   accumulate    dK, dV item partials -> FP32 key accumulators (item order)
+//   accumulate    dK, dV item partials -> FP32 key accumulators (item order);
+//                 the last chunk writes bf16 dK (times scale), dV
 //   dq combine    dQ = scale * sum of the row's block partials (FP64, slot order)
-//   finalize      FP32 key accumulators -> bf16 dK (times scale), dV
 // No floating-point atomics; every sum has a fixed order. Partial records are
 // written and read once each, with non-temporal (streaming) stores and loads.
 #include "attn_kv_common.hpp"
@@ -631,16 +631,22 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
 
 // For chunk c: add each row's item partials (in item order) into the FP32 key
 // accumulators acc[0 = dK, 1 = dV][key][group][dim]. Thread e owns fragment slot e
-// of the partial layout (four keys, one dim). grid (rows, DP / 8).
+// of the partial layout (four keys, one dim). grid (rows, DP / 8). The first chunk
+// stores its sums (every key of every row: no separate clearing pass), the last one
+// writes the bf16 results dK = scale * acc[0], dV = acc[1] instead of acc; a single
+// chunk does both and never touches acc. Per key the value is the same FP32 chain
+// acc = ((s_0 + s_1) + ...) as with a cleared accumulator (0 + s_0 == s_0: the item
+// sums start from +0, so s_0 is never -0).
 template <int DP>
 __global__ __launch_bounds__(256) void kv_bwd_accumulate(const int32_t* __restrict__ cu,
                                                          const int32_t* __restrict__ cu_blocks,
                                                          const int32_t* __restrict__ starts, int nseq, int G, int D,
                                                          int B, int64_t T, const float* __restrict__ kvpart,
-                                                         float* __restrict__ acc) {
+                                                         float* __restrict__ acc, int first, int last, float scale,
+                                                         uint16_t* __restrict__ dk, uint16_t* __restrict__ dv) {
   const int64_t row = blockIdx.x;
   const int i0 = starts[row], i1 = starts[row + 1];
-  if (i0 == i1) return;
+  if (i0 == i1 && !first && !last) return;
   const RowGeom rg = row_geom(cu, cu_blocks, nseq, row, G, B);
   constexpr int NDT = DP / 16;
   const int e = blockIdx.y * 256 + threadIdx.x;  // fragment slot: (wave, dt, lane)
@@ -657,8 +663,18 @@ __global__ __launch_bounds__(256) void kv_bwd_accumulate(const int32_t* __restri
   for (int i = 0; i < 4; ++i) {
     if (kl0 + i < rg.nk) {
       const int64_t off = ((rg.kb + kl0 + i) * G + rg.g) * D + d;
-      acc[off] += sk[i];
-      acc[T * G * D + off] += sv[i];
+      float xk = sk[i], xv = sv[i];
+      if (!first) {
+        xk = acc[off] + xk;
+        xv = acc[T * G * D + off] + xv;
+      }
+      if (last) {
+        if (dk) dk[off] = f32_to_bf16_bits(xk * scale);
+        if (dv) dv[off] = f32_to_bf16_bits(xv);
+      } else {
+        acc[off] = xk;
+        acc[T * G * D + off] = xv;
+      }
     }
   }
 }
@@ -711,20 +727,6 @@ __global__ __launch_bounds__(256) void kv_bwd_dq_combine(const int32_t* __restri
   const uint32_t w1 = f32_to_bf16_bits(static_cast<float>(a2 * scale)) |
                       (static_cast<uint32_t>(f32_to_bf16_bits(static_cast<float>(a3 * scale))) << 16);
   *reinterpret_cast<uint2*>(dq + th * D + 4 * sub) = make_uint2(w0, w1);
-}
-
-__global__ __launch_bounds__(256) void kv_bwd_zero(float* __restrict__ p, int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i < n) p[i] = 0.f;
-}
-
-// FP32 key accumulators -> bf16 dK = scale * acc[0] and dV = acc[1].
-__global__ __launch_bounds__(256) void kv_bwd_finalize(const float* __restrict__ acc, int64_t n, float scale,
-                                                       uint16_t* __restrict__ dk, uint16_t* __restrict__ dv) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= n) return;
-  if (dk) dk[i] = f32_to_bf16_bits(acc[i] * scale);
-  if (dv) dv[i] = f32_to_bf16_bits(acc[n + i]);
 }
 
 static int nk_of_dim(int D) { return D <= 32 ? 1 : (D <= 64 ? 2 : 4); }
@@ -783,7 +785,6 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   const float scale2 = scale * kLog2e;
   const int nk = nk_of_dim(D);
   const bool fd = D == 32 * nk;
-  const int64_t nacc = T * G * D;
   const bool need_kv = dk != nullptr || dv != nullptr;
 
   // With the forward's FP32 output, flat rows take delta = O . dO and the forward's
@@ -792,7 +793,6 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   const int all_rows = o32 == nullptr;
   const uint32_t rmagic = ratio_magic(Hq / G);  // rows x ratio < 512 * 512^2 < 2^32
   hipLaunchKernelGGL(kv_bwd_center, dim3(grid_1d(T * Hq, 8)), dim3(256), 0, st, ob, o32, gb, T * Hq, D, rs);
-  if (need_kv) hipLaunchKernelGGL(kv_bwd_zero, dim3(grid_1d(2 * nacc, 256)), dim3(256), 0, st, acc, 2 * nacc);
   kv_plan_launch(L.stat_plan, row_ptr, qidx, T, sbase, st);
   kv_plan_launch(L.main_plan, row_ptr, qidx, T, mbase, st);
   const KvPlan& sp = L.stat_plan;
@@ -828,18 +828,20 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       if (need_kv) {
         const int32_t* starts = kv_plan_starts(mp, mbase, c);
         const dim3 agrid(static_cast<unsigned>(rows), static_cast<unsigned>(32 * nk / 8));
-        if (nk == 1) hipLaunchKernelGGL(kv_bwd_accumulate<32>, agrid, dim3(256), 0, st, cu, cu_blocks, starts, nseq, G, D, B, T, kvpart, acc);
-        else if (nk == 2) hipLaunchKernelGGL(kv_bwd_accumulate<64>, agrid, dim3(256), 0, st, cu, cu_blocks, starts, nseq, G, D, B, T, kvpart, acc);
-        else hipLaunchKernelGGL(kv_bwd_accumulate<128>, agrid, dim3(256), 0, st, cu, cu_blocks, starts, nseq, G, D, B, T, kvpart, acc);
+        const int first = c == 0, last = c + 1 == sp.nch;
+        auto* dkb = static_cast<uint16_t*>(dk);
+        auto* dvb = static_cast<uint16_t*>(dv);
+#define MSA_BWD_ACC(DPV) hipLaunchKernelGGL(kv_bwd_accumulate<DPV>, agrid, dim3(256), 0, st, cu, cu_blocks, starts, nseq, G, D, B, T, kvpart, acc, first, last, scale, dkb, dvb)
+        if (nk == 1) MSA_BWD_ACC(32);
+        else if (nk == 2) MSA_BWD_ACC(64);
+        else MSA_BWD_ACC(128);
+#undef MSA_BWD_ACC
       }
     }
     if (dq)
       hipLaunchKernelGGL(kv_bwd_dq_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu, nseq, t0,
                          t1, Hq, G, D, K, B, static_cast<double>(scale), dqpart, static_cast<uint16_t*>(dq));
   }
-  if (need_kv)
-    hipLaunchKernelGGL(kv_bwd_finalize, dim3(grid_1d(nacc, 256)), dim3(256), 0, st, acc, nacc, scale,
-                       static_cast<uint16_t*>(dk), static_cast<uint16_t*>(dv));
   return status_from(hipGetLastError());
 }
 
