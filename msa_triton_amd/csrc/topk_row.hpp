@@ -40,9 +40,43 @@ __device__ __forceinline__ uint64_t row16_max_u64(uint64_t v) {
   return v;
 }
 
+// A lane's sorted cache of its four largest keys below a bound (0 = empty slot):
+// c[0] > c[1] > c[2] > c[3]. Keys are unique (the block id is in the low word).
+struct Top4 {
+  uint64_t c[4];
+  __device__ __forceinline__ void insert(uint64_t x) {
+    // x enters at the bottom when it beats the smallest entry, then bubbles up
+    if (x > c[3]) c[3] = x;
+#pragma unroll
+    for (int i = 3; i > 0; --i) {
+      const uint64_t hi = c[i] > c[i - 1] ? c[i] : c[i - 1];
+      const uint64_t lo = c[i] > c[i - 1] ? c[i - 1] : c[i];
+      c[i - 1] = hi;
+      c[i] = lo;
+    }
+  }
+  template <int VPL>
+  __device__ __forceinline__ void fill(const uint64_t (&key)[VPL], uint64_t below) {
+    c[0] = c[1] = c[2] = c[3] = 0;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v)
+      if (key[v] < below) insert(key[v]);
+  }
+  __device__ __forceinline__ void pop() {
+    c[0] = c[1];
+    c[1] = c[2];
+    c[2] = c[3];
+    c[3] = 0;
+  }
+};
+
 // Sixteen lanes (one DPP row) per (token, group) row, four rows per wavefront: lane
 // j of a row holds blocks j, j + 16, ... (VPL values). Each pick is a 16-lane DPP
-// max of the lanes' running best keys; only the owner lane rescans its values.
+// max of the lanes' best remaining keys. A lane keeps its four largest remaining keys
+// sorted (Top4); the owner of a pick pops it and refills from its values below the
+// popped key only once its cache is empty. The picks are those of a full rescan
+// after every pick: the cache always holds the lane's largest keys below its last
+// popped one.
 // Every lane of the wavefront must call it (row >= rows: no output, but the lanes
 // still take part in the DPP and shuffle steps). The selection key is the ordered
 // float bits << 32 | ~block, so one 64-bit comparison implements "larger value,
@@ -72,26 +106,21 @@ __device__ __forceinline__ void topk_row16(const float* __restrict__ scores, con
     }
     key[v] = (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(b));
   }
-  uint64_t best = 0;
-#pragma unroll
-  for (int v = 0; v < VPL; ++v) best = key[v] > best ? key[v] : best;
+  Top4 top;
+  top.fill(key, ~uint64_t(0));
 
   // every row of the wave runs the same number of picks (the wave maximum)
   int sel_w = sel;
 #pragma unroll
   for (int o = 16; o < 64; o <<= 1) sel_w = max(sel_w, __shfl_xor(sel_w, o, kWave));
   for (int it = 0; it < sel_w; ++it) {
-    const uint64_t win = row16_max_u64(best);
+    const uint64_t win = row16_max_u64(top.c[0]);
     const int b = static_cast<int>(~static_cast<uint32_t>(win));
     const uint32_t k = static_cast<uint32_t>(win >> 32);
     if (sub == 0 && it < sel) dst[it] = (k == kKeyNegInf) ? -1 : b;
-    if ((b & 15) == sub && it < sel) {
-      best = 0;
-#pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        if (key[v] == win) key[v] = 0;
-        best = key[v] > best ? key[v] : best;
-      }
+    if ((b & 15) == sub && it < sel) {  // win == top.c[0] of this lane
+      top.pop();
+      if (top.c[0] == 0) top.fill(key, win);
     }
   }
   if (live)
