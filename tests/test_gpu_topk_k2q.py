@@ -154,3 +154,24 @@ def test_k2q_baseline_sized(lengths, groups, k, block, device):
     scores = torch.randn(total, groups, (max(lengths) + block - 1) // block, generator=gen)
     ids = msa.m3_topk(scores.to(device), cu_tensor(lengths, device), block_size=block, topk_blocks=k, local_blocks=1)
     _check_csr(ids.cpu(), lengths, block, device)
+
+
+@pytest.mark.parametrize("length,block,k", [(1024, 4, 16), (512, 4, 12), (2048, 4, 32)])
+def test_topk_winners_concentrated_in_one_lane(length, block, k, device):
+    """Sixteen lanes share a row (lane j holds blocks j, j + 16, ...) and each keeps a
+    cache of its four largest remaining keys: rows whose winners all sit in one lane
+    (blocks b with b % 16 == row % 16 lead by 10) refill that cache several times;
+    some leaders tie (ascending block order) and a few are -inf."""
+    gen = torch.Generator().manual_seed(29)
+    groups, nb = 2, (length + block - 1) // block
+    scores = torch.randn(length, groups, nb, generator=gen)
+    rows = torch.arange(length).view(-1, 1, 1)
+    lead = (torch.arange(nb).view(1, 1, -1) % 16) == (rows % 16)
+    scores = torch.where(lead, scores + 10.0, scores)
+    scores[::5, :, ::32] = 12.5  # ties among the leaders (and among the other lanes' blocks)
+    scores[::9, 1, 16::48] = float("-inf")
+    cu = cu_tensor([length], device)
+    for local in (0, 1, 3):
+        got = msa.m3_topk(scores.to(device), cu, block_size=block, topk_blocks=k, local_blocks=local)
+        ref = O.topk(scores.numpy(), [0, length], block_size=block, topk_blocks=k, local_blocks=local)
+        np.testing.assert_array_equal(got.cpu().numpy(), ref)
