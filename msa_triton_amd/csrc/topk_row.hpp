@@ -40,15 +40,16 @@ __device__ __forceinline__ uint64_t row16_max_u64(uint64_t v) {
   return v;
 }
 
-// A lane's sorted cache of its four largest keys below a bound (0 = empty slot):
-// c[0] > c[1] > c[2] > c[3]. Keys are unique (the block id is in the low word).
-struct Top4 {
-  uint64_t c[4];
+// A lane's sorted cache of its N largest keys below a bound (0 = empty slot):
+// c[0] > c[1] > ... > c[N - 1]. Keys are unique (the block id is in the low word).
+template <int N>
+struct TopN {
+  uint64_t c[N];
   __device__ __forceinline__ void insert(uint64_t x) {
     // x enters at the bottom when it beats the smallest entry, then bubbles up
-    if (x > c[3]) c[3] = x;
+    if (x > c[N - 1]) c[N - 1] = x;
 #pragma unroll
-    for (int i = 3; i > 0; --i) {
+    for (int i = N - 1; i > 0; --i) {
       const uint64_t hi = c[i] > c[i - 1] ? c[i] : c[i - 1];
       const uint64_t lo = c[i] > c[i - 1] ? c[i - 1] : c[i];
       c[i - 1] = hi;
@@ -57,23 +58,24 @@ struct Top4 {
   }
   template <int VPL>
   __device__ __forceinline__ void fill(const uint64_t (&key)[VPL], uint64_t below) {
-    c[0] = c[1] = c[2] = c[3] = 0;
+#pragma unroll
+    for (int i = 0; i < N; ++i) c[i] = 0;
 #pragma unroll
     for (int v = 0; v < VPL; ++v)
       if (key[v] < below) insert(key[v]);
   }
   __device__ __forceinline__ void pop() {
-    c[0] = c[1];
-    c[1] = c[2];
-    c[2] = c[3];
-    c[3] = 0;
+#pragma unroll
+    for (int i = 0; i + 1 < N; ++i) c[i] = c[i + 1];
+    c[N - 1] = 0;
   }
 };
 
 // Sixteen lanes (one DPP row) per (token, group) row, four rows per wavefront: lane
 // j of a row holds blocks j, j + 16, ... (VPL values). Each pick is a 16-lane DPP
-// max of the lanes' best remaining keys. A lane keeps its four largest remaining keys
-// sorted (Top4); the owner of a pick pops it and refills from its values below the
+// max of the lanes' best remaining keys. A lane keeps its largest remaining keys
+// sorted (TopN: 4 for up to 16 values per lane, 8 above, where a lane more often
+// holds several winners); the owner of a pick pops it and refills from its values below the
 // popped key only once its cache is empty. The picks are those of a full rescan
 // after every pick: the cache always holds the lane's largest keys below its last
 // popped one.
@@ -106,7 +108,7 @@ __device__ __forceinline__ void topk_row16(const float* __restrict__ scores, con
     }
     key[v] = (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(b));
   }
-  Top4 top;
+  TopN<(VPL > 16 ? 8 : 4)> top;
   top.fill(key, ~uint64_t(0));
 
   // every row of the wave runs the same number of picks (the wave maximum)
