@@ -170,7 +170,8 @@ __global__ __launch_bounds__(1024) void k2q_ptrscan(const int32_t* __restrict__ 
 // in order through per-wave id counts, and a running count per id carries the
 // order across steps. The position is row_ptr[row] + the tile's offset in the row
 // (from k2q_rowscan) + that rank, i.e. the same (query, slot) order as the
-// sequential scatter, duplicates included.
+// sequential scatter, duplicates included. The first two terms are staged in LDS per
+// id once, and each step's indices are loaded one step ahead.
 constexpr int kParIds = 1024;
 constexpr int kParIdBits = 10;
 
@@ -184,6 +185,7 @@ __global__ __launch_bounds__(256) void k2q_scatter_par(const int32_t* __restrict
                                                        int32_t* __restrict__ slot_idx) {
   __shared__ int32_t running[kParIds];
   __shared__ int32_t wcnt[4][kParIds];
+  __shared__ int32_t rbase[kParIds];  // row_ptr[row of id] + the tile's offset inside that row
   const TileInfo ti = tile_info(blockIdx.x, cu, cu_blocks, tri_prefix, nseq, G, B);
   const int g = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
@@ -207,25 +209,31 @@ __global__ __launch_bounds__(256) void k2q_scatter_par(const int32_t* __restrict
     }
     return;
   }
+  const int32_t* cnt = counters + ti.counter_base;  // the tile's offset inside each row
+  const int64_t row_base = static_cast<int64_t>(cu_blocks[ti.seq]) * G;
   for (int i = tid; i < nid; i += 256) {
     running[i] = 0;
     wcnt[0][i] = wcnt[1][i] = wcnt[2][i] = wcnt[3][i] = 0;
+    const int64_t lr = static_cast<int64_t>(i) * G + g;
+    rbase[i] = row_ptr[row_base + lr] + cnt[lr];
   }
   __syncthreads();
-  const int32_t* cnt = counters + ti.counter_base;  // the tile's offset inside each row
-  const int64_t row_base = static_cast<int64_t>(cu_blocks[ti.seq]) * G;
-  const int64_t nedge = (ti.tok_end - ti.tok_begin) * K;
+  // a tile holds at most B tokens: B * K < 2^31 edges (checked on the host)
+  const int nedge = static_cast<int>((ti.tok_end - ti.tok_begin) * K);
   const uint64_t lt = (uint64_t(1) << lane) - 1;
-  for (int64_t base = 0; base < nedge; base += 256) {
-    const int64_t e = base + tid;
-    int id = -1, slot = 0;
-    int64_t t = 0;
-    if (e < nedge) {
-      t = ti.tok_begin + e / K;
-      slot = static_cast<int>(e % K);
-      const int v = indices[(t * G + g) * K + slot];
-      if (v >= 0 && v < nb && v <= ti.qb) id = v;
-    }
+  auto load_id = [&](int e) {
+    int v = -1;
+    if (e < nedge) v = indices[((ti.tok_begin + e / K) * G + g) * K + e % K];
+    return v;
+  };
+  int vnext = load_id(tid);
+  for (int base = 0; base < nedge; base += 256) {
+    const int e = base + tid;
+    const int v = vnext;
+    vnext = load_id(e + 256);  // next step's index, in flight during this one
+    const int64_t t = ti.tok_begin + e / K;
+    const int slot = e % K;
+    const int id = (e < nedge && v >= 0 && v < nb && v <= ti.qb) ? v : -1;
     const bool on = id >= 0;
     uint64_t match = __ballot(on);
 #pragma unroll
@@ -240,8 +248,7 @@ __global__ __launch_bounds__(256) void k2q_scatter_par(const int32_t* __restrict
     if (on) {
       int before = running[id] + rank;
       for (int w2 = 0; w2 < wid; ++w2) before += wcnt[w2][id];
-      const int64_t lr = static_cast<int64_t>(id) * G + g;
-      const int64_t pos = static_cast<int64_t>(row_ptr[row_base + lr]) + cnt[lr] + before;
+      const int64_t pos = static_cast<int64_t>(rbase[id]) + before;
       query_idx[pos] = static_cast<int32_t>(t);
       slot_idx[pos] = slot;
     }
