@@ -28,7 +28,6 @@ if ROOT not in sys.path:
 
 MFMA_BF16_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 FLOP/clk (dense bf16)
 HBM_PEAK_GBPS = 8000.0
-ENTRY_NAMES = {"attn_fwd": "msa_attn_fwd", "attn_bwd": "msa_attn_bwd"}
 
 # BASELINE.json configs (c1 is the reference's CPU-runnable case).
 CONFIGS = {
@@ -88,27 +87,48 @@ def stage_work(cfg):
     topk_bytes = causal_blocks * g * 4 + T * g * k * 4
     rows = sum((n + b - 1) // b for n in cfg["lengths"]) * g
     csr_bytes = T * g * k * 4 + (rows + 1) * 4 + 2 * T * g * k * 4 + (len(cfg["lengths"]) + 1) * 4
-    # score backward: read ds and the tie codes of every valid (t, g, b), gather one index_k row
-    # (dq) and one index_q row (dk) per valid entry, write dq and dk
-    score_bwd_bytes = causal_blocks * g * (4 + 4 + 2 * di * 2) + T * g * di * 2 + T * di * 2
+    # score backward, unavoidable HBM bytes: ds and the tie code of every valid (t, g, b) read,
+    # index_q / index_k read once, dq / dk written (the per-entry winner-row gathers, 512 B per
+    # valid entry at Di = 128, come from the caches: both inputs total 40 MiB at c4)
+    score_bwd_bytes = causal_blocks * g * (4 + 4) + 2 * (T * g * di * 2 + T * di * 2)
     return score_flops, topk_bytes, csr_bytes, score_bwd_bytes
 
 
-def measured_traffic(config, entry):
-    """HBM bytes per call of a C-ABI entry point from the committed rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE, calibrated against a copy of known size), if present."""
+def measured_traffic(config, name, table="kernels"):
+    """HBM bytes per call of one kernel (table "kernels": summed over its launches in one
+    entry-point call) or one entry point (table "entries") from the committed rocprofv3
+    PMC summary (FETCH_SIZE and WRITE_SIZE, calibrated against a copy of known size), if
+    present."""
     path = os.path.join(ROOT, "profiles", f"attn_{config}_traffic.json")
     try:
         with open(path) as f:
             data = json.load(f)
-        return data["entries"][entry]["bytes_per_call"]
+        return data[table][name]["bytes_per_call"]
     except (OSError, KeyError, ValueError):
         return None
 
 
-def _pmc_rows(directory, counter):
-    """(dispatch id, kernel name, value in bytes) of one rocprofv3 counter pass, in dispatch order.
-    FETCH_SIZE / WRITE_SIZE are reported in KiB per dispatch."""
+def cpu_info():
+    """Host CPU description for the CPU baseline: logical CPUs, the CPUs this process may
+    run on, the model name and torch's intra-op threads."""
+    import torch
+
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity_cpus": len(os.sched_getaffinity(0)), "cpu_model": model,
+            "torch_threads": torch.get_num_threads()}
+
+
+def _pmc_rows(directory, counter, unit=1024.0):
+    """(dispatch id, kernel name, value x unit) of one rocprofv3 counter pass, in dispatch order.
+    FETCH_SIZE / WRITE_SIZE are reported in KiB per dispatch (unit 1024: bytes)."""
     import csv
     import glob
 
@@ -117,7 +137,7 @@ def _pmc_rows(directory, counter):
         with open(path) as f:
             for r in csv.DictReader(f):
                 if r["Counter_Name"] == counter:
-                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"]) * 1024.0))
+                    rows.append((int(r["Dispatch_Id"]), r["Kernel_Name"], float(r["Counter_Value"]) * unit))
     rows.sort()
     return rows
 
@@ -142,20 +162,36 @@ def summarize_pmc(config, fetch_dir, write_dir):
         out["calibration"][f"{key}_reported_bytes"] = calib
         out["calibration"][f"{key}_scale"] = round(scale, 4)
         first_bwd = next(i for i, r in enumerate(rows) if "kv_bwd_" in r[1])
+        last_bwd = max(i for i, r in enumerate(rows) if "kv_bwd_" in r[1])
         first_fwd = max(i for i, r in enumerate(rows[:first_bwd]) if "kv_chunk_bounds" in r[1])
-        for i, (_, name, value) in enumerate(rows[first_fwd:], start=first_fwd):
-            entry = "msa_attn_fwd" if i < first_bwd else "msa_attn_bwd"
+        for i, (_, name, value) in enumerate(rows):
+            if "copy" in name.lower():
+                continue
+            entry = ("msa_attn_fwd" if first_fwd <= i < first_bwd else
+                     "msa_attn_bwd" if first_bwd <= i <= last_bwd else "stages")
             short = name.split("(")[0].replace("void ", "").replace("msa::", "")
             d = per_kernel.setdefault((entry, short), {"dispatches": 0, "read": 0.0, "write": 0.0})
             if key == "read":
                 d["dispatches"] += 1
             d[key] += value * scale
-            e = out["entries"].setdefault(entry, {"read_bytes": 0.0, "write_bytes": 0.0})
-            e[f"{key}_bytes"] += value * scale
+            if entry != "stages":
+                e = out["entries"].setdefault(entry, {"read_bytes": 0.0, "write_bytes": 0.0})
+                e[f"{key}_bytes"] += value * scale
     for e in out["entries"].values():
         e["read_bytes"] = int(e["read_bytes"])
         e["write_bytes"] = int(e["write_bytes"])
         e["bytes_per_call"] = e["read_bytes"] + e["write_bytes"]
+    out["kernels"] = {}
+    for (entry, name), d in per_kernel.items():
+        base = name.split("<")[0]
+        if entry == "stages" and base.startswith("kv_"):  # the indexer KL's work plans
+            base = "kl_" + base
+        k = out["kernels"].setdefault(base, {"entry": entry, "dispatches": 0, "read_bytes": 0, "write_bytes": 0})
+        k["dispatches"] += d["dispatches"]
+        k["read_bytes"] += int(d["read"])
+        k["write_bytes"] += int(d["write"])
+    for k in out["kernels"].values():
+        k["bytes_per_call"] = k["read_bytes"] + k["write_bytes"]
     path = os.path.join(ROOT, "profiles", f"attn_{config}_traffic.json")
     with open(path, "w") as f:
         json.dump(out, f, indent=1)
@@ -172,6 +208,65 @@ def summarize_pmc(config, fetch_dir, write_dir):
         print(f"| {entry} | {e['read_bytes'] / gib:.2f} | {e['write_bytes'] / gib:.2f} | {tot / 1e9:.2f} | "
               f"{tot / 8e12 * 1e3:.2f} ms |")
     print(f"wrote {path}", file=sys.stderr)
+
+
+SQ_COUNTERS = ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_MFMA_MOPS_BF16", "SQ_VALU_MFMA_BUSY_CYCLES",
+               "SQ_BUSY_CYCLES", "SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT", "SQ_WAVES")
+SHADER_ENGINES = 32    # MI355X: 8 XCDs x 4 shader engines; SQ_BUSY_CYCLES is summed over them
+SIMDS = 1024           # 256 CUs x 4 SIMDs; SQ_VALU_MFMA_BUSY_CYCLES is summed over them
+
+
+def summarize_sq(config, directory, stats_csv=None):
+    """Per-kernel instruction and MFMA counters of one --pmc-pass run (one call of every
+    stage) as a markdown table: VALU, MFMA and LDS instructions; bf16 MFMA FLOPs
+    (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512); MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (SIMDS x
+    SQ_BUSY_CYCLES / SHADER_ENGINES), the share of the kernel's cycles the SIMDs' matrix
+    cores were busy; LDS bank-conflict cycles per LDS instruction; LDS bytes per workgroup
+    and scratch bytes per lane of the dispatch. With a rocprofv3 kernel-stats CSV, also the
+    counted bf16 FLOPs over the traced average duration against the 2.4 GHz peak."""
+    import csv
+    import glob
+
+    per, res, dispatches = {}, {}, {}
+    for path in glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True):
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] not in SQ_COUNTERS:
+                    continue
+                short = r["Kernel_Name"].split("(")[0].replace("void ", "").replace("msa::", "")
+                d = per.setdefault(short, {})
+                d[r["Counter_Name"]] = d.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+                res[short] = (r.get("LDS_Block_Size"), r.get("Scratch_Size"))
+                dispatches.setdefault(short, set()).add(r["Dispatch_Id"])
+    durations = {}
+    if stats_csv:
+        with open(stats_csv) as f:
+            for r in csv.DictReader(f):
+                short = r["Name"].split("(")[0].replace("void ", "").replace("msa::", "")
+                durations[short] = float(r["AverageNs"]) * 1e-9
+    print(f"Counters of one --pmc-pass run (config {config}; sums over a kernel's dispatches in one call).")
+    print()
+    print("| kernel | dispatches | VALU insts | MFMA insts | VALU:MFMA | bf16 MFMA TFLOP | MFMA busy | "
+          "MFMA FLOP rate / peak | LDS insts | LDS conflict cycles / inst | LDS B | scratch B |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|")
+    for name, d in per.items():
+        valu, mfma = d.get("SQ_INSTS_VALU", 0.0), d.get("SQ_INSTS_MFMA", 0.0)
+        if valu == 0 and mfma == 0 or name.startswith("at::") or name.startswith("__amd"):
+            continue
+        flops = d.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) * 512
+        busy = d.get("SQ_BUSY_CYCLES", 0.0) / SHADER_ENGINES
+        mbusy = d.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+        lds = d.get("SQ_INSTS_LDS", 0.0)
+        conf = d.get("SQ_LDS_BANK_CONFLICT", 0.0)
+        ratio = f"{valu / mfma:.1f}" if mfma else "-"
+        disp = len(dispatches[name])
+        rate = "-"
+        if flops and name in durations:
+            rate = f"{flops / (durations[name] * disp) / (MFMA_BF16_PEAK_TFLOPS * 1e12):.1%}"
+        ldsb, scr = res.get(name, (None, None))
+        print(f"| `{name}` | {disp} | {valu:.3g} | {mfma:.3g} | {ratio} | {flops / 1e12:.3f} | "
+              f"{(mbusy / (SIMDS * busy) if busy and mfma else 0):.1%} | {rate} | {lds:.3g} | "
+              f"{(conf / lds if lds else 0):.2f} | {ldsb} | {scr} |")
 
 
 class Harness:
@@ -275,17 +370,32 @@ def time_events(fn, repeats, warmup=1):
             "p90": samples[min(len(samples) - 1, int(0.9 * len(samples)))]}
 
 
+def peak_bytes(fn):
+    """Device memory one call of fn allocates at its peak above what was allocated before
+    it (torch caching-allocator statistics, reset before the call)."""
+    import torch
+
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    fn()
+    torch.cuda.synchronize()
+    return torch.cuda.max_memory_allocated() - base
+
+
 def cpu_baseline(cfg, tensors, ids_cpu, budget_s):
     """Eager CPU restatement (oracle/eager_baseline.py) on the last query rows of the
     first sequence, row-chunked, until ~budget_s seconds of CPU work; returns the
-    effective fwd+bwd TFLOP/s of the sample."""
+    effective fwd+bwd TFLOP/s of the sample. Also times the eager score (fp32 Q.K^T over
+    the dense key range + block amax) on the last query rows for ~budget_s / 3 seconds
+    and the eager top-k selection on every row of the first sequence."""
     import torch
 
-    from oracle.eager_baseline import eager_rows_fwd_bwd
+    from oracle.eager_baseline import eager_rows_fwd_bwd, eager_score_rows, eager_topk
 
     iq, ik, q, k, v, dout = tensors
     n0 = cfg["lengths"][0]
-    b, kk, hq, d = cfg["block"], cfg["topk"], cfg["hq"], cfg["d"]
+    b, kk, hq, d, g = cfg["block"], cfg["topk"], cfg["hq"], cfg["d"], cfg["g"]
     chunk = 64
     flops = 0.0
     rows_done = 0
@@ -304,14 +414,52 @@ def cpu_baseline(cfg, tensors, ids_cpu, budget_s):
         if time.perf_counter() - t0 > budget_s:
             break
     elapsed = time.perf_counter() - t0
+
+    # eager score on the last query rows (causal pairs counted, like the GPU stage figure)
+    score_flops, score_rows = 0.0, 0
+    ts = time.perf_counter()
+    r1 = n0
+    with torch.no_grad():
+        while r1 > 0:
+            r0 = max(0, r1 - 256)
+            eager_score_rows(iq[:n0], ik[:n0], (r0, r1), block_size=b)
+            score_flops += 2.0 * cfg["di"] * g * sum(p + 1 for p in range(r0, r1))
+            score_rows += r1 - r0
+            r1 = r0
+            if time.perf_counter() - ts > budget_s / 3:
+                break
+    score_s = time.perf_counter() - ts
+
+    # eager top-k over every row of the first sequence
+    nb = (max(cfg["lengths"]) + b - 1) // b
+    gen = torch.Generator().manual_seed(5)
+    scores = torch.randn(n0, g, nb, generator=gen)
+    positions = torch.arange(n0)
+    tt = time.perf_counter()
+    eager_topk(scores, positions, block_size=b, topk_blocks=kk, local_blocks=cfg["local"])
+    topk_s = time.perf_counter() - tt
+    topk_bytes = sum(p // b + 1 for p in range(n0)) * g * 4 + n0 * g * kk * 4
+
+    info = cpu_info()
     return {
         "value": flops / elapsed / 1e12,
         "unit": "TFLOP/s",
-        "cores": torch.get_num_threads(),
+        "cores": info["torch_threads"],
         "kind": "port",
         "sample": (f"eager bf16 restatement (eager/ops.py:153-180 math, dense masked rows, torch CPU autograd) "
                    f"fwd+bwd of the last {rows_done} query rows of the {n0}-token sequence in {chunk}-row chunks, "
                    f"{elapsed:.1f} s; effective FLOPs counted like the GPU value"),
+        "host": info,
+        "stages": {
+            "score_fwd": {"value": round(score_flops / score_s / 1e12, 6), "unit": "TFLOP/s",
+                          "sample": f"eager fp32 score (eager/ops.py:45-67) of the last {score_rows} query rows over "
+                                    f"the dense {n0}-key range, {score_s:.1f} s; causal pairs counted",
+                          "full_config_ms_extrapolated": round(score_s * 1e3 * (2.0 * cfg['di'] * g * sum(
+                              n * (n + 1) // 2 for n in cfg["lengths"])) / max(score_flops, 1.0), 1)},
+            "topk": {"value": round(topk_bytes / topk_s / 1e9, 3), "unit": "GB/s", "ms": round(topk_s * 1e3, 2),
+                     "sample": f"eager masked_fill + torch.topk (eager/ops.py:112-129) over all {n0} rows x {g} "
+                               f"groups x {nb} blocks of random fp32 scores; causal bytes counted"},
+        },
     }
 
 
@@ -326,14 +474,21 @@ def main():
     parser.add_argument("--cpu-seconds", type=float, default=15.0)
     parser.add_argument("--no-stages", action="store_true")
     parser.add_argument("--pmc-pass", action="store_true",
-                        help="for rocprofv3 --pmc: a 256 MiB calibration copy, then one attention forward and one "
-                             "backward call (direct C ABI) and exit")
+                        help="for rocprofv3 --pmc: a 256 MiB calibration copy, one attention forward and one "
+                             "backward call (direct C ABI), then one call of each other stage (score forward with "
+                             "its backward state, score backward, top-k, k2q CSR, indexer KL) and exit")
     parser.add_argument("--pmc-summarize", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                         help="read the counter CSVs of two --pmc-pass runs (FETCH_SIZE, WRITE_SIZE), write "
                              "profiles/attn_<config>_traffic.json and print a markdown table; no GPU needed")
+    parser.add_argument("--sq-summarize", metavar="SQ_DIR",
+                        help="read the counter CSVs of a --pmc-pass run with the SQ_COUNTERS and print a "
+                             "per-kernel markdown table; no GPU needed")
     args = parser.parse_args()
     if args.pmc_summarize:
         summarize_pmc(args.config, *args.pmc_summarize)
+        return
+    if args.sq_summarize:
+        summarize_sq(args.config, args.sq_summarize)
         return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (this path does not shard "
@@ -343,6 +498,7 @@ def main():
     import torch
 
     import msa_triton_amd as msa
+    from msa_triton_amd import _lib
     from msa_triton_amd.k2q import build_k2q_csr
 
     device = torch.device("cuda:0")
@@ -382,6 +538,18 @@ def main():
         torch.cuda.synchronize()
         h.bwd()
         torch.cuda.synchronize()
+        iqg, ikg = iq.detach().clone().requires_grad_(), ik.detach().clone().requires_grad_()
+        s = msa.m3_index_score(iqg, ikg, cu, max_len, block_size=block)
+        torch.cuda.synchronize()
+        s.backward(torch.ones_like(s))
+        torch.cuda.synchronize()
+        msa.m3_topk(s.detach(), cu, block_size=block, topk_blocks=topk, local_blocks=local)
+        torch.cuda.synchronize()
+        build_k2q_csr(ids, cu, block_size=block)
+        torch.cuda.synchronize()
+        iqk, ikk = iq.detach().clone().requires_grad_(), ik.detach().clone().requires_grad_()
+        msa.m3_indexer_kl(iqk, ikk, q, k, ids, cu, max_len, block_size=block).backward()
+        torch.cuda.synchronize()
         log("pmc pass done")
         return
 
@@ -405,22 +573,34 @@ def main():
     wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
     ms = ev0.elapsed_time(ev1) / args.steps
     log(f"attention fwd+bwd: {ms:.3f} ms/step (events), {wall_ms:.3f} ms/step (wall)")
+    # the same step timed one at a time: median / min / p90
+    step_stats = time_events(step, args.steps, warmup=0)
+    log(f"per-step: median {step_stats['median']:.3f} min {step_stats['min']:.3f} p90 {step_stats['p90']:.3f} ms")
 
-    # ---- per-kernel timings (direct C-ABI launches, HIP events on the launch stream)
+    # ---- per-kernel timings: direct C-ABI launches, each kernel bracketed by HIP events on
+    # its launch stream (the library's profiling hook), summed per kernel kind per call
     h = Harness(cfg, (iq, ik, q, k, v, dout), ids, cu, device)
-    kern = {
-        "attn_fwd": (h.fwd, fwd_flops),
-        "attn_bwd": (h.bwd, 2.5 * fwd_flops),
-    }
     h.fwd()
-    kt = {name: time_events(fn, args.repeats) for name, (fn, _) in kern.items()}
-    dom = max(kt, key=lambda n: kt[n]["median"])
-    achieved = kern[dom][1] / (kt[dom]["median"] * 1e-3) / 1e12
-    for name in kern:
-        log(f"{name}: {kt[name]['median']:.3f} ms, {kern[name][1] / (kt[name]['median'] * 1e-3) / 1e12:.1f} "
-            "TFLOP/s algorithmic")
+    kt = {"attn_fwd": time_events(h.fwd, args.repeats), "attn_bwd": time_events(h.bwd, args.repeats)}
+    torch.cuda.synchronize()
+    with _lib.kernel_timer() as timer:
+        for _ in range(args.repeats):
+            h.fwd()
+            h.bwd()
+    kernel_ms = {name: round(v / args.repeats, 4) for name, v in timer.ms.items() if timer.launches[name]}
+    kernel_launches = {name: timer.launches[name] // args.repeats for name in kernel_ms}
+    for name in kernel_ms:
+        log(f"  {name}: {kernel_ms[name]:.3f} ms per call ({kernel_launches[name]} launches)")
+    bwd_flops = 2.5 * fwd_flops
+    dom = "kv_bwd_main_kernel"
+    dom_ms = kernel_ms[dom]
+    achieved = bwd_flops / (dom_ms * 1e-3) / 1e12
+    entry_achieved = bwd_flops / (kt["attn_bwd"]["median"] * 1e-3) / 1e12
+    log(f"attn_fwd: {kt['attn_fwd']['median']:.3f} ms, attn_bwd: {kt['attn_bwd']['median']:.3f} ms; "
+        f"{dom}: {dom_ms:.3f} ms per backward = {achieved:.1f} TFLOP/s algorithmic")
 
     stages = {}
+    peak_mem = {}
     if not args.no_stages:
         def score_fwd():
             with torch.no_grad():
@@ -469,6 +649,20 @@ def main():
             iqg.grad = ikg.grad = None
             msa.m3_index_score(iqg, ikg, cu, max_len, block_size=block).backward(ones)
 
+        # the whole layer: score -> top-k -> attention forward, then the attention backward
+        # (dQ, dK, dV) and the score backward (an N(0,1) gradient on the valid scores)
+        iqp, ikp = iq.detach().clone().requires_grad_(), ik.detach().clone().requires_grad_()
+        qp, kp, vp = (x.detach().clone().requires_grad_() for x in (q, k, v))
+        dscore = torch.randn(scores.shape, generator=torch.Generator().manual_seed(9)).to(device)
+        dscore = dscore.masked_fill(torch.isinf(scores), 0)
+
+        def pipeline_fwd_bwd():
+            iqp.grad = ikp.grad = qp.grad = kp.grad = vp.grad = None
+            s = msa.m3_index_score(iqp, ikp, cu, max_len, block_size=block)
+            i2 = msa.m3_topk(s.detach(), cu, block_size=block, topk_blocks=topk, local_blocks=local)
+            msa.m3_sparse_attention(qp, kp, vp, i2, cu, max_len, block_size=block).backward(dout)
+            s.backward(dscore)
+
         iqk, ikk = iq.detach().clone().requires_grad_(), ik.detach().clone().requires_grad_()
 
         def indexer_kl():
@@ -489,11 +683,13 @@ def main():
                          ("topk_prepared_ms", sel_prepared), ("k2q_csr_prepared_ms", csr_prepared),
                          ("attention_fwd_ms", attn_fwd), ("pipeline_fwd_ms", pipeline_fwd),
                          ("score_fwd_bwd_ms", score_fwd_bwd), ("score_topk_fused_ms", score_topk_fused),
-                         ("pipeline_fwd_fused_ms", pipeline_fwd_fused), ("indexer_kl_fwd_bwd_ms", indexer_kl),
-                         ("indexer_kl_teacher_lse_fwd_bwd_ms", indexer_kl_lse)):
+                         ("pipeline_fwd_fused_ms", pipeline_fwd_fused), ("pipeline_fwd_bwd_ms", pipeline_fwd_bwd),
+                         ("indexer_kl_fwd_bwd_ms", indexer_kl), ("indexer_kl_teacher_lse_fwd_bwd_ms", indexer_kl_lse)):
             stages[name] = round(time_events(fn, reps)["median"], 4)
-            log(f"{name}: {stages[name]:.3f}")
+            peak_mem[name.replace("_ms", "")] = round(peak_bytes(fn) / 2**20, 1)
+            log(f"{name}: {stages[name]:.3f} (peak {peak_mem[name.replace('_ms', '')]:.0f} MiB)")
         stages["attention_fwd_bwd_ms"] = round(ms, 4)
+        peak_mem["attention_fwd_bwd"] = round(peak_bytes(step) / 2**20, 1)
         # the same autograd step with prepared sequence metadata (no host reads of
         # cu_seqlens), eager and replayed from a HIP graph capture
         seqs = msa.prepare_sequences(cu, block_size=block)
@@ -519,6 +715,20 @@ def main():
         del graph
         stages["attention_bwd_kernel_ms"] = round(kt["attn_bwd"]["median"], 4)
         stages["attention_fwd_kernel_ms"] = round(kt["attn_fwd"]["median"], 4)
+        # backward sub-stages (HIP events around each kernel): prep = centre + work plans +
+        # statistics pass of the peaked rows; main = the S / dP / dV / dK / dQ products;
+        # dkdv = item partials into dK / dV; dq = slot-order dQ merge
+        km = kernel_ms.get
+        stages["attention_bwd_prep_ms"] = round(km("kv_bwd_center", 0) + km("bwd_plan", 0) +
+                                                km("kv_bwd_stats_kernel", 0) + km("kv_bwd_stats_combine", 0), 4)
+        stages["attention_bwd_main_ms"] = km(dom, 0)
+        stages["attention_bwd_dkdv_ms"] = km("kv_bwd_accumulate", 0)
+        stages["attention_bwd_dq_ms"] = km("kv_bwd_dq_combine", 0)
+        stages["attention_fwd_partial_ms"] = km("attn_fwd_partial_kernel", 0)
+        stages["attention_fwd_combine_ms"] = km("attn_fwd_combine", 0)
+        stages["kernel_ms_per_call"] = kernel_ms
+        stages["kernel_launches_per_call"] = kernel_launches
+        stages["peak_mem_mib"] = peak_mem
         score_flops, topk_bytes, csr_bytes, score_bwd_bytes = stage_work(cfg)
         score_bwd_ms = max(stages["score_fwd_bwd_ms"] - stages["score_fwd_ms"], 1e-6)
 
@@ -529,6 +739,8 @@ def main():
         stages["roofline"] = {
             "score_fwd": {"bound": "mfma", "unit": "TFLOP/s", **frac(score_flops, stages["score_fwd_ms"],
                                                                       MFMA_BF16_PEAK_TFLOPS, 1e12)},
+            # score backward on its unavoidable HBM bytes (ds and tie codes read, the rows of
+            # index_q / index_k read once, dq / dk written); its row gathers hit the caches
             "score_bwd": {"bound": "hbm", "unit": "GB/s", **frac(score_bwd_bytes, score_bwd_ms, HBM_PEAK_GBPS, 1e9)},
             # top-k and CSR on their prepared-metadata timings (the plain stage times add host reads)
             "topk": {"bound": "hbm", "unit": "GB/s", **frac(topk_bytes, stages["topk_prepared_ms"], HBM_PEAK_GBPS, 1e9)},
@@ -536,9 +748,15 @@ def main():
                         **frac(csr_bytes, stages["k2q_csr_prepared_ms"], HBM_PEAK_GBPS, 1e9)},
             "attention_fwd": {"bound": "mfma", "unit": "TFLOP/s",
                               **frac(fwd_flops, stages["attention_fwd_kernel_ms"], MFMA_BF16_PEAK_TFLOPS, 1e12)},
+            "attention_fwd_partial_kernel": {"bound": "mfma", "unit": "TFLOP/s",
+                                             **frac(fwd_flops, stages["attention_fwd_partial_ms"],
+                                                    MFMA_BF16_PEAK_TFLOPS, 1e12)},
             "attention_bwd": {"bound": "mfma", "unit": "TFLOP/s",
-                              **frac(2.5 * fwd_flops, stages["attention_bwd_kernel_ms"], MFMA_BF16_PEAK_TFLOPS,
-                                     1e12)},
+                              **frac(bwd_flops, stages["attention_bwd_kernel_ms"], MFMA_BF16_PEAK_TFLOPS, 1e12)},
+            "kv_bwd_main_kernel": {"bound": "mfma", "unit": "TFLOP/s",
+                                   **frac(bwd_flops, dom_ms, MFMA_BF16_PEAK_TFLOPS, 1e12)},
+            "attention_fwd_bwd": {"bound": "mfma", "unit": "TFLOP/s",
+                                  **frac(step_flops, ms, MFMA_BF16_PEAK_TFLOPS, 1e12)},
             # per visible (token, group, key): teacher logits 2 D R, student logits 2 Di,
             # d_iq and d_ik 2 Di each
             "indexer_kl": {"bound": "mfma", "unit": "TFLOP/s",
@@ -550,7 +768,7 @@ def main():
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         baseline = cpu_baseline(cfg, tensors_cpu, ids.cpu(), args.cpu_seconds)
-        log(f"cpu baseline: {baseline['value']:.4f} TFLOP/s on {baseline['cores']} threads")
+        log(f"cpu baseline: {baseline['value']:.4f} TFLOP/s on {baseline['cores']} threads ({baseline['host']})")
 
     result = {
         "metric": "sparse-attn fwd+bwd TFLOP/s and per-stage ms @32K tokens on 1xMI355X",
@@ -560,6 +778,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 4),
+        "step_ms": {k_: round(v_, 4) for k_, v_ in step_stats.items()},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -569,11 +788,17 @@ def main():
                                f"D={cfg['d']} Di={cfg['di']} block={block} topk={topk} local={local}; "
                                "step = m3_sparse_attention fwd+bwd (dQ,dK,dV)",
                    "effective_tflop_per_step": round(step_flops / 1e12, 4)},
-        "roofline": {"bound": "mfma", "kernel": ENTRY_NAMES[dom], "achieved": round(achieved, 2),
+        # the dominant kernel: the backward's main KV pass, which performs the whole
+        # algorithmic backward (2.5 x forward FLOPs) in kernel_launches launches per call
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": round(achieved, 2),
                      "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "traffic": measured_traffic(args.config, ENTRY_NAMES[dom]),
-                     "kernel_ms": round(kt[dom]["median"], 4)},
+                     "traffic": measured_traffic(args.config, dom),
+                     "kernel_ms_per_call": dom_ms, "kernel_launches": kernel_launches[dom],
+                     "entry": {"name": "msa_attn_bwd", "ms": round(kt["attn_bwd"]["median"], 4),
+                               "achieved": round(entry_achieved, 2),
+                               "frac": round(entry_achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+                               "traffic": measured_traffic(args.config, "msa_attn_bwd", "entries")}},
         "cpu_baseline": baseline,
         "stages": stages,
     }

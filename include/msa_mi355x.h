@@ -174,6 +174,31 @@ int msa_indexer_kl(const void* index_q, const void* index_k, const void* q, cons
                    const float* teacher_lse, float* loss, float* row_kl, float* grad_index_q,
                    float* grad_index_k, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* Testing hook; no counterpart in the reference. Overrides the byte budgets that size
+ * the query-token chunks of the KV-major bf16 passes: msa_attn_fwd (default 1 GiB of
+ * per-(token, head, slot) partial records per chunk), msa_attn_bwd (4 GiB) and
+ * msa_indexer_kl (1 GiB); a value <= 0 restores that default. A chunk holds at least
+ * 64 tokens. Chunking changes only how sums are split into per-chunk partial sums,
+ * not what is computed; tests use it to drive small cases through many chunks.
+ * Process-wide: set it only while no other thread queries workspace sizes or calls
+ * those entry points, and query the workspace sizes again after a change. Returns 0. */
+int msa_set_chunk_budgets(int64_t fwd_bytes, int64_t bwd_bytes, int64_t kl_bytes);
+
+/* Profiling hook; no counterpart in the reference (bench.py reports its figures).
+ * msa_profile_begin arms per-launch timing: until msa_profile_end, every kernel launch
+ * of msa_attn_fwd and msa_attn_bwd is bracketed by two HIP events recorded on the
+ * call's stream (at most 16384 launches). msa_profile_end waits for those events and
+ * writes, for each kernel kind k < kinds, the summed duration in ms (ms[k]) and the
+ * number of launches (launches[k]); either array may be NULL. Kinds, in order:
+ * 0 forward work plan (kv_chunk_bounds + kv_item_scan), 1 attn_fwd_partial_kernel,
+ * 2 attn_fwd_combine, 3 backward work plans, 4 kv_bwd_center, 5 kv_bwd_stats_kernel,
+ * 6 kv_bwd_stats_combine, 7 kv_bwd_main_kernel, 8 kv_bwd_accumulate,
+ * 9 kv_bwd_dq_combine. Returns the number of kinds the library defines (10), or -1
+ * if an event could not be read. Armed, the event records add a short gap between
+ * kernels. Process-wide; not for concurrent use from several threads. */
+int msa_profile_begin(void);
+int64_t msa_profile_end(double* ms, int64_t* launches, int64_t kinds);
+
 #ifdef __cplusplus
 }
 #endif

@@ -48,7 +48,15 @@ SIGNATURES = {
     "msa_indexer_kl_workspace_bytes": (_i64, [_i32, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "msa_indexer_kl": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                               _f64, _f64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
+    "msa_set_chunk_budgets": (_i32, [_i64, _i64, _i64]),
+    "msa_profile_begin": (_i32, []),
+    "msa_profile_end": (_i64, [_vp, _vp, _i64]),
 }
+
+# Kernel kinds of msa_profile_end, in order.
+PROFILE_KINDS = ("fwd_plan", "attn_fwd_partial_kernel", "attn_fwd_combine", "bwd_plan", "kv_bwd_center",
+                 "kv_bwd_stats_kernel", "kv_bwd_stats_combine", "kv_bwd_main_kernel", "kv_bwd_accumulate",
+                 "kv_bwd_dq_combine")
 
 STATUS_TEXT = {1: "invalid argument", 2: "unsupported configuration", 3: "HIP launch failure"}
 
@@ -100,3 +108,43 @@ def require_gpu(tensor: torch.Tensor, what: str) -> None:
             f"{what}: MI355X HIP kernels require ROCm device tensors (got {tensor.device}); "
             "there is no CPU execution path"
         )
+
+
+class chunk_budgets:
+    """Context manager over ``msa_set_chunk_budgets`` (a testing hook): runs the body with
+    the given per-chunk record budgets in bytes for the KV-major attention forward,
+    backward and indexer KL (None keeps a pass's default), then restores the defaults."""
+
+    def __init__(self, fwd: int | None = None, bwd: int | None = None, kl: int | None = None):
+        self.values = tuple(0 if x is None else int(x) for x in (fwd, bwd, kl))
+
+    def __enter__(self):
+        check(lib().msa_set_chunk_budgets(*self.values), "msa_set_chunk_budgets")
+        return self
+
+    def __exit__(self, *exc):
+        lib().msa_set_chunk_budgets(0, 0, 0)
+        return False
+
+
+class kernel_timer:
+    """Context manager over the library's profiling hook (``msa_profile_begin`` /
+    ``msa_profile_end``): every kernel the attention entry points launch inside the body
+    is timed with HIP events on its stream. After exit, ``ms`` and ``launches`` map each
+    kernel kind of PROFILE_KINDS to its summed duration and launch count."""
+
+    def __enter__(self):
+        check(lib().msa_profile_begin(), "msa_profile_begin")
+        self.ms, self.launches = {}, {}
+        return self
+
+    def __exit__(self, *exc):
+        n = len(PROFILE_KINDS)
+        ms = (ctypes.c_double * n)()
+        launches = (ctypes.c_int64 * n)()
+        got = lib().msa_profile_end(ms, launches, n)
+        if got < 0:
+            raise RuntimeError("msa_profile_end failed to read its events")
+        self.ms = {name: ms[i] for i, name in enumerate(PROFILE_KINDS)}
+        self.launches = {name: launches[i] for i, name in enumerate(PROFILE_KINDS)}
+        return False

@@ -22,6 +22,7 @@
 // No floating-point atomics; every sum has a fixed order. Partial records are
 // written and read once each, with non-temporal (streaming) stores and loads.
 #include "attn_kv_common.hpp"
+#include "profile.hpp"
 
 // Logits are x = fl(acc * scale2) and exponent arguments fl(x - lse2), each with its
 // own rounding and formed identically in the stats and main passes, so the p_j
@@ -63,7 +64,7 @@ struct StatSmem {
   static constexpr int KS = lds_row_stride<DP>();
   alignas(16) uint16_t k[128 * KS];
   alignas(16) uint16_t v[128 * KS];
-  int32_t th[kStatItemRows];   // token * Hq + head of each (compacted) row
+  int32_t th[kStatItemRows];   // (token - t0) * Hq + head of each (compacted) row (chunk-local)
   int32_t rec[kStatItemRows];
   float lse2[kStatItemRows];
   float cen[kStatItemRows];
@@ -169,8 +170,8 @@ __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
       const int eo = rho / R;
       const int h = rg.g * R + (rho - eo * R);
       const int tok = qidx[e_begin + eo];
-      th = tok * Hq + h;  // < 2^31: token-head products are checked on the host
-      const double* rs = row_state + static_cast<int64_t>(th) * 4;
+      th = (tok - t0) * Hq + h;  // < tc * Hq (chunk records fit in int32, checked on the host)
+      const double* rs = row_state + (static_cast<int64_t>(tok) * Hq + h) * 4;
       const double2 lm = *reinterpret_cast<const double2*>(rs);
       take = all_rows || lm.y < 0.0;
       rec = ((tok - t0) * Hq + h) * K + sidx[e_begin + eo];
@@ -231,8 +232,8 @@ __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
     for (int rt = 0; rt < kStatRT; ++rt) {
       const int rho = rbase + 16 * rt + c;
       const bool ok = rho < nsel;
-      const int64_t th = ok ? sm.th[rho] : 0;
-      const int64_t vis = ok ? static_cast<int64_t>(sm.th[rho] / Hq) - rg.kb + 1 : 0;
+      const int64_t th = ok ? static_cast<int64_t>(t0) * Hq + sm.th[rho] : 0;
+      const int64_t vis = ok ? static_cast<int64_t>(t0) + sm.th[rho] / Hq - rg.kb + 1 : 0;
       lim[rt] = vis < rg.nk ? static_cast<int>(vis) : rg.nk;
       lse2[rt] = ok ? sm.lse2[rho] : 0.f;
       cen[rt] = ok ? sm.cen[rho] : 0.f;
@@ -741,7 +742,7 @@ static BwdLayout bwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t
   const int64_t rows = total_blocks * G;
   const int64_t R = Hq / (G > 0 ? G : 1);
   const int64_t DP = 32 * nk_of_dim(static_cast<int>(D));
-  const int64_t tc = kv_chunk_tokens(T, Hq, K, D * 4 + 8, int64_t(1) << 32);
+  const int64_t tc = kv_chunk_tokens(T, Hq, K, D * 4 + 8, kv_chunk_budget(kPassBwd, int64_t(1) << 32));
   int64_t sepi = static_cast<int64_t>(kStatItemRows) / (R > 0 ? R : 1);
   if (sepi < 1) sepi = 1;
   b.stat_plan = kv_plan_layout(T, rows, G, K, tc, sepi);
@@ -768,7 +769,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   const int64_t rows = total_blocks * G;
   const BwdLayout L = bwd_layout(T, Hq, G, D, K, total_blocks);
   if (ws_bytes < L.total) return kErrInvalidArgument;
-  if (T * Hq * (K > 0 ? K : 1) >= (int64_t(1) << 31) || rows >= (int64_t(1) << 31)) return kErrUnsupported;
+  if (!kv_csr_fits(T, G, K, rows) || !kv_chunk_records_fit(L.main_plan.tc, Hq, K)) return kErrUnsupported;
   if (T == 0) return kOk;
   char* base = static_cast<char*>(ws);
   void* sbase = base + L.stat_base;
@@ -792,15 +793,22 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   // every row does.
   const int all_rows = o32 == nullptr;
   const uint32_t rmagic = ratio_magic(Hq / G);  // rows x ratio < 512 * 512^2 < 2^32
-  hipLaunchKernelGGL(kv_bwd_center, dim3(grid_1d(T * Hq, 8)), dim3(256), 0, st, ob, o32, gb, T * Hq, D, rs);
-  kv_plan_launch(L.stat_plan, row_ptr, qidx, T, sbase, st);
-  kv_plan_launch(L.main_plan, row_ptr, qidx, T, mbase, st);
+  {
+    ProfScope ps(kProfBwdCenter, st);
+    hipLaunchKernelGGL(kv_bwd_center, dim3(grid_1d(T * Hq, 8)), dim3(256), 0, st, ob, o32, gb, T * Hq, D, rs);
+  }
+  {
+    ProfScope ps(kProfBwdPlan, st);
+    kv_plan_launch(L.stat_plan, row_ptr, qidx, T, sbase, st);
+    kv_plan_launch(L.main_plan, row_ptr, qidx, T, mbase, st);
+  }
   const KvPlan& sp = L.stat_plan;
   const KvPlan& mp = L.main_plan;
   for (int64_t c = 0; c < sp.nch; ++c) {
     const int64_t t0 = c * sp.tc, t1 = t0 + sp.tc < T ? t0 + sp.tc : T;
     const int it0 = static_cast<int>(t0);
     if (rows > 0) {
+      ProfScope ps(kProfBwdStats, st);
       const int32_t* hi = kv_plan_hi(sp, sbase, c);
       const int32_t* nit = kv_plan_count(sp, sbase, c);
       const int2* its = kv_plan_items(sp, sbase, c);
@@ -812,20 +820,27 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       else { if (fd) MSA_BWD_STATS(4, true); else MSA_BWD_STATS(4, false); }
 #undef MSA_BWD_STATS
     }
-    hipLaunchKernelGGL(kv_bwd_stats_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu, nseq,
-                       t0, t1, Hq, G, K, B, all_rows, spart, rs);
+    {
+      ProfScope ps(kProfBwdStatsCombine, st);
+      hipLaunchKernelGGL(kv_bwd_stats_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu,
+                         nseq, t0, t1, Hq, G, K, B, all_rows, spart, rs);
+    }
     if (rows > 0) {
       const int32_t* hi = kv_plan_hi(mp, mbase, c);
       const int32_t* nit = kv_plan_count(mp, mbase, c);
       const int2* its = kv_plan_items(mp, mbase, c);
       const int mepi = static_cast<int>(mp.epi);
       const dim3 grid(static_cast<unsigned>(mp.max_items)), block(kMainThreads);
+      {
+        ProfScope ps(kProfBwdMain, st);
 #define MSA_BWD_MAIN(NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, dqpart, kvpart)
-      if (nk == 1) { if (fd) MSA_BWD_MAIN(1, true); else MSA_BWD_MAIN(1, false); }
-      else if (nk == 2) { if (fd) MSA_BWD_MAIN(2, true); else MSA_BWD_MAIN(2, false); }
-      else { if (fd) MSA_BWD_MAIN(4, true); else MSA_BWD_MAIN(4, false); }
+        if (nk == 1) { if (fd) MSA_BWD_MAIN(1, true); else MSA_BWD_MAIN(1, false); }
+        else if (nk == 2) { if (fd) MSA_BWD_MAIN(2, true); else MSA_BWD_MAIN(2, false); }
+        else { if (fd) MSA_BWD_MAIN(4, true); else MSA_BWD_MAIN(4, false); }
 #undef MSA_BWD_MAIN
+      }
       if (need_kv) {
+        ProfScope ps(kProfBwdAccumulate, st);
         const int32_t* starts = kv_plan_starts(mp, mbase, c);
         const dim3 agrid(static_cast<unsigned>(rows), static_cast<unsigned>(32 * nk / 8));
         const int first = c == 0, last = c + 1 == sp.nch;
@@ -838,9 +853,11 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
 #undef MSA_BWD_ACC
       }
     }
-    if (dq)
+    if (dq) {
+      ProfScope ps(kProfBwdDqCombine, st);
       hipLaunchKernelGGL(kv_bwd_dq_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu, nseq, t0,
                          t1, Hq, G, D, K, B, static_cast<double>(scale), dqpart, static_cast<uint16_t*>(dq));
+    }
   }
   return status_from(hipGetLastError());
 }

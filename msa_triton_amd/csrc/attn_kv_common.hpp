@@ -63,6 +63,23 @@ inline uint32_t ratio_magic(int64_t r) {
 // backward with ~4 GiB (fewer per-chunk key-block reloads and item tails).
 int64_t kv_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t record_bytes, int64_t budget);
 
+// Chunk budgets of the KV-major passes: `dflt` unless msa_set_chunk_budgets set one.
+enum KvPass { kPassFwd = 0, kPassBwd = 1, kPassKl = 2 };
+int64_t kv_chunk_budget(KvPass pass, int64_t dflt);
+
+// Chunk-local record indices ((token - t0) * heads + head) * K + slot are int32: a
+// chunk may hold at most 2^31 - 1 records (with the default budgets it holds far fewer).
+inline bool kv_chunk_records_fit(int64_t tc, int64_t heads, int64_t K) {
+  return tc * heads * (K > 0 ? K : 1) < (int64_t(1) << 31);
+}
+
+// The capacity limit of the KV-major kernels is the k2q CSR's (triton/k2q.py:65-69):
+// T * G * K edges and the (block, group) rows must fit in int32. Token ids, token-head
+// indices and element offsets are formed in int64.
+inline bool kv_csr_fits(int64_t T, int64_t G, int64_t K, int64_t rows) {
+  return T * G * (K > 0 ? K : 1) < (int64_t(1) << 31) && rows < (int64_t(1) << 31);
+}
+
 struct KvPlan {
   int64_t rows, tc, nch, epi, max_items;  // max_items: per-chunk upper bound on work items
   int64_t bounds, starts, items, bytes;   // byte offsets of the arrays inside the plan area, total size

@@ -22,7 +22,10 @@
 // The logits use the K row fragment and the Q row fragment over the same dims
 // in the same k order as the backward kernels. P.V is computed exactly in its
 // products: P is split into three bf16 terms (hi + mid + lo == P).
+#include <atomic>
+
 #include "attn_kv_common.hpp"
+#include "profile.hpp"
 
 // Logits are x = fl(acc * scale2) with their own rounding, and exponent arguments
 // x - m with another: no fused multiply-adds, so a row's maximum gets p == 1 exactly.
@@ -42,7 +45,7 @@ struct FwdSmem {
   static constexpr int KS = DP + 8;   // row stride of the K and V blocks (bf16)
   alignas(16) uint16_t k[128 * KS];
   alignas(16) uint16_t v[128 * KS];
-  int32_t th[kItemRows];   // token * Hq + head
+  int32_t th[kItemRows];   // (token - t0) * Hq + head (chunk-local)
   int32_t tok[kItemRows];  // query token
   int32_t rec[kItemRows];  // partial record ((token - t0) * Hq + head) * K + slot
 };
@@ -62,7 +65,7 @@ __global__ __launch_bounds__(256) void kv_chunk_bounds(const int32_t* __restrict
     const int64_t t = c * tc < T ? c * tc : T;
     int32_t lo = a, hi = b;
     while (lo < hi) {
-      const int32_t mid = (lo + hi) >> 1;
+      const int32_t mid = lo + ((hi - lo) >> 1);  // lo + hi may exceed INT32_MAX
       if (qidx[mid] < t) lo = mid + 1; else hi = mid;
     }
     bounds[c * rows + r] = (c == nch) ? b : lo;
@@ -175,7 +178,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     if (rho < nrows) {
       const int eo = rho / R;
       const int h = rg.g * R + (rho - eo * R);
-      sm.th[rho] = mtok[j] * Hq + h;
+      sm.th[rho] = (mtok[j] - t0) * Hq + h;  // < tc * Hq: chunk records fit in int32 (checked on the host)
       sm.tok[rho] = mtok[j];
       sm.rec[rho] = ((mtok[j] - t0) * Hq + h) * K + mslot[j];
     }
@@ -190,7 +193,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     for (int rt = 0; rt < 2; ++rt) {
       const int rho = r0 + 32 * wid + 16 * rt + c;
       const bool ok = rho < nrows;
-      const int64_t th = ok ? sm.th[rho] : 0;
+      const int64_t th = ok ? static_cast<int64_t>(t0) * Hq + sm.th[rho] : 0;
 #pragma unroll
       for (int kk = 0; kk < NK; ++kk) {
         const int d0 = 32 * kk + 8 * q4;
@@ -446,6 +449,15 @@ static int64_t fwd_epi(int64_t R) {
   return e < 1 ? 1 : e;
 }
 
+namespace {
+std::atomic<int64_t> g_chunk_budget[3] = {{0}, {0}, {0}};
+}  // namespace
+
+int64_t kv_chunk_budget(KvPass pass, int64_t dflt) {
+  const int64_t b = g_chunk_budget[pass].load(std::memory_order_relaxed);
+  return b > 0 ? b : dflt;
+}
+
 int64_t kv_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t record_bytes, int64_t budget) {
   const int64_t per_token = Hq * (K > 0 ? K : 1) * record_bytes;
   int64_t tc = budget / (per_token > 0 ? per_token : 1);
@@ -489,7 +501,7 @@ struct FwdLayout {
 
 static FwdLayout fwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks) {
   FwdLayout f;
-  const int64_t tc = kv_chunk_tokens(T, Hq, K, (D + 2) * 4, int64_t(1) << 30);
+  const int64_t tc = kv_chunk_tokens(T, Hq, K, (D + 2) * 4, kv_chunk_budget(kPassFwd, int64_t(1) << 30));
   f.plan = kv_plan_layout(T, total_blocks * G, G, K, tc, fwd_epi(Hq / (G > 0 ? G : 1)));
   f.opart = f.plan.bytes;
   f.ml = f.opart + align256(tc * Hq * K * D * 4);
@@ -508,8 +520,7 @@ int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indi
   const int64_t rows = total_blocks * G;
   const FwdLayout f = fwd_layout(T, Hq, G, D, K, total_blocks);
   if (ws_bytes < f.total) return kErrInvalidArgument;
-  // 32-bit token-head, record and row arithmetic inside the kernels
-  if (T * Hq * (K > 0 ? K : 1) >= (int64_t(1) << 31) || rows >= (int64_t(1) << 31)) return kErrUnsupported;
+  if (!kv_csr_fits(T, G, K, rows) || !kv_chunk_records_fit(f.plan.tc, Hq, K)) return kErrUnsupported;
   if (T == 0) return kOk;
   char* base = static_cast<char*>(ws);
   float* opart = reinterpret_cast<float*>(base + f.opart);
@@ -521,10 +532,14 @@ int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indi
   const auto* kb = static_cast<const uint16_t*>(k);
   const auto* vb = static_cast<const uint16_t*>(v);
   auto* ob = static_cast<uint16_t*>(out);
-  kv_plan_launch(pl, row_ptr, qidx, T, base, st);
+  {
+    ProfScope ps(kProfFwdPlan, st);
+    kv_plan_launch(pl, row_ptr, qidx, T, base, st);
+  }
   for (int64_t c = 0; c < pl.nch; ++c) {
     const int64_t t0 = c * pl.tc, t1 = t0 + pl.tc < T ? t0 + pl.tc : T;
     if (rows > 0) {
+      ProfScope ps(kProfFwdPartial, st);
       const dim3 grid(static_cast<unsigned>(pl.max_items)), block(256);
       const int32_t* hi = kv_plan_hi(pl, base, c);
       const int32_t* nit = kv_plan_count(pl, base, c);
@@ -538,6 +553,7 @@ int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indi
       else { if (fd) MSA_FWD_PARTIAL(4, true); else MSA_FWD_PARTIAL(4, false); }
 #undef MSA_FWD_PARTIAL
     }
+    ProfScope ps(kProfFwdCombine, st);
     hipLaunchKernelGGL(attn_fwd_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu, nseq, t0, t1,
                        Hq, G, D, K, B, opart, ml, ob, lse, rs, o32);
   }
@@ -545,3 +561,10 @@ int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indi
 }
 
 }  // namespace msa
+
+extern "C" int msa_set_chunk_budgets(int64_t fwd_bytes, int64_t bwd_bytes, int64_t kl_bytes) {
+  msa::g_chunk_budget[msa::kPassFwd].store(fwd_bytes > 0 ? fwd_bytes : 0, std::memory_order_relaxed);
+  msa::g_chunk_budget[msa::kPassBwd].store(bwd_bytes > 0 ? bwd_bytes : 0, std::memory_order_relaxed);
+  msa::g_chunk_budget[msa::kPassKl].store(kl_bytes > 0 ? kl_bytes : 0, std::memory_order_relaxed);
+  return msa::kOk;
+}

@@ -654,7 +654,7 @@ KlLayout kl_layout(int64_t T, int64_t Hq, int64_t G, int64_t Di, int64_t K, int6
   const int64_t rows = total_blocks * G;
   // per (token, slot): teacher (m, l) per head, student (m, l), KL and d_iq per group
   const int64_t rec = Hq * 8 + G * (8 + 4 + 4 * Di);
-  const int64_t tc = kv_chunk_tokens(T, 1, K, rec, int64_t(1) << 30);
+  const int64_t tc = kv_chunk_tokens(T, 1, K, rec, kv_chunk_budget(kPassKl, int64_t(1) << 30));
   L.plan = kv_plan_layout(T, rows, G, K, tc, kKlEdges);
   int64_t off = align256(L.plan.bytes);
   L.tpart = off;   off += align256(tc * Hq * K * 8);
@@ -702,11 +702,12 @@ extern "C" int msa_indexer_kl(const void* index_q, const void* index_k, const vo
     hipLaunchKernelGGL(kl_zero, dim3(1), dim3(256), 0, st, loss, 1);
     return status_from(hipGetLastError());
   }
-  if (T * Hq * (K > 0 ? K : 1) >= (int64_t(1) << 31) || total_blocks * G >= (int64_t(1) << 31)) return kErrUnsupported;
+  if (!kv_csr_fits(T, G, K, total_blocks * G)) return kErrUnsupported;
   if (!cu_block_lens || !row_ptr || !workspace || !indices || !cu_seqlens || (K > 0 && (!query_indices || !slot_indices)))
     return kErrInvalidArgument;
   const KlLayout L = kl_layout(T, Hq, G, Di, K, total_blocks);
   if (workspace_bytes < L.total) return kErrInvalidArgument;
+  if (!kv_chunk_records_fit(L.plan.tc, Hq, K)) return kErrUnsupported;
   char* base = static_cast<char*>(workspace);
   auto* tpart = reinterpret_cast<float2*>(base + L.tpart);
   auto* spart = reinterpret_cast<float2*>(base + L.spart);

@@ -1,4 +1,4 @@
-"""CPU restatement of the reference's eager sparse attention -- TEST / BASELINE INFRASTRUCTURE ONLY.
+"""CPU restatement of the reference's eager path -- TEST / BASELINE INFRASTRUCTURE ONLY.
 
 Follows eager/ops.py:153-180 (sparse_attention_bsnd) of the reference for one
 packed sequence: bf16 Q.K^T * scale over the dense key range with the block
@@ -6,7 +6,9 @@ keep mask (eager/ops.py:132-150), masked_fill(-inf), fp32 softmax cast back to
 bf16, bf16 P.V, and torch autograd for the backward. It is used only as the
 ``cpu_baseline`` leg of bench.py, row-chunked so that a bounded sample of query
 rows can be timed (softmax rows are independent, so chunking changes no value
-and the work adds up linearly over chunks). Never imported by the product path.
+and the work adds up linearly over chunks). ``eager_score_rows`` and ``eager_topk``
+restate the eager indexer score (eager/ops.py:45-67) and selection
+(eager/ops.py:112-129) for the same purpose. Never imported by the product path.
 """
 
 from __future__ import annotations
@@ -49,3 +51,41 @@ def eager_rows_fwd_bwd(q, k, v, indices, rows, *, block_size, scale, dout, key_l
     out = torch.matmul(probs, value).transpose(0, 1)  # [n, Hq, D]
     out.backward(dout[r0:r1])
     return out.detach(), qr.grad, kk.grad, vv.grad
+
+
+def eager_score_rows(index_q, index_k, rows, *, block_size, scale=1.0):
+    """Scores of query rows ``rows`` of a single sequence starting at token 0, as the
+    reference's eager index_score_bsnd computes them (eager/ops.py:45-67): fp32
+    Q.K^T over the dense key range of the sequence, causal mask, -inf padding to
+    whole blocks and a block amax. Returns fp32 [n, G, blocks]."""
+    r0, r1 = rows
+    length = index_k.shape[0]
+    q = index_q[r0:r1].float().transpose(0, 1)  # [G, n, Di]
+    k = index_k.float().transpose(0, 1)  # [1, S, Di]
+    scores = torch.matmul(q, k.transpose(-1, -2))  # [G, n, S]
+    if scale != 1.0:
+        scores = scores * scale
+    keep = torch.arange(length)[None, :] <= torch.arange(r0, r1)[:, None]
+    scores = scores.masked_fill(~keep[None], float("-inf"))
+    blocks = (length + block_size - 1) // block_size
+    scores = torch.nn.functional.pad(scores, (0, blocks * block_size - length), value=float("-inf"))
+    scores = scores.reshape(scores.shape[0], r1 - r0, blocks, block_size).amax(-1)
+    return scores.transpose(0, 1)
+
+
+@torch.no_grad()
+def eager_topk(scores, positions, *, block_size, topk_blocks, local_blocks):
+    """The reference's eager m3_topk selection (eager/ops.py:112-129) for rows with
+    sequence-local ``positions``: causal mask, +inf local boost, torch.topk, -inf ->
+    -1, right padding to topk_blocks. Returns int32 [n, G, topk_blocks]."""
+    blocks = torch.arange(scores.shape[-1])
+    query_block = positions // block_size
+    valid = blocks[None, None, :] <= query_block[:, None, None]
+    boosted = scores.masked_fill(~valid, float("-inf"))
+    if local_blocks:
+        local = (blocks[None, None, :] > query_block[:, None, None] - local_blocks) & valid
+        boosted = boosted.masked_fill(local, float("inf"))
+    count = min(topk_blocks, scores.shape[-1])
+    values, indices = boosted.topk(count, dim=-1)
+    indices = indices.masked_fill(values == float("-inf"), -1).to(torch.int32)
+    return torch.nn.functional.pad(indices, (0, topk_blocks - count), value=-1)

@@ -18,6 +18,9 @@ Functions and the reference code they restate:
                        for parity at sizes where the dense form does not fit.
   index_score_rows / topk_rows   index_score / topk for a subset of query
                        rows (pinned against the full restatements).
+  index_score_backward_rows / _keys   index_score_backward's dq for a subset of
+                       query tokens / dk for a subset of key tokens (pinned against
+                       the full restatement).
   indexer_kl (+ _rows, _key_rows)   the indexer KL branch, not implemented
                        upstream: restated from docs/msa_training_flow.md:92-138
                        and docs/implementation_plan.md:66-69 (pinned by closed
@@ -201,6 +204,75 @@ def index_score_rows(iq, ik, cu, tokens, nb, *, block_size=128, scale=1.0):
     return out, out.astype(np.float32)
 
 
+def _amax_weights(directed, allowed, ds_col, scale):
+    """amax subgradient weights over the last axis: ds * scale split evenly over the exact
+    maxima of the directed dots among the allowed keys (0 where none is allowed)."""
+    directed = np.where(allowed, directed, -np.inf)
+    best = directed.max(-1, keepdims=True)
+    winners = (directed == best) & allowed
+    count = np.maximum(winners.sum(-1, keepdims=True), 1)
+    return winners * (ds_col[..., None] * scale / count)
+
+
+def index_score_backward_rows(iq, ik, cu, ds, tokens, *, block_size=128, scale=1.0):
+    """``index_score_backward``'s dq [n, G, Di] for the given query tokens only.
+    ``ds`` is the full [T, G, NB] upstream gradient."""
+    q = np.asarray(iq, dtype=np.float64)
+    k = np.asarray(ik, dtype=np.float64)[:, 0, :]
+    bounds = bounds_of(cu)
+    _, start = _token_positions(bounds)
+    tokens = np.asarray(tokens, dtype=np.int64)
+    groups, dim = q.shape[1], q.shape[2]
+    sign = 1.0 if scale > 0 else (-1.0 if scale < 0 else 0.0)
+    dq = np.zeros((len(tokens), groups, dim))
+    for i, t in enumerate(tokens):
+        t = int(t)
+        a = int(start[t])
+        pos = t - a
+        nblk = pos // block_size + 1
+        width = nblk * block_size
+        keys = a + np.arange(width)
+        allowed = (np.arange(width) <= pos).reshape(nblk, block_size)
+        kk = k[np.minimum(keys, t)]  # keys past t are masked
+        dots = (sign * (q[t] @ kk.T)).reshape(groups, nblk, block_size)
+        w = _amax_weights(dots, allowed[None], np.asarray(ds[t, :, :nblk], dtype=np.float64), scale)
+        dq[i] = w.reshape(groups, width)[:, : pos + 1] @ k[a : t + 1]
+    return dq
+
+
+def index_score_backward_keys(iq, ik, cu, ds, keys, *, block_size=128, scale=1.0):
+    """``index_score_backward``'s dk [n, Di] for the given key tokens only (every query
+    token of the key's sequence at or after it, all groups). ``ds`` is the full
+    [T, G, NB] upstream gradient."""
+    q = np.asarray(iq, dtype=np.float64)
+    k = np.asarray(ik, dtype=np.float64)[:, 0, :]
+    bounds = bounds_of(cu)
+    seq, _ = _token_positions(bounds)
+    keys = np.asarray(keys, dtype=np.int64)
+    dim = q.shape[2]
+    sign = 1.0 if scale > 0 else (-1.0 if scale < 0 else 0.0)
+    dk = np.zeros((len(keys), dim))
+    blocks = {}
+    for i, j in enumerate(keys):
+        s = int(seq[int(j)])
+        blocks.setdefault((s, (int(j) - bounds[s]) // block_size), []).append(i)
+    for (s, blk), members in blocks.items():
+        a, b = bounds[s], bounds[s + 1]
+        k0 = a + blk * block_size
+        k1 = min(k0 + block_size, b)
+        kk = k[k0:k1]
+        for t0 in range(k0, b, 4096):  # query tokens in slabs (memory)
+            t1 = min(t0 + 4096, b)
+            qs = q[t0:t1]  # [n, G, Di]
+            allowed = (np.arange(k0, k1)[None, :] <= np.arange(t0, t1)[:, None])[:, None, :]
+            n, groups = qs.shape[0], qs.shape[1]
+            dots = sign * (qs.reshape(n * groups, dim) @ kk.T).reshape(n, groups, k1 - k0)
+            w = _amax_weights(dots, allowed, np.asarray(ds[t0:t1, :, blk], dtype=np.float64), scale)
+            for i in members:
+                dk[i] += w[:, :, int(keys[i]) - k0].reshape(-1) @ qs.reshape(n * groups, dim)
+    return dk[:, None, :]
+
+
 # --------------------------------------------------------------------------- k2q CSR
 
 
@@ -355,8 +427,63 @@ def attention_rows(q, k, v, indices, cu, tokens, *, block_size=128, scale=None, 
     return res
 
 
+def _rows_lse_delta(q, k, v, do, ids, bounds, tokens, g, ratio, scale, block_size):
+    """Per (token, head) of group g over the given (sorted, distinct) tokens: lse [n, R]
+    and the softmax derivative centre delta = sum_j p_j dp_j [n, R], the values
+    attention_rows computes. Evaluated block by block (each selected key block is one
+    product over all the rows that chose it) with an online FP64 merge of
+    (max, sum exp, sum exp * dp) per row."""
+    hs = slice(g * ratio, (g + 1) * ratio)
+    tokens = np.asarray(tokens, dtype=np.int64)
+    n = len(tokens)
+    m = np.full((n, ratio), -np.inf)
+    l = np.zeros((n, ratio))
+    u = np.zeros((n, ratio))
+    if n:
+        seq, start = _token_positions(bounds)
+        ends = np.asarray(bounds[1:], dtype=np.int64)[seq[tokens]]
+        sel = np.asarray(ids[tokens, g, :], dtype=np.int64)  # [n, K]
+        qb = (tokens - start[tokens]) // block_size
+        valid = (sel >= 0) & (sel <= qb[:, None])
+        for slot in range(1, sel.shape[1]):  # a block selected twice counts once
+            valid[:, slot] &= ~(sel[:, :slot] == sel[:, slot : slot + 1]).any(-1)
+        rows, slots = np.nonzero(valid)
+        kb = start[tokens[rows]] + sel[rows, slots] * block_size  # first key of the block
+        order = np.argsort(kb, kind="stable")
+        rows, kb = rows[order], kb[order]
+        cuts = np.flatnonzero(np.diff(kb)) + 1
+        for seg_rows, seg_kb in zip(np.split(rows, cuts), np.split(kb, cuts)):
+            k0 = int(seg_kb[0])
+            k1 = min(k0 + block_size, int(ends[seg_rows[0]]))
+            t = tokens[seg_rows]
+            nr, nk = len(t), k1 - k0
+            x = (q[t, hs].reshape(nr * ratio, -1) @ k[k0:k1, g].T).reshape(nr, ratio, nk) * scale
+            vis = (np.arange(k0, k1)[None, :] <= t[:, None])[:, None, :]
+            x = np.where(vis, x, -np.inf)
+            mb = x.max(-1)  # every such row sees key k0
+            e = np.where(vis, np.exp(x - mb[..., None]), 0.0)
+            dp = (do[t, hs].reshape(nr * ratio, -1) @ v[k0:k1, g].T).reshape(nr, ratio, nk)
+            lb, ub = e.sum(-1), (e * dp).sum(-1)
+            mo = m[seg_rows]
+            mn = np.maximum(mo, mb)
+            wo, wb = np.exp(mo - mn), np.exp(mb - mn)
+            l[seg_rows] = l[seg_rows] * wo + lb * wb
+            u[seg_rows] = u[seg_rows] * wo + ub * wb
+            m[seg_rows] = mn
+    has = l > 0
+    lse = np.where(has, m + np.log(np.where(has, l, 1.0)), -np.inf)
+    delta = np.where(has, u / np.where(has, l, 1.0), 0.0)
+    return lse, delta
+
+
 def attention_kv_rows(q, k, v, indices, cu, dout, keys, *, block_size=128, scale=None):
-    """Sparse FP64 dK/dV for selected key tokens (all groups): returns (dk, dv) [n,G,D]."""
+    """Sparse FP64 dK/dV for selected key tokens (all groups): returns (dk, dv) [n,G,D].
+
+    Key j of block b (its sequence's numbering) receives, from every query token t >= j
+    of its sequence whose group-g selection holds b, and each head h of that group:
+    dv += p dO[t,h], dk += scale p (dp - delta) q[t,h], with p = exp(scale q.k_j - lse),
+    dp = dO[t,h].v_j and the row's lse / delta (tests/reference_fp64.py:48-85; the
+    gradient of sparse_attention restricted to the sampled keys)."""
     q = np.asarray(q, dtype=np.float64)
     k = np.asarray(k, dtype=np.float64)
     v = np.asarray(v, dtype=np.float64)
@@ -371,26 +498,27 @@ def attention_kv_rows(q, k, v, indices, cu, dout, keys, *, block_size=128, scale
     keys = np.asarray(keys, dtype=np.int64)
     dk = np.zeros((len(keys), groups, dim))
     dv = np.zeros((len(keys), groups, dim))
-    cache = {}
-    for i, j in enumerate(keys):
-        j = int(j)
-        s = int(seq[j])
-        a, b = bounds[s], bounds[s + 1]
-        blk = (j - a) // block_size
-        for g in range(groups):
-            hits = np.nonzero((ids[j:b, g, :] == blk).any(-1))[0] + j  # query tokens that selected j's block
-            for t in hits:
-                t = int(t)
-                if (t, g) not in cache:
-                    row = attention_rows(q, k, v, ids, cu, [t], block_size=block_size, scale=scale, dout=do)
-                    cache[(t, g)] = (row["lse"][0], row["delta"][0])
-                lse_t, delta_t = cache[(t, g)]
-                hs = slice(g * ratio, (g + 1) * ratio)
-                logit = q[t, hs] @ k[j, g] * scale  # [R]
-                p = np.exp(logit - lse_t[hs])
-                dp = do[t, hs] @ v[j, g]
-                dk[i, g] += scale * (p * (dp - delta_t[hs])) @ q[t, hs]
-                dv[i, g] += p @ do[t, hs]
+    for g in range(groups):
+        hs = slice(g * ratio, (g + 1) * ratio)
+        hits = []
+        for j in keys:
+            j = int(j)
+            s = int(seq[j])
+            a, b = bounds[s], bounds[s + 1]
+            blk = (j - a) // block_size
+            hits.append(np.nonzero((ids[j:b, g, :] == blk).any(-1))[0] + j)  # tokens that selected j's block
+        needed = np.unique(np.concatenate(hits + [np.zeros(0, dtype=np.int64)]))
+        lse_n, delta_n = _rows_lse_delta(q, k, v, do, ids, bounds, needed, g, ratio, scale, block_size)
+        for i, j in enumerate(keys):
+            t = hits[i]
+            if t.size == 0:
+                continue
+            r = np.searchsorted(needed, t)
+            qh, dh = q[t, hs], do[t, hs]  # [n, R, D]
+            p = np.exp(qh @ k[int(j), g] * scale - lse_n[r])  # [n, R]
+            dp = dh @ v[int(j), g]
+            dk[i, g] = scale * np.einsum("nr,nrd->d", p * (dp - delta_n[r]), qh)
+            dv[i, g] = np.einsum("nr,nrd->d", p, dh)
     return dk, dv
 
 

@@ -29,7 +29,7 @@ def _declared():
     text = open(HEADER).read()
     decls = {}
     for match in re.finditer(r"^(?:int|int64_t)\s+(msa_\w+)\(([^;]*)\);", text, flags=re.M | re.S):
-        params = [p for p in match.group(2).split(",") if p.strip()]
+        params = [p for p in match.group(2).split(",") if p.strip() and p.strip() != "void"]
         decls[match.group(1)] = len(params)
     return decls
 

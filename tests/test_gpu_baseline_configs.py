@@ -59,16 +59,49 @@ def _sample_tokens(lengths, block, rng, extra=4):
     return np.array(sorted(out), dtype=np.int64)
 
 
+def _bwd_chunk_tokens(cfg, total):
+    """Query tokens per backward chunk at the default 4 GiB budget (kv_chunk_tokens: records of
+    D * 4 + 8 bytes per (token, head, slot), at least 64 tokens, balanced chunks)."""
+    per_token = cfg["hq"] * cfg["topk"] * (cfg["d"] * 4 + 8)
+    tc = max(64, (1 << 32) // per_token)
+    if total <= tc:
+        return total
+    nch = -(-total // tc)
+    return -(-total // nch)
+
+
 def _sample_keys(lengths, block, name):
-    """Keys of the last blocks of the longest sequence (few query tokens see them), plus
-    earlier blocks where the oracle's per-key walk stays affordable."""
+    """Keys of the last blocks of the longest sequence (few query tokens see them), and
+    early keys whose blocks are selected by query tokens of several backward chunks, so
+    that their dK / dV are sums the backward carries across chunks: c3's third sequence
+    (tokens 5120-10239 straddle the chunk boundary at 8192), c4 blocks 0, 40 and 120
+    (three chunks), c5 blocks 0 and 3 (seventeen chunks)."""
     bounds = _bounds(lengths)
     s = int(np.argmax(lengths))
     a, n = bounds[s], lengths[s]
     keys = {a + n - 1, a + n - block, a + max(0, n - 3 * block) + 5}
     if name in ("c1", "c2", "c3"):
         keys.update({a, a + block // 2, a + n // 2})
+    if name == "c3":
+        keys.update({bounds[2], bounds[2] + 77, bounds[2] + 10 * block + 3})
+    if name == "c4":
+        keys.update({0, 5, 40 * block + 3, 120 * block + 77})
+    if name == "c5":
+        keys.update({0, 3 * block + 50})
     return np.array(sorted(keys), dtype=np.int64)
+
+
+def _assert_multi_chunk_keys(cfg, name, ids_np, bounds, keys):
+    """Each early key of c3-c5 gets edges from at least two backward chunks."""
+    tc = _bwd_chunk_tokens(cfg, bounds[-1])
+    spanning = 0
+    for j in keys:
+        s = int(np.searchsorted(bounds, j, side="right") - 1)
+        blk = (int(j) - bounds[s]) // cfg["block"]
+        hit = np.nonzero((ids_np[j:bounds[s + 1]] == blk).any(-1).any(-1))[0] + j
+        spanning += len(np.unique(hit // tc)) >= 2
+    if name in ("c3", "c4", "c5"):
+        assert spanning >= 2, f"{name}: only {spanning} sampled keys span several backward chunks"
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4", "c5"])
@@ -124,6 +157,7 @@ def test_pipeline_against_oracle(name, device):
     else:
         rows = O.attention_rows(q64, k64, v64, ids_np, cu_np, tokens, block_size=B, dout=do64)
         keys = _sample_keys(lengths, B, name)
+        _assert_multi_chunk_keys(cfg, name, ids_np, bounds, keys)
         dk_ref, dv_ref = O.attention_kv_rows(q64, k64, v64, ids_np, cu_np, do64, keys, block_size=B)
     _check_bf16(out[tokens], rows["out"], f"{name}: out")
     _check_bf16(qd.grad[tokens], rows["dq"], f"{name}: dq")
@@ -144,3 +178,36 @@ def test_pipeline_against_oracle(name, device):
         dq_ref, dk_ref = O.index_score_backward(iq64, ik64, cu_np, max_len, g.double().numpy(), block_size=B)
         _check_bf16(a.grad, dq_ref, f"{name}: score dq")
         _check_bf16(b.grad, dk_ref, f"{name}: score dk")
+
+
+@pytest.mark.parametrize("name", ["c2", "c3", "c4", "c5"])
+def test_score_backward_against_oracle(name, device):
+    """Stage-1 backward at the large configs with an N(0,1) upstream gradient: dq of sampled
+    query tokens and dk of sampled keys (early blocks: heavy fan-in over many 8192-row
+    segments; late blocks) against the FP64 amax subgradient (index_score_backward_rows /
+    _keys, pinned against the dense restatement on the CPU)."""
+    cfg = bench.CONFIGS[name]
+    lengths, B = cfg["lengths"], cfg["block"]
+    bounds = _bounds(lengths)
+    max_len = max(lengths)
+    cu_np = np.array(bounds, dtype=np.int32)
+    iq, ik = bench.make_inputs(cfg)[:2]
+    cu = torch.tensor(bounds, dtype=torch.int32, device=device)
+    print(f"[{name}] score backward T={bounds[-1]} G={cfg['g']}", flush=True)
+    a = iq.to(device).requires_grad_()
+    b = ik.to(device).requires_grad_()
+    sc = msa.m3_index_score(a, b, cu, max_len, block_size=B)
+    g = torch.randn(sc.shape, generator=torch.Generator().manual_seed(9)).masked_fill(torch.isinf(sc.detach().cpu()), 0)
+    sc.backward(g.to(device))
+    torch.cuda.synchronize()
+    g_np = g.numpy()
+    iq64, ik64 = iq.double().numpy(), ik.double().numpy()
+    tokens = _sample_tokens(lengths, B, np.random.default_rng(2025))
+    dq_ref = O.index_score_backward_rows(iq64, ik64, cu_np, g_np, tokens, block_size=B)
+    _check_bf16(a.grad[tokens], dq_ref, f"{name}: score dq")
+    s = int(np.argmax(lengths))
+    keys = {bounds[s], bounds[s] + 77, bounds[s] + lengths[s] // 2, bounds[s + 1] - 1}
+    keys.update(bounds[i] + 3 for i in range(len(lengths)))
+    keys = np.array(sorted(keys), dtype=np.int64)
+    dk_ref = O.index_score_backward_keys(iq64, ik64, cu_np, g_np, keys, block_size=B)
+    _check_bf16(b.grad[keys], dk_ref, f"{name}: score dk")

@@ -108,3 +108,26 @@ def test_sampled_rows_match_dense_oracle():
     gk, gv = O.attention_kv_rows(np64(q), np64(k), np64(v), ids.numpy(), cu.numpy(), np64(grad), keys, block_size=8)
     np.testing.assert_allclose(gk, dk[keys], rtol=1e-11, atol=1e-13)
     np.testing.assert_allclose(gv, dv[keys], rtol=1e-11, atol=1e-13)
+
+
+def test_sampled_key_rows_match_dense_oracle_multigroup():
+    """attention_kv_rows (batched row statistics) against the dense oracle on a ragged
+    multi-group pack with random selections, every key of the pack."""
+    from tests.helpers import random_selection
+
+    gen = torch.Generator().manual_seed(21)
+    lengths, groups, ratio, dim, block, topk = [50, 0, 33, 17], 3, 2, 8, 4, 5
+    total = sum(lengths)
+    q = torch.randn(total, groups * ratio, dim, generator=gen).bfloat16()
+    k = torch.randn(total, groups, dim, generator=gen).bfloat16()
+    v = torch.randn(total, groups, dim, generator=gen).bfloat16()
+    grad = torch.randn(q.shape, generator=gen).bfloat16()
+    ids = random_selection(total, groups, topk, lengths, block, 1, gen)
+    cu = np.array([0, 50, 50, 83, 100])
+    _, _, _, dk, dv = O.sparse_attention(np64(q), np64(k), np64(v), ids.numpy(), cu, block_size=block,
+                                         dout=np64(grad), scale=0.3)
+    keys = np.arange(total)
+    gk, gv = O.attention_kv_rows(np64(q), np64(k), np64(v), ids.numpy(), cu, np64(grad), keys, block_size=block,
+                                 scale=0.3)
+    np.testing.assert_allclose(gk, dk, rtol=1e-11, atol=1e-13)
+    np.testing.assert_allclose(gv, dv, rtol=1e-11, atol=1e-13)

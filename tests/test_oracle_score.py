@@ -172,3 +172,45 @@ def test_index_score_rows_matches_full(scale):
     r64, r32 = O.index_score_rows(iq, ik, cu, rows, f64.shape[2], block_size=8, scale=scale)
     np.testing.assert_array_equal(r64, f64[rows])
     np.testing.assert_array_equal(r32, f32[rows])
+
+
+@pytest.mark.parametrize("scale", [1.0, -0.5, 0.0])
+def test_backward_row_and_key_subsets_match_dense(scale):
+    """index_score_backward_rows / _keys (the sampled-row restatements the large-config GPU
+    tests use) equal the dense index_score_backward on a ragged pack with several groups,
+    including exact ties (small-integer inputs) and an empty sequence."""
+    rng = np.random.default_rng(5)
+    lengths = [37, 0, 70, 9]
+    cu = cu_list(lengths)
+    total, groups, dim, block = cu[-1], 3, 6, 8
+    q = rng.integers(-2, 3, size=(total, groups, dim)).astype(np.float64)  # many exact ties
+    k = rng.integers(-2, 3, size=(total, 1, dim)).astype(np.float64)
+    max_seqlen = max(lengths)
+    nb = (max_seqlen + block - 1) // block
+    ds = rng.standard_normal((total, groups, nb))
+    dq, dk = O.index_score_backward(q, k, cu, max_seqlen, ds, block_size=block, scale=scale)
+    tokens = np.array([0, 7, 8, 36, 37, 38, 60, 106, 107, 115])
+    got_q = O.index_score_backward_rows(q, k, cu, ds, tokens, block_size=block, scale=scale)
+    np.testing.assert_allclose(got_q, dq[tokens], rtol=1e-13, atol=1e-13)
+    keys = np.array([0, 5, 8, 36, 37, 44, 45, 100, 106, 107, 115])
+    got_k = O.index_score_backward_keys(q, k, cu, ds, keys, block_size=block, scale=scale)
+    np.testing.assert_allclose(got_k, dk[keys], rtol=1e-13, atol=1e-13)
+    # every key: the subsets add up to the dense result (block grouping, slab edges)
+    got_all = O.index_score_backward_keys(q, k, cu, ds, np.arange(total), block_size=block, scale=scale)
+    np.testing.assert_allclose(got_all, dk, rtol=1e-13, atol=1e-13)
+
+
+def test_backward_key_subset_spans_query_slabs():
+    """A sequence longer than the key restatement's 4096-token query slab."""
+    rng = np.random.default_rng(11)
+    lengths = [4300]
+    cu = cu_list(lengths)
+    q = rng.standard_normal((4300, 2, 4))
+    k = rng.standard_normal((4300, 1, 4))
+    block = 512
+    nb = (4300 + block - 1) // block
+    ds = rng.standard_normal((4300, 2, nb))
+    _, dk = O.index_score_backward(q, k, cu, 4300, ds, block_size=block)
+    keys = np.array([0, 1, 511, 4095, 4096, 4299])
+    got = O.index_score_backward_keys(q, k, cu, ds, keys, block_size=block)
+    np.testing.assert_allclose(got, dk[keys], rtol=1e-12, atol=1e-12)

@@ -167,3 +167,20 @@ def test_topk_rows_matches_full_topk(local_blocks):
     starts = np.where(rows < 37, 0, 37)
     part = O.topk_rows(scores[rows], rows - starts, block_size=block, topk_blocks=5, local_blocks=local_blocks)
     np.testing.assert_array_equal(part, full[rows])
+
+
+def test_eager_baseline_score_and_topk_match_oracle():
+    """The CPU baseline's eager score / top-k restatements (oracle/eager_baseline.py) agree
+    with the oracle: scores to fp32 rounding of the dot, the selection as a set per row."""
+    from oracle.eager_baseline import eager_score_rows, eager_topk
+
+    gen = torch.Generator().manual_seed(3)
+    n, groups, dim, block = 300, 2, 16, 32
+    iq = torch.randn(n, groups, dim, generator=gen).bfloat16()
+    ik = torch.randn(n, 1, dim, generator=gen).bfloat16()
+    _, ref32, _ = O.index_score(iq.double().numpy(), ik.double().numpy(), [0, n], n, block_size=block)
+    got = eager_score_rows(iq, ik, (100, 300), block_size=block).numpy()
+    np.testing.assert_allclose(got, ref32[100:300], rtol=1e-5, atol=1e-5)
+    ids = eager_topk(torch.from_numpy(ref32), torch.arange(n), block_size=block, topk_blocks=4, local_blocks=1)
+    ref_ids = O.topk(ref32, [0, n], block_size=block, topk_blocks=4, local_blocks=1)
+    assert np.array_equal(np.sort(ids.numpy(), -1), np.sort(ref_ids, -1))
