@@ -47,6 +47,24 @@ int msa_k2q_build(const int32_t* indices, const int32_t* cu_seqlens, const int32
                   int64_t counter_elems, int32_t* row_ptr, int32_t* query_indices,
                   int32_t* slot_indices, int32_t* workspace, void* stream);
 
+/* msa_k2q_build without the workspace argument; allocates nothing. No counterpart in
+ * the reference: for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc). Its workspace is a
+ * fixed device array inside the library, one per GPU, held until the process ends:
+ * MSA_K2Q_NOALLOC_MAX_ELEMS int32 (16 MiB). Returns 2 (unsupported) without launching
+ * anything when counter_elems + total_blocks * groups exceeds that (for one sequence
+ * of nb blocks, G * nb (nb + 3) / 2 entries: up to 1022 blocks at G = 8, i.e. 130,816
+ * tokens at block 128). All calls on one GPU share the array: calls that overlap in
+ * time on one GPU (different streams or threads) race and must be serialised by the
+ * caller. The stream must belong to the current device. Outputs and semantics are
+ * those of msa_k2q_build. */
+#define MSA_K2Q_NOALLOC_MAX_ELEMS (1 << 22)
+int msa_k2q_build_noalloc(const int32_t* indices, const int32_t* cu_seqlens, const int32_t* cu_block_lens,
+                          const int64_t* tri_prefix, int64_t num_seqs, int64_t total_tokens, int64_t groups,
+                          int64_t topk_slots, int64_t block_size, int64_t total_blocks,
+                          int64_t counter_elems, int32_t* row_ptr, int32_t* query_indices,
+                          int32_t* slot_indices, void* stream);
+
 /* Stage 1 forward: per-group causal block maxima of scale * (index_q . index_k).
  * Replaces triton/index_score.py:93-136 (_index_score_forward) and the launch at
  * :237-265. scores = fl32(scale * exact winning dot); -inf for blocks with no

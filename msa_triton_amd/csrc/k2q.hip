@@ -20,7 +20,10 @@
 //                    edges on their block id places each edge at row_ptr[row] +
 //                    tile offset + its rank among the tile's edges of that row.
 //   5. k2q_tail    : entries at or beyond row_ptr[rows] become -1.
+#include <mutex>
+
 #include "common.hpp"
+#include "msa_mi355x.h"
 
 namespace msa {
 
@@ -298,19 +301,19 @@ extern "C" int64_t msa_k2q_counter_elems(int64_t num_seqs, const int32_t* host_c
   return counters;
 }
 
-// workspace: int32 [counter_elems + total_blocks * groups].
-// tri_prefix: int64 [num_seqs + 1], tri_prefix[s] = G * sum_{s'<s} nb(nb+1)/2.
-extern "C" int msa_k2q_build(const int32_t* indices, const int32_t* cu_seqlens,
-                             const int32_t* cu_block_lens, const int64_t* tri_prefix,
-                             int64_t num_seqs, int64_t total_tokens, int64_t groups, int64_t topk_slots,
-                             int64_t block_size, int64_t total_blocks, int64_t counter_elems,
-                             int32_t* row_ptr, int32_t* query_indices, int32_t* slot_indices,
-                             int32_t* workspace, void* stream) {
-  if (num_seqs <= 0 || total_tokens < 0 || groups <= 0 || topk_slots < 0 || block_size <= 0 ||
-      total_blocks < 0 || counter_elems < 0)
-    return kErrInvalidArgument;
-  if (block_size * groups * topk_slots >= (int64_t(1) << 31)) return kErrUnsupported;  // edges per tile in int32
-  hipStream_t st = static_cast<hipStream_t>(stream);
+namespace msa {
+
+namespace {
+
+// The five launches of the build over a caller-provided int32 workspace of
+// counter_elems + total_blocks * groups entries (the tile histograms are cleared by
+// k2q_count itself and the row totals are written before they are read, so the
+// workspace may hold anything on entry).
+int k2q_build_launch(const int32_t* indices, const int32_t* cu_seqlens, const int32_t* cu_block_lens,
+                     const int64_t* tri_prefix, int64_t num_seqs, int64_t total_tokens, int64_t groups,
+                     int64_t topk_slots, int64_t block_size, int64_t total_blocks, int64_t counter_elems,
+                     int32_t* row_ptr, int32_t* query_indices, int32_t* slot_indices, int32_t* workspace,
+                     hipStream_t st) {
   const int64_t rows = total_blocks * groups;
   const int64_t capacity = total_tokens * groups * topk_slots;
   if (capacity == 0 || rows == 0) {
@@ -332,4 +335,79 @@ extern "C" int msa_k2q_build(const int32_t* indices, const int32_t* cu_seqlens,
   hipLaunchKernelGGL(k2q_tail, dim3(capped_grid(capacity)), dim3(256), 0, st, row_ptr, rows, capacity,
                      query_indices, slot_indices);
   return status_from(hipGetLastError());
+}
+
+bool k2q_args_valid(int64_t num_seqs, int64_t total_tokens, int64_t groups, int64_t topk_slots, int64_t block_size,
+                    int64_t total_blocks, int64_t counter_elems) {
+  return num_seqs > 0 && total_tokens >= 0 && groups > 0 && topk_slots >= 0 && block_size > 0 &&
+         total_blocks >= 0 && counter_elems >= 0;
+}
+
+// Workspace of msa_k2q_build_noalloc: a fixed device array, one copy per GPU (the
+// module is loaded on every device the library runs on). Host code never uses the
+// symbol's name as an address: each device's address is looked up once, with that
+// device current, and kept in scratch_addr.
+constexpr int64_t kNoAllocElems = MSA_K2Q_NOALLOC_MAX_ELEMS;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) int32_t scratch[kNoAllocElems];
+std::mutex g_scratch_mu;
+int32_t* g_scratch_addr[kMaxDevices] = {};
+
+// The current device's copy of `scratch`, or nullptr (status in *rc) when it cannot be found.
+int32_t* scratch_addr(int* rc) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    *rc = kErrUnsupported;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      *rc = kErrLaunch;
+      return nullptr;
+    }
+    g_scratch_addr[dev] = static_cast<int32_t*>(p);
+  }
+  *rc = kOk;
+  return g_scratch_addr[dev];
+}
+
+}  // namespace
+
+}  // namespace msa
+
+// workspace: int32 [counter_elems + total_blocks * groups].
+// tri_prefix: int64 [num_seqs + 1], tri_prefix[s] = G * sum_{s'<s} nb(nb+1)/2.
+extern "C" int msa_k2q_build(const int32_t* indices, const int32_t* cu_seqlens,
+                             const int32_t* cu_block_lens, const int64_t* tri_prefix,
+                             int64_t num_seqs, int64_t total_tokens, int64_t groups, int64_t topk_slots,
+                             int64_t block_size, int64_t total_blocks, int64_t counter_elems,
+                             int32_t* row_ptr, int32_t* query_indices, int32_t* slot_indices,
+                             int32_t* workspace, void* stream) {
+  if (!k2q_args_valid(num_seqs, total_tokens, groups, topk_slots, block_size, total_blocks, counter_elems))
+    return kErrInvalidArgument;
+  if (block_size * groups * topk_slots >= (int64_t(1) << 31)) return kErrUnsupported;  // edges per tile in int32
+  return k2q_build_launch(indices, cu_seqlens, cu_block_lens, tri_prefix, num_seqs, total_tokens, groups,
+                          topk_slots, block_size, total_blocks, counter_elems, row_ptr, query_indices, slot_indices,
+                          workspace, static_cast<hipStream_t>(stream));
+}
+
+// msa_k2q_build with the library's fixed per-GPU scratch array as the workspace.
+extern "C" int msa_k2q_build_noalloc(const int32_t* indices, const int32_t* cu_seqlens,
+                                     const int32_t* cu_block_lens, const int64_t* tri_prefix, int64_t num_seqs,
+                                     int64_t total_tokens, int64_t groups, int64_t topk_slots, int64_t block_size,
+                                     int64_t total_blocks, int64_t counter_elems, int32_t* row_ptr,
+                                     int32_t* query_indices, int32_t* slot_indices, void* stream) {
+  if (!k2q_args_valid(num_seqs, total_tokens, groups, topk_slots, block_size, total_blocks, counter_elems))
+    return kErrInvalidArgument;
+  if (block_size * groups * topk_slots >= (int64_t(1) << 31)) return kErrUnsupported;  // edges per tile in int32
+  if (counter_elems + total_blocks * groups > kNoAllocElems) return kErrUnsupported;  // beyond the scratch array
+  int rc = kOk;
+  int32_t* ws = scratch_addr(&rc);
+  if (!ws) return rc;
+  return k2q_build_launch(indices, cu_seqlens, cu_block_lens, tri_prefix, num_seqs, total_tokens, groups,
+                          topk_slots, block_size, total_blocks, counter_elems, row_ptr, query_indices, slot_indices,
+                          ws, static_cast<hipStream_t>(stream));
 }
