@@ -300,20 +300,35 @@ __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
   }
 }
 
+// The main pass's per-row record (lse2, 1 / mass, c, w) in fp32, from the fp64 row state:
+// p = 2^(x - lse2) / mass and dS = P ((dp - c) - w).
+__device__ __forceinline__ float4 main_row_record(double lse2, double mass, double c, double w) {
+  return make_float4(static_cast<float>(lse2), static_cast<float>(1.0 / fabs(mass)), static_cast<float>(c),
+                     static_cast<float>(w));
+}
+
 // mass = sum_s A_s, delta = sum_s B_s / mass over the row's valid slots (FP64);
 // 32 lanes per (token, head), slots lane-parallel then a fixed shuffle tree. Rows
 // outside the pass (flat rows, unless all_rows) keep the forward's mass. The mass
 // keeps the sign of the forward's mark, so a repeated backward selects the same rows.
+// Every row of the chunk then gets the main pass's fp32 record in rowf.
 __global__ __launch_bounds__(256) void kv_bwd_stats_combine(const int32_t* __restrict__ indices,
                                                             const int32_t* __restrict__ cu, int nseq, int64_t t0,
                                                             int64_t t1, int Hq, int G, int K, int B, int all_rows,
                                                             const float2* __restrict__ spart,
-                                                            double* __restrict__ row_state) {
+                                                            double* __restrict__ row_state,
+                                                            float4* __restrict__ rowf) {
   const int sub = threadIdx.x & 31;
   const int64_t th = t0 * Hq + static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
   if (th >= t1 * Hq) return;
   const double mark = row_state[th * 4 + 1];
-  if (!all_rows && mark > 0.0) return;  // uniform over the row's 32 lanes
+  if (!all_rows && mark > 0.0) {  // uniform over the row's 32 lanes
+    if (sub == 0) {
+      const double4 rs = *reinterpret_cast<const double4*>(row_state + th * 4);
+      rowf[th] = main_row_record(rs.x, rs.y, rs.z, rs.w);
+    }
+    return;
+  }
   const int64_t t = th / Hq;
   const int h = static_cast<int>(th % Hq);
   const int g = h / (Hq / G);
@@ -337,8 +352,10 @@ __global__ __launch_bounds__(256) void kv_bwd_stats_combine(const int32_t* __res
   }
   if (sub == 0) {
     const bool has = a > 0.0;
-    row_state[th * 4 + 1] = copysign(has ? a : 1.0, mark);
-    row_state[th * 4 + 3] = has ? b / a : 0.0;
+    const double mass = copysign(has ? a : 1.0, mark), delta = has ? b / a : 0.0;
+    row_state[th * 4 + 1] = mass;
+    row_state[th * 4 + 3] = delta;
+    rowf[th] = main_row_record(row_state[th * 4], mass, row_state[th * 4 + 2], delta);
   }
 }
 
@@ -362,12 +379,12 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     const uint16_t* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx, const int32_t* __restrict__ sidx,
     const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items, const int2* __restrict__ items, int nseq,
-    int Hq, int G, int D, int K, int B, float scale2, int epi, int t0, uint32_t rmagic, float* __restrict__ dqpart,
-    float* __restrict__ kvpart) {
+    int Hq, int G, int D, int K, int B, float scale2, int epi, int t0, uint32_t rmagic, int rshift,
+    const float4* __restrict__ rowf, float* __restrict__ dqpart, float* __restrict__ kvpart) {
   constexpr int DP = 32 * NK, NDT = DP / 16, KS = MainSmem<NK>::KS;
   constexpr int RV = DP / 8;             // 16-byte chunks per row
-  constexpr int TV = 32 * RV;            // chunks per tile and tensor
-  constexpr int SI = (TV + 255) / 256;   // chunks per staging thread (threads 0-255: Q, 256-511: dO)
+  constexpr int CPT = RV >= 8 ? RV / 8 : 1;  // chunks per staging thread (threads 0-255: Q, 256-511: dO)
+  constexpr int TPR = RV / CPT;          // staging threads per row
   __shared__ MainSmem<NK> sm;
   const int item = blockIdx.x;
   if (item >= *n_items) return;
@@ -434,58 +451,57 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       kt[dt2][kc] = dq_active ? frag_tr(sm.k, KS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 32 * dq + 16 * dt2, c)
                               : zero_frag();
 
-  // ---- row staging: thread tid loads 16-byte chunks of Q (tid < 256) or dO rows of a
-  // tile; threads 0-31 also fetch the per-row statistics, visible keys and record.
+  // ---- row staging: a tile is 32 rows of Q (threads 0-255) and of dO (threads 256-511);
+  // TPR threads per row, each CPT consecutive 16-byte chunks, so a thread forms one row
+  // address per tile. The first thread of each Q row also fetches the row's fp32 record
+  // (rowf), its visible keys and its dQ record (spread over waves 0-3).
+  const int lt = tid & 255;
+  const int srow = lt / TPR;  // tile row of this thread
+  const bool stager = srow < 32;
+  const int sc0 = (lt % TPR) * CPT;
+  const bool meta_thread = tid < 256 && stager && (lt % TPR) == 0;
   const uint16_t* src = tid < 256 ? q : dout;
-  uint4 pf[SI];
-  double4 pst = make_double4(0.0, 1.0, 0.0, 0.0);
+  uint4 pf[CPT];
+  float4 pst = make_float4(0.f, 1.f, 0.f, 0.f);
   int prec = -1, pvis = 0;
 #define MSA_MAIN_ISSUE(R0)                                                                                  \
-  {                                                                                                         \
-    _Pragma("unroll") for (int i = 0; i < SI; ++i) {                                                        \
-      const int idx = (tid & 255) + 256 * i;                                                                \
-      if (TV % 256 == 0 || idx < TV) {                                                                      \
-        const int rr = idx / RV, d0 = 8 * (idx % RV);                                                       \
-        const int rho = (R0) + rr < nrows ? (R0) + rr : nrows - 1;                                          \
-        const int eo = div_by_ratio(rho, rmagic);                                                           \
-        const int64_t th = static_cast<int64_t>(sm.etok[eo]) * Hq + rg.g * R + (rho - eo * R);              \
-        const int d0c = (FULLD || d0 < D) ? d0 : D - 8;                                                     \
-        pf[i] = *reinterpret_cast<const uint4*>(src + th * D + d0c);                                        \
-      }                                                                                                     \
+  if (stager) {                                                                                             \
+    const int rho = (R0) + srow < nrows ? (R0) + srow : nrows - 1;                                          \
+    const int eo = rshift >= 0 ? rho >> rshift : div_by_ratio(rho, rmagic);                                 \
+    const int h = rg.g * R + (rho - eo * R);                                                                \
+    const int tk = sm.etok[eo];                                                                             \
+    const int64_t th = static_cast<int64_t>(tk) * Hq + h;                                                   \
+    const uint16_t* rowp = src + th * D;                                                                    \
+    _Pragma("unroll") for (int j = 0; j < CPT; ++j) {                                                       \
+      const int d0 = 8 * (sc0 + j);                                                                         \
+      pf[j] = *reinterpret_cast<const uint4*>(rowp + ((FULLD || d0 < D) ? d0 : D - 8));                     \
     }                                                                                                       \
-    if (tid < 32) {                                                                                         \
-      const int rho = (R0) + tid;                                                                           \
-      if (rho < nrows) {                                                                                    \
-        const int eo = div_by_ratio(rho, rmagic);                                                           \
-        const int h = rg.g * R + (rho - eo * R);                                                            \
-        const int tk = sm.etok[eo];                                                                         \
-        pst = *reinterpret_cast<const double4*>(row_state + (static_cast<int64_t>(tk) * Hq + h) * 4);       \
+    if (meta_thread) {                                                                                      \
+      if ((R0) + srow < nrows) {                                                                            \
+        pst = rowf[th];                                                                                     \
         prec = ((tk - t0) * Hq + h) * K + sm.eslot[eo];                                                     \
         const int64_t vk = static_cast<int64_t>(tk) - rg.kb + 1;                                            \
         pvis = vk < rg.nk ? static_cast<int>(vk) : rg.nk;                                                   \
       } else {                                                                                              \
-        pst = make_double4(0.0, 1.0, 0.0, 0.0);                                                             \
+        pst = make_float4(0.f, 1.f, 0.f, 0.f);                                                              \
         prec = -1;                                                                                          \
         pvis = 0;                                                                                           \
       }                                                                                                     \
     }                                                                                                       \
   }
 #define MSA_MAIN_COMMIT(R0, BUF)                                                                            \
-  {                                                                                                         \
-    uint16_t* dstt = tid < 256 ? sm.qs[BUF] : sm.gs[BUF];                                                   \
-    _Pragma("unroll") for (int i = 0; i < SI; ++i) {                                                        \
-      const int idx = (tid & 255) + 256 * i;                                                                \
-      if (TV % 256 == 0 || idx < TV) {                                                                      \
-        const int rr = idx / RV, d0 = 8 * (idx % RV);                                                       \
-        const bool ok = (R0) + rr < nrows && (FULLD || d0 < D);                                             \
-        *reinterpret_cast<uint4*>(dstt + rr * KS + d0) = ok ? pf[i] : make_uint4(0u, 0u, 0u, 0u);          \
-      }                                                                                                     \
+  if (stager) {                                                                                             \
+    uint16_t* dstt = (tid < 256 ? sm.qs[BUF] : sm.gs[BUF]) + srow * KS;                                     \
+    const bool rok = (R0) + srow < nrows;                                                                   \
+    _Pragma("unroll") for (int j = 0; j < CPT; ++j) {                                                       \
+      const int d0 = 8 * (sc0 + j);                                                                         \
+      const bool ok = rok && (FULLD || d0 < D);                                                             \
+      *reinterpret_cast<uint4*>(dstt + d0) = ok ? pf[j] : make_uint4(0u, 0u, 0u, 0u);                       \
     }                                                                                                       \
-    if (tid < 32) {                                                                                         \
-      sm.st[BUF][tid] = make_float4(static_cast<float>(pst.x), static_cast<float>(1.0 / fabs(pst.y)),        \
-                                    static_cast<float>(pst.z), static_cast<float>(pst.w));                   \
-      sm.vis[BUF][tid] = pvis;                                                                              \
-      sm.rec[BUF][tid] = prec;                                                                              \
+    if (meta_thread) {                                                                                      \
+      sm.st[BUF][srow] = pst;                                                                               \
+      sm.vis[BUF][srow] = pvis;                                                                             \
+      sm.rec[BUF][srow] = prec;                                                                             \
     }                                                                                                       \
   }
 
@@ -612,7 +628,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
         for (int dt2 = 0; dt2 < 2; ++dt2) {
           const int d0 = 32 * dq + 16 * dt2 + 4 * q4;
           if (FULLD || d0 < D)
-            __builtin_nontemporal_store(acc[dt2], reinterpret_cast<f32x4*>(dqpart + static_cast<int64_t>(myrec) * D + d0));
+            __builtin_nontemporal_store(acc[dt2], reinterpret_cast<f32x4*>(dqpart + static_cast<uint32_t>(myrec * D + d0)));
         }
       }
     }
@@ -734,7 +750,7 @@ static int nk_of_dim(int D) { return D <= 32 ? 1 : (D <= 64 ? 2 : 4); }
 
 struct BwdLayout {
   KvPlan stat_plan, main_plan;
-  int64_t stat_base, main_base, spart, dqpart, kvpart, acc, total;
+  int64_t stat_base, main_base, spart, dqpart, kvpart, acc, rowf, total;
 };
 
 static BwdLayout bwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks) {
@@ -753,7 +769,8 @@ static BwdLayout bwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t
   b.dqpart = b.spart + align256(tc * Hq * K * 8);
   b.kvpart = b.dqpart + align256(tc * Hq * K * D * 4);
   b.acc = b.kvpart + align256(b.main_plan.max_items * 2 * 128 * DP * 4);
-  b.total = b.acc + align256(2 * T * G * D * 4);
+  b.rowf = b.acc + align256(2 * T * G * D * 4);
+  b.total = b.rowf + align256(T * Hq * 16);
   return b;
 }
 
@@ -769,7 +786,8 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   const int64_t rows = total_blocks * G;
   const BwdLayout L = bwd_layout(T, Hq, G, D, K, total_blocks);
   if (ws_bytes < L.total) return kErrInvalidArgument;
-  if (!kv_csr_fits(T, G, K, rows) || !kv_chunk_records_fit(L.main_plan.tc, Hq, K)) return kErrUnsupported;
+  // dQ partial element offsets (record * D + dim) are 32-bit
+  if (!kv_csr_fits(T, G, K, rows) || !kv_chunk_records_fit(L.main_plan.tc, Hq, K * D)) return kErrUnsupported;
   if (T == 0) return kOk;
   char* base = static_cast<char*>(ws);
   void* sbase = base + L.stat_base;
@@ -778,6 +796,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   float* dqpart = reinterpret_cast<float*>(base + L.dqpart);
   float* kvpart = reinterpret_cast<float*>(base + L.kvpart);
   float* acc = reinterpret_cast<float*>(base + L.acc);
+  float4* rowf = reinterpret_cast<float4*>(base + L.rowf);
   const auto* qb = static_cast<const uint16_t*>(q);
   const auto* kb = static_cast<const uint16_t*>(k);
   const auto* vb = static_cast<const uint16_t*>(v);
@@ -793,6 +812,8 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   // every row does.
   const int all_rows = o32 == nullptr;
   const uint32_t rmagic = ratio_magic(Hq / G);  // rows x ratio < 512 * 512^2 < 2^32
+  const int ratio = Hq / G;
+  const int rshift = (ratio & (ratio - 1)) == 0 ? __builtin_ctz(ratio) : -1;  // power-of-two ratios shift
   {
     ProfScope ps(kProfBwdCenter, st);
     hipLaunchKernelGGL(kv_bwd_center, dim3(grid_1d(T * Hq, 8)), dim3(256), 0, st, ob, o32, gb, T * Hq, D, rs);
@@ -823,7 +844,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
     {
       ProfScope ps(kProfBwdStatsCombine, st);
       hipLaunchKernelGGL(kv_bwd_stats_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu,
-                         nseq, t0, t1, Hq, G, K, B, all_rows, spart, rs);
+                         nseq, t0, t1, Hq, G, K, B, all_rows, spart, rs, rowf);
     }
     if (rows > 0) {
       const int32_t* hi = kv_plan_hi(mp, mbase, c);
@@ -833,7 +854,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       const dim3 grid(static_cast<unsigned>(mp.max_items)), block(kMainThreads);
       {
         ProfScope ps(kProfBwdMain, st);
-#define MSA_BWD_MAIN(NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, dqpart, kvpart)
+#define MSA_BWD_MAIN(NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, rshift, rowf, dqpart, kvpart)
         if (nk == 1) { if (fd) MSA_BWD_MAIN(1, true); else MSA_BWD_MAIN(1, false); }
         else if (nk == 2) { if (fd) MSA_BWD_MAIN(2, true); else MSA_BWD_MAIN(2, false); }
         else { if (fd) MSA_BWD_MAIN(4, true); else MSA_BWD_MAIN(4, false); }

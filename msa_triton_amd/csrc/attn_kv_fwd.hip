@@ -42,7 +42,11 @@ constexpr int kItemRows = kRowsPerTile * kTilesPerItem;
 template <int NK>
 struct FwdSmem {
   static constexpr int DP = 32 * NK;
-  static constexpr int KS = DP + 8;   // row stride of the K and V blocks (bf16)
+  // Row stride of the K and V blocks (bf16): DP + 16 halves (288 bytes at DP = 128) puts
+  // both the row-fragment reads of K (ds_read_b128, lane c -> row c) and the transposed
+  // reads of V (ds_read_b64_tr_b16, four rows x 32 bytes per 16 lanes) on distinct banks;
+  // DP + 8 leaves both 2-way conflicted.
+  static constexpr int KS = DP + 16;
   alignas(16) uint16_t k[128 * KS];
   alignas(16) uint16_t v[128 * KS];
   int32_t th[kItemRows];   // (token - t0) * Hq + head (chunk-local)
