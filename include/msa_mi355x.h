@@ -65,16 +65,20 @@ int msa_k2q_build_noalloc(const int32_t* indices, const int32_t* cu_seqlens, con
                           int64_t counter_elems, int32_t* row_ptr, int32_t* query_indices,
                           int32_t* slot_indices, void* stream);
 
+/* Stage 1 forward workspace in bytes (the squared norm of every index key, fp32 [T]). */
+int64_t msa_score_fwd_workspace_bytes(int64_t total_tokens);
+
 /* Stage 1 forward: per-group causal block maxima of scale * (index_q . index_k).
  * Replaces triton/index_score.py:93-136 (_index_score_forward) and the launch at
  * :237-265. scores = fl32(scale * exact winning dot); -inf for blocks with no
  * causal key. tie_info (nullable, int32 [T,G,NB]): winner offset + 1 for a
  * unique exact maximum, -count for exact ties, 0 for invalid blocks
- * (same encoding as index_score.py:128-136). */
+ * (same encoding as index_score.py:128-136). workspace: at least
+ * msa_score_fwd_workspace_bytes(total_tokens) bytes, 4-byte aligned. */
 int msa_score_fwd(const void* index_q, const void* index_k, int32_t dtype,
                   const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
                   int64_t groups, int64_t index_dim, int64_t num_blocks, int64_t block_size,
-                  double scale, float* scores, int32_t* tie_info, void* stream);
+                  double scale, float* scores, int32_t* tie_info, void* workspace, void* stream);
 
 /* Stage 1 forward fused with stage 2: the scores of msa_score_fwd and, from them,
  * the causal top-k selection of msa_topk (int32 [T,G,K], same semantics and tie
@@ -82,12 +86,12 @@ int msa_score_fwd(const void* index_q, const void* index_k, int32_t dtype,
  * triton/index_score.py:298-357 and triton/topk.py:11-47 as two operators; this
  * is the score -> top-k fusion the reference's survey lists as follow-on work,
  * as one call: the selection is a second launch on the same stream (selecting
- * inside the score kernel's tiles measured slower). */
+ * inside the score kernel's tiles measured slower). workspace as for msa_score_fwd. */
 int msa_index_score_topk(const void* index_q, const void* index_k, int32_t dtype,
                          const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
                          int64_t groups, int64_t index_dim, int64_t num_blocks, int64_t block_size,
                          double scale, int64_t topk_blocks, int64_t local_blocks, float* scores,
-                         int32_t* tie_info, int32_t* indices, void* stream);
+                         int32_t* tie_info, int32_t* indices, void* workspace, void* stream);
 
 /* Score backward workspace in bytes (block-major tie/grad copies and the FP64
  * per-segment dk sums). */

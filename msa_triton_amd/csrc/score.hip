@@ -623,13 +623,13 @@ static int64_t dk_nseg(int64_t rows) { return (rows + kDkSeg - 1) / kDkSeg; }
 template <int DT>
 int score_fwd_launch(const void* iq, const void* ik, const int32_t* cu, int nseq, int64_t rows, int G,
                      int Di, int NB, int B, double scale, float* scores, int32_t* tie, int K, int L, int32_t* sel,
-                     hipStream_t st) {
+                     void* ws, hipStream_t st) {
   // sel != null: the top-k selection follows on the same stream (topk.hip). Selecting
   // inside the MFMA kernel's tiles, from the scores just written, was measured slower
   // at c4 (2.43-2.81 ms vs 2.27 ms for the two launches): the score kernel runs two
   // workgroups per CU and the selection's registers cost its main loop.
   if (DT == kBF16 && score_mfma_supported(Di, B, scale)) {
-    const int rc = score_fwd_mfma_launch(iq, ik, cu, nseq, rows, G, Di, NB, B, scale, scores, tie, st);
+    const int rc = score_fwd_mfma_launch(iq, ik, cu, nseq, rows, G, Di, NB, B, scale, scores, tie, ws, st);
     if (rc != kOk || !sel) return rc;
     return topk_launch(scores, cu, nseq, rows, G, NB, B, K, L, sel, st);
   }
@@ -685,10 +685,14 @@ int score_bwd_launch(const void* iq, const void* ik, const int32_t* cu, const in
 
 using namespace msa;
 
+extern "C" int64_t msa_score_fwd_workspace_bytes(int64_t total_tokens) {
+  return score_fwd_mfma_workspace_bytes(total_tokens);
+}
+
 extern "C" int msa_score_fwd(const void* index_q, const void* index_k, int32_t dtype,
                              const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
                              int64_t groups, int64_t index_dim, int64_t num_blocks, int64_t block_size,
-                             double scale, float* scores, int32_t* tie_info, void* stream) {
+                             double scale, float* scores, int32_t* tie_info, void* workspace, void* stream) {
   if (num_seqs <= 0 || total_tokens < 0 || groups <= 0 || index_dim <= 0 || num_blocks <= 0 ||
       block_size <= 0)
     return kErrInvalidArgument;
@@ -700,9 +704,9 @@ extern "C" int msa_score_fwd(const void* index_q, const void* index_k, int32_t d
   const int Di = static_cast<int>(index_dim), NB = static_cast<int>(num_blocks);
   const int B = static_cast<int>(block_size);
   switch (dtype) {
-    case kF32: return score_fwd_launch<kF32>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, 0, 0, nullptr, st);
-    case kF16: return score_fwd_launch<kF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, 0, 0, nullptr, st);
-    case kBF16: return score_fwd_launch<kBF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, 0, 0, nullptr, st);
+    case kF32: return score_fwd_launch<kF32>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, 0, 0, nullptr, workspace, st);
+    case kF16: return score_fwd_launch<kF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, 0, 0, nullptr, workspace, st);
+    case kBF16: return score_fwd_launch<kBF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, 0, 0, nullptr, workspace, st);
     default: return kErrInvalidArgument;
   }
 }
@@ -711,7 +715,7 @@ extern "C" int msa_index_score_topk(const void* index_q, const void* index_k, in
                                     const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
                                     int64_t groups, int64_t index_dim, int64_t num_blocks, int64_t block_size,
                                     double scale, int64_t topk_blocks, int64_t local_blocks, float* scores,
-                                    int32_t* tie_info, int32_t* indices, void* stream) {
+                                    int32_t* tie_info, int32_t* indices, void* workspace, void* stream) {
   if (num_seqs <= 0 || total_tokens < 0 || groups <= 0 || index_dim <= 0 || num_blocks <= 0 ||
       block_size <= 0 || topk_blocks < 0 || local_blocks < 0 || local_blocks > topk_blocks ||
       (topk_blocks > 0 && !indices))
@@ -726,9 +730,9 @@ extern "C" int msa_index_score_topk(const void* index_q, const void* index_k, in
   const int L = static_cast<int>(local_blocks);
   int32_t* sel = K > 0 ? indices : nullptr;
   switch (dtype) {
-    case kF32: return score_fwd_launch<kF32>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, K, L, sel, st);
-    case kF16: return score_fwd_launch<kF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, K, L, sel, st);
-    case kBF16: return score_fwd_launch<kBF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, K, L, sel, st);
+    case kF32: return score_fwd_launch<kF32>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, K, L, sel, workspace, st);
+    case kF16: return score_fwd_launch<kF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, K, L, sel, workspace, st);
+    case kBF16: return score_fwd_launch<kBF16>(index_q, index_k, cu_seqlens, nseq, rows, G, Di, NB, B, scale, scores, tie_info, K, L, sel, workspace, st);
     default: return kErrInvalidArgument;
   }
 }

@@ -7,15 +7,24 @@
 // 32 x 128 logits on v_mfma_f32_16x16x32_bf16 (exact bf16 products, fp32
 // accumulation) against the block held in LDS. Key blocks are double-buffered:
 // the next block is fetched from memory while the current one is used, so one
-// barrier per block orders all LDS traffic. Tiles are issued heaviest first
-// (the last rows of a sequence see the most blocks).
+// barrier per block orders all LDS traffic. With the index dim a multiple of 32
+// the blocks go from memory straight to LDS (global_load_lds_dwordx4: 16 bytes
+// per lane, no staging registers) into unpadded rows whose 16-byte chunks are
+// XOR-swizzled by row, so the fragment reads stay bank-conflict free. Tiles are
+// issued heaviest first (the last rows of a sequence see the most blocks).
+// Squared key norms (for the error bound below) are computed once per key by a
+// pre-pass (score_key_norms) instead of per tile.
 //
 // Exactness (the public score must equal fl32(scale * exact winning dot) and
 // the winner set must be the exact one, index_score.py:121-136): with
 //   E = (Di_pad + 8) * 2^-22 * ||q|| * max_k ||k||  >=  |s_mfma - s_exact|,
 // every key whose approximate directed logit is below (max_approx - 2E) is
-// certainly beaten by the approximate winner. If exactly one key survives,
-// it is the unique exact winner and only its dot is evaluated in FP64: a lane
+// certainly beaten by the approximate winner. The running maximum and runner-up
+// are tracked on logits whose 7 low mantissa bits are replaced by the key's
+// position (16 kt + i; the quarter q4 is recovered after the cross-lane merge),
+// which moves each by < 2^-16 of its magnitude: the test therefore also allows
+// 2^-15 max(|max|, |runner-up|) plus the smallest normal float. If exactly one key
+// survives, it is the unique exact winner and only its dot is evaluated in FP64: a lane
 // pair owns the row, each lane runs one half of exact_dot's fixed order (two
 // sequential FMA chains over the halves of the index dim) from the query half
 // it keeps in registers and the key row in LDS, and the halves are added in
@@ -23,6 +32,8 @@
 // block in FP64 (same order) and takes max / tie count / first winner exactly.
 // A negative scale flips the query signs once (exact), so every comparison is
 // on the directed dot.
+#include <type_traits>
+
 #include "mfma_util.hpp"
 #include "score_mfma.hpp"
 
@@ -36,11 +47,31 @@ constexpr int kThreads = 256;
 template <int NK>
 struct ScoreSmem {
   static constexpr int DP = 32 * NK;
-  static constexpr int RS = DP + 8;  // row stride (bf16) of a key block: conflict-free 16-byte row reads
-  alignas(16) uint16_t k[2][128 * RS];
-  float kmax2[2][4];  // per-wave max squared key norm of the buffered block
+  static constexpr int RS = DP + 8;  // row stride (bf16) of a padded key block (index dim below DP)
+  alignas(16) uint16_t k[2][128 * RS];  // full-width blocks use the first 128 * DP entries (swizzled rows)
   uint32_t qrow[4][DP / 2];  // per-wave query row of an ambiguous row (packed bf16)
 };
+
+// Offset (bf16 elements) of dims [d, d + 8) of key `row` in a buffered block (d a
+// multiple of 8). Full width: rows DP apart, 16-byte chunk c at c ^ swz(row), with
+// swz chosen so the 16 rows one fragment read touches land on 16 distinct bank
+// groups. Otherwise: rows DP + 8 apart, unswizzled.
+template <int NK, bool FULLD>
+__device__ __forceinline__ int key_off(int row, int d) {
+  constexpr int DP = 32 * NK, CPK = DP / 8;
+  if constexpr (FULLD) {
+    constexpr int SH = NK == 4 ? 0 : (NK == 2 ? 1 : 2);  // rows sharing a bank base: 16 / CPK apart
+    return row * DP + 8 * ((d >> 3) ^ ((row >> SH) & (CPK - 1)));
+  } else {
+    return row * (DP + 8) + d;
+  }
+}
+
+// Logit bits with the key position in the 7 low mantissa bits (see the header comment).
+__device__ __forceinline__ float pack_key(float v, uint32_t pos) {
+  return __uint_as_float((__float_as_uint(v) & 0xffffff80u) | pos);
+}
+constexpr float kMaskedLogit = -3.0e38f;  // a finite stand-in for masked keys (packing keeps it finite)
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -77,17 +108,37 @@ __device__ __forceinline__ BlockCursor next_block(const int32_t* __restrict__ cu
 
 }  // namespace
 
+// Squared norm of every index key, rounded up by 1.0001 (bounds the fp32 rounding of
+// the sum): the max over a key block enters the MFMA logits' error bound.
+__global__ __launch_bounds__(256) void score_key_norms(const uint16_t* __restrict__ ik, int64_t T, int Di,
+                                                       float* __restrict__ knorm2) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (j >= T) return;
+  float n2 = 0.f;
+  for (int d = 0; d < Di; d += 8) {
+    const uint4 w = *reinterpret_cast<const uint4*>(ik + j * Di + d);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      n2 = fmaf(bf16_lo(ws[u]), bf16_lo(ws[u]), n2);
+      n2 = fmaf(bf16_hi(ws[u]), bf16_hi(ws[u]), n2);
+    }
+  }
+  knorm2[j] = n2 * 1.0001f;
+}
+
 template <int NK, bool FULLD>
 __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint16_t* __restrict__ iq,
                                                                      const uint16_t* __restrict__ ik,
                                                                      const int32_t* __restrict__ cu, int nseq,
                                                                      int64_t rows, int G, int Di, int NB, int B,
-                                                                     double scale, float* __restrict__ scores,
+                                                                     double scale, const float* __restrict__ knorm2,
+                                                                     float* __restrict__ scores,
                                                                      int32_t* __restrict__ tie) {
-  constexpr int DP = 32 * NK, RS = ScoreSmem<NK>::RS;
+  constexpr int DP = 32 * NK;
   constexpr int CPK = DP / 8;                 // 16-byte chunks per key row
   constexpr int KCH = 128 * CPK / kThreads;   // chunks per thread per key block
-  constexpr int HW = DP / 4;                  // max 32-bit words of a query half (Di / 2 <= DP / 2)
+  constexpr int HF = DP / 2;                  // max dims of a query half (Di / 2 <= DP / 2)
   __shared__ ScoreSmem<NK> sm;
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
   const int64_t r0 = static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * kTileRows;  // heaviest tiles first
@@ -126,10 +177,10 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
   const int pr = lane & 31, hf = lane >> 5;
   const int prow = wr0 + pr;
   const bool pin = prow < nr;
-  uint32_t qh[HW];
+  uint32_t qh[HF / 2];
   float pn2 = 0.f;
 #pragma unroll
-  for (int w4 = 0; w4 < HW / 2; ++w4) {  // 8-byte loads: 4 dims each
+  for (int w4 = 0; w4 < HF / 4; ++w4) {  // 8-byte loads: 4 dims each
     uint2 x = make_uint2(0u, 0u);
     if (pin && 4 * w4 < h) x = *reinterpret_cast<const uint2*>(iq + (r0 + prow) * Di + hf * h + 4 * w4);
     x.x ^= flip;
@@ -148,42 +199,62 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
   for (int rt = 0; rt < 2; ++rt) mnorm[rt] = __shfl(pnorm, 16 * rt + c, kWave);
   const int64_t ptok = pin ? (r0 + prow) / G : -1;
 
-  // ---- key block staging: thread tid holds KCH 16-byte chunks (keys (tid + 256 i) / CPK)
-  uint4 kreg[KCH];
-  auto fetch = [&](const BlockCursor& bc) {
+  // ---- key block staging
+  uint4 kreg[FULLD ? 1 : KCH];  // register staging of partial-width blocks
+  auto fetch = [&](const BlockCursor& bc, int into) {
     if (bc.s >= nseq) return;
     const int64_t kb = cu[bc.s] + static_cast<int64_t>(bc.b) * B;
     const int64_t end = cu[bc.s + 1];
     const int nk = static_cast<int>(end - kb < B ? end - kb : B);
+    if constexpr (FULLD) {
+      // wave wid's instruction i fills physical chunks p = (wid KCH + i) 64 + lane of the
+      // buffer (1 KiB each); rows past the block's end repeat its last key (masked later)
+      char* dst = reinterpret_cast<char*>(sm.k[into]) + wid * KCH * 1024;
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int e = tid + kThreads * i;
-      const int kl = e / CPK, d0 = 8 * (e % CPK);
-      kreg[i] = (kl < nk && d0 < Di) ? *reinterpret_cast<const uint4*>(ik + (kb + kl) * Di + d0)
-                                     : make_uint4(0u, 0u, 0u, 0u);
+      for (int i = 0; i < KCH; ++i) {
+        const int p = (wid * KCH + i) * 64 + lane;
+        const int row = p / CPK, pc = p % CPK;
+        constexpr int SH = NK == 4 ? 0 : (NK == 2 ? 1 : 2);
+        const int lc = pc ^ ((row >> SH) & (CPK - 1));
+        const int rowc = row < nk ? row : nk - 1;
+        __builtin_amdgcn_global_load_lds(ik + (kb + rowc) * Di + 8 * lc,
+                                         (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < KCH; ++i) {
+        const int e = tid + kThreads * i;
+        const int kl = e / CPK, d0 = 8 * (e % CPK);
+        kreg[i] = (kl < nk && d0 < Di) ? *reinterpret_cast<const uint4*>(ik + (kb + kl) * Di + d0)
+                                       : make_uint4(0u, 0u, 0u, 0u);
+      }
     }
   };
-  auto commit = [&](int buf) {
-    float n2 = 0.f;
+  auto commit = [&](int into) {
+    if constexpr (!FULLD) {
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int e = tid + kThreads * i;
-      const int kl = e / CPK, d0 = 8 * (e % CPK);
-      *reinterpret_cast<uint4*>(sm.k[buf] + kl * RS + d0) = kreg[i];
-      float part = 0.f;
-      const uint32_t ws[4] = {kreg[i].x, kreg[i].y, kreg[i].z, kreg[i].w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        part = fmaf(bf16_lo(ws[j]), bf16_lo(ws[j]), part);
-        part = fmaf(bf16_hi(ws[j]), bf16_hi(ws[j]), part);
+      for (int i = 0; i < KCH; ++i) {
+        const int e = tid + kThreads * i;
+        const int kl = e / CPK, d0 = 8 * (e % CPK);
+        *reinterpret_cast<uint4*>(sm.k[into] + key_off<NK, FULLD>(kl, d0)) = kreg[i];
       }
-#pragma unroll
-      for (int o = 1; o < CPK; o <<= 1) part += __shfl_xor(part, o, kWave);  // CPK consecutive lanes per key
-      n2 = fmaxf(n2, part);
     }
+  };
+  // squared key norms of a block (lanes l and l + 64) and the block's max norm
+  auto norm_loads = [&](const BlockCursor& bc, float& n0, float& n1) {
+    n0 = n1 = 0.f;
+    if (bc.s >= nseq) return;
+    const int64_t kb = cu[bc.s] + static_cast<int64_t>(bc.b) * B;
+    const int64_t end = cu[bc.s + 1];
+    const int nk = static_cast<int>(end - kb < B ? end - kb : B);
+    if (lane < nk) n0 = knorm2[kb + lane];
+    if (lane + 64 < nk) n1 = knorm2[kb + lane + 64];
+  };
+  auto block_kmax = [&](float n0, float n1) {
+    float m = fmaxf(n0, n1);
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) n2 = fmaxf(n2, __shfl_xor(n2, o, kWave));
-    if (lane == 0) sm.kmax2[buf][wid] = n2 * 1.0001f;
+    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
+    return sqrtf(m);
   };
 
   // first (sequence, block) of the tile
@@ -193,13 +264,19 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
     const int s0 = find_seq(cu, nseq, t_first);
     cur = BlockCursor{s0, 0, last_block_of(cu, s0, r0, nr, G, B)};
   }
-  fetch(cur);
+  float cn0, cn1;
+  norm_loads(cur, cn0, cn1);
+  fetch(cur, 0);
   commit(0);
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's direct-to-LDS loads have landed
   __syncthreads();
+  float kmax = block_kmax(cn0, cn1);
   int buf = 0;
   while (cur.s < nseq) {
     const BlockCursor nxt = next_block(cu, nseq, cur, r0, nr, G, B);
-    fetch(nxt);  // in flight while this block is evaluated
+    float nn0, nn1;
+    norm_loads(nxt, nn0, nn1);
+    fetch(nxt, buf ^ 1);  // in flight while this block is evaluated (that buffer's readers passed the last barrier)
 
     const int64_t start = cu[cur.s], end = cu[cur.s + 1];
     const int64_t kb = start + static_cast<int64_t>(cur.b) * B;
@@ -214,18 +291,17 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
     }
     const bool wave_on = __ballot(lim[0] > 0 || lim[1] > 0) != 0;  // wave-uniform
     const uint16_t* kt_base = sm.k[buf];
-    // approximate logits, 16 keys at a time, folded into a per-row running top 2:
-    // m1 the maximum, o1 the lane-local offset (16 kt + i) of its first key, m2 the
-    // largest other value (med3(m1, v, m2) is the new second largest)
-    float m1[2] = {-__builtin_inff(), -__builtin_inff()}, m2[2] = {-__builtin_inff(), -__builtin_inff()};
-    int o1[2] = {0, 0};
-    if (wave_on) {
-      const bool full = __ballot(lim[0] < 128 || lim[1] < 128) == 0;  // no key masked in the wave
+    // approximate logits, 16 keys at a time, key position packed into their low bits,
+    // folded into a per-row running top 2: m1 the maximum, m2 the largest other value
+    // (med3(m1, v, m2) is the new second largest)
+    float m1[2] = {kMaskedLogit, kMaskedLogit}, m2[2] = {kMaskedLogit, kMaskedLogit};
+    // (med3 with +inf is the maximum; unlike fmaxf it needs no canonicalised inputs)
+    auto scan = [&](auto masked) {
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
         bf16x8 kf[NK];
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) kf[kk] = load_frag(kt_base + (16 * kt + c) * RS + 32 * kk + 8 * q4);
+        for (int kk = 0; kk < NK; ++kk) kf[kk] = load_frag(kt_base + key_off<NK, FULLD>(16 * kt + c, 32 * kk + 8 * q4));
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
           f32x4 a = {0.f, 0.f, 0.f, 0.f};
@@ -234,36 +310,41 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             float v = a[i];
-            if (!full) v = 16 * kt + 4 * q4 + i < lim[rt] ? v : -__builtin_inff();
-            o1[rt] = v > m1[rt] ? 16 * kt + i : o1[rt];
+            if constexpr (decltype(masked)::value) v = 16 * kt + 4 * q4 + i < lim[rt] ? v : kMaskedLogit;
+            v = pack_key(v, 16 * kt + i);
             m2[rt] = __builtin_amdgcn_fmed3f(m1[rt], v, m2[rt]);
-            m1[rt] = fmaxf(m1[rt], v);
+            m1[rt] = __builtin_amdgcn_fmed3f(m1[rt], v, __builtin_inff());
           }
         }
       }
+    };
+    if (wave_on) {
+      if (__ballot(lim[0] < 128 || lim[1] < 128) == 0)  // no key masked in the wave
+        scan(std::false_type{});
+      else
+        scan(std::true_type{});
     }
     if (wave_on) {
-      const float kmax = sqrtf(fmaxf(fmaxf(sm.kmax2[buf][0], sm.kmax2[buf][1]),
-                                     fmaxf(sm.kmax2[buf][2], sm.kmax2[buf][3])));
       // merge the four key quarters of each row; the winner is certified unique iff no
-      // other key comes within 2E of the maximum
+      // other key comes within the bound of the maximum
       int widx[2], wcnt[2];
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         float a1 = m1[rt], a2 = m2[rt];
-        int ai = o1[rt] + 4 * q4;
 #pragma unroll
         for (int o = 16; o <= 32; o <<= 1) {
           const float b1 = __shfl_xor(a1, o, kWave);
           const float b2 = __shfl_xor(a2, o, kWave);
-          const int bi = __shfl_xor(ai, o, kWave);
           a2 = fmaxf(fmaxf(a2, b2), fminf(a1, b1));
-          if (b1 > a1 || (b1 == a1 && bi < ai)) ai = bi;
           a1 = fmaxf(a1, b1);
         }
-        const float thr = a1 - 2.f * cerr * mnorm[rt] * kmax;
-        widx[rt] = ai;
-        wcnt[rt] = a2 >= thr ? 2 : 1;  // 2: at least two candidates
+        // the quarter holding the maximum (unique whenever the row is certified)
+        int wq = m1[rt] == a1 ? q4 : 4;
+        wq = min(wq, __shfl_xor(wq, 16, kWave));
+        wq = min(wq, __shfl_xor(wq, 32, kWave));
+        widx[rt] = static_cast<int>(__float_as_uint(a1) & 0x7fu) + 4 * wq;
+        const float bound = 2.f * cerr * mnorm[rt] * kmax + 0x1p-15f * fmaxf(fabsf(a1), fabsf(a2)) + 0x1p-126f;
+        wcnt[rt] = a2 >= a1 - bound ? 2 : 1;  // 2: at least two candidates
       }
       // lane pair (pr, hf): row wr0 + pr = 16 rt + c with rt = pr >> 4 -- this lane's c matches
       const int prt = pr >> 4;
@@ -271,34 +352,31 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
       const int mycnt = prt ? wcnt[1] : wcnt[0];
       const int mylim = prt ? lim[1] : lim[0];
       const bool row_ok = pin && mylim > 0;
-      // unique winner: its exact dot, half per lane, in exact_dot's order
+      // unique winner: its exact dot, half per lane, in exact_dot's order (products of bf16
+      // values converted to FP64, FP64 fused multiply-adds)
       double half = 0.0;
       if (row_ok && mycnt == 1) {
-        const uint16_t* krow = kt_base + myidx * RS + hf * h;
-        if constexpr (FULLD) {
 #pragma unroll
-          for (int j8 = 0; j8 < HW / 4; ++j8) {  // 8 dims per 16-byte read
+        for (int j8 = 0; j8 < HF / 8; ++j8) {  // 8 dims per 16-byte read
+          if (FULLD || 8 * j8 < h) {
             // opaque to the optimiser: keeps the FP64 widening of the query inside the
-            // block loop instead of 2 x 64 hoisted registers
+            // block loop instead of 2 x HF hoisted registers
             asm volatile("" : "+v"(qh[4 * j8]), "+v"(qh[4 * j8 + 1]), "+v"(qh[4 * j8 + 2]), "+v"(qh[4 * j8 + 3]));
-            const uint4 kw = *reinterpret_cast<const uint4*>(krow + 8 * j8);
-            const uint32_t kx[4] = {kw.x, kw.y, kw.z, kw.w};
+            const uint16_t* kp = kt_base + key_off<NK, FULLD>(myidx, hf * h + 8 * j8);
+            uint32_t kx[4];
+            if (FULLD || 8 * j8 + 8 <= h) {
+              const uint4 kw = *reinterpret_cast<const uint4*>(kp);
+              kx[0] = kw.x, kx[1] = kw.y, kx[2] = kw.z, kx[3] = kw.w;
+            } else {  // h % 8 == 4: the last four dims of the half
+              const uint2 kw = *reinterpret_cast<const uint2*>(kp);
+              kx[0] = kw.x, kx[1] = kw.y, kx[2] = kx[3] = 0u;
+            }
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-              half = fma(static_cast<double>(bf16_lo(qh[4 * j8 + u])), static_cast<double>(bf16_lo(kx[u])), half);
-              half = fma(static_cast<double>(bf16_hi(qh[4 * j8 + u])), static_cast<double>(bf16_hi(kx[u])), half);
-            }
-          }
-        } else {
-#pragma unroll
-          for (int w4 = 0; w4 < HW / 2; ++w4) {
-            if (4 * w4 < h) {
-              asm volatile("" : "+v"(qh[2 * w4]), "+v"(qh[2 * w4 + 1]));
-              const uint2 kw = *reinterpret_cast<const uint2*>(krow + 4 * w4);
-              half = fma(static_cast<double>(bf16_lo(qh[2 * w4])), static_cast<double>(bf16_lo(kw.x)), half);
-              half = fma(static_cast<double>(bf16_hi(qh[2 * w4])), static_cast<double>(bf16_hi(kw.x)), half);
-              half = fma(static_cast<double>(bf16_lo(qh[2 * w4 + 1])), static_cast<double>(bf16_lo(kw.y)), half);
-              half = fma(static_cast<double>(bf16_hi(qh[2 * w4 + 1])), static_cast<double>(bf16_hi(kw.y)), half);
+              if (FULLD || 8 * j8 + 2 * u < h) {
+                half = fma(static_cast<double>(bf16_lo(qh[4 * j8 + u])), static_cast<double>(bf16_lo(kx[u])), half);
+                half = fma(static_cast<double>(bf16_hi(qh[4 * j8 + u])), static_cast<double>(bf16_hi(kx[u])), half);
+              }
             }
           }
         }
@@ -318,7 +396,7 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
         slow &= slow - 1;
         if (pr == j) {
 #pragma unroll
-          for (int w = 0; w < HW; ++w)
+          for (int w = 0; w < HF / 2; ++w)
             if (2 * w < h) sm.qrow[wid][hf * (h / 2) + w] = qh[w];
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -334,15 +412,15 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
         for (int kh = 0; kh < 2; ++kh) {
           const int kl = lane + 64 * kh;
           if (kl < vis) {
-            const uint16_t* krow = kt_base + kl * RS;
             double a0 = 0.0, a1 = 0.0;
 #pragma unroll
-            for (int w4 = 0; w4 < HW / 2; ++w4) {
+            for (int w4 = 0; w4 < HF / 4; ++w4) {
               if (4 * w4 < h) {
                 const uint2 q0 = *reinterpret_cast<const uint2*>(qw + 2 * w4);
                 const uint2 q1 = *reinterpret_cast<const uint2*>(qw + h / 2 + 2 * w4);
-                const uint2 k0 = *reinterpret_cast<const uint2*>(krow + 4 * w4);
-                const uint2 k1 = *reinterpret_cast<const uint2*>(krow + h + 4 * w4);
+                const int d0 = 4 * w4, d1 = h + 4 * w4;
+                const uint2 k0 = *reinterpret_cast<const uint2*>(kt_base + key_off<NK, FULLD>(kl, d0 & ~7) + (d0 & 4));
+                const uint2 k1 = *reinterpret_cast<const uint2*>(kt_base + key_off<NK, FULLD>(kl, d1 & ~7) + (d1 & 4));
                 a0 = fma(static_cast<double>(bf16_lo(q0.x)), static_cast<double>(bf16_lo(k0.x)), a0);
                 a1 = fma(static_cast<double>(bf16_lo(q1.x)), static_cast<double>(bf16_lo(k1.x)), a1);
                 a0 = fma(static_cast<double>(bf16_hi(q0.x)), static_cast<double>(bf16_hi(k0.x)), a0);
@@ -376,7 +454,9 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
       }
     }
     if (nxt.s < nseq) commit(buf ^ 1);  // that buffer's readers finished before the last barrier
+    __builtin_amdgcn_s_waitcnt(0);       // the next block's direct-to-LDS loads have landed
     __syncthreads();  // this block's readers are done; the next block is visible
+    kmax = block_kmax(nn0, nn1);
     buf ^= 1;
     cur = nxt;
   }
@@ -399,12 +479,18 @@ bool score_mfma_supported(int Di, int B, double scale) {
   return scale != 0.0 && Di >= 8 && Di <= 128 && Di % 8 == 0 && B >= 1 && B <= 128;
 }
 
+int64_t score_fwd_mfma_workspace_bytes(int64_t total_tokens) { return (total_tokens > 0 ? total_tokens : 1) * 4; }
+
 int score_fwd_mfma_launch(const void* iq, const void* ik, const int32_t* cu, int nseq, int64_t rows, int G, int Di,
-                          int NB, int B, double scale, float* scores, int32_t* tie, hipStream_t st) {
+                          int NB, int B, double scale, float* scores, int32_t* tie, void* ws, hipStream_t st) {
+  if (!ws) return kErrInvalidArgument;
   const dim3 grid(grid_1d(rows, kTileRows)), block(kThreads);
   const auto* q = static_cast<const uint16_t*>(iq);
   const auto* k = static_cast<const uint16_t*>(ik);
-#define MSA_SCORE_MFMA(NKV, FD) hipLaunchKernelGGL((score_fwd_mfma_kernel<NKV, FD>), grid, block, 0, st, q, k, cu, nseq, rows, G, Di, NB, B, scale, scores, tie)
+  float* knorm2 = static_cast<float*>(ws);
+  const int64_t T = rows / G;
+  hipLaunchKernelGGL(score_key_norms, dim3(grid_1d(T, 256)), dim3(256), 0, st, k, T, Di, knorm2);
+#define MSA_SCORE_MFMA(NKV, FD) hipLaunchKernelGGL((score_fwd_mfma_kernel<NKV, FD>), grid, block, 0, st, q, k, cu, nseq, rows, G, Di, NB, B, scale, knorm2, scores, tie)
   const int nk = Di <= 32 ? 1 : (Di <= 64 ? 2 : 4);
   const bool fd = Di == 32 * nk;
   if (nk == 1) { if (fd) MSA_SCORE_MFMA(1, true); else MSA_SCORE_MFMA(1, false); }

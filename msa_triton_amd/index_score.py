@@ -29,11 +29,13 @@ def _score_forward(q, k, cu, meta, max_seqlen, block_size, scale, save_state):
     scores = torch.empty((total, groups, blocks), dtype=torch.float32, device=q.device)
     tie = torch.empty((total, groups, blocks), dtype=torch.int32, device=q.device) if save_state else None
     if total:
+        lib = _lib.lib()
+        workspace = torch.empty(lib.msa_score_fwd_workspace_bytes(total), dtype=torch.uint8, device=q.device)
         with torch.cuda.device(q.device):
-            status = _lib.lib().msa_score_fwd(
+            status = lib.msa_score_fwd(
                 q.data_ptr(), k.data_ptr(), _lib.DTYPE_CODE[q.dtype], cu.data_ptr(), meta.num_seqs,
                 total, groups, dim, blocks, block_size, scale, scores.data_ptr(),
-                None if tie is None else tie.data_ptr(), _lib.stream_of(q.device),
+                None if tie is None else tie.data_ptr(), workspace.data_ptr(), _lib.stream_of(q.device),
             )
         _lib.check(status, "msa_score_fwd")
     return scores, tie
@@ -167,11 +169,14 @@ class _IndexScoreTopk(torch.autograd.Function):
         tie = torch.empty((total, groups, blocks), dtype=torch.int32, device=q.device) if save_state else None
         indices = torch.empty((total, groups, topk_blocks), dtype=torch.int32, device=q.device)
         if total:
+            lib = _lib.lib()
+            workspace = torch.empty(lib.msa_score_fwd_workspace_bytes(total), dtype=torch.uint8, device=q.device)
             with torch.cuda.device(q.device):
-                status = _lib.lib().msa_index_score_topk(
+                status = lib.msa_index_score_topk(
                     q.data_ptr(), k.data_ptr(), _lib.DTYPE_CODE[q.dtype], cu.data_ptr(), meta.num_seqs,
                     total, groups, dim, blocks, block_size, scale, topk_blocks, local_blocks, scores.data_ptr(),
-                    None if tie is None else tie.data_ptr(), indices.data_ptr(), _lib.stream_of(q.device),
+                    None if tie is None else tie.data_ptr(), indices.data_ptr(), workspace.data_ptr(),
+                    _lib.stream_of(q.device),
                 )
             _lib.check(status, "msa_index_score_topk")
         if save_state:
