@@ -65,8 +65,10 @@ int msa_k2q_build_noalloc(const int32_t* indices, const int32_t* cu_seqlens, con
                           int64_t counter_elems, int32_t* row_ptr, int32_t* query_indices,
                           int32_t* slot_indices, void* stream);
 
-/* Stage 1 forward workspace in bytes (the squared norm of every index key, fp32 [T]). */
-int64_t msa_score_fwd_workspace_bytes(int64_t total_tokens);
+/* Stage 1 forward workspace in bytes: the squared norm of every index key (fp32 [T])
+ * and one bit per (token, group, block) marking the pairs whose winner the bf16 MFMA
+ * pass could not certify. 0 for invalid sizes. */
+int64_t msa_score_fwd_workspace_bytes(int64_t total_tokens, int64_t groups, int64_t num_blocks);
 
 /* Stage 1 forward: per-group causal block maxima of scale * (index_q . index_k).
  * Replaces triton/index_score.py:93-136 (_index_score_forward) and the launch at
@@ -74,7 +76,8 @@ int64_t msa_score_fwd_workspace_bytes(int64_t total_tokens);
  * causal key. tie_info (nullable, int32 [T,G,NB]): winner offset + 1 for a
  * unique exact maximum, -count for exact ties, 0 for invalid blocks
  * (same encoding as index_score.py:128-136). workspace: at least
- * msa_score_fwd_workspace_bytes(total_tokens) bytes, 4-byte aligned. */
+ * msa_score_fwd_workspace_bytes(total_tokens, groups, num_blocks) bytes, 4-byte
+ * aligned. */
 int msa_score_fwd(const void* index_q, const void* index_k, int32_t dtype,
                   const int32_t* cu_seqlens, int64_t num_seqs, int64_t total_tokens,
                   int64_t groups, int64_t index_dim, int64_t num_blocks, int64_t block_size,

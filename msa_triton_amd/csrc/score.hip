@@ -685,8 +685,9 @@ int score_bwd_launch(const void* iq, const void* ik, const int32_t* cu, const in
 
 using namespace msa;
 
-extern "C" int64_t msa_score_fwd_workspace_bytes(int64_t total_tokens) {
-  return score_fwd_mfma_workspace_bytes(total_tokens);
+extern "C" int64_t msa_score_fwd_workspace_bytes(int64_t total_tokens, int64_t groups, int64_t num_blocks) {
+  if (total_tokens < 0 || groups <= 0 || num_blocks <= 0) return 0;
+  return score_fwd_mfma_workspace_bytes(total_tokens, total_tokens * groups, num_blocks);
 }
 
 extern "C" int msa_score_fwd(const void* index_q, const void* index_k, int32_t dtype,

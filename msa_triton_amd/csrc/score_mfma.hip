@@ -26,10 +26,20 @@
 // 2^-15 max(|max|, |runner-up|) plus the smallest normal float. If exactly one key
 // survives, it is the unique exact winner and only its dot is evaluated in FP64: a lane
 // pair owns the row, each lane runs one half of exact_dot's fixed order (two
-// sequential FMA chains over the halves of the index dim) from the query half
-// it keeps in registers and the key row in LDS, and the halves are added in
-// that order. Otherwise the whole wave re-evaluates every visible key of the
-// block in FP64 (same order) and takes max / tie count / first winner exactly.
+// sequential chains over the halves of the index dim) from the query half it keeps in
+// registers and the key row in LDS, and the halves are added in that order. Each
+// bf16 x bf16 product comes from v_dot2_f32_bf16 against a key word with the other
+// half masked to zero: exact in fp32 when every nonzero element of the query row and
+// the key block lies in [2^-60, 2^55) ("safe": products then are normal fp32 numbers,
+// and no MFMA sum can overflow), and adding that exact product in FP64 gives the bits
+// of exact_dot's fused multiply-add. Pairs of an unsafe row or block go to the resolve
+// kernel below.
+// Otherwise the (row, block) pair is marked in a bitmap that a second
+// kernel (score_fwd_resolve) settles after the main pass: one wave re-evaluates
+// every visible key of the block in FP64 (same order) and takes max / tie count /
+// first winner exactly. Deferring keeps the rare ambiguous rows (a few per
+// thousand on random data) from holding the other waves of a workgroup at the
+// next block barrier.
 // A negative scale flips the query signs once (exact), so every comparison is
 // on the directed dot.
 #include <type_traits>
@@ -41,15 +51,25 @@ namespace msa {
 
 namespace {
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
 constexpr int kTileRows = 128;  // 4 waves x 32 rows
 constexpr int kThreads = 256;
+
+// Workspace: squared key norms (fp32 per key), then the ambiguous-pair bitmap,
+// block-major: bit block * rows_pad + row of 32-bit words, rows_pad = rows rounded up
+// to a whole number of resolve chunks.
+constexpr int kResolveRows = 8192;  // rows per resolve workgroup
+int64_t align256(int64_t x) { return (x + 255) & ~int64_t{255}; }
+int64_t ws_bitmap_offset(int64_t T) { return align256(4 * (T > 0 ? T : 1)); }
+int64_t rows_padded(int64_t rows) { return (rows + kResolveRows - 1) / kResolveRows * kResolveRows; }
+int64_t bitmap_words(int64_t rows, int64_t NB) { return rows_padded(rows) / 32 * NB; }
 
 template <int NK>
 struct ScoreSmem {
   static constexpr int DP = 32 * NK;
   static constexpr int RS = DP + 8;  // row stride (bf16) of a padded key block (index dim below DP)
   alignas(16) uint16_t k[2][128 * RS];  // full-width blocks use the first 128 * DP entries (swizzled rows)
-  uint32_t qrow[4][DP / 2];  // per-wave query row of an ambiguous row (packed bf16)
 };
 
 // Offset (bf16 elements) of dims [d, d + 8) of key `row` in a buffered block (d a
@@ -73,8 +93,35 @@ __device__ __forceinline__ float pack_key(float v, uint32_t pos) {
 }
 constexpr float kMaskedLogit = -3.0e38f;  // a finite stand-in for masked keys (packing keeps it finite)
 
+// v_max3_f32 on finite values. Written out because the optimiser, given fmaxf, adds a
+// canonicalisation of every operand whose bits it cannot trace to an FP operation.
+__device__ __forceinline__ float max3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Both bf16 of a word zero or of magnitude in [2^-60, 2^55) (biased exponent 67 .. 181):
+// the product of two such values is zero or a normal fp32 number below 2^110, and a
+// sum of up to 128 of them stays below 2^117.
+__device__ __forceinline__ bool bf16_safe(uint32_t x16) {
+  const uint32_t e = (x16 >> 7) & 0xffu;
+  return (x16 & 0x7fffu) == 0u || (e >= 67u && e <= 181u);
+}
+__device__ __forceinline__ bool word_safe(uint32_t w) { return bf16_safe(w & 0xffffu) && bf16_safe(w >> 16); }
+
+// fp32 product of the low (lo) or high bf16 of a and of b, exact when both are safe.
+__device__ __forceinline__ float prod_lo(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b & 0xffffu),
+                                         0.0f, false);
+}
+__device__ __forceinline__ float prod_hi(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
+                                         __builtin_bit_cast(bf16x2_t, b & 0xffff0000u), 0.0f, false);
+}
 
 // Iteration space of a tile: (sequence, block) pairs for every sequence overlapping
 // the tile rows [r0, r0 + nr), blocks 0 .. the last row's query block.
@@ -109,12 +156,17 @@ __device__ __forceinline__ BlockCursor next_block(const int32_t* __restrict__ cu
 }  // namespace
 
 // Squared norm of every index key, rounded up by 1.0001 (bounds the fp32 rounding of
-// the sum): the max over a key block enters the MFMA logits' error bound.
+// the sum): the max over a key block enters the MFMA logits' error bound. The sign bit
+// is set for a key that is not safe (a nonzero element outside [2^-60, 2^55)).
+// Also clears the ambiguous-pair bitmap the main pass marks.
 __global__ __launch_bounds__(256) void score_key_norms(const uint16_t* __restrict__ ik, int64_t T, int Di,
-                                                       float* __restrict__ knorm2) {
+                                                       float* __restrict__ knorm2, uint32_t* __restrict__ amb,
+                                                       int64_t amb_words) {
   const int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (j < amb_words) amb[j] = 0u;
   if (j >= T) return;
   float n2 = 0.f;
+  bool safe = true;
   for (int d = 0; d < Di; d += 8) {
     const uint4 w = *reinterpret_cast<const uint4*>(ik + j * Di + d);
     const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
@@ -122,17 +174,21 @@ __global__ __launch_bounds__(256) void score_key_norms(const uint16_t* __restric
     for (int u = 0; u < 4; ++u) {
       n2 = fmaf(bf16_lo(ws[u]), bf16_lo(ws[u]), n2);
       n2 = fmaf(bf16_hi(ws[u]), bf16_hi(ws[u]), n2);
+      safe = safe && word_safe(ws[u]);
     }
   }
-  knorm2[j] = n2 * 1.0001f;
+  knorm2[j] = safe ? n2 * 1.0001f : -(n2 * 1.0001f) - 1.0f;  // unsafe: negative
 }
 
+// Two workgroups per CU; one for the widest partial-width variant (index dim 72..120),
+// whose register staging of the next block does not fit beside two.
 template <int NK, bool FULLD>
-__global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint16_t* __restrict__ iq,
+__global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd_mfma_kernel(const uint16_t* __restrict__ iq,
                                                                      const uint16_t* __restrict__ ik,
                                                                      const int32_t* __restrict__ cu, int nseq,
                                                                      int64_t rows, int G, int Di, int NB, int B,
                                                                      double scale, const float* __restrict__ knorm2,
+                                                                     uint32_t* __restrict__ amb, int64_t rows_pad,
                                                                      float* __restrict__ scores,
                                                                      int32_t* __restrict__ tie) {
   constexpr int DP = 32 * NK;
@@ -140,7 +196,8 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
   constexpr int KCH = 128 * CPK / kThreads;   // chunks per thread per key block
   constexpr int HF = DP / 2;                  // max dims of a query half (Di / 2 <= DP / 2)
   __shared__ ScoreSmem<NK> sm;
-  const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar) index
   const int64_t r0 = static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * kTileRows;  // heaviest tiles first
   const int nr = static_cast<int>(rows - r0 < kTileRows ? rows - r0 : kTileRows);
   const bool neg = scale < 0.0;
@@ -179,6 +236,7 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
   const bool pin = prow < nr;
   uint32_t qh[HF / 2];
   float pn2 = 0.f;
+  bool psafe = true;
 #pragma unroll
   for (int w4 = 0; w4 < HF / 4; ++w4) {  // 8-byte loads: 4 dims each
     uint2 x = make_uint2(0u, 0u);
@@ -191,34 +249,56 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
     pn2 = fmaf(bf16_hi(x.x), bf16_hi(x.x), pn2);
     pn2 = fmaf(bf16_lo(x.y), bf16_lo(x.y), pn2);
     pn2 = fmaf(bf16_hi(x.y), bf16_hi(x.y), pn2);
+    psafe = psafe && word_safe(x.x) && word_safe(x.y);
   }
   pn2 += __shfl_xor(pn2, 32, kWave);
+  psafe = psafe && __shfl_xor(static_cast<int>(psafe), 32, kWave) != 0;  // both halves of the row
   const float pnorm = sqrtf(pn2) * 1.0001f;  // ||q|| of row prow, rounded up
   float mnorm[2];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) mnorm[rt] = __shfl(pnorm, 16 * rt + c, kWave);
+  bool msafe[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) msafe[rt] = __shfl(static_cast<int>(psafe), 16 * rt + c, kWave) != 0;
   const int64_t ptok = pin ? (r0 + prow) / G : -1;
 
   // ---- key block staging
   uint4 kreg[FULLD ? 1 : KCH];  // register staging of partial-width blocks
+  // Full width: wave wid's instruction i fills physical chunks p = (wid KCH + i) 64 + lane
+  // of the buffer (1 KiB per instruction), holding row p / CPK, logical chunk
+  // (p % CPK) ^ swz(row). Rows advance by 16 every KCH / 2 instructions and the swizzle
+  // repeats every 16 rows, so the offsets of the first half serve the second.
+  constexpr int SH = NK == 4 ? 0 : (NK == 2 ? 1 : 2);
+  constexpr int NP = FULLD ? KCH / 2 : 1;
+  // element offset of instruction i's chunk within a complete block (block-invariant)
+  auto chunk_off = [&](int i) {
+    const int p = (wid * KCH + i % NP) * 64 + lane;
+    const int row = p / CPK, pc = p % CPK;
+    return static_cast<uint32_t>(row * DP + 8 * (pc ^ ((row >> SH) & (CPK - 1))) + (i < NP ? 0 : 16 * DP));
+  };
   auto fetch = [&](const BlockCursor& bc, int into) {
     if (bc.s >= nseq) return;
     const int64_t kb = cu[bc.s] + static_cast<int64_t>(bc.b) * B;
     const int64_t end = cu[bc.s + 1];
     const int nk = static_cast<int>(end - kb < B ? end - kb : B);
     if constexpr (FULLD) {
-      // wave wid's instruction i fills physical chunks p = (wid KCH + i) 64 + lane of the
-      // buffer (1 KiB each); rows past the block's end repeat its last key (masked later)
       char* dst = reinterpret_cast<char*>(sm.k[into]) + wid * KCH * 1024;
+      if (nk == 128) {  // a complete block: scalar base plus the precomputed offsets
+        const uint16_t* src = ik + kb * DP;
 #pragma unroll
-      for (int i = 0; i < KCH; ++i) {
-        const int p = (wid * KCH + i) * 64 + lane;
-        const int row = p / CPK, pc = p % CPK;
-        constexpr int SH = NK == 4 ? 0 : (NK == 2 ? 1 : 2);
-        const int lc = pc ^ ((row >> SH) & (CPK - 1));
-        const int rowc = row < nk ? row : nk - 1;
-        __builtin_amdgcn_global_load_lds(ik + (kb + rowc) * Di + 8 * lc,
-                                         (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, 0, 0);
+        for (int i = 0; i < KCH; ++i)
+          __builtin_amdgcn_global_load_lds(src + static_cast<int>(chunk_off(i)),
+                                           (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, 0, 0);
+      } else {  // rows past the block's end repeat its last key (masked later)
+#pragma unroll
+        for (int i = 0; i < KCH; ++i) {
+          const int p = (wid * KCH + i) * 64 + lane;
+          const int row = p / CPK, pc = p % CPK;
+          const int lc = pc ^ ((row >> SH) & (CPK - 1));
+          const int rowc = row < nk ? row : nk - 1;
+          __builtin_amdgcn_global_load_lds(ik + (kb + rowc) * Di + 8 * lc,
+                                           (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, 0, 0);
+        }
       }
     } else {
 #pragma unroll
@@ -250,12 +330,13 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
     if (lane < nk) n0 = knorm2[kb + lane];
     if (lane + 64 < nk) n1 = knorm2[kb + lane + 64];
   };
-  auto block_kmax = [&](float n0, float n1) {
-    float m = fmaxf(n0, n1);
+  auto block_kmax = [&](float n0, float n1) {  // (an unsafe key's entry is -(n2 + 1))
+    float m = fmaxf(fabsf(n0), fabsf(n1));
 #pragma unroll
     for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
     return sqrtf(m);
   };
+  auto block_safe = [&](float n0, float n1) { return __ballot(n0 < 0.f || n1 < 0.f) == 0; };
 
   // first (sequence, block) of the tile
   BlockCursor cur{nseq, 0, -1};
@@ -271,6 +352,7 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
   __builtin_amdgcn_s_waitcnt(0);  // this thread's direct-to-LDS loads have landed
   __syncthreads();
   float kmax = block_kmax(cn0, cn1);
+  bool bsafe = block_safe(cn0, cn1);
   int buf = 0;
   while (cur.s < nseq) {
     const BlockCursor nxt = next_block(cu, nseq, cur, r0, nr, G, B);
@@ -295,7 +377,11 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
     // folded into a per-row running top 2: m1 the maximum, m2 the largest other value
     // (med3(m1, v, m2) is the new second largest)
     float m1[2] = {kMaskedLogit, kMaskedLogit}, m2[2] = {kMaskedLogit, kMaskedLogit};
-    // (med3 with +inf is the maximum; unlike fmaxf it needs no canonicalised inputs)
+    // med3(m1, v, +inf) is the maximum; unlike fmaxf it needs no canonicalised inputs. The
+    // +inf sits in a register the optimiser cannot see through, or it would turn the med3
+    // back into a maximum with canonicalisations.
+    float pinf = __builtin_inff();
+    asm volatile("" : "+v"(pinf));
     auto scan = [&](auto masked) {
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
@@ -308,12 +394,17 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
 #pragma unroll
           for (int kk = 0; kk < NK; ++kk) a = mfma(kf[kk], qf[rt][kk], a);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float v = a[i];
-            if constexpr (decltype(masked)::value) v = 16 * kt + 4 * q4 + i < lim[rt] ? v : kMaskedLogit;
-            v = pack_key(v, 16 * kt + i);
-            m2[rt] = __builtin_amdgcn_fmed3f(m1[rt], v, m2[rt]);
-            m1[rt] = __builtin_amdgcn_fmed3f(m1[rt], v, __builtin_inff());
+          for (int i = 0; i < 4; i += 2) {  // two logits x, y at a time (m1 >= m2 throughout):
+            float x = a[i], y = a[i + 1];     // second largest of {m1, m2, x, y} = max(m2, med3(m1, x, y))
+            if constexpr (decltype(masked)::value) {
+              x = 16 * kt + 4 * q4 + i < lim[rt] ? x : kMaskedLogit;
+              y = 16 * kt + 4 * q4 + i + 1 < lim[rt] ? y : kMaskedLogit;
+            }
+            x = pack_key(x, 16 * kt + i);
+            y = pack_key(y, 16 * kt + i + 1);
+            const float t = __builtin_amdgcn_fmed3f(m1[rt], x, y);
+            m2[rt] = __builtin_amdgcn_fmed3f(m2[rt], t, pinf);
+            m1[rt] = max3(m1[rt], x, y);
           }
         }
       }
@@ -344,7 +435,8 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
         wq = min(wq, __shfl_xor(wq, 32, kWave));
         widx[rt] = static_cast<int>(__float_as_uint(a1) & 0x7fu) + 4 * wq;
         const float bound = 2.f * cerr * mnorm[rt] * kmax + 0x1p-15f * fmaxf(fabsf(a1), fabsf(a2)) + 0x1p-126f;
-        wcnt[rt] = a2 >= a1 - bound ? 2 : 1;  // 2: at least two candidates
+        // 2: at least two candidates, or products not certainly exact in fp32
+        wcnt[rt] = (a2 >= a1 - bound || !(bsafe && msafe[rt])) ? 2 : 1;
       }
       // lane pair (pr, hf): row wr0 + pr = 16 rt + c with rt = pr >> 4 -- this lane's c matches
       const int prt = pr >> 4;
@@ -352,16 +444,13 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
       const int mycnt = prt ? wcnt[1] : wcnt[0];
       const int mylim = prt ? lim[1] : lim[0];
       const bool row_ok = pin && mylim > 0;
-      // unique winner: its exact dot, half per lane, in exact_dot's order (products of bf16
-      // values converted to FP64, FP64 fused multiply-adds)
+      // unique winner: its exact dot, half per lane, in exact_dot's order (exact fp32
+      // products of safe bf16 values added in FP64)
       double half = 0.0;
       if (row_ok && mycnt == 1) {
 #pragma unroll
         for (int j8 = 0; j8 < HF / 8; ++j8) {  // 8 dims per 16-byte read
           if (FULLD || 8 * j8 < h) {
-            // opaque to the optimiser: keeps the FP64 widening of the query inside the
-            // block loop instead of 2 x HF hoisted registers
-            asm volatile("" : "+v"(qh[4 * j8]), "+v"(qh[4 * j8 + 1]), "+v"(qh[4 * j8 + 2]), "+v"(qh[4 * j8 + 3]));
             const uint16_t* kp = kt_base + key_off<NK, FULLD>(myidx, hf * h + 8 * j8);
             uint32_t kx[4];
             if (FULLD || 8 * j8 + 8 <= h) {
@@ -374,8 +463,8 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
               if (FULLD || 8 * j8 + 2 * u < h) {
-                half = fma(static_cast<double>(bf16_lo(qh[4 * j8 + u])), static_cast<double>(bf16_lo(kx[u])), half);
-                half = fma(static_cast<double>(bf16_hi(qh[4 * j8 + u])), static_cast<double>(bf16_hi(kx[u])), half);
+                half += static_cast<double>(prod_lo(qh[4 * j8 + u], kx[u]));
+                half += static_cast<double>(prod_hi(qh[4 * j8 + u], kx[u]));
               }
             }
           }
@@ -387,76 +476,17 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
         scores[out] = static_cast<float>(ascale * (half + other));
         if (tie) tie[out] = myidx + 1;
       }
-      // ambiguous rows: every visible key of the block in FP64, whole wave (rare). The
-      // row's query (sign-flipped) goes through this wave's LDS slot; lane l takes keys
-      // l and l + 64 and runs exact_dot's two half chains for each.
-      uint64_t slow = __ballot(row_ok && mycnt != 1 && hf == 0);
-      while (slow) {
-        const int j = __builtin_ctzll(slow);
-        slow &= slow - 1;
-        if (pr == j) {
-#pragma unroll
-          for (int w = 0; w < HF / 2; ++w)
-            if (2 * w < h) sm.qrow[wid][hf * (h / 2) + w] = qh[w];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int64_t srow = r0 + wr0 + j;
-        const int64_t st = srow / G;
-        const int vis = static_cast<int>(st - kb + 1 < nk ? st - kb + 1 : nk);
-        const uint32_t* qw = sm.qrow[wid];
-        double best = -__builtin_inf();
-        int count = 0, first = 0x7fffffff;
-#pragma unroll
-        for (int kh = 0; kh < 2; ++kh) {
-          const int kl = lane + 64 * kh;
-          if (kl < vis) {
-            double a0 = 0.0, a1 = 0.0;
-#pragma unroll
-            for (int w4 = 0; w4 < HF / 4; ++w4) {
-              if (4 * w4 < h) {
-                const uint2 q0 = *reinterpret_cast<const uint2*>(qw + 2 * w4);
-                const uint2 q1 = *reinterpret_cast<const uint2*>(qw + h / 2 + 2 * w4);
-                const int d0 = 4 * w4, d1 = h + 4 * w4;
-                const uint2 k0 = *reinterpret_cast<const uint2*>(kt_base + key_off<NK, FULLD>(kl, d0 & ~7) + (d0 & 4));
-                const uint2 k1 = *reinterpret_cast<const uint2*>(kt_base + key_off<NK, FULLD>(kl, d1 & ~7) + (d1 & 4));
-                a0 = fma(static_cast<double>(bf16_lo(q0.x)), static_cast<double>(bf16_lo(k0.x)), a0);
-                a1 = fma(static_cast<double>(bf16_lo(q1.x)), static_cast<double>(bf16_lo(k1.x)), a1);
-                a0 = fma(static_cast<double>(bf16_hi(q0.x)), static_cast<double>(bf16_hi(k0.x)), a0);
-                a1 = fma(static_cast<double>(bf16_hi(q1.x)), static_cast<double>(bf16_hi(k1.x)), a1);
-                a0 = fma(static_cast<double>(bf16_lo(q0.y)), static_cast<double>(bf16_lo(k0.y)), a0);
-                a1 = fma(static_cast<double>(bf16_lo(q1.y)), static_cast<double>(bf16_lo(k1.y)), a1);
-                a0 = fma(static_cast<double>(bf16_hi(q0.y)), static_cast<double>(bf16_hi(k0.y)), a0);
-                a1 = fma(static_cast<double>(bf16_hi(q1.y)), static_cast<double>(bf16_hi(k1.y)), a1);
-              }
-            }
-            const double v = a0 + a1;
-            if (v > best) {
-              best = v;
-              count = 1;
-              first = kl;
-            } else if (v == best) {
-              ++count;
-            }
-          }
-        }
-        const double wbest = wave_max_f64(best);
-        const int wc = wave_sum_i32((best == wbest && count > 0) ? count : 0);
-        int wf = (best == wbest && count > 0) ? first : 0x7fffffff;
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) wf = min(wf, __shfl_xor(wf, o, kWave));
-        if (lane == 0) {
-          const int64_t out = srow * NB + cur.b;
-          scores[out] = static_cast<float>(ascale * wbest);
-          if (tie) tie[out] = wc == 1 ? wf + 1 : -wc;
-        }
+      // ambiguous rows: marked for score_fwd_resolve
+      if (row_ok && mycnt != 1 && hf == 0) {
+        const int64_t bit = static_cast<int64_t>(cur.b) * rows_pad + r0 + prow;
+        atomicOr(amb + (bit >> 5), 1u << (bit & 31));
       }
     }
     if (nxt.s < nseq) commit(buf ^ 1);  // that buffer's readers finished before the last barrier
     __builtin_amdgcn_s_waitcnt(0);       // the next block's direct-to-LDS loads have landed
     __syncthreads();  // this block's readers are done; the next block is visible
     kmax = block_kmax(nn0, nn1);
+    bsafe = block_safe(nn0, nn1);
     buf ^= 1;
     cur = nxt;
   }
@@ -475,11 +505,142 @@ __global__ __launch_bounds__(kThreads, 2) void score_fwd_mfma_kernel(const uint1
   }
 }
 
+// The ambiguous (row, block) pairs the main pass marked, settled exactly. Workgroup
+// (b, c) takes block b for rows [c, c + kResolveRows): it lists the marked rows in
+// order, and for each run of listed rows of one sequence stages that sequence's block
+// b in LDS; the four waves then take windows of up to kResolvePairs rows of the run
+// independently. In a window, lane l runs exact_dot's two FMA chains (over the halves
+// of the index dim) for keys l and l + 64 and every row of the window at once (each
+// key element and each query element converted to FP64 once per window), from the
+// window's query rows staged in the wave's LDS slot (sign-directed bf16), and adds
+// the halves half 0 first; the maximum is reduced over the wave, tie count and first
+// winner come from ballots. The score and tie code are written as the exact kernel
+// writes them.
+constexpr int kResolvePairs = 4;
+__global__ __launch_bounds__(256) void score_fwd_resolve(const uint16_t* __restrict__ iq,
+                                                         const uint16_t* __restrict__ ik,
+                                                         const int32_t* __restrict__ cu, int nseq, int64_t rows,
+                                                         int64_t rows_pad, int G, int Di, int NB, int B,
+                                                         double scale, const uint32_t* __restrict__ amb,
+                                                         float* __restrict__ scores, int32_t* __restrict__ tie) {
+  constexpr int KS = 136;  // key row stride in LDS (bf16): consecutive rows hit distinct 16-byte bank groups
+  constexpr int P = kResolvePairs;
+  __shared__ alignas(16) uint16_t keys[128 * KS];
+  __shared__ alignas(16) uint16_t qs[4][P][128];
+  __shared__ uint16_t list[kResolveRows];
+  __shared__ int wsum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int b = blockIdx.x;
+  const int64_t c0 = static_cast<int64_t>(blockIdx.y) * kResolveRows;
+  // ---- the marked rows of this chunk, ascending (one bitmap word per thread)
+  constexpr int NW = kResolveRows / 32;  // bitmap words of the chunk (<= threads)
+  static_assert(NW <= 256, "one bitmap word per thread");
+  uint32_t mine = tid < NW ? amb[(static_cast<int64_t>(b) * rows_pad + c0) / 32 + tid] : 0u;
+  const int cnt = __popc(mine);
+  int incl = cnt;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, kWave);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) wsum[wv] = incl;
+  if (__syncthreads_or(mine != 0u) == 0) return;  // nothing marked (uniform)
+  int o = incl - cnt;
+  for (int w = 0; w < wv; ++w) o += wsum[w];
+  for (; mine; mine &= mine - 1) list[o++] = static_cast<uint16_t>(32 * tid + __builtin_ctz(mine));
+  const int n = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  const uint16_t flip = scale < 0.0 ? 0x8000u : 0u;
+  const int h = Di / 2;  // a multiple of 4
+  __syncthreads();  // the list is complete
+  for (int i = 0; i < n;) {  // runs of rows of one sequence (uniform)
+    const int s = find_seq(cu, nseq, (c0 + list[i]) / G);
+    const int64_t start = cu[s], end = cu[s + 1];
+    const int64_t end_row = end * G - c0;  // chunk-relative end of the sequence's rows
+    int j = i + 1;
+    while (j < n && list[j] < end_row) ++j;
+    const int64_t k0 = start + static_cast<int64_t>(b) * B;
+    const int nk = static_cast<int>((k0 + B < end ? k0 + B : end) - k0);  // >= 1: a listed row sees block b
+    const int cpr = Di / 8;
+    for (int e = tid; e < nk * cpr; e += 256) {
+      const int r = e / cpr, c = e % cpr;
+      *reinterpret_cast<uint4*>(keys + r * KS + 8 * c) = *reinterpret_cast<const uint4*>(ik + (k0 + r) * Di + 8 * c);
+    }
+    __syncthreads();  // the block is staged
+    for (int w0 = i + P * wv; w0 < j; w0 += 4 * P) {  // this wave's windows
+      const int np = j - w0 < P ? j - w0 : P;
+      for (int e = lane; e < np * Di; e += kWave) {
+        const int p = e / Di, d = e % Di;
+        qs[wv][p][d] = iq[(c0 + list[w0 + p]) * Di + d] ^ flip;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      double acc[2][2][P];  // [key lane / lane + 64][half][row]
+#pragma unroll
+      for (int kh = 0; kh < 2; ++kh)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int p = 0; p < P; ++p) acc[kh][hh][p] = 0.0;
+      for (int d = 0; d < h; d += 4) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          double qv[P][4];
+#pragma unroll
+          for (int p = 0; p < P; ++p) {
+            const uint2 w = *reinterpret_cast<const uint2*>(&qs[wv][p][hh * h + d]);
+            qv[p][0] = static_cast<double>(bf16_lo(w.x));
+            qv[p][1] = static_cast<double>(bf16_hi(w.x));
+            qv[p][2] = static_cast<double>(bf16_lo(w.y));
+            qv[p][3] = static_cast<double>(bf16_hi(w.y));
+          }
+#pragma unroll
+          for (int kh = 0; kh < 2; ++kh) {
+            const uint2 w = *reinterpret_cast<const uint2*>(keys + (lane + 64 * kh) * KS + hh * h + d);
+            const double k4[4] = {static_cast<double>(bf16_lo(w.x)), static_cast<double>(bf16_hi(w.x)),
+                                  static_cast<double>(bf16_lo(w.y)), static_cast<double>(bf16_hi(w.y))};
+#pragma unroll
+            for (int p = 0; p < P; ++p) {
+              double a = acc[kh][hh][p];
+#pragma unroll
+              for (int u = 0; u < 4; ++u) a = fma(qv[p][u], k4[u], a);
+              acc[kh][hh][p] = a;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < P; ++p) {
+        if (p < np) {
+          const int64_t row = c0 + list[w0 + p];
+          const int vis = static_cast<int>((row / G + 1 < k0 + nk ? row / G + 1 : k0 + nk) - k0);
+          const double v0 = lane < vis ? acc[0][0][p] + acc[0][1][p] : -__builtin_inf();
+          const double v1 = lane + 64 < vis ? acc[1][0][p] + acc[1][1][p] : -__builtin_inf();
+          const double wbest = wave_max_f64(fmax(v0, v1));
+          const uint64_t m0 = __ballot(v0 == wbest), m1 = __ballot(v1 == wbest);  // vis >= 1: wbest is finite
+          if (lane == 0) {
+            const int count = __popcll(m0) + __popcll(m1);
+            const int first = m0 ? __builtin_ctzll(m0) : 64 + __builtin_ctzll(m1);
+            const int64_t out = row * NB + b;
+            scores[out] = static_cast<float>(fabs(scale) * wbest);
+            if (tie) tie[out] = count == 1 ? first + 1 : -count;
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();  // qs is rewritten by the next window
+    }
+    __syncthreads();  // the block's readers are done before the next run restages it
+    i = j;
+  }
+}
+
 bool score_mfma_supported(int Di, int B, double scale) {
   return scale != 0.0 && Di >= 8 && Di <= 128 && Di % 8 == 0 && B >= 1 && B <= 128;
 }
 
-int64_t score_fwd_mfma_workspace_bytes(int64_t total_tokens) { return (total_tokens > 0 ? total_tokens : 1) * 4; }
+int64_t score_fwd_mfma_workspace_bytes(int64_t total_tokens, int64_t rows, int64_t NB) {
+  return ws_bitmap_offset(total_tokens) + 4 * bitmap_words(rows, NB);
+}
 
 int score_fwd_mfma_launch(const void* iq, const void* ik, const int32_t* cu, int nseq, int64_t rows, int G, int Di,
                           int NB, int B, double scale, float* scores, int32_t* tie, void* ws, hipStream_t st) {
@@ -487,16 +648,23 @@ int score_fwd_mfma_launch(const void* iq, const void* ik, const int32_t* cu, int
   const dim3 grid(grid_1d(rows, kTileRows)), block(kThreads);
   const auto* q = static_cast<const uint16_t*>(iq);
   const auto* k = static_cast<const uint16_t*>(ik);
-  float* knorm2 = static_cast<float*>(ws);
   const int64_t T = rows / G;
-  hipLaunchKernelGGL(score_key_norms, dim3(grid_1d(T, 256)), dim3(256), 0, st, k, T, Di, knorm2);
-#define MSA_SCORE_MFMA(NKV, FD) hipLaunchKernelGGL((score_fwd_mfma_kernel<NKV, FD>), grid, block, 0, st, q, k, cu, nseq, rows, G, Di, NB, B, scale, knorm2, scores, tie)
+  char* wsb = static_cast<char*>(ws);
+  float* knorm2 = reinterpret_cast<float*>(wsb);
+  auto* amb = reinterpret_cast<uint32_t*>(wsb + ws_bitmap_offset(T));
+  const int64_t words = bitmap_words(rows, NB);
+  const int64_t rows_pad = rows_padded(rows);
+  hipLaunchKernelGGL(score_key_norms, dim3(grid_1d(T > words ? T : words, 256)), dim3(256), 0, st, k, T, Di,
+                     knorm2, amb, words);
+#define MSA_SCORE_MFMA(NKV, FD) hipLaunchKernelGGL((score_fwd_mfma_kernel<NKV, FD>), grid, block, 0, st, q, k, cu, nseq, rows, G, Di, NB, B, scale, knorm2, amb, rows_pad, scores, tie)
   const int nk = Di <= 32 ? 1 : (Di <= 64 ? 2 : 4);
   const bool fd = Di == 32 * nk;
   if (nk == 1) { if (fd) MSA_SCORE_MFMA(1, true); else MSA_SCORE_MFMA(1, false); }
   else if (nk == 2) { if (fd) MSA_SCORE_MFMA(2, true); else MSA_SCORE_MFMA(2, false); }
   else { if (fd) MSA_SCORE_MFMA(4, true); else MSA_SCORE_MFMA(4, false); }
 #undef MSA_SCORE_MFMA
+  hipLaunchKernelGGL(score_fwd_resolve, dim3(NB, static_cast<unsigned>(rows_pad / kResolveRows)), dim3(256), 0, st,
+                     q, k, cu, nseq, rows, rows_pad, G, Di, NB, B, scale, amb, scores, tie);
   return status_from(hipGetLastError());
 }
 

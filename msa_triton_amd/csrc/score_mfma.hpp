@@ -86,7 +86,7 @@ __device__ void for_each_winner(const void* __restrict__ iq, int64_t qoff, const
 
 // MFMA score path (bf16). Declared here, defined in score_mfma.hip.
 bool score_mfma_supported(int Di, int B, double scale);
-int64_t score_fwd_mfma_workspace_bytes(int64_t total_tokens);
+int64_t score_fwd_mfma_workspace_bytes(int64_t total_tokens, int64_t rows, int64_t NB);
 int score_fwd_mfma_launch(const void* iq, const void* ik, const int32_t* cu, int nseq, int64_t rows, int G,
                           int Di, int NB, int B, double scale, float* scores, int32_t* tie, void* ws,
                           hipStream_t st);

@@ -30,7 +30,7 @@ def _score_forward(q, k, cu, meta, max_seqlen, block_size, scale, save_state):
     tie = torch.empty((total, groups, blocks), dtype=torch.int32, device=q.device) if save_state else None
     if total:
         lib = _lib.lib()
-        workspace = torch.empty(lib.msa_score_fwd_workspace_bytes(total), dtype=torch.uint8, device=q.device)
+        workspace = torch.empty(lib.msa_score_fwd_workspace_bytes(total, groups, blocks), dtype=torch.uint8, device=q.device)
         with torch.cuda.device(q.device):
             status = lib.msa_score_fwd(
                 q.data_ptr(), k.data_ptr(), _lib.DTYPE_CODE[q.dtype], cu.data_ptr(), meta.num_seqs,
@@ -170,7 +170,7 @@ class _IndexScoreTopk(torch.autograd.Function):
         indices = torch.empty((total, groups, topk_blocks), dtype=torch.int32, device=q.device)
         if total:
             lib = _lib.lib()
-            workspace = torch.empty(lib.msa_score_fwd_workspace_bytes(total), dtype=torch.uint8, device=q.device)
+            workspace = torch.empty(lib.msa_score_fwd_workspace_bytes(total, groups, blocks), dtype=torch.uint8, device=q.device)
             with torch.cuda.device(q.device):
                 status = lib.msa_index_score_topk(
                     q.data_ptr(), k.data_ptr(), _lib.DTYPE_CODE[q.dtype], cu.data_ptr(), meta.num_seqs,

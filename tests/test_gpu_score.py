@@ -168,3 +168,29 @@ def test_score_medium_sizes_bit_exact(lengths, groups, dim, block, seed, device)
     got = msa.m3_index_score(q.to(device), k.to(device), cu_tensor(lengths, device), max(lengths), block_size=block)
     _, exp32, _ = O.index_score(q.double().numpy(), k.double().numpy(), cu_list(lengths), max(lengths), block_size=block)
     np.testing.assert_array_equal(got.cpu().numpy(), exp32)
+
+
+@pytest.mark.parametrize("scale", [1.0, -0.75])
+def test_score_extreme_magnitudes_bit_exact(scale, device):
+    """Query rows and keys with elements outside [2^-60, 2^55) (tiny rows, huge keys,
+    bf16 subnormals mixed into normal rows): the MFMA pass cannot take their fp32
+    products as exact, so these pairs are settled by the FP64 resolve pass; the FP64
+    sums of the subnormal rows round, so the fixed summation order is what is checked."""
+    gen = torch.Generator().manual_seed(61 + int(4 * scale))
+    lengths, groups, dim, block = [700, 333], 2, 128, 128
+    total = sum(lengths)
+    q = torch.randn(total, groups, dim, generator=gen)
+    k = torch.randn(total, 1, dim, generator=gen)
+    q[0:40] *= 2.0 ** -70                      # tiny rows
+    q[100:140, :, ::3] = 2.0 ** -130           # bf16 subnormals among normal elements
+    q[150:160] *= 2.0 ** 62                    # huge rows
+    k[5:9] *= 2.0 ** 64                        # huge keys in block 0 of sequence 0
+    k[300:310, :, ::5] = 2.0 ** -128           # subnormal elements in block 2
+    k[760:765] *= 2.0 ** -66                   # tiny keys in sequence 1
+    q, k = q.bfloat16(), k.bfloat16()
+    got = msa.m3_index_score(q.to(device), k.to(device), cu_tensor(lengths, device), max(lengths), block_size=block,
+                             scale=scale)
+    with np.errstate(over="ignore"):  # huge rows x huge keys overflow fp32 (inf), as on the GPU
+        _, exp32, _ = O.index_score(q.double().numpy(), k.double().numpy(), cu_list(lengths), max(lengths),
+                                    block_size=block, scale=scale)
+    np.testing.assert_array_equal(got.cpu().numpy(), exp32)
