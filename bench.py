@@ -269,6 +269,23 @@ def summarize_sq(config, directory, stats_csv=None):
               f"{(conf / lds if lds else 0):.2f} | {ldsb} | {scr} |")
 
 
+def summarize_trace(stats_csv):
+    """Per-kernel rows of a rocprofv3 --kernel-trace --stats run (its kernel_stats.csv) as a
+    markdown table, heaviest total first: calls, average / min / max duration and total."""
+    import csv
+
+    with open(stats_csv) as f:
+        rows = list(csv.DictReader(f))
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    print("| kernel | calls | avg ms | min ms | max ms | total ms | share |")
+    print("|---|---:|---:|---:|---:|---:|---:|")
+    for r in rows:
+        short = r["Name"].split("(")[0].replace("void ", "").replace("msa::", "")
+        print(f"| `{short}` | {r['Calls']} | {float(r['AverageNs']) * 1e-6:.4f} | {float(r['MinNs']) * 1e-6:.4f} | "
+              f"{float(r['MaxNs']) * 1e-6:.4f} | {float(r['TotalDurationNs']) * 1e-6:.3f} | "
+              f"{float(r['Percentage']):.2f} % |")
+
+
 class Harness:
     """Direct C-ABI launches on preallocated buffers, for per-kernel timing."""
 
@@ -483,12 +500,18 @@ def main():
     parser.add_argument("--sq-summarize", metavar="SQ_DIR",
                         help="read the counter CSVs of a --pmc-pass run with the SQ_COUNTERS and print a "
                              "per-kernel markdown table; no GPU needed")
+    parser.add_argument("--trace-summarize", metavar="STATS_CSV",
+                        help="print the per-kernel table of a rocprofv3 --kernel-trace --stats run "
+                             "(its kernel_stats.csv); no GPU needed")
     args = parser.parse_args()
     if args.pmc_summarize:
         summarize_pmc(args.config, *args.pmc_summarize)
         return
     if args.sq_summarize:
         summarize_sq(args.config, args.sq_summarize)
+        return
+    if args.trace_summarize:
+        summarize_trace(args.trace_summarize)
         return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (this path does not shard "

@@ -279,12 +279,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
         for (int jj = 0; jj < 4; ++jj) {
           // elements j = 2*jj, 2*jj + 1 -> C tile 2*kc + j/4, entry j%4
           const int j0 = 2 * jj, j1 = 2 * jj + 1;
-          uint32_t h0, m0, l0, h1, m1, l1;
-          split3_bits(s[rt][2 * kc + j0 / 4][j0 % 4], h0, m0, l0);
-          split3_bits(s[rt][2 * kc + j1 / 4][j1 % 4], h1, m1, l1);
-          wh[jj] = pack_hi16(h0, h1);
-          wm[jj] = pack_hi16(m0, m1);
-          wl[jj] = pack_hi16(l0, l1);
+          split3_pk(s[rt][2 * kc + j0 / 4][j0 % 4], s[rt][2 * kc + j1 / 4][j1 % 4], wh[jj], wm[jj], wl[jj]);
         }
         ph[rt] = __builtin_bit_cast(bf16x8, make_uint4(wh[0], wh[1], wh[2], wh[3]));
         pm[rt] = __builtin_bit_cast(bf16x8, make_uint4(wm[0], wm[1], wm[2], wm[3]));

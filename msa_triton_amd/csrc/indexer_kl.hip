@@ -452,17 +452,8 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
     }
     // ---- dz split: words of edges (4 q4, 4 q4 + 1) and (4 q4 + 2, 4 q4 + 3) per term
     uint32_t w[3][2];
-    {
-      uint32_t hh[4], mm[4], ll[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) split3_bits(dz[i], hh[i], mm[i], ll[i]);
-      w[0][0] = pack_hi16(hh[0], hh[1]);
-      w[0][1] = pack_hi16(hh[2], hh[3]);
-      w[1][0] = pack_hi16(mm[0], mm[1]);
-      w[1][1] = pack_hi16(mm[2], mm[3]);
-      w[2][0] = pack_hi16(ll[0], ll[1]);
-      w[2][1] = pack_hi16(ll[2], ll[3]);
-    }
+    split3_pk(dz[0], dz[1], w[0][0], w[1][0], w[2][0]);
+    split3_pk(dz[2], dz[3], w[0][1], w[1][1], w[2][1]);
     if (need_dik) {
       // d_ik[key][dim 16 dt + c'] += dz^T[key][edges] iq[edges][dim]: A = dz (lane c = key,
       // edges 4 q4 + j), B[edges 4 q4 + j][dim 16 dt + c] read transposed from the iq rows

@@ -32,6 +32,39 @@ __device__ __forceinline__ void split3_bits(float x, uint32_t& hi, uint32_t& mid
   lo = __float_as_uint(r1 - __uint_as_float(mid & 0xffff0000u));
 }
 
+typedef __bf16 bf16x2_pk __attribute__((ext_vector_type(2)));
+typedef float f32x2_pk __attribute__((ext_vector_type(2)));
+
+// Two fp32 values rounded to nearest bf16, packed (x0 in the low half): v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float x0, float x1) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_pk){x0, x1}, bf16x2_pk));
+}
+
+// x - (bf16 half of w) as one v_dot2_f32_bf16 against (-1, -0): the products are -h and
+// +-0 (exact) and the difference is representable (below), so the result is exact. The
+// other half is -0, not +0: the word (-1 in the low half, +0 high) would be emitted as the
+// inline constant -1.0, which the hardware reads as the fp32 pattern (-1 in the high half).
+__device__ __forceinline__ float sub_lo_half(uint32_t w, float x) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_pk, w), __builtin_bit_cast(bf16x2_pk, 0x8000bf80u), x,
+                                         false);
+}
+__device__ __forceinline__ float sub_hi_half(uint32_t w, float x) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_pk, w), __builtin_bit_cast(bf16x2_pk, 0xbf808000u), x,
+                                         false);
+}
+
+// Exact split of two fp32 values into three packed bf16 words by round-to-nearest:
+// hi = rn(x), mid = rn(x - hi), lo = rn(x - hi - mid) with x0 in the low halves. For
+// normal x: x - hi is a multiple of ulp(x) below half an ulp of hi (<= 16 significant
+// bits, exact in fp32), x - hi - mid has <= 8 significant bits, so lo is exact and
+// x == hi + mid + lo. Seven VALU operations per pair (packing included).
+__device__ __forceinline__ void split3_pk(float x0, float x1, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+  hi = cvt_pk_bf16(x0, x1);
+  const float r0 = sub_lo_half(hi, x0), r1 = sub_hi_half(hi, x1);
+  mid = cvt_pk_bf16(r0, r1);
+  lo = cvt_pk_bf16(sub_lo_half(mid, r0), sub_hi_half(mid, r1));
+}
+
 // One 32-bit word holding the bf16 truncations (upper halves) of a (low half) and b (high half).
 __device__ __forceinline__ uint32_t pack_hi16(uint32_t a, uint32_t b) {
   return __builtin_amdgcn_perm(b, a, 0x07060302u);
