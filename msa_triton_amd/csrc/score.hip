@@ -220,6 +220,8 @@ __global__ __launch_bounds__(256) void score_bwd_dq(const void* __restrict__ iq,
 // slot + RPI, ... of the list into FP64 sums of its 8 dims, and the RPI slot sums
 // are added in slot order at the end (a fixed order). Exact ties (rare) are added
 // by every slot-0 lane after the chunk's unique winners, in block order.
+constexpr int kDqWideUnroll = 8;  // key-row gather instructions in flight per wave
+
 template <int DT, int LPR>
 __global__ __launch_bounds__(256) void score_bwd_dq_wide(const void* __restrict__ iq,
                                                          const void* __restrict__ ik,
@@ -259,19 +261,30 @@ __global__ __launch_bounds__(256) void score_bwd_dq_wide(const void* __restrict_
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const int n = __popcll(um);
-    for (int e0 = 0; e0 < n; e0 += 4 * RPI) {
-      uint4 kv[4];
-      double wv[4];
+    for (int e0 = 0; e0 < n; e0 += kDqWideUnroll * RPI) {
+      // all list reads, then all key-row loads (clamped entries, in bounds), then the sums
+      uint4 kv[kDqWideUnroll];
+      double wv[kDqWideUnroll];
+      int kk[kDqWideUnroll];
+      float wf[kDqWideUnroll];
+      bool ok[kDqWideUnroll];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kDqWideUnroll; ++u) {
         const int e = e0 + u * RPI + slot;
-        const bool ok = e < n;
-        const int64_t key = start + lkey[wid][ok ? e : 0];
-        kv[u] = ok ? *reinterpret_cast<const uint4*>(kb16 + key * Di + 8 * dch) : make_uint4(0u, 0u, 0u, 0u);
-        wv[u] = ok ? static_cast<double>(lw[wid][e]) * scale : 0.0;
+        ok[u] = e < n;
+        kk[u] = lkey[wid][ok[u] ? e : 0];
+        wf[u] = lw[wid][ok[u] ? e : 0];
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < kDqWideUnroll; ++u)
+        kv[u] = *reinterpret_cast<const uint4*>(kb16 + (start + kk[u]) * Di + 8 * dch);
+#pragma unroll
+      for (int u = 0; u < kDqWideUnroll; ++u) {
+        if (!ok[u]) kv[u] = make_uint4(0u, 0u, 0u, 0u);
+        wv[u] = ok[u] ? static_cast<double>(wf[u]) * scale : 0.0;
+      }
+#pragma unroll
+      for (int u = 0; u < kDqWideUnroll; ++u) {
         const uint32_t x[4] = {kv[u].x, kv[u].y, kv[u].z, kv[u].w};
 #pragma unroll
         for (int q2 = 0; q2 < 4; ++q2) {
@@ -358,13 +371,14 @@ __device__ __forceinline__ void dk_add_row(double (&acc)[8], double wgt, const v
 
 constexpr int kDkSeg = 8192;
 constexpr int kDkBatch = 16;
+constexpr int kDkWideUnroll = 8;  // row-gather instructions in flight per wave (4 rows each)
 constexpr int kDkTieCap = 256;
 
 template <int DT, int DPL>
 __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
     const void* __restrict__ iq, const void* __restrict__ ik, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, int nseq, const int32_t* __restrict__ tie_t,
-    const float* __restrict__ ds_t, int64_t rows, int G, int Di, int B, int nseg, double scale,
+    const float* __restrict__ ds_t, int64_t rows, int G, int Di, int B, int64_t nblk, int nseg, double scale,
     double* __restrict__ part) {
   __shared__ uint16_t lrow[kDkSeg];   // bucketed row offsets (within the segment)
   __shared__ float lds_w[kDkSeg];     // their ds
@@ -375,9 +389,18 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
   __shared__ int32_t tie_count[kDkTieCap];
   __shared__ int32_t ntie_s;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  const int64_t w = blockIdx.x;  // (gb, sg)
-  const int sg = static_cast<int>(w % nseg);
-  const int64_t gb = w / nseg;
+  // Workgroups are dispatched to the 8 XCDs round-robin (workgroup i on XCD i % 8), each
+  // with its own L2. Logical work L = (i % 8) * ceil(n / 8) + i / 8, segment-major, gives
+  // every XCD a contiguous run of (segment, block) pairs, so the query rows it gathers
+  // (one 2 MiB segment at a time) stay in its L2.
+  // The grid is padded to 8 x ceil(n / 8) workgroups so that this covers every L < n.
+  const int64_t nwork = nblk * nseg;
+  const int64_t per_xcd = gridDim.x / 8;
+  const int64_t lw = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (lw >= nwork) return;  // whole workgroup (padding)
+  const int sg = static_cast<int>(lw / nblk);
+  const int64_t gb = lw % nblk;
+  const int64_t w = gb * nseg + sg;  // (gb, sg): index of this pair's partial sums
   const int kc = blockIdx.y, kchunks = gridDim.y;
   int s = upper_index(cu_blocks, nseq + 1, gb);
   while (s < nseq && cu_blocks[s + 1] <= gb) ++s;
@@ -397,15 +420,26 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
     wcnt[0][tid] = wcnt[1][tid] = wcnt[2][tid] = wcnt[3][tid] = 0;
   }
   if (tid == 0) ntie_s = 0;
+  // the segment's tie codes and ds, row tid + 256 j in register j: all loads in flight at once
+  constexpr int kPer = kDkSeg / 256;
+  int32_t tcs[kPer];
+  float dvs[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = tid + 256 * j;
+    tcs[j] = i < nseg_rows ? tcol[i] : 0;
+    dvs[j] = i < nseg_rows ? dcol[i] : 0.f;
+  }
   __syncthreads();
   // ---- histogram of winners in this key chunk; list the exact ties
-  for (int i = tid; i < nseg_rows; i += 256) {
-    const int32_t tc = tcol[i];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int32_t tc = tcs[j];
     const int o = tc - 1 - o_lo;
     if (tc > 0 && o >= 0 && o < 128) atomicAdd(&cnt[o], 1);
     if (tc < 0) {
       const int slot = atomicAdd(&ntie_s, 1);
-      if (slot < kDkTieCap) tie_row[slot] = i;
+      if (slot < kDkTieCap) tie_row[slot] = tid + 256 * j;
     }
   }
   __syncthreads();
@@ -423,14 +457,13 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
   __syncthreads();
   // ---- stable scatter, 256 rows per step
   const uint64_t lt = (uint64_t(1) << lane) - 1;
-  for (int base = 0; base < nseg_rows; base += 256) {
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int base = 256 * j;
+    if (base >= nseg_rows) break;  // workgroup-uniform
     const int i = base + tid;
-    int32_t tc = 0;
-    float dv = 0.f;
-    if (i < nseg_rows) {
-      tc = tcol[i];
-      dv = dcol[i];
-    }
+    const int32_t tc = tcs[j];  // 0 past the segment end
+    const float dv = dvs[j];
     const int o = tc - 1 - o_lo;
     const bool on = tc > 0 && o >= 0 && o < 128;
     uint64_t match = __ballot(on);
@@ -500,19 +533,32 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
     if (wide) {
       // lane (slot, dch) adds entries e0 + slot, e0 + slot + RPI, ... over dims 8 dch .. +7
       const uint16_t* q16 = static_cast<const uint16_t*>(iq);
-      for (int e = e0; e < e1; e += 4 * kWideRpi) {
-        uint4 qw[4];
-        double wv[4];
+      for (int e = e0; e < e1; e += kDkWideUnroll * kWideRpi) {
+        // all list reads, then all row loads (from clamped, in-bounds entries), then the sums:
+        // no per-load branch or LDS wait between the gathers
+        uint4 qw[kDkWideUnroll];
+        double wv[kDkWideUnroll];
+        int ro[kDkWideUnroll];
+        float wf[kDkWideUnroll];
+        bool ok[kDkWideUnroll];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kDkWideUnroll; ++u) {
           const int ee = e + u * kWideRpi + slot;
-          const bool ok = ee < e1;
-          const int64_t row = r_begin + lrow[ok ? ee : e0];
-          qw[u] = ok ? *reinterpret_cast<const uint4*>(q16 + row * 128 + 8 * dch) : make_uint4(0u, 0u, 0u, 0u);
-          wv[u] = ok ? static_cast<double>(lds_w[ee]) * scale : 0.0;
+          ok[u] = ee < e1;
+          const int ec = ok[u] ? ee : e0;
+          ro[u] = lrow[ec];
+          wf[u] = lds_w[ec];
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
+        for (int u = 0; u < kDkWideUnroll; ++u)
+          qw[u] = *reinterpret_cast<const uint4*>(q16 + (r_begin + ro[u]) * 128 + 8 * dch);
+#pragma unroll
+        for (int u = 0; u < kDkWideUnroll; ++u) {
+          if (!ok[u]) qw[u] = make_uint4(0u, 0u, 0u, 0u);
+          wv[u] = ok[u] ? static_cast<double>(wf[u]) * scale : 0.0;
+        }
+#pragma unroll
+        for (int u = 0; u < kDkWideUnroll; ++u) {
           const uint32_t x[4] = {qw[u].x, qw[u].y, qw[u].z, qw[u].w};
 #pragma unroll
           for (int q2 = 0; q2 < 4; ++q2) {
@@ -667,8 +713,8 @@ int score_bwd_launch(const void* iq, const void* ik, const int32_t* cu, const in
     hipLaunchKernelGGL(score_bwd_transpose, tgrid, dim3(256), 0, st, tie, ds, rows, NB, tie_t, ds_t);
     const int nseg = static_cast<int>(dk_nseg(rows));
     const int kchunks = (B + 127) / 128;
-    const dim3 grid(static_cast<unsigned>(total_blocks * nseg), static_cast<unsigned>(kchunks));
-#define MSA_DK_PART(DPLV) hipLaunchKernelGGL((score_bwd_dk_part<DT, DPLV>), grid, dim3(256), 0, st, iq, ik, cu, cu_blocks, nseq, tie_t, ds_t, rows, G, Di, B, nseg, scale, part)
+    const dim3 grid(static_cast<unsigned>(8 * ((total_blocks * nseg + 7) / 8)), static_cast<unsigned>(kchunks));
+#define MSA_DK_PART(DPLV) hipLaunchKernelGGL((score_bwd_dk_part<DT, DPLV>), grid, dim3(256), 0, st, iq, ik, cu, cu_blocks, nseq, tie_t, ds_t, rows, G, Di, B, total_blocks, nseg, scale, part)
     if (Di <= 64) MSA_DK_PART(1);
     else if (Di <= 128) MSA_DK_PART(2);
     else if (Di <= 256) MSA_DK_PART(4);
