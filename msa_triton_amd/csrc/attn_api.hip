@@ -44,7 +44,7 @@ extern "C" int msa_attn_fwd(const void* q, const void* k, const void* v, int32_t
   if (!valid_common(num_seqs, total_tokens, q_heads, kv_groups, head_dim, block_size) || topk_slots < 0)
     return kErrInvalidArgument;
   if (total_tokens == 0) return kOk;
-  if (head_dim > 512) return kErrUnsupported;
+  if (head_dim > 2048) return kErrUnsupported;  // VALU path: the q (and dO) rows of a workgroup in LDS
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nseq = static_cast<int>(num_seqs), Hq = static_cast<int>(q_heads), G = static_cast<int>(kv_groups);
   const int D = static_cast<int>(head_dim), K = static_cast<int>(topk_slots), B = static_cast<int>(block_size);
@@ -83,7 +83,7 @@ extern "C" int msa_attn_bwd(const void* q, const void* k, const void* v, int32_t
       total_blocks < 0 || row_state == nullptr)
     return kErrInvalidArgument;
   if (total_tokens == 0 || (!grad_q && !grad_k && !grad_v)) return kOk;
-  if (head_dim > 512) return kErrUnsupported;
+  if (head_dim > 2048) return kErrUnsupported;  // VALU path: the q (and dO) rows of a workgroup in LDS
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nseq = static_cast<int>(num_seqs), Hq = static_cast<int>(q_heads), G = static_cast<int>(kv_groups);
   const int D = static_cast<int>(head_dim), K = static_cast<int>(topk_slots), B = static_cast<int>(block_size);

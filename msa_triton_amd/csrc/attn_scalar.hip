@@ -43,7 +43,8 @@ __global__ __launch_bounds__(256) void attn_fwd_valu(const void* __restrict__ q,
                                                      const int32_t* __restrict__ cu, int nseq, int64_t T,
                                                      int Hq, int G, int D, int K, int B, double scale,
                                                      void* __restrict__ out, float* __restrict__ lse,
-                                                     double* __restrict__ row_state, float* __restrict__ o32) {
+                                                     double* __restrict__ row_state, float* __restrict__ o32,
+                                                     int dc0) {
   extern __shared__ float smem[];
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t th = static_cast<int64_t>(blockIdx.x) * 4 + wid;
@@ -89,7 +90,7 @@ __global__ __launch_bounds__(256) void attn_fwd_valu(const void* __restrict__ q,
         const int64_t off = ((base + i) * G + g) * D;
 #pragma unroll
         for (int j = 0; j < DPL; ++j) {
-          const int d = lane + j * kWave;
+          const int d = dc0 + lane + j * kWave;
           if (d < D) o[j] = fma(pi, static_cast<double>(load_as_f32<DT>(v, off + d)), o[j]);
         }
       }
@@ -98,11 +99,11 @@ __global__ __launch_bounds__(256) void attn_fwd_valu(const void* __restrict__ q,
   }
 #pragma unroll
   for (int j = 0; j < DPL; ++j) {
-    const int d = lane + j * kWave;
+    const int d = dc0 + lane + j * kWave;
     if (d < D) {
-      const float r = l > 0.0 ? static_cast<float>(o[j] / l) : 0.f;
-      store_from_f32<DT>(out, th * D + d, r);
-      if (o32) o32[th * D + d] = r;
+      const double r = l > 0.0 ? o[j] / l : 0.0;
+      store_from_f64<DT>(out, th * D + d, r);
+      if (o32) o32[th * D + d] = static_cast<float>(r);
     }
   }
   if (lane == 0) {
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_valu(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
     const void* __restrict__ out, const void* __restrict__ dout, double* __restrict__ row_state,
     const int32_t* __restrict__ indices, const int32_t* __restrict__ cu, int nseq, int64_t T, int Hq, int G,
-    int D, int K, int B, double scale, void* __restrict__ dq) {
+    int D, int K, int B, double scale, void* __restrict__ dq, int dc0) {
   extern __shared__ float smem[];
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t th = static_cast<int64_t>(blockIdx.x) * 4 + wid;
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_valu(
           const int64_t off = ((base + i) * G + g) * D;
 #pragma unroll
           for (int j = 0; j < DPL; ++j) {
-            const int d = lane + j * kWave;
+            const int d = dc0 + lane + j * kWave;
             if (d < D) {
               const double kv = load_as_f32<DT>(k, off + d);
               a[j] = fma(ui, kv, a[j]);
@@ -196,10 +197,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_valu(
   if (dq) {
 #pragma unroll
     for (int j = 0; j < DPL; ++j) {
-      const int d = lane + j * kWave;
+      const int d = dc0 + lane + j * kWave;
       if (d < D) {
         const double val = has ? static_cast<double>(scale) * (a[j] - dhat * bsum[j]) / msum : 0.0;
-        store_from_f32<DT>(dq, th * D + d, static_cast<float>(val));
+        store_from_f64<DT>(dq, th * D + d, val);
       }
     }
   }
@@ -217,7 +218,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_valu(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
     const void* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ row_ptr,
     const int32_t* __restrict__ qidx, int nseq, int64_t T, int Hq, int G, int D, int B, double scale,
-    void* __restrict__ dk, void* __restrict__ dv) {
+    void* __restrict__ dk, void* __restrict__ dv, int dc0) {
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int64_t jg = static_cast<int64_t>(blockIdx.x) * 4 + wid;
   if (jg >= T * G) return;
@@ -228,11 +229,15 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_valu(
   const int64_t row = (static_cast<int64_t>(cu_blocks[s]) + blk) * G + g;
   const int64_t e0 = row_ptr[row], e1 = row_ptr[row + 1];
   const int R = Hq / G;
+  // This launch's dims are dc0 + lane + 64 i (i < DPL). When they are all of D the key
+  // and value rows stay in registers for the logits; otherwise (D above 64 x DPL, one
+  // launch per 64 DPL dims) the logits loop over every dim from memory, in the same order.
+  const bool whole = dc0 == 0 && D <= DPL * kWave;
   float kr[DPL], vr[DPL];
   double gk[DPL], gv[DPL];
 #pragma unroll
   for (int i = 0; i < DPL; ++i) {
-    const int d = lane + i * kWave;
+    const int d = dc0 + lane + i * kWave;
     kr[i] = d < D ? load_as_f32<DT>(k, jg * D + d) : 0.f;
     vr[i] = d < D ? load_as_f32<DT>(v, jg * D + d) : 0.f;
     gk[i] = gv[i] = 0.0;
@@ -246,11 +251,19 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_valu(
       double sp = 0.0, dp = 0.0;
 #pragma unroll
       for (int i = 0; i < DPL; ++i) {
-        const int d = lane + i * kWave;
+        const int d = dc0 + lane + i * kWave;
         qv[i] = d < D ? load_as_f32<DT>(q, th * D + d) : 0.f;
         gdv[i] = d < D ? load_as_f32<DT>(dout, th * D + d) : 0.f;
-        sp = fma(static_cast<double>(qv[i]), static_cast<double>(kr[i]), sp);
-        dp = fma(static_cast<double>(gdv[i]), static_cast<double>(vr[i]), dp);
+        if (whole) {
+          sp = fma(static_cast<double>(qv[i]), static_cast<double>(kr[i]), sp);
+          dp = fma(static_cast<double>(gdv[i]), static_cast<double>(vr[i]), dp);
+        }
+      }
+      if (!whole) {
+        for (int d = lane; d < D; d += kWave) {
+          sp = fma(static_cast<double>(load_as_f32<DT>(q, th * D + d)), static_cast<double>(load_as_f32<DT>(k, jg * D + d)), sp);
+          dp = fma(static_cast<double>(load_as_f32<DT>(dout, th * D + d)), static_cast<double>(load_as_f32<DT>(v, jg * D + d)), dp);
+        }
       }
       sp = wave_sum_f64(sp);
       dp = wave_sum_f64(dp);
@@ -267,10 +280,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_valu(
   }
 #pragma unroll
   for (int i = 0; i < DPL; ++i) {
-    const int d = lane + i * kWave;
+    const int d = dc0 + lane + i * kWave;
     if (d < D) {
-      if (dk) store_from_f32<DT>(dk, jg * D + d, static_cast<float>(gk[i]));
-      if (dv) store_from_f32<DT>(dv, jg * D + d, static_cast<float>(gv[i]));
+      if (dk) store_from_f64<DT>(dk, jg * D + d, gk[i]);
+      if (dv) store_from_f64<DT>(dv, jg * D + d, gv[i]);
     }
   }
 }
@@ -279,8 +292,9 @@ template <int DT, int DPL>
 int attn_valu_launch_fwd(const void* q, const void* k, const void* v, const int32_t* idx, const int32_t* cu,
                          int nseq, int64_t T, int Hq, int G, int D, int K, int B, double scale, void* out,
                          float* lse, double* rs, float* o32, hipStream_t st) {
-  hipLaunchKernelGGL((attn_fwd_valu<DT, DPL>), dim3(grid_1d(T * Hq, 4)), dim3(256), 4 * D * sizeof(float), st, q,
-                     k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse, rs, o32);
+  for (int dc0 = 0; dc0 < D; dc0 += DPL * kWave)
+    hipLaunchKernelGGL((attn_fwd_valu<DT, DPL>), dim3(grid_1d(T * Hq, 4)), dim3(256), 4 * D * sizeof(float), st, q,
+                       k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse, rs, o32, dc0);
   return status_from(hipGetLastError());
 }
 
@@ -288,8 +302,9 @@ template <int DT, int DPL>
 int attn_valu_launch_dq(const void* q, const void* k, const void* v, const void* out, const void* dout, double* rs,
                         const int32_t* idx, const int32_t* cu, int nseq, int64_t T, int Hq, int G, int D, int K,
                         int B, double scale, void* dq, hipStream_t st) {
-  hipLaunchKernelGGL((attn_bwd_dq_valu<DT, DPL>), dim3(grid_1d(T * Hq, 4)), dim3(256), 8 * D * sizeof(float),
-                     st, q, k, v, out, dout, rs, idx, cu, nseq, T, Hq, G, D, K, B, scale, dq);
+  for (int dc0 = 0; dc0 < D; dc0 += DPL * kWave)
+    hipLaunchKernelGGL((attn_bwd_dq_valu<DT, DPL>), dim3(grid_1d(T * Hq, 4)), dim3(256), 8 * D * sizeof(float),
+                       st, q, k, v, out, dout, rs, idx, cu, nseq, T, Hq, G, D, K, B, scale, dq, dc0);
   return status_from(hipGetLastError());
 }
 
@@ -298,8 +313,9 @@ int attn_valu_launch_dkdv(const void* q, const void* k, const void* v, const voi
                           const int32_t* cu, const int32_t* cu_blocks, const int32_t* row_ptr, const int32_t* qidx,
                           int nseq, int64_t T, int Hq, int G, int D, int B, double scale, void* dk, void* dv,
                           hipStream_t st) {
-  hipLaunchKernelGGL((attn_bwd_dkdv_valu<DT, DPL>), dim3(grid_1d(T * G, 4)), dim3(256), 0, st, q, k, v, dout, rs,
-                     cu, cu_blocks, row_ptr, qidx, nseq, T, Hq, G, D, B, scale, dk, dv);
+  for (int dc0 = 0; dc0 < D; dc0 += DPL * kWave)
+    hipLaunchKernelGGL((attn_bwd_dkdv_valu<DT, DPL>), dim3(grid_1d(T * G, 4)), dim3(256), 0, st, q, k, v, dout, rs,
+                       cu, cu_blocks, row_ptr, qidx, nseq, T, Hq, G, D, B, scale, dk, dv, dc0);
   return status_from(hipGetLastError());
 }
 

@@ -45,6 +45,15 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
 
 __device__ __forceinline__ float bf16_round(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
 
+// x rounded to fp32 toward zero with any inexact remainder folded into the last bit
+// ("round to odd"). Rounding that value to nearest in a format of at most 22 significand
+// bits (fp16) gives the correctly rounded x itself: no double-rounding error from going
+// through fp32. NaN stays NaN, infinities and overflow round as x would.
+__device__ __forceinline__ float f64_to_f32_odd(double x) {
+  const float f = __double2float_rz(x);
+  return static_cast<double>(f) == x ? f : __uint_as_float(__float_as_uint(f) | 1u);
+}
+
 template <int DT>
 __device__ __forceinline__ float load_as_f32(const void* base, int64_t i) {
   if constexpr (DT == kF32) {
@@ -64,6 +73,22 @@ __device__ __forceinline__ void store_from_f32(void* base, int64_t i, float v) {
     static_cast<_Float16*>(base)[i] = static_cast<_Float16>(v);
   } else {
     static_cast<uint16_t*>(base)[i] = f32_to_bf16_bits(v);
+  }
+}
+
+// An FP64 result in the output dtype, rounded as the reference's casts round it: fp32
+// once; fp16 once (torch's float64 -> float16 cast rounds once); bf16 through fp32 (the
+// reference computes in fp32 and casts to bf16, and torch's float64 -> bfloat16 cast also
+// goes through fp32, which keeps FP64 results a few ulps apart on the same side of a
+// bf16 rounding midpoint).
+template <int DT>
+__device__ __forceinline__ void store_from_f64(void* base, int64_t i, double v) {
+  if constexpr (DT == kF32) {
+    static_cast<float*>(base)[i] = static_cast<float>(v);
+  } else if constexpr (DT == kF16) {
+    static_cast<_Float16*>(base)[i] = static_cast<_Float16>(f64_to_f32_odd(v));
+  } else {
+    static_cast<uint16_t*>(base)[i] = f32_to_bf16_bits(static_cast<float>(v));
   }
 }
 

@@ -103,13 +103,15 @@ __device__ __forceinline__ float half_of(uint32_t w, int hi) {
   }
 }
 
+// Two FP64 values in the 2-byte output dtype (rounded as store_from_f64 does), packed.
 template <int DT>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+__device__ __forceinline__ uint32_t pack2(double lo, double hi) {
   if constexpr (DT == kBF16) {
-    return static_cast<uint32_t>(f32_to_bf16_bits(lo)) | (static_cast<uint32_t>(f32_to_bf16_bits(hi)) << 16);
+    return static_cast<uint32_t>(f32_to_bf16_bits(static_cast<float>(lo))) |
+           (static_cast<uint32_t>(f32_to_bf16_bits(static_cast<float>(hi))) << 16);
   } else {
-    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(lo))) |
-           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(hi))) << 16);
+    return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f64_to_f32_odd(lo)))) |
+           (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f64_to_f32_odd(hi)))) << 16);
   }
 }
 __device__ __forceinline__ float lane_f32(float v, int l) {
@@ -117,7 +119,8 @@ __device__ __forceinline__ float lane_f32(float v, int l) {
 }
 
 // dq[t,g] = sum over valid blocks of w * k[winner] (ties: w/count per tied key).
-// One wavefront per row, lane j of the wave owns dims DPL j .. DPL j + DPL - 1. The
+// One wavefront per row, lane j of the wave owns dims dc0 + DPL j .. + DPL - 1 (one
+// launch per 64 DPL dims: each dim's sum is independent of the others). The
 // row's blocks are taken 64 at a time (lane = block); unique winners are added in
 // block order with kDqBatch key rows in flight (block / key broadcast by readlane),
 // then the chunk's exact ties (rare) in block order. FP64 accumulation.
@@ -129,7 +132,7 @@ __global__ __launch_bounds__(256) void score_bwd_dq(const void* __restrict__ iq,
                                                     const int32_t* __restrict__ tie,
                                                     const float* __restrict__ ds, int64_t rows, int G,
                                                     int Di, int NB, int B, double scale,
-                                                    void* __restrict__ dq) {
+                                                    void* __restrict__ dq, int dc0) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
@@ -141,7 +144,7 @@ __global__ __launch_bounds__(256) void score_bwd_dq(const void* __restrict__ iq,
   double acc[DPL];
 #pragma unroll
   for (int i = 0; i < DPL; ++i) acc[i] = 0.0;
-  const int dbase = DPL * lane;
+  const int dbase = dc0 + DPL * lane;  // this pass's dims (index dims above 64 x DPL take several passes)
   for (int b0 = 0; b0 < nvalid; b0 += 64) {
     const int bl = b0 + lane;
     const int32_t my_tie = bl < nvalid ? tie[row * NB + bl] : 0;
@@ -209,7 +212,7 @@ __global__ __launch_bounds__(256) void score_bwd_dq(const void* __restrict__ iq,
 #pragma unroll
   for (int j = 0; j < DPL; ++j) {
     const int d = dbase + j;
-    if (d < Di) store_from_f32<DT>(dq, row * Di + d, static_cast<float>(acc[j]));
+    if (d < Di) store_from_f64<DT>(dq, row * Di + d, acc[j]);
   }
 }
 
@@ -336,7 +339,7 @@ __global__ __launch_bounds__(256) void score_bwd_dq_wide(const void* __restrict_
     uint32_t o[4];
 #pragma unroll
     for (int q2 = 0; q2 < 4; ++q2)
-      o[q2] = pack2<DT>(static_cast<float>(acc[2 * q2]), static_cast<float>(acc[2 * q2 + 1]));
+      o[q2] = pack2<DT>(acc[2 * q2], acc[2 * q2 + 1]);
     *reinterpret_cast<uint4*>(static_cast<uint16_t*>(dq) + row * Di + 8 * dch) = make_uint4(o[0], o[1], o[2], o[3]);
   }
 }
@@ -379,7 +382,7 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
     const void* __restrict__ iq, const void* __restrict__ ik, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, int nseq, const int32_t* __restrict__ tie_t,
     const float* __restrict__ ds_t, int64_t rows, int G, int Di, int B, int64_t nblk, int nseg, double scale,
-    double* __restrict__ part) {
+    double* __restrict__ part, int dc0) {
   __shared__ uint16_t lrow[kDkSeg];   // bucketed row offsets (within the segment)
   __shared__ float lds_w[kDkSeg];     // their ds
   __shared__ int32_t cnt[128], bstart[128], running[128];
@@ -516,8 +519,9 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
     }
   }
   __syncthreads();
-  // ---- per-key sums: wave w takes keys w, w + 4, ...
-  const int dbase = DPL * lane;
+  // ---- per-key sums: wave w takes keys w, w + 4, ...; lane dims dc0 + DPL lane .. + DPL - 1
+  // (index dims above 64 x DPL take one launch per 64 DPL dims)
+  const int dbase = dc0 + DPL * lane;
   const int64_t kchunk_end = k0 + B < end ? k0 + B : end;
   constexpr int kWideLpr = 16;                  // lanes per 128-dim row (wide gathers, Di == 128)
   constexpr int kWideRpi = 64 / kWideLpr;       // rows per load instruction
@@ -661,7 +665,7 @@ __global__ __launch_bounds__(256) void score_bwd_dk_reduce(const int32_t* __rest
     const int64_t w = gb * nseg + sg;
     sum += part[((w * kchunks + kc) * 128 + o % 128) * static_cast<int64_t>(Di) + d];
   }
-  store_from_f32<DT>(dk, i, static_cast<float>(sum));
+  store_from_f64<DT>(dk, i, sum);
 }
 
 static int64_t dk_nseg(int64_t rows) { return (rows + kDkSeg - 1) / kDkSeg; }
@@ -700,10 +704,12 @@ int score_bwd_launch(const void* iq, const void* ik, const int32_t* cu, const in
     }
   } else if (dq) {
     const dim3 grid(grid_1d(rows, 4)), block(256);
-    if (Di <= 64) hipLaunchKernelGGL((score_bwd_dq<DT, 1>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq);
-    else if (Di <= 128) hipLaunchKernelGGL((score_bwd_dq<DT, 2>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq);
-    else if (Di <= 256) hipLaunchKernelGGL((score_bwd_dq<DT, 4>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq);
-    else hipLaunchKernelGGL((score_bwd_dq<DT, 8>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq);
+    if (Di <= 64) hipLaunchKernelGGL((score_bwd_dq<DT, 1>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq, 0);
+    else if (Di <= 128) hipLaunchKernelGGL((score_bwd_dq<DT, 2>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq, 0);
+    else if (Di <= 256) hipLaunchKernelGGL((score_bwd_dq<DT, 4>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq, 0);
+    else
+      for (int dc0 = 0; dc0 < Di; dc0 += 512)
+        hipLaunchKernelGGL((score_bwd_dq<DT, 8>), grid, block, 0, st, iq, ik, cu, nseq, tie, ds, rows, G, Di, NB, B, scale, dq, dc0);
   }
   if (dk && total_blocks > 0) {
     int32_t* tie_t = static_cast<int32_t*>(ws);
@@ -714,11 +720,12 @@ int score_bwd_launch(const void* iq, const void* ik, const int32_t* cu, const in
     const int nseg = static_cast<int>(dk_nseg(rows));
     const int kchunks = (B + 127) / 128;
     const dim3 grid(static_cast<unsigned>(8 * ((total_blocks * nseg + 7) / 8)), static_cast<unsigned>(kchunks));
-#define MSA_DK_PART(DPLV) hipLaunchKernelGGL((score_bwd_dk_part<DT, DPLV>), grid, dim3(256), 0, st, iq, ik, cu, cu_blocks, nseq, tie_t, ds_t, rows, G, Di, B, total_blocks, nseg, scale, part)
-    if (Di <= 64) MSA_DK_PART(1);
-    else if (Di <= 128) MSA_DK_PART(2);
-    else if (Di <= 256) MSA_DK_PART(4);
-    else MSA_DK_PART(8);
+#define MSA_DK_PART(DPLV, DC0) hipLaunchKernelGGL((score_bwd_dk_part<DT, DPLV>), grid, dim3(256), 0, st, iq, ik, cu, cu_blocks, nseq, tie_t, ds_t, rows, G, Di, B, total_blocks, nseg, scale, part, DC0)
+    if (Di <= 64) MSA_DK_PART(1, 0);
+    else if (Di <= 128) MSA_DK_PART(2, 0);
+    else if (Di <= 256) MSA_DK_PART(4, 0);
+    else
+      for (int dc0 = 0; dc0 < Di; dc0 += 512) MSA_DK_PART(8, dc0);
 #undef MSA_DK_PART
     const int64_t T = rows / G;
     hipLaunchKernelGGL(score_bwd_dk_reduce<DT>, dim3(grid_1d(T * Di, 256)), dim3(256), 0, st, cu, cu_blocks, nseq, T,
@@ -745,7 +752,6 @@ extern "C" int msa_score_fwd(const void* index_q, const void* index_k, int32_t d
     return kErrInvalidArgument;
   const int64_t rows = total_tokens * groups;
   if (rows == 0) return kOk;
-  if (index_dim > 512) return kErrUnsupported;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nseq = static_cast<int>(num_seqs), G = static_cast<int>(groups);
   const int Di = static_cast<int>(index_dim), NB = static_cast<int>(num_blocks);
@@ -769,7 +775,6 @@ extern "C" int msa_index_score_topk(const void* index_q, const void* index_k, in
     return kErrInvalidArgument;
   const int64_t rows = total_tokens * groups;
   if (rows == 0) return kOk;
-  if (index_dim > 512 || num_blocks > 16 * 256) return kErrUnsupported;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nseq = static_cast<int>(num_seqs), G = static_cast<int>(groups);
   const int Di = static_cast<int>(index_dim), NB = static_cast<int>(num_blocks);
@@ -806,7 +811,6 @@ extern "C" int msa_score_bwd(const void* index_q, const void* index_k, int32_t d
     return kErrInvalidArgument;
   const int64_t rows = total_tokens * groups;
   if (rows == 0) return kOk;
-  if (index_dim > 512) return kErrUnsupported;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nseq = static_cast<int>(num_seqs), G = static_cast<int>(groups);
   const int Di = static_cast<int>(index_dim), NB = static_cast<int>(num_blocks);

@@ -38,6 +38,16 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict_
   topk_row64<VPL>(scores, cu, nseq, G, NB, B, K, L, out, row, threadIdx.x & 63);
 }
 
+// One wavefront per row, row streamed from memory (more than 4096 blocks): topk_row_stream.
+__global__ __launch_bounds__(256) void topk_stream_kernel(const float* __restrict__ scores,
+                                                          const int32_t* __restrict__ cu, int nseq, int64_t rows,
+                                                          int G, int NB, int B, int K, int L,
+                                                          int32_t* __restrict__ out) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  topk_row_stream(scores, cu, nseq, G, NB, B, K, L, out, row, threadIdx.x & 63);
+}
+
 }  // namespace msa
 
 using namespace msa;
@@ -60,7 +70,8 @@ int topk_launch(const float* scores, const int32_t* cu_seqlens, int nseq, int64_
   else if (NB <= 512) MSA_TOPK_LAUNCH(32);
   else if (NB <= 1024) MSA_TOPK_LAUNCH(64);
   else if (NB <= 2048) MSA_TOPK_WAVE(32);
-  else MSA_TOPK_WAVE(64);
+  else if (NB <= 4096) MSA_TOPK_WAVE(64);
+  else hipLaunchKernelGGL(topk_stream_kernel, dim3(grid_1d(rows, 4)), block, 0, st, scores, cu_seqlens, nseq, rows, G, NB, B, K, L, indices);
 #undef MSA_TOPK_LAUNCH
 #undef MSA_TOPK_WAVE
   return status_from(hipGetLastError());
@@ -74,7 +85,6 @@ extern "C" int msa_topk(const float* scores, const int32_t* cu_seqlens, int64_t 
   if (total_tokens < 0 || groups <= 0 || num_blocks <= 0 || block_size <= 0 || topk_blocks < 0 ||
       local_blocks < 0 || local_blocks > topk_blocks || num_seqs <= 0)
     return kErrInvalidArgument;
-  if (num_blocks > 16 * 256) return kErrUnsupported;
   return topk_launch(scores, cu_seqlens, static_cast<int>(num_seqs), total_tokens * groups, static_cast<int>(groups),
                      static_cast<int>(num_blocks), static_cast<int>(block_size), static_cast<int>(topk_blocks),
                      static_cast<int>(local_blocks), indices, static_cast<hipStream_t>(stream));

@@ -130,7 +130,7 @@ __device__ __forceinline__ void topk_row16(const float* __restrict__ scores, con
 }
 
 // Host launch of the stand-alone selection (topk.hip): 16-lane rows up to 1024
-// blocks, one wavefront per row up to 4096.
+// blocks, one wavefront per row with the row in registers up to 4096, streamed above.
 int topk_launch(const float* scores, const int32_t* cu_seqlens, int nseq, int64_t rows, int G, int NB, int B, int K,
                 int L, int32_t* indices, hipStream_t st);
 
@@ -171,6 +171,45 @@ __device__ __forceinline__ void topk_row64(const float* __restrict__ scores, con
         if (key[v] == win) key[v] = 0;
         best = key[v] > best ? key[v] : best;
       }
+    }
+  }
+  for (int it = sel + lane; it < K; it += kWave) dst[it] = -1;
+}
+
+// One wavefront per row with the row left in memory, for any number of blocks (used
+// above 4096): lane j scans blocks j, j + 64, ... and keeps its eight largest keys
+// below its last pick (TopN<8>); it rescans its blocks only when that cache runs empty,
+// so a row is read about once. Picks, order and padding are those of topk_row64.
+__device__ __forceinline__ void topk_row_stream(const float* __restrict__ scores, const int32_t* __restrict__ cu,
+                                                int nseq, int G, int NB, int B, int K, int L,
+                                                int32_t* __restrict__ out, int64_t row, int lane) {
+  const int64_t t = row / G;
+  const int s = find_seq(cu, nseq, t);
+  const int64_t qb = (t - cu[s]) / B;
+  const int n = static_cast<int>(qb + 1 < NB ? qb + 1 : NB);
+  const int count = K < NB ? K : NB;
+  const int sel = count < n ? count : n;
+  const float* src = scores + row * NB;
+  int32_t* dst = out + row * static_cast<int64_t>(K);
+  TopN<8> top;
+  auto fill = [&](uint64_t below) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) top.c[i] = 0;
+    for (int b = lane; b < n; b += kWave) {
+      const uint32_t k = (L > 0 && b > qb - L) ? kKeyPosInf : ordered_key(src[b]);
+      const uint64_t x = (static_cast<uint64_t>(k) << 32) | static_cast<uint32_t>(~static_cast<uint32_t>(b));
+      if (x < below) top.insert(x);
+    }
+  };
+  fill(~uint64_t(0));
+  for (int it = 0; it < sel; ++it) {
+    const uint64_t win = wave_max_u64(top.c[0]);
+    const int b = static_cast<int>(~static_cast<uint32_t>(win));
+    const uint32_t k = static_cast<uint32_t>(win >> 32);
+    if (lane == 0) dst[it] = (k == kKeyNegInf) ? -1 : b;
+    if ((b & 63) == lane) {  // win == top.c[0] of this lane
+      top.pop();
+      if (top.c[0] == 0) fill(win);
     }
   }
   for (int it = sel + lane; it < K; it += kWave) dst[it] = -1;

@@ -209,7 +209,5 @@ def m3_index_score_topk(index_q, index_k, cu_seqlens, max_seqlen, *, block_size=
     if not isinstance(local_blocks, int) or not 0 <= local_blocks <= topk_blocks:
         raise ValueError("local_blocks must satisfy 0 <= local_blocks <= topk_blocks")
     cu, meta, seqs, save_state = _validate(index_q, index_k, cu_seqlens, max_seqlen, block_size, scale)
-    if (max_seqlen + block_size - 1) // block_size > 4096:
-        raise NotImplementedError("m3_topk supports at most 4096 block columns")
     return _IndexScoreTopk.apply(index_q, index_k, cu, max_seqlen, block_size, float(scale), save_state, meta,
                                  None if seqs is None else seqs.cu_block_lens, topk_blocks, local_blocks)

@@ -47,8 +47,6 @@ def m3_topk(scores, cu_seqlens, *, block_size=128, topk_blocks=16, local_blocks=
     result = torch.empty((total, groups, topk_blocks), dtype=torch.int32, device=scores.device)
     if total == 0 or topk_blocks == 0:
         return result.fill_(-1)
-    if blocks > 4096:
-        raise NotImplementedError("m3_topk supports at most 4096 block columns")
     scores = scores.contiguous()
     cu = cu.contiguous()
     with torch.cuda.device(scores.device):

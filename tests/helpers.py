@@ -72,6 +72,23 @@ def random_selection(total, groups, topk, lengths, block_size, local_blocks, gen
     return ids
 
 
+def rounded(x, dtype):
+    """FP64 oracle values in `dtype`, rounded as the kernels round their FP64 results:
+    float32 and float16 once (numpy's direct casts), bfloat16 through float32 (as the
+    reference's fp32 kernels followed by a bf16 cast, and torch's float64 -> bfloat16
+    cast). torch's float64 -> float16 cast also goes through float32; a value just past
+    a float16 midpoint then lands on it and rounds to even, numpy's cast does not."""
+    x = np.asarray(x, dtype=np.float64)
+    if dtype == torch.float64:
+        return torch.from_numpy(x.copy())
+    if dtype == torch.float32:
+        return torch.from_numpy(x.astype(np.float32))
+    if dtype == torch.float16:
+        return torch.from_numpy(x.astype(np.float16))
+    assert dtype == torch.bfloat16, dtype
+    return torch.from_numpy(x.astype(np.float32)).to(torch.bfloat16)
+
+
 def check_bf16_stated(actual, expected, what):
     """The stated bf16 tolerance for large outputs: every element within 1e-4 + 2^-8 |x|
     of the FP64 value x, and at most 0.1 % (at least one) outside the reference's gate
@@ -79,7 +96,7 @@ def check_bf16_stated(actual, expected, what):
     ~2^-22 of a bf16 rounding midpoint undecided, ~5e-5 of the elements here."""
     act = actual.detach().float().cpu().numpy().astype(np.float64).ravel()
     exp = np.asarray(expected, dtype=np.float64).ravel()
-    ref_r = torch.from_numpy(exp).to(torch.bfloat16).double().numpy()
+    ref_r = rounded(exp, torch.bfloat16).double().numpy()
     gate = np.abs(act - ref_r) <= 1e-4 + 1e-4 * np.abs(ref_r)
     bad = int((~gate).sum())
     err = np.abs(act - exp)

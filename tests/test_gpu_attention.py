@@ -18,7 +18,7 @@ import torch
 
 import msa_triton_amd as msa
 from oracle import msa_oracle as O
-from tests.helpers import attention_inputs, check_bf16_stated, np64
+from tests.helpers import attention_inputs, check_bf16_stated, np64, rounded
 
 pytestmark = pytest.mark.gpu
 
@@ -34,7 +34,7 @@ def _oracle(tensors, indices, cu, block_size, scale=None, dout=None):
 
 
 def _close(actual, expected_np, dtype=torch.bfloat16):
-    torch.testing.assert_close(actual.detach().cpu(), torch.from_numpy(expected_np).to(dtype), atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(actual.detach().cpu(), rounded(expected_np, dtype), atol=1e-4, rtol=1e-4)
 
 
 def _assert_lse(actual, expected):
@@ -294,3 +294,22 @@ def test_backward_with_and_without_fp32_output(lengths, groups, ratio, dimension
                 _close(actual, ref)
     # rows that take the statistics pass either way get the same dQ bit for bit
     torch.testing.assert_close(runs["fp32"][0][peaked], runs["stats"][0][peaked], atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("dimension,dtype", [(640, torch.bfloat16), (1100, torch.float32), (2048, torch.float16)])
+def test_head_dims_beyond_512_against_fp64(dimension, dtype, device):
+    """Head dims above 512 run the VALU kernels in passes of 512 output dims (the logits
+    always cover every dim); forward, lse and all gradients within the reference gate."""
+    _, indices, cu = attention_inputs([9, 6], 2, 2, 8, 4, 2)
+    generator = torch.Generator().manual_seed(dimension)
+    shapes = ((15, 4, dimension), (15, 2, dimension), (15, 2, dimension))
+    cpu = tuple((0.25 * torch.randn(s, generator=generator)).to(dtype) for s in shapes)
+    grad = torch.randn(cpu[0].shape, generator=generator).to(dtype)
+    out, lse, dq, dk, dv = _oracle(cpu, indices, cu, 4, None, grad)
+    tensors, indices_d, cu_d = _to(device, cpu, indices, cu)
+    actual, actual_lse = msa.m3_sparse_attention(*tensors, indices_d, cu_d, 9, block_size=4, return_lse=True)
+    _close(actual, out, dtype)
+    _assert_lse(actual_lse, lse)
+    actual.backward(grad.to(device))
+    for tensor, ref in zip(tensors, (dq, dk, dv)):
+        _close(tensor.grad, ref, dtype)

@@ -14,7 +14,7 @@ import torch
 
 import msa_triton_amd as msa
 from oracle import msa_oracle as O
-from tests.helpers import cu_list, cu_tensor
+from tests.helpers import cu_list, cu_tensor, rounded
 
 pytestmark = pytest.mark.gpu
 
@@ -33,8 +33,8 @@ def _run(q_cpu, k_cpu, lengths, max_seqlen, block_size, scale, upstream, device)
     dq, dk = O.index_score_backward(q_cpu.double().numpy(), k_cpu.double().numpy(), cu_list(lengths), max_seqlen,
                                     upstream.double().numpy(), block_size=block_size, scale=scale)
     dtype = q_cpu.dtype
-    torch.testing.assert_close(q.grad.cpu(), torch.from_numpy(dq).to(dtype), atol=1e-4, rtol=1e-4)
-    torch.testing.assert_close(k.grad.cpu(), torch.from_numpy(dk).to(dtype), atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(q.grad.cpu(), rounded(dq, dtype), atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(k.grad.cpu(), rounded(dk, dtype), atol=1e-4, rtol=1e-4)
     return actual
 
 
@@ -194,3 +194,16 @@ def test_score_extreme_magnitudes_bit_exact(scale, device):
         _, exp32, _ = O.index_score(q.double().numpy(), k.double().numpy(), cu_list(lengths), max(lengths),
                                     block_size=block, scale=scale)
     np.testing.assert_array_equal(got.cpu().numpy(), exp32)
+
+
+@pytest.mark.parametrize("dim,dtype", [(640, torch.bfloat16), (1100, torch.float32)])
+def test_score_index_dims_beyond_512(dim, dtype, device):
+    """Index dims above 512 (no cap upstream): the exact forward, and the backward in
+    passes of 512 dims; bit-exact scores, gradients within the reference gate."""
+    gen = torch.Generator().manual_seed(dim)
+    lengths, groups, block = [70, 45], 2, 16
+    q_cpu = torch.randn(sum(lengths), groups, dim, generator=gen).to(dtype)
+    k_cpu = torch.randn(sum(lengths), 1, dim, generator=gen).to(dtype)
+    nb = (max(lengths) + block - 1) // block
+    upstream = torch.randn((sum(lengths), groups, nb), generator=gen).to(torch.bfloat16).float()
+    _run(q_cpu, k_cpu, lengths, max(lengths), block, 1.0, upstream, device)

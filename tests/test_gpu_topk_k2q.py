@@ -175,3 +175,21 @@ def test_topk_winners_concentrated_in_one_lane(length, block, k, device):
         got = msa.m3_topk(scores.to(device), cu, block_size=block, topk_blocks=k, local_blocks=local)
         ref = O.topk(scores.numpy(), [0, length], block_size=block, topk_blocks=k, local_blocks=local)
         np.testing.assert_array_equal(got.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("tokens,block,k,local", [(9000, 2, 24, 2), (4500, 1, 40, 1)])
+def test_topk_rows_beyond_4096_blocks(tokens, block, k, local, device):
+    """Rows of 4500 blocks: one wavefront per row with the row streamed from memory. In
+    every row the blocks of one lane (b % 64 == row % 64) lead, so that lane's cache of
+    eight keys empties and refills several times; integer scores tie, some are -inf."""
+    gen = torch.Generator().manual_seed(tokens + k)
+    groups, nb = 2, (tokens + block - 1) // block
+    scores = torch.randint(-4, 5, (tokens, groups, nb), generator=gen).float()
+    rows = torch.arange(tokens).view(-1, 1, 1)
+    lead = (torch.arange(nb).view(1, 1, -1) % 64) == (rows % 64)
+    scores = torch.where(lead, scores + 20.0, scores)
+    scores[::7, 0, ::5] = float("-inf")
+    got = msa.m3_topk(scores.to(device), cu_tensor([tokens], device), block_size=block, topk_blocks=k,
+                      local_blocks=local)
+    ref = O.topk(scores.numpy(), [0, tokens], block_size=block, topk_blocks=k, local_blocks=local)
+    np.testing.assert_array_equal(got.cpu().numpy(), ref)
