@@ -58,9 +58,10 @@ inline uint32_t ratio_magic(int64_t r) {
 }
 
 // Query tokens per chunk: per-(token, head, slot) records of `record_bytes` each
-// within `budget` bytes, chunks of equal size. The forward partial pass runs
-// best with ~1 GiB chunks (its gathered query rows stay cache-resident), the
-// backward with ~4 GiB (fewer per-chunk key-block reloads and item tails).
+// within `budget` bytes, chunks of equal size. Measured at c4 (T = 32768): the forward
+// partial pass runs best with ~2 GiB chunks (5 chunks; 1 GiB: +1.5 %), the backward with
+// ~6 GiB (2 chunks; 4 GiB: +2 %, fewer per-chunk key-block reloads and item tails); the
+// backward's 32-bit dQ record offsets bound its budget below 8 GiB.
 int64_t kv_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t record_bytes, int64_t budget);
 
 // Chunk budgets of the KV-major passes: `dflt` unless msa_set_chunk_budgets set one.

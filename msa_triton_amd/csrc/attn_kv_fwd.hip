@@ -500,7 +500,7 @@ struct FwdLayout {
 
 static FwdLayout fwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks) {
   FwdLayout f;
-  const int64_t tc = kv_chunk_tokens(T, Hq, K, (D + 2) * 4, kv_chunk_budget(kPassFwd, int64_t(1) << 30));
+  const int64_t tc = kv_chunk_tokens(T, Hq, K, (D + 2) * 4, kv_chunk_budget(kPassFwd, int64_t(2) << 30));
   f.plan = kv_plan_layout(T, total_blocks * G, G, K, tc, fwd_epi(Hq / (G > 0 ? G : 1)));
   f.opart = f.plan.bytes;
   f.ml = f.opart + align256(tc * Hq * K * D * 4);
