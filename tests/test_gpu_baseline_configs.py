@@ -31,6 +31,7 @@ import torch
 
 import bench
 import msa_triton_amd as msa
+from msa_triton_amd import _lib
 from msa_triton_amd.k2q import build_k2q_csr
 from oracle import msa_oracle as O
 from tests.helpers import check_bf16_stated as _check_bf16
@@ -59,11 +60,16 @@ def _sample_tokens(lengths, block, rng, extra=4):
     return np.array(sorted(out), dtype=np.int64)
 
 
-def _bwd_chunk_tokens(cfg, total):
-    """Query tokens per backward chunk at the default 4 GiB budget (kv_chunk_tokens: records of
+# Backward chunk budget per config: the default (6 GiB) except c3, which fits in one chunk
+# there; at 2 GiB its third sequence's keys are summed across three chunks.
+BWD_BUDGET = {"c3": 2 << 30}
+
+
+def _bwd_chunk_tokens(cfg, total, budget):
+    """Query tokens per backward chunk at `budget` bytes (kv_chunk_tokens: records of
     D * 4 + 8 bytes per (token, head, slot), at least 64 tokens, balanced chunks)."""
     per_token = cfg["hq"] * cfg["topk"] * (cfg["d"] * 4 + 8)
-    tc = max(64, (1 << 32) // per_token)
+    tc = max(64, budget // per_token)
     if total <= tc:
         return total
     nch = -(-total // tc)
@@ -74,8 +80,8 @@ def _sample_keys(lengths, block, name):
     """Keys of the last blocks of the longest sequence (few query tokens see them), and
     early keys whose blocks are selected by query tokens of several backward chunks, so
     that their dK / dV are sums the backward carries across chunks: c3's third sequence
-    (tokens 5120-10239 straddle the chunk boundary at 8192), c4 blocks 0, 40 and 120
-    (three chunks), c5 blocks 0 and 3 (seventeen chunks)."""
+    (tokens 5120-10239 straddle the chunk boundary at 5462 at its 2 GiB budget), c4 blocks
+    0, 40 and 120 (two chunks), c5 blocks 0 and 3 (eleven chunks)."""
     bounds = _bounds(lengths)
     s = int(np.argmax(lengths))
     a, n = bounds[s], lengths[s]
@@ -93,7 +99,7 @@ def _sample_keys(lengths, block, name):
 
 def _assert_multi_chunk_keys(cfg, name, ids_np, bounds, keys):
     """Each early key of c3-c5 gets edges from at least two backward chunks."""
-    tc = _bwd_chunk_tokens(cfg, bounds[-1])
+    tc = _bwd_chunk_tokens(cfg, bounds[-1], BWD_BUDGET.get(name, 6 << 30))
     spanning = 0
     for j in keys:
         s = int(np.searchsorted(bounds, j, side="right") - 1)
@@ -144,9 +150,10 @@ def test_pipeline_against_oracle(name, device):
 
     # ---- stage 3 forward + backward
     qd, kd, vd = (x.to(device).requires_grad_() for x in (q, k, v))
-    out, lse = msa.m3_sparse_attention(qd, kd, vd, ids, cu, max_len, block_size=B, return_lse=True)
-    out.backward(dout.to(device))
-    torch.cuda.synchronize()
+    with _lib.chunk_budgets(bwd=BWD_BUDGET.get(name)):
+        out, lse = msa.m3_sparse_attention(qd, kd, vd, ids, cu, max_len, block_size=B, return_lse=True)
+        out.backward(dout.to(device))
+        torch.cuda.synchronize()
     q64, k64, v64, do64 = (x.double().numpy() for x in (q, k, v, dout))
     if name == "c1":
         # dense FP64 oracle over every token and key
