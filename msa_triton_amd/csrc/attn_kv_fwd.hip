@@ -23,6 +23,7 @@
 // in the same k order as the backward kernels. P.V is computed exactly in its
 // products: P is split into three bf16 terms (hi + mid + lo == P).
 #include <atomic>
+#include <type_traits>
 
 #include "attn_kv_common.hpp"
 #include "profile.hpp"
@@ -237,67 +238,76 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     if (tile + 1 < ntiles) load_q(r0 + kRowsPerTile);
     // ---- base-2 partial softmax per row (rows of the lane's quad share c):
     // x = fl(acc * scale2), m = max x, p = 2^(x - m) (exactly 1 at the maximum).
+    // Wave-uniform: every row of the wave sees all 128 keys (no masks), or not. The two
+    // cases are separate code paths so the unmasked one carries no per-logit selects.
     const bool full = __ballot(lim[0] < 128 || lim[1] < 128) == 0;
     float mrow[2], lrow[2];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      float m = -__builtin_inff();
-#pragma unroll
-      for (int kt = 0; kt < 8; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float x = s[rt][kt][i] * scale2;
-          if (!full) x = (16 * kt + 4 * q4 + i < lim[rt]) ? x : -__builtin_inff();
-          s[rt][kt][i] = x;
-          m = fmaxf(m, x);
-        }
-      m = quad_max(m);
-      const float base = m == -__builtin_inff() ? 0.f : m;
-      float l = 0.f;
-#pragma unroll
-      for (int kt = 0; kt < 8; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = __builtin_amdgcn_exp2f(s[rt][kt][i] - base);
-          s[rt][kt][i] = p;
-          l += p;
-        }
-      l += __shfl_xor(l, 16, kWave);
-      l += __shfl_xor(l, 32, kWave);
-      mrow[rt] = m;
-      lrow[rt] = l;
-    }
-    // ---- O^T = V^T P^T over 4 chunks of 32 keys: A = V^T[dim c][keys pi], B = P^T[keys pi][row c]
     f32x4 o[2][NDT];
-#pragma unroll
-    for (int kc = 0; kc < 4; ++kc) {
-      bf16x8 ph[2], pm[2], pl[2];
+    auto softmax_pv = [&](auto full_tag) __attribute__((always_inline)) {
+      constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
-        uint32_t wh[4], wm[4], wl[4];
+        float m = -__builtin_inff();
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          // elements j = 2*jj, 2*jj + 1 -> C tile 2*kc + j/4, entry j%4
-          const int j0 = 2 * jj, j1 = 2 * jj + 1;
-          split3_pk(s[rt][2 * kc + j0 / 4][j0 % 4], s[rt][2 * kc + j1 / 4][j1 % 4], wh[jj], wm[jj], wl[jj]);
-        }
-        ph[rt] = __builtin_bit_cast(bf16x8, make_uint4(wh[0], wh[1], wh[2], wh[3]));
-        pm[rt] = __builtin_bit_cast(bf16x8, make_uint4(wm[0], wm[1], wm[2], wm[3]));
-        pl[rt] = __builtin_bit_cast(bf16x8, make_uint4(wl[0], wl[1], wl[2], wl[3]));
+        for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float x = s[rt][kt][i] * scale2;
+            if constexpr (!FULL) x = (16 * kt + 4 * q4 + i < lim[rt]) ? x : -__builtin_inff();
+            s[rt][kt][i] = x;
+            m = fmaxf(m, x);
+          }
+        m = quad_max(m);
+        const float base = m == -__builtin_inff() ? 0.f : m;
+        float l = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p = __builtin_amdgcn_exp2f(s[rt][kt][i] - base);
+            s[rt][kt][i] = p;
+            l += p;
+          }
+        l += __shfl_xor(l, 16, kWave);
+        l += __shfl_xor(l, 32, kWave);
+        mrow[rt] = m;
+        lrow[rt] = l;
       }
+      // ---- O^T = V^T P^T over 4 chunks of 32 keys: A = V^T[dim c][keys pi], B = P^T[keys pi][row c]
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-        // V^T[dim 16*dt + c][keys pi(q4, j)] read transposed from the row-major V block
-        const bf16x8 vb = frag_tr(sm.v, KS, 32 * kc + 4 * q4, 32 * kc + 16 + 4 * q4, 16 * dt, c);
+      for (int kc = 0; kc < 4; ++kc) {
+        bf16x8 ph[2], pm[2], pl[2];
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
-          f32x4 acc = kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : o[rt][dt];
-          acc = mfma(vb, pl[rt], acc);
-          acc = mfma(vb, pm[rt], acc);
-          o[rt][dt] = mfma(vb, ph[rt], acc);
+          uint32_t wh[4], wm[4], wl[4];
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            // elements j = 2*jj, 2*jj + 1 -> C tile 2*kc + j/4, entry j%4
+            const int j0 = 2 * jj, j1 = 2 * jj + 1;
+            split3_pk(s[rt][2 * kc + j0 / 4][j0 % 4], s[rt][2 * kc + j1 / 4][j1 % 4], wh[jj], wm[jj], wl[jj]);
+          }
+          ph[rt] = __builtin_bit_cast(bf16x8, make_uint4(wh[0], wh[1], wh[2], wh[3]));
+          pm[rt] = __builtin_bit_cast(bf16x8, make_uint4(wm[0], wm[1], wm[2], wm[3]));
+          pl[rt] = __builtin_bit_cast(bf16x8, make_uint4(wl[0], wl[1], wl[2], wl[3]));
+        }
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          // V^T[dim 16*dt + c][keys pi(q4, j)] read transposed from the row-major V block
+          const bf16x8 vb = frag_tr(sm.v, KS, 32 * kc + 4 * q4, 32 * kc + 16 + 4 * q4, 16 * dt, c);
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) {
+            f32x4 acc = kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : o[rt][dt];
+            acc = mfma(vb, pl[rt], acc);
+            acc = mfma(vb, pm[rt], acc);
+            o[rt][dt] = mfma(vb, ph[rt], acc);
+          }
         }
       }
-    }
+    };
+    if (full)
+      softmax_pv(std::true_type{});
+    else
+      softmax_pv(std::false_type{});
     // ---- store partials: o lane holds O[row 16*rt + c][dims 16*dt + 4*q4 + 0..3]
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
