@@ -1,7 +1,7 @@
 """The fused first two stages (``m3_index_score_topk``): scores, indices and score
 gradients equal, bit for bit, to ``m3_index_score`` followed by ``m3_topk``. Cases
 cover the MFMA score path (bf16) and the exact one (fp16 / fp32), rows of up to
-1100 blocks, varlen packs with empty sequences, forced local blocks, negative scale
+4500 blocks (above 4096 the selection streams each row from memory), varlen packs with empty sequences, forced local blocks, negative scale
 and exact ties from small-integer inputs."""
 
 from __future__ import annotations
@@ -24,6 +24,7 @@ pytestmark = pytest.mark.gpu
     ([400, 0, 90], 2, 64, 16, 5, 1, 1.0, torch.float16, False),
     ([300], 1, 40, 8, 6, 2, 1.0, torch.float32, True),
     ([129, 1], 2, 128, 128, 20, 1, 1.0, torch.bfloat16, False),   # K > blocks of the row
+    ([9000, 37], 1, 32, 2, 12, 1, 1.0, torch.bfloat16, False),    # 4500 blocks per row
 ])
 def test_fused_score_topk_equals_two_stages(lengths, groups, dim, block, topk, local, scale, dtype, integer, device):
     gen = torch.Generator().manual_seed(sum(lengths) + dim + topk)
