@@ -68,8 +68,15 @@ int64_t kv_chunk_tokens(int64_t T, int64_t Hq, int64_t K, int64_t record_bytes, 
 enum KvPass { kPassFwd = 0, kPassBwd = 1, kPassKl = 2 };
 int64_t kv_chunk_budget(KvPass pass, int64_t dflt);
 
-// Chunk-local record indices ((token - t0) * heads + head) * K + slot are int32: a
-// chunk may hold at most 2^31 - 1 records (with the default budgets it holds far fewer).
+// Chunk-local record index of (token t0 + tl, head, slot): ((tl * K + slot) * heads + head).
+// The heads of one (token, slot) are adjacent, so the rows of one CSR edge (the heads
+// of its group) write one contiguous run of records and of (m, l) pairs.
+__device__ __forceinline__ int64_t kv_record(int64_t tl, int head, int slot, int heads, int K) {
+  return (tl * K + slot) * heads + head;
+}
+
+// Chunk-local record indices are int32: a chunk may hold at most 2^31 - 1 records
+// (with the default budgets it holds far fewer).
 inline bool kv_chunk_records_fit(int64_t tc, int64_t heads, int64_t K) {
   return tc * heads * (K > 0 ? K : 1) < (int64_t(1) << 31);
 }

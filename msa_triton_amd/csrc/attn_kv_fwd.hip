@@ -52,7 +52,7 @@ struct FwdSmem {
   alignas(16) uint16_t v[128 * KS];
   int32_t th[kItemRows];   // (token - t0) * Hq + head (chunk-local)
   int32_t tok[kItemRows];  // query token
-  int32_t rec[kItemRows];  // partial record ((token - t0) * Hq + head) * K + slot
+  int32_t rec[kItemRows];  // partial record kv_record(token - t0, head, slot)
 };
 
 }  // namespace
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
       const int h = rg.g * R + (rho - eo * R);
       sm.th[rho] = (mtok[j] - t0) * Hq + h;  // < tc * Hq: chunk records fit in int32 (checked on the host)
       sm.tok[rho] = mtok[j];
-      sm.rec[rho] = ((mtok[j] - t0) * Hq + h) * K + mslot[j];
+      sm.rec[rho] = kv_record(mtok[j] - t0, h, mslot[j], Hq, K);
     }
   }
   __syncthreads();
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
   const int s = find_seq(cu, nseq, t);
   const int64_t qb = (t - cu[s]) / B;
   const int32_t* sel = indices + (t * G + g) * K;
-  const int64_t rec0 = ((t - t0) * Hq + h) * static_cast<int64_t>(K);
+  const int64_t rec0 = kv_record(t - t0, h, 0, Hq, K);  // slot j: rec0 + j * Hq
 
   // slot sub (and sub + 32, ...) of this row: validity and (m, l)
   float M = -__builtin_inff();
@@ -359,7 +359,7 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
     const int slot = s0 + sub;
     if (slot < K) {
       const int id = sel[slot];
-      if (id >= 0 && id <= qb) M = fmaxf(M, mlpart[rec0 + slot].x);
+      if (id >= 0 && id <= qb) M = fmaxf(M, mlpart[rec0 + slot * Hq].x);
     }
   }
 #pragma unroll
@@ -376,7 +376,7 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
       if (slot < K) {
         const int id = sel[slot];
         if (id >= 0 && id <= qb) {
-          const float2 ml = mlpart[rec0 + slot];
+          const float2 ml = mlpart[rec0 + slot * Hq];
           w = exp2(static_cast<double>(ml.x) - static_cast<double>(M));
           L = fma(w, static_cast<double>(ml.y), L);
         }
@@ -392,7 +392,7 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
 #pragma unroll
         for (int u = 0; u < kCombineBatch; ++u) {
           const int j = j0 + u < n ? j0 + u : n - 1;
-          const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(opart + (rec0 + s0 + j) * D + dcol));
+          const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(opart + (rec0 + static_cast<int64_t>(s0 + j) * Hq) * D + dcol));
           op[u] = make_float4(x[0], x[1], x[2], x[3]);
         }
 #pragma unroll
