@@ -13,7 +13,8 @@
 // XOR-swizzled by row, so the fragment reads stay bank-conflict free. Tiles are
 // issued heaviest first (the last rows of a sequence see the most blocks).
 // Squared key norms (for the error bound below) are computed once per key by a
-// pre-pass (score_key_norms) instead of per tile.
+// pre-pass (score_key_norms), and each key block's largest norm and safety once per
+// block by a second (score_block_norms), instead of per tile.
 //
 // Exactness (the public score must equal fl32(scale * exact winning dot) and
 // the winner set must be the exact one, index_score.py:121-136): with
@@ -21,7 +22,8 @@
 // every key whose approximate directed logit is below (max_approx - 2E) is
 // certainly beaten by the approximate winner. The running maximum and runner-up
 // are tracked on logits whose 7 low mantissa bits are replaced by the key's
-// position (16 kt + i; the quarter q4 is recovered after the cross-lane merge),
+// position (4 kt + i, an inline constant of the and-or; the quarter q4 is
+// recovered after the cross-lane merge and the key is 16 kt + 4 q4 + i),
 // which moves each by < 2^-16 of its magnitude: the test therefore also allows
 // 2^-15 max(|max|, |runner-up|) plus the smallest normal float. If exactly one key
 // survives, it is the unique exact winner and only its dot is evaluated in FP64: a lane
@@ -56,12 +58,14 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 constexpr int kTileRows = 128;  // 4 waves x 32 rows
 constexpr int kThreads = 256;
 
-// Workspace: squared key norms (fp32 per key), then the ambiguous-pair bitmap,
-// block-major: bit block * rows_pad + row of 32-bit words, rows_pad = rows rounded up
-// to a whole number of resolve chunks.
+// Workspace: squared key norms (fp32 per key), the key blocks' norms (fp32, at each
+// block's first key), then the ambiguous-pair bitmap, block-major: bit
+// block * rows_pad + row of 32-bit words, rows_pad = rows rounded up to a whole number
+// of resolve chunks.
 constexpr int kResolveRows = 8192;  // rows per resolve workgroup
 int64_t align256(int64_t x) { return (x + 255) & ~int64_t{255}; }
-int64_t ws_bitmap_offset(int64_t T) { return align256(4 * (T > 0 ? T : 1)); }
+int64_t ws_bnorm_offset(int64_t T) { return align256(4 * (T > 0 ? T : 1)); }
+int64_t ws_bitmap_offset(int64_t T) { return 2 * ws_bnorm_offset(T); }
 int64_t rows_padded(int64_t rows) { return (rows + kResolveRows - 1) / kResolveRows * kResolveRows; }
 int64_t bitmap_words(int64_t rows, int64_t NB) { return rows_padded(rows) / 32 * NB; }
 
@@ -99,6 +103,27 @@ __device__ __forceinline__ float max3(float a, float b, float c) {
   float r;
   asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
   return r;
+}
+
+__device__ __forceinline__ float min2(float a, float b) {
+  float r;
+  asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+
+// The value of this lane and that of lane ^ 32 (or ^ 16), in an order that depends on
+// the lane: v_permlane32_swap (v_permlane16_swap) of x with itself. For a symmetric
+// combination (max, min, a sum of two) the order does not matter.
+struct LanePair {
+  uint32_t a, b;
+};
+__device__ __forceinline__ LanePair pair_xor32(uint32_t x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+  return LanePair{r[0], r[1]};
+}
+__device__ __forceinline__ LanePair pair_xor16(uint32_t x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+  return LanePair{r[0], r[1]};
 }
 
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -180,6 +205,29 @@ __global__ __launch_bounds__(256) void score_key_norms(const uint16_t* __restric
   knorm2[j] = safe ? n2 * 1.0001f : -(n2 * 1.0001f) - 1.0f;  // unsafe: negative
 }
 
+// Per key block, stored at the block's first key: the largest key norm of the block,
+// sqrt(max |knorm2|), negated when a key of the block is not safe (or not a number).
+// An unsafe key's entry has magnitude >= 1, so a negated value is never zero.
+__global__ __launch_bounds__(256) void score_block_norms(const float* __restrict__ knorm2,
+                                                         const int32_t* __restrict__ cu, int nseq, int64_t T, int B,
+                                                         float* __restrict__ bnorm) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (t >= T) return;
+  const int s = find_seq(cu, nseq, t);
+  const int64_t start = cu[s], end = cu[s + 1];
+  if ((t - start) % B != 0) return;
+  const int64_t e = t + B < end ? t + B : end;
+  float m = 0.f;
+  bool safe = true;
+  for (int64_t j = t; j < e; ++j) {
+    const float v = knorm2[j];
+    m = fmaxf(m, fabsf(v));
+    safe = safe && v >= 0.f;
+  }
+  const float r = sqrtf(m);
+  bnorm[t] = safe ? r : -r;
+}
+
 // Two workgroups per CU; one for the widest partial-width variant (index dim 72..120),
 // whose register staging of the next block does not fit beside two.
 template <int NK, bool FULLD>
@@ -187,7 +235,7 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
                                                                      const uint16_t* __restrict__ ik,
                                                                      const int32_t* __restrict__ cu, int nseq,
                                                                      int64_t rows, int G, int Di, int NB, int B,
-                                                                     double scale, const float* __restrict__ knorm2,
+                                                                     double scale, const float* __restrict__ bnorm,
                                                                      uint32_t* __restrict__ amb, int64_t rows_pad,
                                                                      float* __restrict__ scores,
                                                                      int32_t* __restrict__ tie) {
@@ -320,23 +368,10 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
       }
     }
   };
-  // squared key norms of a block (lanes l and l + 64) and the block's max norm
-  auto norm_loads = [&](const BlockCursor& bc, float& n0, float& n1) {
-    n0 = n1 = 0.f;
-    if (bc.s >= nseq) return;
-    const int64_t kb = cu[bc.s] + static_cast<int64_t>(bc.b) * B;
-    const int64_t end = cu[bc.s + 1];
-    const int nk = static_cast<int>(end - kb < B ? end - kb : B);
-    if (lane < nk) n0 = knorm2[kb + lane];
-    if (lane + 64 < nk) n1 = knorm2[kb + lane + 64];
+  // the block's largest key norm, negated when a key of the block is not safe
+  auto block_norm = [&](const BlockCursor& bc) {
+    return bc.s < nseq ? bnorm[cu[bc.s] + static_cast<int64_t>(bc.b) * B] : 0.f;
   };
-  auto block_kmax = [&](float n0, float n1) {  // (an unsafe key's entry is -(n2 + 1))
-    float m = fmaxf(fabsf(n0), fabsf(n1));
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
-    return sqrtf(m);
-  };
-  auto block_safe = [&](float n0, float n1) { return __ballot(n0 < 0.f || n1 < 0.f) == 0; };
 
   // first (sequence, block) of the tile
   BlockCursor cur{nseq, 0, -1};
@@ -345,19 +380,17 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
     const int s0 = find_seq(cu, nseq, t_first);
     cur = BlockCursor{s0, 0, last_block_of(cu, s0, r0, nr, G, B)};
   }
-  float cn0, cn1;
-  norm_loads(cur, cn0, cn1);
+  const float cn = block_norm(cur);
   fetch(cur, 0);
   commit(0);
   __builtin_amdgcn_s_waitcnt(0);  // this thread's direct-to-LDS loads have landed
   __syncthreads();
-  float kmax = block_kmax(cn0, cn1);
-  bool bsafe = block_safe(cn0, cn1);
+  float kmax = fabsf(cn);
+  bool bsafe = cn >= 0.f;
   int buf = 0;
   while (cur.s < nseq) {
     const BlockCursor nxt = next_block(cu, nseq, cur, r0, nr, G, B);
-    float nn0, nn1;
-    norm_loads(nxt, nn0, nn1);
+    const float nn = block_norm(nxt);
     fetch(nxt, buf ^ 1);  // in flight while this block is evaluated (that buffer's readers passed the last barrier)
 
     const int64_t start = cu[cur.s], end = cu[cur.s + 1];
@@ -400,8 +433,8 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
               x = 16 * kt + 4 * q4 + i < lim[rt] ? x : kMaskedLogit;
               y = 16 * kt + 4 * q4 + i + 1 < lim[rt] ? y : kMaskedLogit;
             }
-            x = pack_key(x, 16 * kt + i);
-            y = pack_key(y, 16 * kt + i + 1);
+            x = pack_key(x, 4 * kt + i);
+            y = pack_key(y, 4 * kt + i + 1);
             const float t = __builtin_amdgcn_fmed3f(m1[rt], x, y);
             m2[rt] = __builtin_amdgcn_fmed3f(m2[rt], t, pinf);
             m1[rt] = max3(m1[rt], x, y);
@@ -423,17 +456,21 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
       for (int rt = 0; rt < 2; ++rt) {
         float a1 = m1[rt], a2 = m2[rt];
 #pragma unroll
-        for (int o = 16; o <= 32; o <<= 1) {
-          const float b1 = __shfl_xor(a1, o, kWave);
-          const float b2 = __shfl_xor(a2, o, kWave);
-          a2 = fmaxf(fmaxf(a2, b2), fminf(a1, b1));
-          a1 = fmaxf(a1, b1);
+        for (int o = 16; o <= 32; o <<= 1) {  // with the quarter of lane ^ o
+          const LanePair p1 = o == 16 ? pair_xor16(__float_as_uint(a1)) : pair_xor32(__float_as_uint(a1));
+          const LanePair p2 = o == 16 ? pair_xor16(__float_as_uint(a2)) : pair_xor32(__float_as_uint(a2));
+          const float u = __uint_as_float(p1.a), v = __uint_as_float(p1.b);
+          a2 = max3(__uint_as_float(p2.a), __uint_as_float(p2.b), min2(u, v));
+          a1 = max3(u, v, v);
         }
         // the quarter holding the maximum (unique whenever the row is certified)
         int wq = m1[rt] == a1 ? q4 : 4;
-        wq = min(wq, __shfl_xor(wq, 16, kWave));
-        wq = min(wq, __shfl_xor(wq, 32, kWave));
-        widx[rt] = static_cast<int>(__float_as_uint(a1) & 0x7fu) + 4 * wq;
+        const LanePair w16 = pair_xor16(static_cast<uint32_t>(wq));
+        wq = min(static_cast<int>(w16.a), static_cast<int>(w16.b));
+        const LanePair w32 = pair_xor32(static_cast<uint32_t>(wq));
+        wq = min(static_cast<int>(w32.a), static_cast<int>(w32.b));
+        const int pos = static_cast<int>(__float_as_uint(a1) & 0x7fu);  // 4 kt + i
+        widx[rt] = 16 * (pos >> 2) + 4 * wq + (pos & 3);
         const float bound = 2.f * cerr * mnorm[rt] * kmax + 0x1p-15f * fmaxf(fabsf(a1), fabsf(a2)) + 0x1p-126f;
         // 2: at least two candidates, or products not certainly exact in fp32
         wcnt[rt] = (a2 >= a1 - bound || !(bsafe && msafe[rt])) ? 2 : 1;
@@ -470,10 +507,15 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
           }
         }
       }
-      const double other = __shfl_xor(half, 32, kWave);
+      // the two halves of the row (lanes pr and pr + 32), summed
+      const uint64_t hbits = static_cast<uint64_t>(__double_as_longlong(half));
+      const LanePair hlo = pair_xor32(static_cast<uint32_t>(hbits));
+      const LanePair hhi = pair_xor32(static_cast<uint32_t>(hbits >> 32));
+      const double h0 = __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hhi.a) << 32) | hlo.a));
+      const double h1 = __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hhi.b) << 32) | hlo.b));
       if (row_ok && mycnt == 1 && hf == 0) {
         const int64_t out = (r0 + prow) * NB + cur.b;
-        scores[out] = static_cast<float>(ascale * (half + other));
+        scores[out] = static_cast<float>(ascale * (h0 + h1));
         if (tie) tie[out] = myidx + 1;
       }
       // ambiguous rows: marked for score_fwd_resolve
@@ -485,8 +527,8 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
     if (nxt.s < nseq) commit(buf ^ 1);  // that buffer's readers finished before the last barrier
     __builtin_amdgcn_s_waitcnt(0);       // the next block's direct-to-LDS loads have landed
     __syncthreads();  // this block's readers are done; the next block is visible
-    kmax = block_kmax(nn0, nn1);
-    bsafe = block_safe(nn0, nn1);
+    kmax = fabsf(nn);
+    bsafe = nn >= 0.f;
     buf ^= 1;
     cur = nxt;
   }
@@ -651,12 +693,14 @@ int score_fwd_mfma_launch(const void* iq, const void* ik, const int32_t* cu, int
   const int64_t T = rows / G;
   char* wsb = static_cast<char*>(ws);
   float* knorm2 = reinterpret_cast<float*>(wsb);
+  float* bnorm = reinterpret_cast<float*>(wsb + ws_bnorm_offset(T));
   auto* amb = reinterpret_cast<uint32_t*>(wsb + ws_bitmap_offset(T));
   const int64_t words = bitmap_words(rows, NB);
   const int64_t rows_pad = rows_padded(rows);
   hipLaunchKernelGGL(score_key_norms, dim3(grid_1d(T > words ? T : words, 256)), dim3(256), 0, st, k, T, Di,
                      knorm2, amb, words);
-#define MSA_SCORE_MFMA(NKV, FD) hipLaunchKernelGGL((score_fwd_mfma_kernel<NKV, FD>), grid, block, 0, st, q, k, cu, nseq, rows, G, Di, NB, B, scale, knorm2, amb, rows_pad, scores, tie)
+  hipLaunchKernelGGL(score_block_norms, dim3(grid_1d(T, 256)), dim3(256), 0, st, knorm2, cu, nseq, T, B, bnorm);
+#define MSA_SCORE_MFMA(NKV, FD) hipLaunchKernelGGL((score_fwd_mfma_kernel<NKV, FD>), grid, block, 0, st, q, k, cu, nseq, rows, G, Di, NB, B, scale, bnorm, amb, rows_pad, scores, tie)
   const int nk = Di <= 32 ? 1 : (Di <= 64 ? 2 : 4);
   const bool fd = Di == 32 * nk;
   if (nk == 1) { if (fd) MSA_SCORE_MFMA(1, true); else MSA_SCORE_MFMA(1, false); }
