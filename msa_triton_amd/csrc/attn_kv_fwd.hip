@@ -7,7 +7,8 @@
 // that selected the block, 128 (edge, head) rows per tile. Each (edge, head)
 // row yields a partial softmax over the block in base 2:
 //   m = max_j s_j, l = sum_j 2^(s_j - m), O = sum_j 2^(s_j - m) v_j   (fp32),
-// with s_j = fl(q.k_j * scale * log2(e)), stored per (token, head, slot). A
+// with s_j = fl(q.k_j * scale * log2(e)), stored per (token, slot, head): the heads
+// of one edge are adjacent, so an edge's rows write one contiguous run. A
 // combine kernel then merges the <= K partials of each (token, head) in slot
 // order in FP64:
 //   M = max m_s, L = sum 2^(m_s - M) l_s, out = sum 2^(m_s - M) O_s / L,
