@@ -17,8 +17,15 @@
 //     per-(edge) KL and d_iq partials (merged per row in slot order, kl_row_combine)
 //     and per-item d_ik partials (summed per key block in group and item order,
 //     kl_accumulate). No floating-point atomics: results are deterministic.
+#include <type_traits>
+
 #include "attn_kv_common.hpp"
 #include "msa_mi355x.h"
+
+// Each logit and exponent argument is rounded as written (no fused multiply-adds):
+// the statistics and main passes then form them identically, and the unmasked and
+// masked code paths of a tile give the same bits.
+#pragma clang fp contract(off)
 
 namespace msa {
 
@@ -119,6 +126,11 @@ __global__ __launch_bounds__(kKlThreads, 2) void kl_stats_kernel(
     const int slot = ok ? sm.slot[e] : 0;
     const int64_t vk = static_cast<int64_t>(tok) - rg.kb + 1;
     const int lim = ok ? (vk < rg.nk ? static_cast<int>(vk) : rg.nk) : 0;
+    // Wave-uniform: every edge of the wave sees all 128 keys (no masks), or not; the two
+    // cases are separate code paths so the unmasked one carries no per-logit selects.
+    const bool full = __ballot(lim < 128) == 0;
+    auto body = [&](auto full_tag) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full_tag)::value;
     float x[8][4];
     // ---- student: z^T = ik_block . iq^T
     {
@@ -132,7 +144,7 @@ __global__ __launch_bounds__(kKlThreads, 2) void kl_stats_kernel(
 #pragma unroll
         for (int kk = 0; kk < NKI; ++kk) a = mfma(load_frag(sm.ik + (16 * kt + c) * KSI + 32 * kk + 8 * q4), bq[kk], a);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[kt][i] = 16 * kt + 4 * q4 + i < lim ? a[i] * zs2 : -__builtin_inff();
+        for (int i = 0; i < 4; ++i) x[kt][i] = FULL || 16 * kt + 4 * q4 + i < lim ? a[i] * zs2 : -__builtin_inff();
       }
       const float2 ml = lane_max_sum(x);
       if (q4 == 0 && ok) spart[((static_cast<int64_t>(tok) - t0) * G + rg.g) * K + slot] = ml;
@@ -151,11 +163,16 @@ __global__ __launch_bounds__(kKlThreads, 2) void kl_stats_kernel(
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk) a = mfma(load_frag(sm.k + (16 * kt + c) * KS + 32 * kk + 8 * q4), bq[kk], a);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[kt][i] = 16 * kt + 4 * q4 + i < lim ? a[i] * as2 : -__builtin_inff();
+        for (int i = 0; i < 4; ++i) x[kt][i] = FULL || 16 * kt + 4 * q4 + i < lim ? a[i] * as2 : -__builtin_inff();
       }
       const float2 ml = lane_max_sum(x);
       if (q4 == 0 && ok) tpart[((static_cast<int64_t>(tok) - t0) * Hq + hq) * K + slot] = ml;
     }
+    };
+    if (full)
+      body(std::true_type{});
+    else
+      body(std::false_type{});
   }
 }
 
@@ -404,6 +421,13 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
     // visible keys of the lane's edges 4 q4 + i
     const int4 vis4 = *reinterpret_cast<const int4*>(&sm.vis[b][4 * q4]);
     const int vv[4] = {vis4.x, vis4.y, vis4.z, vis4.w};
+    // Wave-uniform: all 16 edges of the tile see all of the wave's keys (edges are in
+    // token order, so edge 0 sees the fewest), or not; separate code paths keep the
+    // per-element selects out of the unmasked one.
+    const bool full = 16 * t + 16 <= ne && sm.vis[b][0] >= key - c + 16;
+    float dz[4], klv[4];
+    auto teacher_student = [&](auto full_tag) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full_tag)::value;
     // ---- teacher: T[edge 4 q4 + i][key] = mean_h 2^(a_h * as2 - lse2_h) / mass_h
     float tsum[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -416,7 +440,7 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
         for (int i = 0; i < 4; ++i) {
           const float2 st = sm.tst[b][(4 * q4 + i) * R + h];
           const float p = __builtin_amdgcn_exp2f(a[i] * as2 - st.x) * st.y;
-          tsum[i] += key < vv[i] ? p : 0.f;
+          tsum[i] += FULL || key < vv[i] ? p : 0.f;
         }
       }
     }
@@ -424,11 +448,10 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
     f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < NKI; ++kk) z = mfma(load_frag(sm.iqs[b] + c * KSI + 32 * kk + 8 * q4), ikf[kk], z);
-    float dz[4], klv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float4 st = sm.sst[b][4 * q4 + i];
-      const bool vis = key < vv[i];
+      const bool vis = FULL || key < vv[i];
       const float y = z[i] * zs2 - st.x;  // log2 S - st.z
       const float S = vis ? __builtin_amdgcn_exp2f(y) * st.y : 0.f;
       const float T = vis ? tsum[i] * inv_r : 0.f;
@@ -436,6 +459,11 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
       // base-2 logs (v_log_f32); terms below 2^-100 are dropped
       klv[i] = T > 0x1p-100f ? T * (__builtin_amdgcn_logf(T) - (y + st.z)) : 0.f;
     }
+    };
+    if (full)
+      teacher_student(std::true_type{});
+    else
+      teacher_student(std::false_type{});
     // KL: sum over the wave's 16 keys (lanes c of the quad group), then over waves
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
