@@ -14,6 +14,8 @@ public API, then checks every stage at its stated bar:
     most 0.1 % outside the reference's gate, tests/test_triton_attention.py:58-97 --
     fp32 arithmetic leaves values within ~2^-22 of a bf16 rounding midpoint undecided,
     a few elements in 10^5 on these shapes); lse within 1e-4.
+Two smaller sweeps cover the VALU attention kernels (fp16 / fp32 inputs, head dims off
+the MFMA templates) and the indexer KL (eager/ops.py:153-180 restated in the oracle).
 The shapes are small enough for the oracle to finish in about a second each.
 """
 
@@ -107,3 +109,98 @@ def test_random_shape_pipeline_against_oracle(seed, device):
     out.backward(dout.to(device))
     for name, tensor, ref in (("dq", qd, r_dq), ("dk", kd, r_dk), ("dv", vd, r_dv)):
         check_bf16_stated(tensor.grad, ref, f"case {seed} {name}")
+
+
+def _check_dtype_stated(actual, expected, dtype, what):
+    """fp32: the reference gate (atol = rtol = 1e-4 after rounding the FP64 value to fp32).
+    fp16: every element within 1e-4 + 2^-10 |x| (one fp16 ulp) of the FP64 value and at
+    most 0.1 % (at least one) outside the gate -- the fp16 analogue of check_bf16_stated."""
+    if dtype == torch.float32:
+        torch.testing.assert_close(actual.detach().cpu(), rounded(expected, dtype), atol=1e-4, rtol=1e-4)
+        return
+    act = actual.detach().cpu().double().numpy().ravel()
+    exp = np.asarray(expected, dtype=np.float64).ravel()
+    ref_r = rounded(exp, dtype).double().numpy().ravel()
+    bad = int((np.abs(act - ref_r) > 1e-4 + 1e-4 * np.abs(ref_r)).sum())
+    err = np.abs(act - exp)
+    bound = 1e-4 + 2.0 ** -10 * np.abs(exp)
+    print(f"{what}: {bad} of {act.size} outside the gate; worst err/bound {float((err / bound).max()):.3f}", flush=True)
+    assert bad <= max(1, act.size // 1000), f"{what}: {bad} elements outside the gate"
+    assert np.all(err <= bound), f"{what}: error above 1e-4 + 2^-10 |x|"
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_shape_fp16_fp32_attention_against_oracle(seed, device):
+    """The VALU kernels (fp16 / fp32 inputs, any head dim) on random shapes and selections."""
+    from tests.helpers import random_selection
+
+    rng = np.random.default_rng(2000 + seed)
+    dtype = torch.float16 if seed % 2 else torch.float32
+    lengths = [int(rng.integers(1, 200)) for _ in range(int(rng.integers(1, 3)))]
+    groups, ratio = int(rng.integers(1, 3)), int(rng.choice([1, 2, 3, 5]))
+    dim = int(rng.choice([5, 12, 33, 80, 200]))
+    block = int(rng.choice([1, 4, 16, 64]))
+    topk, local = int(rng.integers(1, 5)), int(rng.integers(0, 2))
+    scale = None if seed % 3 else 0.2
+    print(f"case {seed}: {lengths} G={groups} R={ratio} D={dim} B={block} K={topk} L={local} {dtype}", flush=True)
+    total = sum(lengths)
+    g = torch.Generator().manual_seed(seed)
+    ids = random_selection(total, groups, topk, lengths, block, local, g)
+    q, k, v, dout = (torch.randn(total, h, dim, generator=g).to(dtype) for h in (groups * ratio, groups, groups,
+                                                                                groups * ratio))
+    cu_h = cu_list(lengths)
+    qd, kd, vd = (x.to(device).requires_grad_() for x in (q, k, v))
+    out, lse = msa.m3_sparse_attention(qd, kd, vd, ids.to(device), cu_tensor(lengths, device), max(lengths),
+                                       block_size=block, scale=scale, return_lse=True)
+    r_out, r_lse, r_dq, r_dk, r_dv = O.sparse_attention(np64(q), np64(k), np64(v), ids.numpy(), np.asarray(cu_h),
+                                                        block_size=block, scale=scale, dout=np64(dout))
+    assert out.dtype == dtype
+    _check_dtype_stated(out, r_out, dtype, f"case {seed} out")
+    finite = np.isfinite(r_lse)
+    assert np.array_equal(np.isfinite(lse.cpu().numpy()), finite)
+    np.testing.assert_allclose(lse.cpu().numpy()[finite], r_lse[finite], rtol=1e-4, atol=1e-4)
+    out.backward(dout.to(device))
+    for name, tensor, ref in (("dq", qd, r_dq), ("dk", kd, r_dk), ("dv", vd, r_dv)):
+        _check_dtype_stated(tensor.grad, ref, dtype, f"case {seed} {name}")
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_shape_indexer_kl_against_oracle(seed, device):
+    """m3_indexer_kl (bf16, dims 32 / 64 / 128, up to 8 heads per group) on random shapes:
+    loss and per-pair KL within 1e-6 + 1e-5 |x|, the fp32 gradients within
+    1e-5 max |x| + 1e-4 |x| of the FP64 oracle (the KL tests' stated tolerance)."""
+    from msa_triton_amd.indexer_kl import _launch
+    from msa_triton_amd.layout import sequence_meta
+    from tests.helpers import random_selection
+
+    rng = np.random.default_rng(3000 + seed)
+    lengths = [int(rng.choice([0, int(rng.integers(1, 400))], p=[0.1, 0.9])) for _ in range(int(rng.integers(1, 4)))]
+    if sum(lengths) == 0:
+        lengths[0] = 77
+    groups, ratio = int(rng.integers(1, 4)), int(rng.choice([1, 2, 3, 8]))
+    dim, dim_i = int(rng.choice([32, 64, 128])), int(rng.choice([32, 64, 128]))
+    block = int(rng.choice([4, 16, 64, 128]))
+    topk, local = int(rng.integers(1, 6)), int(rng.integers(0, 2))
+    index_scale = float(rng.choice([1.0, 0.5]))
+    scale = dim ** -0.5 if seed % 2 else 0.2
+    print(f"case {seed}: {lengths} G={groups} R={ratio} D={dim} Di={dim_i} B={block} K={topk} L={local}", flush=True)
+    total = sum(lengths)
+    g = torch.Generator().manual_seed(seed)
+    iq = torch.randn(total, groups, dim_i, generator=g).bfloat16()
+    ik = torch.randn(total, 1, dim_i, generator=g).bfloat16()
+    q = torch.randn(total, groups * ratio, dim, generator=g).bfloat16()
+    k = torch.randn(total, groups, dim, generator=g).bfloat16()
+    ids = random_selection(total, groups, topk, lengths, block, local, g)
+    cu = torch.tensor(cu_list(lengths), dtype=torch.int32)
+    ref = O.indexer_kl(*(x.double().numpy() for x in (iq, ik, q, k)), ids.numpy(), cu.numpy(), block_size=block,
+                       index_scale=index_scale, scale=scale)
+    meta = sequence_meta(cu.tolist(), block)
+    d = [x.to(device) for x in (iq, ik, q, k, ids, cu)]
+    loss, rows, d_iq, d_ik = _launch(*d[:6], meta, None, block, index_scale, scale, True, True, True)
+    assert float(loss) == pytest.approx(ref["loss"], rel=1e-5, abs=1e-6)
+    np.testing.assert_allclose(rows.cpu().double().numpy(), ref["row_kl"], rtol=1e-5, atol=1e-6)
+    for name, got, exp in (("d_iq", d_iq, ref["d_iq"]), ("d_ik", d_ik, ref["d_ik"])):
+        act = got.detach().cpu().double().numpy()
+        bound = 1e-5 * max(np.abs(exp).max(), 1e-30) + 1e-4 * np.abs(exp)
+        err = np.abs(act - exp)
+        assert np.all(err <= bound), f"{name}: max err/bound {float((err / bound).max()):.3f}"
