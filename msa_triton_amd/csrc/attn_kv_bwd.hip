@@ -42,6 +42,7 @@ constexpr int kStatThreads = 64 * kStatWaves;
 constexpr int kStatRowsPerTile = 16 * kStatRT * kStatWaves;  // (edge, head) rows per tile
 constexpr int kStatTilesPerItem = 512 / kStatRowsPerTile;
 constexpr int kStatItemRows = kStatRowsPerTile * kStatTilesPerItem;
+constexpr int kCenterRows = 2;  // rows per 32-lane segment of the centre pass (1: +7 %, 4: same as 2)
 constexpr int kMainEdges = 512;        // B2: CSR edges per work item
 constexpr int kMainThreads = 512;      // B2: 8 waves, 16 keys each (S, dP, dV, dK), 16 rows x 32 dims each (dQ)
 
@@ -90,44 +91,70 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 
 }  // namespace
 
-// O . dO per (token, head) in FP64 (exact products); 32 lanes per row.
+// O . dO per (token, head) in FP64 (exact products); 32 lanes per row, NR rows per
+// 32-lane segment.
 // Rows that take the statistics pass (all rows without o32; with o32 those the
 // forward marked peaked, slot 1 < 0): c = O . dO of the rounded output, the
 // center that pass refines. Other rows (flat, with o32, the forward's FP32
 // output): delta = O . dO itself, kept as c = float(delta) plus the residual
 // delta - c (slots 2 and 3).
+template <int NR>
 __global__ __launch_bounds__(256) void kv_bwd_center(const uint16_t* __restrict__ out, const float* __restrict__ o32,
                                                      const uint16_t* __restrict__ dout, int64_t rows_th, int D,
                                                      double* __restrict__ row_state) {
   const int sub = threadIdx.x & 31;
-  const int64_t th = static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
-  if (th >= rows_th) return;
-  const bool flat = o32 && row_state[th * 4 + 1] > 0.0;  // uniform over the row's 32 lanes
-  double acc = 0.0;
+  // NR consecutive rows per 32-lane segment, all of their loads in flight together
+  const int64_t th0 = (static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5)) * NR;
+  if (th0 >= rows_th) return;
+  double acc[NR];
+  bool flat[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int64_t th = th0 + r < rows_th ? th0 + r : rows_th - 1;
+    flat[r] = o32 && row_state[th * 4 + 1] > 0.0;  // uniform over the row's 32 lanes
+    acc[r] = 0.0;
+  }
   for (int d0 = 4 * sub; d0 < D; d0 += 128) {
-    const uint2 g = *reinterpret_cast<const uint2*>(dout + th * D + d0);
-    float o[4];
-    if (flat) {
-      const float4 x = *reinterpret_cast<const float4*>(o32 + th * D + d0);
-      o[0] = x.x, o[1] = x.y, o[2] = x.z, o[3] = x.w;
-    } else {
-      const uint2 x = *reinterpret_cast<const uint2*>(out + th * D + d0);
-      o[0] = bf16_lo(x.x), o[1] = bf16_hi(x.x), o[2] = bf16_lo(x.y), o[3] = bf16_hi(x.y);
+    uint2 g[NR];
+    float o[NR][4];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int64_t th = th0 + r < rows_th ? th0 + r : rows_th - 1;
+      g[r] = *reinterpret_cast<const uint2*>(dout + th * D + d0);
+      if (flat[r]) {
+        const float4 x = *reinterpret_cast<const float4*>(o32 + th * D + d0);
+        o[r][0] = x.x, o[r][1] = x.y, o[r][2] = x.z, o[r][3] = x.w;
+      } else {
+        const uint2 x = *reinterpret_cast<const uint2*>(out + th * D + d0);
+        o[r][0] = bf16_lo(x.x), o[r][1] = bf16_hi(x.x), o[r][2] = bf16_lo(x.y), o[r][3] = bf16_hi(x.y);
+      }
     }
-    acc = fma(static_cast<double>(o[0]), static_cast<double>(bf16_lo(g.x)), acc);
-    acc = fma(static_cast<double>(o[1]), static_cast<double>(bf16_hi(g.x)), acc);
-    acc = fma(static_cast<double>(o[2]), static_cast<double>(bf16_lo(g.y)), acc);
-    acc = fma(static_cast<double>(o[3]), static_cast<double>(bf16_hi(g.y)), acc);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      acc[r] = fma(static_cast<double>(o[r][0]), static_cast<double>(bf16_lo(g[r].x)), acc[r]);
+      acc[r] = fma(static_cast<double>(o[r][1]), static_cast<double>(bf16_hi(g[r].x)), acc[r]);
+      acc[r] = fma(static_cast<double>(o[r][2]), static_cast<double>(bf16_lo(g[r].y)), acc[r]);
+      acc[r] = fma(static_cast<double>(o[r][3]), static_cast<double>(bf16_hi(g[r].y)), acc[r]);
+    }
   }
 #pragma unroll
-  for (int o = 16; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 32);
+  for (int r = 0; r < NR; ++r) {
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) acc[r] += __shfl_xor(acc[r], o, 32);
+  }
   if (sub == 0) {
-    if (flat) {
-      const double c = static_cast<double>(static_cast<float>(acc));
-      row_state[th * 4 + 2] = c;
-      row_state[th * 4 + 3] = acc - c;
-    } else {
-      row_state[th * 4 + 2] = acc;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int64_t th = th0 + r;
+      if (th < rows_th) {
+        if (flat[r]) {
+          const double c = static_cast<double>(static_cast<float>(acc[r]));
+          row_state[th * 4 + 2] = c;
+          row_state[th * 4 + 3] = acc[r] - c;
+        } else {
+          row_state[th * 4 + 2] = acc[r];
+        }
+      }
     }
   }
 }
@@ -816,7 +843,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   const int rshift = (ratio & (ratio - 1)) == 0 ? __builtin_ctz(ratio) : -1;  // power-of-two ratios shift
   {
     ProfScope ps(kProfBwdCenter, st);
-    hipLaunchKernelGGL(kv_bwd_center, dim3(grid_1d(T * Hq, 8)), dim3(256), 0, st, ob, o32, gb, T * Hq, D, rs);
+    hipLaunchKernelGGL(kv_bwd_center<kCenterRows>, dim3(grid_1d(T * Hq, 8 * kCenterRows)), dim3(256), 0, st, ob, o32, gb, T * Hq, D, rs);
   }
   {
     ProfScope ps(kProfBwdPlan, st);
