@@ -338,51 +338,61 @@ __device__ __forceinline__ float4 main_row_record(double lse2, double mass, doub
 // 32 lanes per (token, head), slots lane-parallel then a fixed shuffle tree. Rows
 // outside the pass (flat rows, unless all_rows) keep the forward's mass. The mass
 // keeps the sign of the forward's mark, so a repeated backward selects the same rows.
-// Every row of the chunk then gets the main pass's fp32 record in rowf.
+// Every row of the chunk then gets the main pass's fp32 record in rowf. A 32-lane
+// segment owns rps consecutive rows (32 when only the forward's peaked rows take the
+// pass, 1 when all do): each lane settles its own row if it is outside the pass, then
+// the segment takes its rows in the pass one after the other.
 __global__ __launch_bounds__(256) void kv_bwd_stats_combine(const int32_t* __restrict__ indices,
                                                             const int32_t* __restrict__ cu, int nseq, int64_t t0,
                                                             int64_t t1, int Hq, int G, int K, int B, int all_rows,
-                                                            const float2* __restrict__ spart,
+                                                            int rps, const float2* __restrict__ spart,
                                                             double* __restrict__ row_state,
                                                             float4* __restrict__ rowf) {
   const int sub = threadIdx.x & 31;
-  const int64_t th = t0 * Hq + static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
-  if (th >= t1 * Hq) return;
-  const double mark = row_state[th * 4 + 1];
-  if (!all_rows && mark > 0.0) {  // uniform over the row's 32 lanes
-    if (sub == 0) {
-      const double4 rs = *reinterpret_cast<const double4*>(row_state + th * 4);
-      rowf[th] = main_row_record(rs.x, rs.y, rs.z, rs.w);
-    }
-    return;
+  const int64_t base = t0 * Hq + (static_cast<int64_t>(blockIdx.x) * 8 + (threadIdx.x >> 5)) * rps;
+  const int64_t end = t1 * Hq;
+  bool in_pass = false;
+  if (sub < rps && base + sub < end) {
+    const int64_t th = base + sub;
+    const double4 rs = *reinterpret_cast<const double4*>(row_state + th * 4);
+    in_pass = all_rows || !(rs.y > 0.0);
+    if (!in_pass) rowf[th] = main_row_record(rs.x, rs.y, rs.z, rs.w);
   }
-  const int64_t t = th / Hq;
-  const int h = static_cast<int>(th % Hq);
-  const int g = h / (Hq / G);
-  const int s = find_seq(cu, nseq, t);
-  const int64_t qb = (t - cu[s]) / B;
-  const int32_t* sel = indices + (t * G + g) * K;
-  const int64_t rec0 = ((t - t0) * Hq + h) * static_cast<int64_t>(K);
-  double a = 0.0, b = 0.0;
-  for (int slot = sub; slot < K; slot += 32) {
-    const int id = sel[slot];
-    if (id >= 0 && id <= qb) {
-      const float2 ab = spart[rec0 + slot];
-      a += static_cast<double>(ab.x);
-      b += static_cast<double>(ab.y);
+  // this segment's rows in the pass (bits of its half of the wave)
+  uint32_t todo = static_cast<uint32_t>(__ballot(in_pass) >> (threadIdx.x & 32));
+  while (todo) {
+    const int j = __builtin_ctz(todo);
+    todo &= todo - 1;
+    const int64_t th = base + j;
+    const double mark = row_state[th * 4 + 1];
+    const int64_t t = th / Hq;
+    const int h = static_cast<int>(th % Hq);
+    const int g = h / (Hq / G);
+    const int s = find_seq(cu, nseq, t);
+    const int64_t qb = (t - cu[s]) / B;
+    const int32_t* sel = indices + (t * G + g) * K;
+    const int64_t rec0 = ((t - t0) * Hq + h) * static_cast<int64_t>(K);
+    double a = 0.0, b = 0.0;
+    for (int slot = sub; slot < K; slot += 32) {
+      const int id = sel[slot];
+      if (id >= 0 && id <= qb) {
+        const float2 ab = spart[rec0 + slot];
+        a += static_cast<double>(ab.x);
+        b += static_cast<double>(ab.y);
+      }
     }
-  }
 #pragma unroll
-  for (int o = 16; o > 0; o >>= 1) {
-    a += __shfl_xor(a, o, 32);
-    b += __shfl_xor(b, o, 32);
-  }
-  if (sub == 0) {
-    const bool has = a > 0.0;
-    const double mass = copysign(has ? a : 1.0, mark), delta = has ? b / a : 0.0;
-    row_state[th * 4 + 1] = mass;
-    row_state[th * 4 + 3] = delta;
-    rowf[th] = main_row_record(row_state[th * 4], mass, row_state[th * 4 + 2], delta);
+    for (int o = 16; o > 0; o >>= 1) {
+      a += __shfl_xor(a, o, 32);
+      b += __shfl_xor(b, o, 32);
+    }
+    if (sub == 0) {
+      const bool has = a > 0.0;
+      const double mass = copysign(has ? a : 1.0, mark), delta = has ? b / a : 0.0;
+      row_state[th * 4 + 1] = mass;
+      row_state[th * 4 + 3] = delta;
+      rowf[th] = main_row_record(row_state[th * 4], mass, row_state[th * 4 + 2], delta);
+    }
   }
 }
 
@@ -870,8 +880,9 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
     }
     {
       ProfScope ps(kProfBwdStatsCombine, st);
-      hipLaunchKernelGGL(kv_bwd_stats_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu,
-                         nseq, t0, t1, Hq, G, K, B, all_rows, spart, rs, rowf);
+      const int rps = all_rows ? 1 : 32;  // rows per 32-lane segment
+      hipLaunchKernelGGL(kv_bwd_stats_combine, dim3(grid_1d((t1 - t0) * Hq, 8 * rps)), dim3(256), 0, st, indices, cu,
+                         nseq, t0, t1, Hq, G, K, B, all_rows, rps, spart, rs, rowf);
     }
     if (rows > 0) {
       const int32_t* hi = kv_plan_hi(mp, mbase, c);
