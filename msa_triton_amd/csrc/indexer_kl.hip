@@ -578,13 +578,26 @@ __global__ __launch_bounds__(256) void kl_row_combine(const int32_t* __restrict_
     if (row_kl) row_kl[t * G + g] = static_cast<float>(kl * kLn2);
   }
   if (diq && 4 * sub < Di) {
+    // slots 8 at a time, all of their loads issued first (every slot's record is in
+    // bounds; invalid slots are masked, never added)
+    constexpr int kBatch = 8;
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int slot = 0; slot < K; ++slot) {
-      const int id = sel[slot];
-      if (id >= 0 && id <= qb) {
-        const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(diqpart + (rec0 + slot) * Di + 4 * sub));
+    for (int s0 = 0; s0 < K; s0 += kBatch) {
+      f32x4 x[kBatch];
+      bool ok[kBatch];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] += static_cast<double>(x[i]);
+      for (int u = 0; u < kBatch; ++u) {
+        const int slot = s0 + u < K ? s0 + u : K - 1;
+        const int id = sel[slot];
+        ok[u] = s0 + u < K && id >= 0 && id <= qb;
+        x[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(diqpart + (rec0 + slot) * Di + 4 * sub));
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (ok[u]) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[i] += static_cast<double>(x[u][i]);
+        }
       }
     }
     *reinterpret_cast<float4*>(diq + (t * G + g) * Di + 4 * sub) =
