@@ -168,12 +168,12 @@ __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx, const int32_t* __restrict__ sidx,
-    const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items, const int2* __restrict__ items, int nseq,
+    const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items, const int2* __restrict__ items, const int32_t* __restrict__ order, int nseq,
     int Hq, int G, int D, int K, int B, float scale2, int epi, int t0, int all_rows, float2* __restrict__ spart) {
   constexpr int DP = 32 * NK, KS = StatSmem<NK>::KS;
   __shared__ StatSmem<NK> sm;
-  const int item = blockIdx.x;
-  if (item >= *n_items) return;
+  if (static_cast<int>(blockIdx.x) >= *n_items) return;
+  const int item = order[blockIdx.x];  // largest items first
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
   const int2 it = items[item];
   const int row = it.x, e_begin = it.y;
@@ -415,16 +415,17 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx, const int32_t* __restrict__ sidx,
-    const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items, const int2* __restrict__ items, int nseq,
-    int Hq, int G, int D, int K, int B, float scale2, int epi, int t0, uint32_t rmagic, int rshift,
-    const float4* __restrict__ rowf, float* __restrict__ dqpart, float* __restrict__ kvpart) {
+    const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items, const int2* __restrict__ items,
+    const int32_t* __restrict__ order, int nseq, int Hq, int G, int D, int K, int B, float scale2, int epi, int t0,
+    uint32_t rmagic, int rshift, const float4* __restrict__ rowf, float* __restrict__ dqpart,
+    float* __restrict__ kvpart) {
   constexpr int DP = 32 * NK, NDT = DP / 16, KS = MainSmem<NK>::KS;
   constexpr int RV = DP / 8;             // 16-byte chunks per row
   constexpr int CPT = RV >= 8 ? RV / 8 : 1;  // chunks per staging thread (threads 0-255: Q, 256-511: dO)
   constexpr int TPR = RV / CPT;          // staging threads per row
   __shared__ MainSmem<NK> sm;
-  const int item = blockIdx.x;
-  if (item >= *n_items) return;
+  if (static_cast<int>(blockIdx.x) >= *n_items) return;
+  const int item = order[blockIdx.x];  // largest items first
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
   const int2 it = items[item];
   const int row = it.x, e_begin = it.y;
@@ -870,9 +871,10 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       const int32_t* hi = kv_plan_hi(sp, sbase, c);
       const int32_t* nit = kv_plan_count(sp, sbase, c);
       const int2* its = kv_plan_items(sp, sbase, c);
+      const int32_t* ord = kv_plan_order(sp, sbase, c);
       const int sepi = static_cast<int>(sp.epi);
       const dim3 grid(static_cast<unsigned>(sp.max_items)), block(kStatThreads);
-#define MSA_BWD_STATS(NKV, FD) hipLaunchKernelGGL((kv_bwd_stats_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, sepi, it0, all_rows, spart)
+#define MSA_BWD_STATS(NKV, FD) hipLaunchKernelGGL((kv_bwd_stats_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, sepi, it0, all_rows, spart)
       if (nk == 1) { if (fd) MSA_BWD_STATS(1, true); else MSA_BWD_STATS(1, false); }
       else if (nk == 2) { if (fd) MSA_BWD_STATS(2, true); else MSA_BWD_STATS(2, false); }
       else { if (fd) MSA_BWD_STATS(4, true); else MSA_BWD_STATS(4, false); }
@@ -888,11 +890,12 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       const int32_t* hi = kv_plan_hi(mp, mbase, c);
       const int32_t* nit = kv_plan_count(mp, mbase, c);
       const int2* its = kv_plan_items(mp, mbase, c);
+      const int32_t* ord = kv_plan_order(mp, mbase, c);
       const int mepi = static_cast<int>(mp.epi);
       const dim3 grid(static_cast<unsigned>(mp.max_items)), block(kMainThreads);
       {
         ProfScope ps(kProfBwdMain, st);
-#define MSA_BWD_MAIN(NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, rshift, rowf, dqpart, kvpart)
+#define MSA_BWD_MAIN(NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, rshift, rowf, dqpart, kvpart)
         if (nk == 1) { if (fd) MSA_BWD_MAIN(1, true); else MSA_BWD_MAIN(1, false); }
         else if (nk == 2) { if (fd) MSA_BWD_MAIN(2, true); else MSA_BWD_MAIN(2, false); }
         else { if (fd) MSA_BWD_MAIN(4, true); else MSA_BWD_MAIN(4, false); }

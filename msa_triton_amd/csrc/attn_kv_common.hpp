@@ -89,14 +89,15 @@ inline bool kv_csr_fits(int64_t T, int64_t G, int64_t K, int64_t rows) {
 }
 
 struct KvPlan {
-  int64_t rows, tc, nch, epi, max_items;  // max_items: per-chunk upper bound on work items
-  int64_t bounds, starts, items, bytes;   // byte offsets of the arrays inside the plan area, total size
+  int64_t rows, tc, nch, epi, max_items;         // max_items: per-chunk upper bound on work items
+  int64_t bounds, starts, items, order, bytes;  // byte offsets of the arrays inside the plan area, total size
 };
 
 KvPlan kv_plan_layout(int64_t T, int64_t rows, int64_t G, int64_t K, int64_t tc, int64_t epi);
 
-// Fills bounds[(nch + 1) x rows], starts[nch x (rows + 1)] and items[nch x max_items]
-// (int2: row, first edge) in the plan area at `base`.
+// Fills bounds[(nch + 1) x rows], starts[nch x (rows + 1)], items[nch x max_items]
+// (int2: row, first edge) and order[nch x max_items] (per chunk, the item indices
+// largest first: the dispatch order of the KV-major kernels) in the plan area at `base`.
 void kv_plan_launch(const KvPlan& p, const int32_t* row_ptr, const int32_t* qidx, int64_t T, void* base,
                     hipStream_t st);
 
@@ -115,6 +116,9 @@ inline const int32_t* kv_plan_starts(const KvPlan& p, const void* base, int64_t 
 }
 inline const int2* kv_plan_items(const KvPlan& p, const void* base, int64_t c) {
   return reinterpret_cast<const int2*>(static_cast<const char*>(base) + p.items) + c * p.max_items;
+}
+inline const int32_t* kv_plan_order(const KvPlan& p, const void* base, int64_t c) {
+  return reinterpret_cast<const int32_t*>(static_cast<const char*>(base) + p.order) + c * p.max_items;
 }
 
 }  // namespace msa

@@ -128,17 +128,70 @@ __global__ __launch_bounds__(1024) void kv_item_scan(const int32_t* __restrict__
   if (threadIdx.x == 0) out[rows] = carry_s;
 }
 
+// For chunk blockIdx.x: order[slot] = the chunk's work items by decreasing edge count
+// (a counting sort on epi - edges, clamped to kOrderBuckets - 1). Launched in this
+// order, the short items (row tails) are the last to start, so the workgroups of a
+// launch finish closer together. Items of equal size take their slots in no fixed
+// order (integer atomics); no result depends on it, as each item writes only its own
+// outputs, indexed by item.
+constexpr int kOrderBuckets = 1024;
+__global__ __launch_bounds__(1024) void kv_item_order(const int32_t* __restrict__ bounds, int64_t rows, int epi,
+                                                       int64_t max_items, const int32_t* __restrict__ item_start,
+                                                       const int2* __restrict__ items, int32_t* __restrict__ order) {
+  __shared__ int32_t cnt[kOrderBuckets];
+  __shared__ int32_t wsum[16];
+  const int64_t c = blockIdx.x;
+  const int32_t* hi_b = bounds + (c + 1) * rows;
+  const int2* its = items + c * max_items;
+  int32_t* out = order + c * max_items;
+  const int32_t n = item_start[c * (rows + 1) + rows];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  auto bucket = [&](int32_t i) {
+    const int2 it = its[i];
+    const int32_t left = hi_b[it.x] - it.y;  // edges from the item's first to the row's end
+    const int32_t b = epi - (left < epi ? left : epi);
+    return b < kOrderBuckets ? b : kOrderBuckets - 1;
+  };
+  cnt[tid] = 0;
+  __syncthreads();
+  for (int32_t i = tid; i < n; i += 1024) atomicAdd(&cnt[bucket(i)], 1);
+  __syncthreads();
+  // exclusive prefix over the buckets (thread tid owns bucket tid)
+  const int32_t own = cnt[tid];
+  int32_t x = own;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int32_t y = __shfl_up(x, o, kWave);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[wid] = x;
+  __syncthreads();
+  if (tid < 16) {
+    int32_t w = wsum[tid];
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      const int32_t y = __shfl_up(w, o, 16);
+      if (tid >= o) w += y;
+    }
+    wsum[tid] = w;
+  }
+  __syncthreads();
+  cnt[tid] = (wid > 0 ? wsum[wid - 1] : 0) + x - own;
+  __syncthreads();
+  for (int32_t i = tid; i < n; i += 1024) out[atomicAdd(&cnt[bucket(i)], 1)] = i;
+}
+
 template <int NK, bool FULLD>
 __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx,
     const int32_t* __restrict__ sidx, const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items,
-    const int2* __restrict__ items, int nseq, int Hq, int G, int D, int K, int B, float scale2, int epi, int t0,
+    const int2* __restrict__ items, const int32_t* __restrict__ order, int nseq, int Hq, int G, int D, int K, int B, float scale2, int epi, int t0,
     float* __restrict__ opart, float2* __restrict__ mlpart) {
   constexpr int DP = 32 * NK, NDT = DP / 16, KS = FwdSmem<NK>::KS;
   __shared__ FwdSmem<NK> sm;
-  const int item = blockIdx.x;
-  if (item >= *n_items) return;
+  if (static_cast<int>(blockIdx.x) >= *n_items) return;
+  const int item = order[blockIdx.x];  // largest items first
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
   const int2 it = items[item];
   const int row = it.x, e_begin = it.y;
@@ -488,7 +541,8 @@ KvPlan kv_plan_layout(int64_t T, int64_t rows, int64_t G, int64_t K, int64_t tc,
   p.bounds = 0;
   p.starts = align256((p.nch + 1) * rows * 4);
   p.items = p.starts + align256(p.nch * (rows + 1) * 4);
-  p.bytes = p.items + align256(p.nch * p.max_items * 8);
+  p.order = p.items + align256(p.nch * p.max_items * 8);
+  p.bytes = p.order + align256(p.nch * p.max_items * 4);
   return p;
 }
 
@@ -502,6 +556,9 @@ void kv_plan_launch(const KvPlan& p, const int32_t* row_ptr, const int32_t* qidx
   hipLaunchKernelGGL(kv_item_scan, dim3(static_cast<unsigned>(p.nch)), dim3(1024), 0, st, bounds, p.rows,
                      static_cast<int>(p.epi), p.max_items, reinterpret_cast<int32_t*>(b + p.starts),
                      reinterpret_cast<int2*>(b + p.items));
+  hipLaunchKernelGGL(kv_item_order, dim3(static_cast<unsigned>(p.nch)), dim3(1024), 0, st, bounds, p.rows,
+                     static_cast<int>(p.epi), p.max_items, reinterpret_cast<const int32_t*>(b + p.starts),
+                     reinterpret_cast<const int2*>(b + p.items), reinterpret_cast<int32_t*>(b + p.order));
 }
 
 struct FwdLayout {
@@ -554,8 +611,9 @@ int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indi
       const int32_t* hi = kv_plan_hi(pl, base, c);
       const int32_t* nit = kv_plan_count(pl, base, c);
       const int2* its = kv_plan_items(pl, base, c);
+      const int32_t* ord = kv_plan_order(pl, base, c);
       const int it0 = static_cast<int>(t0);
-#define MSA_FWD_PARTIAL(NKV, FD) hipLaunchKernelGGL((attn_fwd_partial_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, hi, nit, its, nseq, Hq, G, D, K, B, scale2, epi, it0, opart, ml)
+#define MSA_FWD_PARTIAL(NKV, FD) hipLaunchKernelGGL((attn_fwd_partial_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, epi, it0, opart, ml)
       const int nk = nk_of_dim(D);
       const bool fd = D == 32 * nk;
       if (nk == 1) { if (fd) MSA_FWD_PARTIAL(1, true); else MSA_FWD_PARTIAL(1, false); }

@@ -83,13 +83,13 @@ __global__ __launch_bounds__(kKlThreads, 2) void kl_stats_kernel(
     const uint16_t* __restrict__ iq, const uint16_t* __restrict__ ik, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ k, const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks,
     const int32_t* __restrict__ qidx, const int32_t* __restrict__ sidx, const int32_t* __restrict__ e_hi,
-    const int32_t* __restrict__ n_items, const int2* __restrict__ items, int nseq, int Hq, int G, int K, int B,
+    const int32_t* __restrict__ n_items, const int2* __restrict__ items, const int32_t* __restrict__ order, int nseq, int Hq, int G, int K, int B,
     float zs2, float as2, int epi, int t0, int teacher, float2* __restrict__ tpart, float2* __restrict__ spart) {
   constexpr int D = 32 * NK, Di = 32 * NKI;
   constexpr int KS = KlStatSmem<NK, NKI>::KS, KSI = KlStatSmem<NK, NKI>::KSI;
   __shared__ KlStatSmem<NK, NKI> sm;
-  const int item = blockIdx.x;
-  if (item >= *n_items) return;
+  if (static_cast<int>(blockIdx.x) >= *n_items) return;
+  const int item = order[blockIdx.x];  // largest items first
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
   const int2 it = items[item];
   const int row = it.x, e_begin = it.y;
@@ -282,7 +282,7 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
     const uint16_t* __restrict__ k, const float4* __restrict__ tstate, const float4* __restrict__ sstate,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx,
     const int32_t* __restrict__ sidx, const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items,
-    const int2* __restrict__ items, int nseq, int Hq, int G, int K, int B, float zs2, float as2, int epi, int t0,
+    const int2* __restrict__ items, const int32_t* __restrict__ order, int nseq, int Hq, int G, int K, int B, float zs2, float as2, int epi, int t0,
     int need_diq, int need_dik, float* __restrict__ klpart, float* __restrict__ diqpart,
     float* __restrict__ ikpart) {
   constexpr int D = 32 * NK, Di = 32 * NKI, NDTI = Di / 16;
@@ -290,8 +290,8 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
   constexpr int QV = D / 8, IV = Di / 8;                               // 16-byte chunks per row
   constexpr int QI = (16 * kKlMaxRatio * QV + kKlThreads - 1) / kKlThreads;  // q chunks per staging thread
   __shared__ KlMainSmem<NK, NKI> sm;
-  const int item = blockIdx.x;
-  if (item >= *n_items) return;
+  if (static_cast<int>(blockIdx.x) >= *n_items) return;
+  const int item = order[blockIdx.x];  // largest items first
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
   const int2 it = items[item];
   const int row = it.x, e_begin = it.y;
@@ -772,10 +772,11 @@ extern "C" int msa_indexer_kl(const void* index_q, const void* index_k, const vo
     const int32_t* hi = kv_plan_hi(pl, base, ch);
     const int32_t* nit = kv_plan_count(pl, base, ch);
     const int2* its = kv_plan_items(pl, base, ch);
+    const int32_t* ord = kv_plan_order(pl, base, ch);
     const int epi = static_cast<int>(pl.epi);
     const dim3 grid(static_cast<unsigned>(pl.max_items > 0 ? pl.max_items : 1)), block(kKlThreads);
     if (rows > 0 && pl.max_items > 0) {
-#define MSA_KL_STATS(A, C) hipLaunchKernelGGL((kl_stats_kernel<A, C>), grid, block, 0, st, iqb, ikb, qb, kb, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, teacher_lse ? 0 : 1, tpart, spart)
+#define MSA_KL_STATS(A, C) hipLaunchKernelGGL((kl_stats_kernel<A, C>), grid, block, 0, st, iqb, ikb, qb, kb, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, ord, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, teacher_lse ? 0 : 1, tpart, spart)
 #define MSA_KL_DISPATCH(M)                                   \
   if (nk == 1) { if (nki == 1) M(1, 1); else if (nki == 2) M(1, 2); else M(1, 4); } \
   else if (nk == 2) { if (nki == 1) M(2, 1); else if (nki == 2) M(2, 2); else M(2, 4); } \
@@ -786,7 +787,7 @@ extern "C" int msa_indexer_kl(const void* index_q, const void* index_k, const vo
     hipLaunchKernelGGL(kl_stats_combine, dim3(grid_1d((t1 - t0) * (Hq + G), 16)), dim3(256), 0, st, indices,
                        cu_seqlens, nseq, t0, t1, iHq, iG, iK, iB, tpart, spart, teacher_lse, tstate, sstate);
     if (rows > 0 && pl.max_items > 0) {
-#define MSA_KL_MAIN(A, C) hipLaunchKernelGGL((kl_main_kernel<A, C>), grid, block, 0, st, iqb, ikb, qb, kb, tstate, sstate, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, need_diq, need_dik, klpart, diqpart, ikpart)
+#define MSA_KL_MAIN(A, C) hipLaunchKernelGGL((kl_main_kernel<A, C>), grid, block, 0, st, iqb, ikb, qb, kb, tstate, sstate, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, ord, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, need_diq, need_dik, klpart, diqpart, ikpart)
       MSA_KL_DISPATCH(MSA_KL_MAIN)
 #undef MSA_KL_MAIN
 #undef MSA_KL_DISPATCH
