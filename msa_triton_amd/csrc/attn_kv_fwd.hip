@@ -152,9 +152,17 @@ __global__ __launch_bounds__(1024) void kv_item_order(const int32_t* __restrict_
     const int32_t b = epi - (left < epi ? left : epi);
     return b < kOrderBuckets ? b : kOrderBuckets - 1;
   };
+  // Most items are full (bucket 0): those take one LDS atomic per wave, ranked by ballot.
   cnt[tid] = 0;
   __syncthreads();
-  for (int32_t i = tid; i < n; i += 1024) atomicAdd(&cnt[bucket(i)], 1);
+  for (int32_t i0 = 0; i0 < n; i0 += 1024) {  // whole waves iterate together (ballots)
+    const int32_t i = i0 + tid;
+    const int32_t b = i < n ? bucket(i) : -1;
+    const uint64_t full = __ballot(b == 0);
+    if (full != 0 && lane == static_cast<int>(__ffsll(static_cast<long long>(full)) - 1))
+      atomicAdd(&cnt[0], __popcll(full));
+    if (b > 0) atomicAdd(&cnt[b], 1);
+  }
   __syncthreads();
   // exclusive prefix over the buckets (thread tid owns bucket tid)
   const int32_t own = cnt[tid];
@@ -178,7 +186,17 @@ __global__ __launch_bounds__(1024) void kv_item_order(const int32_t* __restrict_
   __syncthreads();
   cnt[tid] = (wid > 0 ? wsum[wid - 1] : 0) + x - own;
   __syncthreads();
-  for (int32_t i = tid; i < n; i += 1024) out[atomicAdd(&cnt[bucket(i)], 1)] = i;
+  for (int32_t i0 = 0; i0 < n; i0 += 1024) {
+    const int32_t i = i0 + tid;
+    const int32_t b = i < n ? bucket(i) : -1;
+    const uint64_t full = __ballot(b == 0);
+    const int lead = full != 0 ? static_cast<int>(__ffsll(static_cast<long long>(full))) - 1 : 0;
+    int32_t base = 0;
+    if (full != 0 && lane == lead) base = atomicAdd(&cnt[0], __popcll(full));
+    base = __shfl(base, lead, kWave);
+    if (b == 0) out[base + __popcll(full & ((uint64_t(1) << lane) - 1))] = i;
+    else if (b > 0) out[atomicAdd(&cnt[b], 1)] = i;
+  }
 }
 
 template <int NK, bool FULLD>
