@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
   constexpr int DP = 32 * NK, KS = StatSmem<NK>::KS;
   __shared__ StatSmem<NK> sm;
   if (static_cast<int>(blockIdx.x) >= *n_items) return;
-  const int item = order[blockIdx.x];  // largest items first
+  const int item = order ? order[blockIdx.x] : static_cast<int>(blockIdx.x);  // no order: row order
   const int tid = threadIdx.x, wid = tid >> 6, lane = tid & 63, c = lane & 15, q4 = lane >> 4;
   const int2 it = items[item];
   const int row = it.x, e_begin = it.y;
@@ -858,7 +858,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   }
   {
     ProfScope ps(kProfBwdPlan, st);
-    kv_plan_launch(L.stat_plan, row_ptr, qidx, T, sbase, st);
+    kv_plan_launch(L.stat_plan, row_ptr, qidx, T, sbase, st, false);  // row order measured faster here
     kv_plan_launch(L.main_plan, row_ptr, qidx, T, mbase, st);
   }
   const KvPlan& sp = L.stat_plan;
@@ -871,7 +871,7 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       const int32_t* hi = kv_plan_hi(sp, sbase, c);
       const int32_t* nit = kv_plan_count(sp, sbase, c);
       const int2* its = kv_plan_items(sp, sbase, c);
-      const int32_t* ord = kv_plan_order(sp, sbase, c);
+      const int32_t* ord = nullptr;
       const int sepi = static_cast<int>(sp.epi);
       const dim3 grid(static_cast<unsigned>(sp.max_items)), block(kStatThreads);
 #define MSA_BWD_STATS(NKV, FD) hipLaunchKernelGGL((kv_bwd_stats_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, sepi, it0, all_rows, spart)

@@ -95,11 +95,12 @@ struct KvPlan {
 
 KvPlan kv_plan_layout(int64_t T, int64_t rows, int64_t G, int64_t K, int64_t tc, int64_t epi);
 
-// Fills bounds[(nch + 1) x rows], starts[nch x (rows + 1)], items[nch x max_items]
-// (int2: row, first edge) and order[nch x max_items] (per chunk, the item indices
-// largest first: the dispatch order of the KV-major kernels) in the plan area at `base`.
+// Fills bounds[(nch + 1) x rows], starts[nch x (rows + 1)] and items[nch x max_items]
+// (int2: row, first edge) in the plan area at `base`, and with `ordered` also
+// order[nch x max_items] (per chunk, the item indices largest first: the dispatch order
+// of the KV-major kernels; a kernel given no order takes the items in row order).
 void kv_plan_launch(const KvPlan& p, const int32_t* row_ptr, const int32_t* qidx, int64_t T, void* base,
-                    hipStream_t st);
+                    hipStream_t st, bool ordered = true);
 
 // Per chunk views of a launched plan.
 inline const int32_t* kv_plan_hi(const KvPlan& p, const void* base, int64_t c) {

@@ -565,7 +565,7 @@ KvPlan kv_plan_layout(int64_t T, int64_t rows, int64_t G, int64_t K, int64_t tc,
 }
 
 void kv_plan_launch(const KvPlan& p, const int32_t* row_ptr, const int32_t* qidx, int64_t T, void* base,
-                    hipStream_t st) {
+                    hipStream_t st, bool ordered) {
   if (p.rows <= 0) return;
   char* b = static_cast<char*>(base);
   int32_t* bounds = reinterpret_cast<int32_t*>(b + p.bounds);
@@ -574,9 +574,10 @@ void kv_plan_launch(const KvPlan& p, const int32_t* row_ptr, const int32_t* qidx
   hipLaunchKernelGGL(kv_item_scan, dim3(static_cast<unsigned>(p.nch)), dim3(1024), 0, st, bounds, p.rows,
                      static_cast<int>(p.epi), p.max_items, reinterpret_cast<int32_t*>(b + p.starts),
                      reinterpret_cast<int2*>(b + p.items));
-  hipLaunchKernelGGL(kv_item_order, dim3(static_cast<unsigned>(p.nch)), dim3(1024), 0, st, bounds, p.rows,
-                     static_cast<int>(p.epi), p.max_items, reinterpret_cast<const int32_t*>(b + p.starts),
-                     reinterpret_cast<const int2*>(b + p.items), reinterpret_cast<int32_t*>(b + p.order));
+  if (ordered)
+    hipLaunchKernelGGL(kv_item_order, dim3(static_cast<unsigned>(p.nch)), dim3(1024), 0, st, bounds, p.rows,
+                       static_cast<int>(p.epi), p.max_items, reinterpret_cast<const int32_t*>(b + p.starts),
+                       reinterpret_cast<const int2*>(b + p.items), reinterpret_cast<int32_t*>(b + p.order));
 }
 
 struct FwdLayout {
