@@ -133,7 +133,8 @@ __global__ __launch_bounds__(256) void score_bwd_dq(const void* __restrict__ iq,
                                                     const float* __restrict__ ds, int64_t rows, int G,
                                                     int Di, int NB, int B, double scale,
                                                     void* __restrict__ dq, int dc0) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  // heaviest rows first: a row's work grows with its position in the sequence
+  const int64_t row = static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   const int64_t t = row / G;
@@ -237,7 +238,7 @@ __global__ __launch_bounds__(256) void score_bwd_dq_wide(const void* __restrict_
   __shared__ int32_t lkey[4][64];
   __shared__ float lw[4][64];
   const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + wid;
+  const int64_t row = static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * 4 + wid;  // heaviest rows first
   if (row >= rows) return;  // whole wave
   const int slot = lane / LPR, dch = lane % LPR;
   const int64_t t = row / G;

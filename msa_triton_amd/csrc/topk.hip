@@ -17,14 +17,16 @@
 
 namespace msa {
 
-// Sixteen lanes per row, four rows per wavefront (topk_row16).
+// Sixteen lanes per row, four rows per wavefront (topk_row16). In these kernels the
+// workgroups take the rows from the last one back: a row's work grows with its
+// position in the sequence, so the heaviest rows start first.
 template <int VPL>
 __global__ __launch_bounds__(256) void topk_kernel(const float* __restrict__ scores,
                                                    const int32_t* __restrict__ cu, int nseq,
                                                    int64_t rows, int G, int NB, int B, int K, int L,
                                                    int32_t* __restrict__ out) {
   topk_row16<VPL>(scores, cu, nseq, rows, G, NB, B, K, L, out,
-                  static_cast<int64_t>(blockIdx.x) * 16 + (threadIdx.x >> 4), threadIdx.x & 15);
+                  static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * 16 + (threadIdx.x >> 4), threadIdx.x & 15);
 }
 
 // One wavefront per row for long rows (more than 1024 blocks): topk_row64.
@@ -33,7 +35,7 @@ __global__ __launch_bounds__(256) void topk_wave_kernel(const float* __restrict_
                                                         const int32_t* __restrict__ cu, int nseq,
                                                         int64_t rows, int G, int NB, int B, int K, int L,
                                                         int32_t* __restrict__ out) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t row = static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   topk_row64<VPL>(scores, cu, nseq, G, NB, B, K, L, out, row, threadIdx.x & 63);
 }
@@ -43,7 +45,7 @@ __global__ __launch_bounds__(256) void topk_stream_kernel(const float* __restric
                                                           const int32_t* __restrict__ cu, int nseq, int64_t rows,
                                                           int G, int NB, int B, int K, int L,
                                                           int32_t* __restrict__ out) {
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t row = static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   topk_row_stream(scores, cu, nseq, G, NB, B, K, L, out, row, threadIdx.x & 63);
 }
