@@ -200,14 +200,22 @@ int msa_indexer_kl(const void* index_q, const void* index_k, const void* q, cons
                    float* grad_index_k, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Testing hook; no counterpart in the reference. Overrides the byte budgets that size
- * the query-token chunks of the KV-major bf16 passes: msa_attn_fwd (default 1 GiB of
- * per-(token, head, slot) partial records per chunk), msa_attn_bwd (4 GiB) and
+ * the query-token chunks of the KV-major bf16 passes: msa_attn_fwd (default 2 GiB of
+ * per-(token, head, slot) partial records per chunk), msa_attn_bwd (6 GiB) and
  * msa_indexer_kl (1 GiB); a value <= 0 restores that default. A chunk holds at least
  * 64 tokens. Chunking changes only how sums are split into per-chunk partial sums,
  * not what is computed; tests use it to drive small cases through many chunks.
  * Process-wide: set it only while no other thread queries workspace sizes or calls
  * those entry points, and query the workspace sizes again after a change. Returns 0. */
 int msa_set_chunk_budgets(int64_t fwd_bytes, int64_t bwd_bytes, int64_t kl_bytes);
+
+/* Testing hook; no counterpart in the reference. The KV-major bf16 passes of
+ * msa_attn_fwd, msa_attn_bwd and msa_indexer_kl launch their work items largest first
+ * (enabled != 0, the default); enabled == 0 launches them in row order instead. Every
+ * work item writes only its own outputs, so results are bitwise the same either way;
+ * tests use it to check exactly that. Process-wide, like msa_set_chunk_budgets.
+ * Returns 0. */
+int msa_set_item_order(int enabled);
 
 /* Profiling hook; no counterpart in the reference (bench.py reports its figures).
  * msa_profile_begin arms per-launch timing: until msa_profile_end, every kernel launch

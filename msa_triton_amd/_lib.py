@@ -52,6 +52,7 @@ SIGNATURES = {
     "msa_indexer_kl": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                               _f64, _f64, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _vp]),
     "msa_set_chunk_budgets": (_i32, [_i64, _i64, _i64]),
+    "msa_set_item_order": (_i32, [_i32]),
     "msa_profile_begin": (_i32, []),
     "msa_profile_end": (_i64, [_vp, _vp, _i64]),
 }
@@ -127,6 +128,19 @@ class chunk_budgets:
 
     def __exit__(self, *exc):
         lib().msa_set_chunk_budgets(0, 0, 0)
+        return False
+
+
+class row_order:
+    """Context manager over ``msa_set_item_order`` (a testing hook): inside the body the
+    KV-major passes launch their work items in row order instead of largest first."""
+
+    def __enter__(self):
+        check(lib().msa_set_item_order(0), "msa_set_item_order")
+        return self
+
+    def __exit__(self, *exc):
+        lib().msa_set_item_order(1)
         return False
 
 

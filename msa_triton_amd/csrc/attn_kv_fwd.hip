@@ -137,7 +137,8 @@ __global__ __launch_bounds__(1024) void kv_item_scan(const int32_t* __restrict__
 constexpr int kOrderBuckets = 1024;
 __global__ __launch_bounds__(1024) void kv_item_order(const int32_t* __restrict__ bounds, int64_t rows, int epi,
                                                        int64_t max_items, const int32_t* __restrict__ item_start,
-                                                       const int2* __restrict__ items, int32_t* __restrict__ order) {
+                                                       const int2* __restrict__ items, int32_t* __restrict__ order,
+                                                       int row_order) {
   __shared__ int32_t cnt[kOrderBuckets];
   __shared__ int32_t wsum[16];
   const int64_t c = blockIdx.x;
@@ -146,6 +147,10 @@ __global__ __launch_bounds__(1024) void kv_item_order(const int32_t* __restrict_
   int32_t* out = order + c * max_items;
   const int32_t n = item_start[c * (rows + 1) + rows];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  if (row_order) {  // the identity (testing hook)
+    for (int32_t i = tid; i < n; i += 1024) out[i] = i;
+    return;
+  }
   auto bucket = [&](int32_t i) {
     const int2 it = its[i];
     const int32_t left = hi_b[it.x] - it.y;  // edges from the item's first to the row's end
@@ -532,6 +537,7 @@ static int64_t fwd_epi(int64_t R) {
 
 namespace {
 std::atomic<int64_t> g_chunk_budget[3] = {{0}, {0}, {0}};
+std::atomic<int> g_item_order{1};
 }  // namespace
 
 int64_t kv_chunk_budget(KvPass pass, int64_t dflt) {
@@ -577,7 +583,8 @@ void kv_plan_launch(const KvPlan& p, const int32_t* row_ptr, const int32_t* qidx
   if (ordered)
     hipLaunchKernelGGL(kv_item_order, dim3(static_cast<unsigned>(p.nch)), dim3(1024), 0, st, bounds, p.rows,
                        static_cast<int>(p.epi), p.max_items, reinterpret_cast<const int32_t*>(b + p.starts),
-                       reinterpret_cast<const int2*>(b + p.items), reinterpret_cast<int32_t*>(b + p.order));
+                       reinterpret_cast<const int2*>(b + p.items), reinterpret_cast<int32_t*>(b + p.order),
+                       g_item_order.load(std::memory_order_relaxed) ? 0 : 1);
 }
 
 struct FwdLayout {
@@ -648,6 +655,11 @@ int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indi
 }
 
 }  // namespace msa
+
+extern "C" int msa_set_item_order(int enabled) {
+  msa::g_item_order.store(enabled != 0 ? 1 : 0, std::memory_order_relaxed);
+  return msa::kOk;
+}
 
 extern "C" int msa_set_chunk_budgets(int64_t fwd_bytes, int64_t bwd_bytes, int64_t kl_bytes) {
   msa::g_chunk_budget[msa::kPassFwd].store(fwd_bytes > 0 ? fwd_bytes : 0, std::memory_order_relaxed);

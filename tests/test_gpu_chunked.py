@@ -157,3 +157,38 @@ def test_score_backward_through_several_row_segments(device):
                                         ds.double().numpy(), block_size=block, scale=0.7)
     check_bf16_stated(a.grad, dq_r, "segmented score dq")
     check_bf16_stated(b.grad, dk_r, "segmented score dk")
+
+
+@pytest.mark.parametrize("chunked", [False, True])
+def test_dispatch_order_leaves_results_bitwise_equal(chunked, device):
+    """The KV-major passes launch their work items largest first (``kv_item_order``);
+    every item writes only its own records and partial slot, so row-order dispatch (the
+    ``msa_set_item_order`` testing hook) must give the same bits in every output."""
+    lengths, groups, ratio, dim, block, topk = [2100, 1500, 37], 2, 8, 128, 64, 8
+    q, k, v, grad, ids, cu = _attn_case(lengths, groups, ratio, dim, block, topk, 53)
+    gen = torch.Generator().manual_seed(54)
+    total = sum(lengths)
+    iq = torch.randn(total, groups, 64, generator=gen).bfloat16()
+    ik = torch.randn(total, 1, 64, generator=gen).bfloat16()
+    meta = sequence_meta(cu.tolist(), block)
+    scale = dim ** -0.5
+    qd, kd, vd, gd, idd, cud, iqd, ikd = (x.to(device) for x in (q, k, v, grad, ids, cu, iq, ik))
+    budgets = dict(fwd=1, bwd=1, kl=1) if chunked else {}
+
+    def run():
+        with _lib.chunk_budgets(**budgets):
+            out, lse, rs, o32, csr = _attn_forward(qd, kd, vd, idd, cud, meta, block, scale, None, save_f32=True)
+            dq, dk, dv = _attn_backward(qd, kd, vd, idd, cud, out, rs, gd, meta, block, scale, None, True, True,
+                                        True, csr, o32)
+            kl = kl_launch(iqd, ikd, qd, kd, idd, cud, meta, None, block, 0.5, scale, True, True, True)
+        torch.cuda.synchronize()
+        return [x.detach().clone() for x in (out, lse, dq, dk, dv, *kl)]
+
+    ordered = run()
+    with _lib.row_order():
+        in_rows = run()
+    ordered_again = run()
+    names = ("out", "lse", "dq", "dk", "dv", "kl loss", "kl rows", "d_iq", "d_ik")
+    for a, b, c, what in zip(ordered, in_rows, ordered_again, names):
+        assert torch.equal(a, b), f"{what}: row-order dispatch changed the result"
+        assert torch.equal(a, c), f"{what}: a second ordered run changed the result"
