@@ -514,8 +514,8 @@ def main():
         summarize_trace(args.trace_summarize)
         return
     if args.gpus != 1:
-        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (this path does not shard "
-              "across GPUs; see DESIGN.md for how it would).", file=sys.stderr)
+        print(f"bench.py measures one MI355X: --gpus {args.gpus} is not supported (this path runs on one GPU "
+              "and does not shard across GPUs).", file=sys.stderr)
         sys.exit(2)
 
     import torch
