@@ -355,27 +355,20 @@ __global__ __launch_bounds__(256) void score_bwd_dq_wide(const void* __restrict_
 // exact ties (rare) follow in row order. The sums go to
 // part[((gb * nseg + sg) * kchunks + kc) * 128 + key][Di]; score_bwd_dk_reduce adds
 // the segments in order.
-// acc += w * q[row] over this lane's dims (wide layout: 8 dims 8 dch .. +7, only the
-// slot-0 lanes' sums are kept; otherwise DPL dims from dbase).
+// acc += w * q[row] over this lane's dims dbase .. dbase + DPL - 1.
 template <int DT, int DPL>
 __device__ __forceinline__ void dk_add_row(double (&acc)[8], double wgt, const void* __restrict__ iq, int64_t row,
-                                           int Di, bool wide, int dch, int dbase) {
-  if (wide) {
+                                           int Di, int dbase) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      acc[j] = fma(wgt, static_cast<double>(load_as_f32<DT>(iq, row * Di + 8 * dch + j)), acc[j]);
-  } else {
-#pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      const int d = dbase + j;
-      if (d < Di) acc[j] = fma(wgt, static_cast<double>(load_as_f32<DT>(iq, row * Di + d)), acc[j]);
-    }
+  for (int j = 0; j < DPL; ++j) {
+    const int d = dbase + j;
+    if (d < Di) acc[j] = fma(wgt, static_cast<double>(load_as_f32<DT>(iq, row * Di + d)), acc[j]);
   }
 }
 
 constexpr int kDkSeg = 8192;
 constexpr int kDkBatch = 16;
-constexpr int kDkWideUnroll = 8;  // row-gather instructions in flight per wave (4 rows each)
+constexpr int kDkWideUnroll = 8;  // row-gather instructions per batch (4 rows each; two batches in flight)
 constexpr int kDkTieCap = 256;
 
 template <int DT, int DPL>
@@ -520,97 +513,20 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
     }
   }
   __syncthreads();
-  // ---- per-key sums: wave w takes keys w, w + 4, ...; lane dims dc0 + DPL lane .. + DPL - 1
-  // (index dims above 64 x DPL take one launch per 64 DPL dims)
-  const int dbase = dc0 + DPL * lane;
+  // ---- per-key sums: wave w takes keys w, w + 4, ... of this chunk
   const int64_t kchunk_end = k0 + B < end ? k0 + B : end;
-  constexpr int kWideLpr = 16;                  // lanes per 128-dim row (wide gathers, Di == 128)
-  constexpr int kWideRpi = 64 / kWideLpr;       // rows per load instruction
-  const bool wide = (DT != kF32) && Di == 128;  // 16-byte gathers
-  const int slot = lane / kWideLpr, dch = lane % kWideLpr;
-  for (int o = wid; o < 128; o += 4) {
-    const int64_t key = k0 + o_lo + o;
-    if (key >= kchunk_end || o_lo + o >= B) break;  // keys past the block (wave-uniform)
-    double acc[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = 0.0;
-    const int e0 = bstart[o], e1 = e0 + cnt[o];
-    if (wide) {
-      // lane (slot, dch) adds entries e0 + slot, e0 + slot + RPI, ... over dims 8 dch .. +7
-      const uint16_t* q16 = static_cast<const uint16_t*>(iq);
-      for (int e = e0; e < e1; e += kDkWideUnroll * kWideRpi) {
-        // all list reads, then all row loads (from clamped, in-bounds entries), then the sums:
-        // no per-load branch or LDS wait between the gathers
-        uint4 qw[kDkWideUnroll];
-        double wv[kDkWideUnroll];
-        int ro[kDkWideUnroll];
-        float wf[kDkWideUnroll];
-        bool ok[kDkWideUnroll];
-#pragma unroll
-        for (int u = 0; u < kDkWideUnroll; ++u) {
-          const int ee = e + u * kWideRpi + slot;
-          ok[u] = ee < e1;
-          const int ec = ok[u] ? ee : e0;
-          ro[u] = lrow[ec];
-          wf[u] = lds_w[ec];
-        }
-#pragma unroll
-        for (int u = 0; u < kDkWideUnroll; ++u)
-          qw[u] = *reinterpret_cast<const uint4*>(q16 + (r_begin + ro[u]) * 128 + 8 * dch);
-#pragma unroll
-        for (int u = 0; u < kDkWideUnroll; ++u) {
-          if (!ok[u]) qw[u] = make_uint4(0u, 0u, 0u, 0u);
-          wv[u] = ok[u] ? static_cast<double>(wf[u]) * scale : 0.0;
-        }
-#pragma unroll
-        for (int u = 0; u < kDkWideUnroll; ++u) {
-          const uint32_t x[4] = {qw[u].x, qw[u].y, qw[u].z, qw[u].w};
-#pragma unroll
-          for (int q2 = 0; q2 < 4; ++q2) {
-            acc[2 * q2] = fma(wv[u], static_cast<double>(half_of<DT>(x[q2], 0)), acc[2 * q2]);
-            acc[2 * q2 + 1] = fma(wv[u], static_cast<double>(half_of<DT>(x[q2], 1)), acc[2 * q2 + 1]);
-          }
-        }
-      }
-      // slot sums in slot order; every lane then holds the key's sums of its chunk's 8 dims
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        double tot = 0.0;
-#pragma unroll
-        for (int sl = 0; sl < kWideRpi; ++sl) tot += __shfl(acc[j], sl * kWideLpr + dch, kWave);
-        acc[j] = tot;
-      }
-    } else {
-      for (int e = e0; e < e1; e += kDkBatch) {
-        float qv[kDkBatch][DPL];
-#pragma unroll
-        for (int u = 0; u < kDkBatch; ++u) {
-          const int64_t row = r_begin + lrow[e + u < e1 ? e + u : e0];
-#pragma unroll
-          for (int j = 0; j < DPL; ++j) {
-            const int d = dbase + j;
-            qv[u][j] = (e + u < e1 && d < Di) ? load_as_f32<DT>(iq, row * Di + d) : 0.f;
-          }
-        }
-#pragma unroll
-        for (int u = 0; u < kDkBatch; ++u) {
-          if (e + u < e1) {
-            const double wgt = static_cast<double>(lds_w[e + u]) * scale;
-#pragma unroll
-            for (int j = 0; j < DPL; ++j) acc[j] = fma(wgt, static_cast<double>(qv[u][j]), acc[j]);
-          }
-        }
-      }
-    }
-    // exact ties: rows in order; the key takes w / count when its exact dot attains the maximum
+  const int nkeys_c = static_cast<int>(kchunk_end - k0 - o_lo < 128 ? kchunk_end - k0 - o_lo : 128);
+  if (wid >= nkeys_c) return;  // whole wave: no keys (no barrier follows)
+  // exact ties: the key takes w / count of each tied row (row order) whose exact dot attains the maximum
+  auto add_ties = [&](double (&acc)[8], int64_t key, int dbase, auto dpl) {
+    constexpr int kDpl = decltype(dpl)::value;
     if (!tie_overflow) {
       for (int x = 0; x < ntie; ++x) {
         const int64_t row = r_begin + tie_row[x];
-        const int64_t t = row / G;
-        if (key > t) continue;  // not visible from this row
+        if (key > row / G) continue;  // not visible from this row
         if (directed(exact_dot<DT>(iq, row * Di, ik, key * Di, Di), scale) != tie_best[x]) continue;
         const double wgt = static_cast<double>(dcol[tie_row[x]]) * scale / static_cast<double>(tie_count[x]);
-        dk_add_row<DT, DPL>(acc, wgt, iq, row, Di, wide, dch, dbase);
+        dk_add_row<DT, kDpl>(acc, wgt, iq, row, Di, dbase);
       }
     } else {
       // more ties than the list holds: rescan the segment in row order
@@ -623,21 +539,137 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
         const BlockMax bm = block_max_exact<DT>(iq, row * Di, ik, k0, k1, Di, scale, lane);
         if (directed(exact_dot<DT>(iq, row * Di, ik, key * Di, Di), scale) != bm.best) continue;
         const double wgt = static_cast<double>(dcol[i]) * scale / static_cast<double>(bm.count);
-        dk_add_row<DT, DPL>(acc, wgt, iq, row, Di, wide, dch, dbase);
+        dk_add_row<DT, kDpl>(acc, wgt, iq, row, Di, dbase);
       }
     }
+  };
+  if ((DT != kF32) && Di == 128) {
+    // 128-dim 2-byte rows: lane (slot, dch) reads 16 bytes (dims 8 dch .. +7) of entry slot of
+    // every 4, i.e. 4 rows per load instruction. A key's entries go in batches of kDkWideUnroll
+    // load instructions; the next batch (of the same key or of the wave's next key) is loaded
+    // while one is summed. Each batch issues all of its loads (entries past the key's end read
+    // the segment's first row and are not added), so the wait for a batch leaves the next
+    // batch's loads in flight.
+    constexpr int kLpr = 16, kRpi = 4, kSpan = kDkWideUnroll * kRpi;
+    const int slot = lane / kLpr, dch = lane % kLpr;
+    const uint16_t* q16 = static_cast<const uint16_t*>(iq);
+    struct Batch {
+      int o, e, kend;
+    };
+    auto first_of = [&](int o) {  // wave-uniform: kept in scalar registers
+      const int e = __builtin_amdgcn_readfirstlane(bstart[o]);
+      return Batch{o, e, e + __builtin_amdgcn_readfirstlane(cnt[o])};
+    };
+    auto next_of = [&](const Batch& x) {
+      Batch y{x.o, x.e + kSpan, x.kend};
+      if (y.e >= y.kend) {
+        y.o = x.o + 4;
+        y = y.o < nkeys_c ? first_of(y.o) : Batch{y.o, 0, 0};
+      }
+      return Batch{__builtin_amdgcn_readfirstlane(y.o), __builtin_amdgcn_readfirstlane(y.e),
+                   __builtin_amdgcn_readfirstlane(y.kend)};
+    };
+    auto issue = [&](const Batch& x, uint4 (&qw)[kDkWideUnroll], float (&wf)[kDkWideUnroll]) {
+      int ro[kDkWideUnroll];
+#pragma unroll
+      for (int u = 0; u < kDkWideUnroll; ++u) {
+        const int ee = x.e + u * kRpi + slot;
+        const int ec = ee < kDkSeg ? ee : kDkSeg - 1;  // always inside the list (value unused past the key)
+        const int r = lrow[ec];
+        const float wv = lds_w[ec];
+        const bool ok = ee < x.kend;
+        ro[u] = ok ? r : 0;
+        wf[u] = ok ? wv : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kDkWideUnroll; ++u)
+        qw[u] = *reinterpret_cast<const uint4*>(q16 + (r_begin + ro[u]) * 128 + 8 * dch);
+    };
+    double acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0;
+    auto consume = [&](const Batch& x, const uint4 (&qw)[kDkWideUnroll], const float (&wf)[kDkWideUnroll]) {
+#pragma unroll
+      for (int u = 0; u < kDkWideUnroll; ++u) {
+        if (x.e + u * kRpi >= x.kend) break;  // wave-uniform
+        const double wv = x.e + u * kRpi + slot < x.kend ? static_cast<double>(wf[u]) * scale : 0.0;
+        const uint32_t w4[4] = {qw[u].x, qw[u].y, qw[u].z, qw[u].w};
+#pragma unroll
+        for (int q2 = 0; q2 < 4; ++q2) {
+          acc[2 * q2] = fma(wv, static_cast<double>(half_of<DT>(w4[q2], 0)), acc[2 * q2]);
+          acc[2 * q2 + 1] = fma(wv, static_cast<double>(half_of<DT>(w4[q2], 1)), acc[2 * q2 + 1]);
+        }
+      }
+      if (x.e + kSpan >= x.kend) {  // the key's last batch: slot sums in slot order, ties, store
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          double tot = 0.0;
+#pragma unroll
+          for (int sl = 0; sl < kRpi; ++sl) tot += __shfl(acc[j], sl * kLpr + dch, kWave);
+          acc[j] = tot;
+        }
+        if (ntie > 0 || tie_overflow) add_ties(acc, k0 + o_lo + x.o, 8 * dch, std::integral_constant<int, 8>{});
+        if (slot == 0) {
+          double* dst = part + ((w * kchunks + kc) * 128 + x.o) * static_cast<int64_t>(Di) + 8 * dch;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) dst[j] = acc[j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = 0.0;
+      }
+    };
+    uint4 qa[kDkWideUnroll], qb[kDkWideUnroll];
+    float wa[kDkWideUnroll], wb[kDkWideUnroll];
+    Batch x0 = first_of(wid);
+    issue(x0, qa, wa);
+    for (;;) {
+      const Batch x1 = next_of(x0);
+      issue(x1, qb, wb);
+      consume(x0, qa, wa);
+      if (x1.o >= nkeys_c) break;
+      const Batch x2 = next_of(x1);
+      issue(x2, qa, wa);
+      consume(x1, qb, wb);
+      if (x2.o >= nkeys_c) break;
+      x0 = x2;
+    }
+    return;
+  }
+  // other dtypes / dims: lanes over dims dc0 + DPL lane .. + DPL - 1 (index dims above 64 x DPL
+  // take one launch per 64 DPL dims), query rows streamed kDkBatch at a time
+  const int dbase = dc0 + DPL * lane;
+  for (int o = wid; o < nkeys_c; o += 4) {
+    const int64_t key = k0 + o_lo + o;
+    double acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0;
+    const int e0 = bstart[o], e1 = e0 + cnt[o];
+    for (int e = e0; e < e1; e += kDkBatch) {
+      float qv[kDkBatch][DPL];
+#pragma unroll
+      for (int u = 0; u < kDkBatch; ++u) {
+        const int64_t row = r_begin + lrow[e + u < e1 ? e + u : e0];
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) {
+          const int d = dbase + j;
+          qv[u][j] = (e + u < e1 && d < Di) ? load_as_f32<DT>(iq, row * Di + d) : 0.f;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < kDkBatch; ++u) {
+        if (e + u < e1) {
+          const double wgt = static_cast<double>(lds_w[e + u]) * scale;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) acc[j] = fma(wgt, static_cast<double>(qv[u][j]), acc[j]);
+        }
+      }
+    }
+    add_ties(acc, key, dbase, std::integral_constant<int, DPL>{});
     double* dst = part + ((w * kchunks + kc) * 128 + o) * static_cast<int64_t>(Di);
-    if (wide) {
-      if (slot == 0) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) dst[8 * dch + j] = acc[j];
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < DPL; ++j) {
-        const int d = dbase + j;
-        if (d < Di) dst[d] = acc[j];
-      }
+    for (int j = 0; j < DPL; ++j) {
+      const int d = dbase + j;
+      if (d < Di) dst[d] = acc[j];
     }
   }
 }

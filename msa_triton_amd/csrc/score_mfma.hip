@@ -207,7 +207,8 @@ __global__ __launch_bounds__(256) void score_key_norms(const uint16_t* __restric
 
 // Per key block, stored at the block's first key: the largest key norm of the block,
 // sqrt(max |knorm2|), negated when a key of the block is not safe (or not a number).
-// An unsafe key's entry has magnitude >= 1, so a negated value is never zero.
+// Safety is read from the sign bit: a block whose only unsafe key is NaN (fmaxf skips
+// its NaN entry) and whose other keys are zero stores -0.
 __global__ __launch_bounds__(256) void score_block_norms(const float* __restrict__ knorm2,
                                                          const int32_t* __restrict__ cu, int nseq, int64_t T, int B,
                                                          float* __restrict__ bnorm) {
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
   __builtin_amdgcn_s_waitcnt(0);  // this thread's direct-to-LDS loads have landed
   __syncthreads();
   float kmax = fabsf(cn);
-  bool bsafe = cn >= 0.f;
+  bool bsafe = !__builtin_signbit(cn);  // -0 marks an unsafe block too
   int buf = 0;
   while (cur.s < nseq) {
     const BlockCursor nxt = next_block(cu, nseq, cur, r0, nr, G, B);
@@ -490,9 +491,12 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
           if (FULLD || 8 * j8 < h) {
             const uint16_t* kp = kt_base + key_off<NK, FULLD>(myidx, hf * h + 8 * j8);
             uint32_t kx[4];
-            if (FULLD || 8 * j8 + 8 <= h) {
+            if (FULLD) {
               const uint4 kw = *reinterpret_cast<const uint4*>(kp);
               kx[0] = kw.x, kx[1] = kw.y, kx[2] = kw.z, kx[3] = kw.w;
+            } else if (8 * j8 + 8 <= h) {  // the second half may start 8 bytes into a 16-byte unit (h % 8 == 4)
+              const uint2 ka = *reinterpret_cast<const uint2*>(kp), kb = *reinterpret_cast<const uint2*>(kp + 4);
+              kx[0] = ka.x, kx[1] = ka.y, kx[2] = kb.x, kx[3] = kb.y;
             } else {  // h % 8 == 4: the last four dims of the half
               const uint2 kw = *reinterpret_cast<const uint2*>(kp);
               kx[0] = kw.x, kx[1] = kw.y, kx[2] = kx[3] = 0u;
@@ -528,7 +532,7 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
     __builtin_amdgcn_s_waitcnt(0);       // the next block's direct-to-LDS loads have landed
     __syncthreads();  // this block's readers are done; the next block is visible
     kmax = fabsf(nn);
-    bsafe = nn >= 0.f;
+    bsafe = !__builtin_signbit(nn);
     buf ^= 1;
     cur = nxt;
   }
@@ -659,7 +663,9 @@ __global__ __launch_bounds__(256) void score_fwd_resolve(const uint16_t* __restr
           const double v0 = lane < vis ? acc[0][0][p] + acc[0][1][p] : -__builtin_inf();
           const double v1 = lane + 64 < vis ? acc[1][0][p] + acc[1][1][p] : -__builtin_inf();
           const double wbest = wave_max_f64(fmax(v0, v1));
-          const uint64_t m0 = __ballot(v0 == wbest), m1 = __ballot(v1 == wbest);  // vis >= 1: wbest is finite
+          // visible keys only: with NaN dots (skipped by the maximum) wbest may be -inf, the value
+          // of the masked lanes; a row without any non-NaN visible dot gets count 0 (code 0)
+          const uint64_t m0 = __ballot(lane < vis && v0 == wbest), m1 = __ballot(lane + 64 < vis && v1 == wbest);
           if (lane == 0) {
             const int count = __popcll(m0) + __popcll(m1);
             const int first = m0 ? __builtin_ctzll(m0) : 64 + __builtin_ctzll(m1);

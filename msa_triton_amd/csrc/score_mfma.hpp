@@ -50,7 +50,8 @@ __device__ BlockMax block_max_exact(const void* __restrict__ iq, int64_t qoff, c
       best = v;
       count = 1;
       first = static_cast<int>(kk - k0);
-    } else if (v == best) {
+    } else if (v == best) {  // also a first key whose dot is -inf (NaN dots are skipped)
+      if (count == 0) first = static_cast<int>(kk - k0);
       ++count;
     }
   }

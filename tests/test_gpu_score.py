@@ -196,6 +196,57 @@ def test_score_extreme_magnitudes_bit_exact(scale, device):
     np.testing.assert_array_equal(got.cpu().numpy(), exp32)
 
 
+@pytest.mark.parametrize("dim", [64, 40])
+def test_score_nan_keys_mfma_and_exact_paths_agree(dim, device):
+    """Keys holding NaN elements. No reference fixture pins NaN (numpy's max, like the
+    eager path's amax, propagates it; fmax-style maxima skip it), so this checks that
+    the two GPU paths agree bitwise on scores and tie codes: the bf16 MFMA pass with its
+    FP64 resolve, and the FP64 exact kernel on the same values as fp32. NaN dots are
+    skipped; a block whose visible dots are all NaN scores -inf with code 0. Cases: a
+    block whose only unsafe key is NaN and whose other keys are zero (its stored norm is
+    -0), a block of NaN keys, single NaN keys among normal ones; dim 40 puts the second
+    query half 8 bytes into a 16-byte unit."""
+    from msa_triton_amd.index_score import _score_forward
+    from msa_triton_amd.layout import sequence_meta
+
+    lengths, groups, block = [300, 200], 2, 32
+    total = sum(lengths)
+    gen = torch.Generator().manual_seed(5)
+    q = torch.randn(total, groups, dim, generator=gen)
+    k = torch.randn(total, 1, dim, generator=gen)
+    k[0:32] = 0.0
+    k[3, 0, 7] = float("nan")        # sequence 0, block 0: zero keys and one NaN key
+    k[64:96, 0, 5] = float("nan")    # block 2: every key NaN
+    k[130, 0, :] = float("nan")      # block 4: one NaN key among normal keys
+    k[340, 0, 1] = float("nan")      # sequence 1, block 1
+    qb, kb = q.bfloat16(), k.bfloat16()
+    bounds = cu_list(lengths)
+    meta = sequence_meta(bounds, block)
+    cu = cu_tensor(lengths, device)
+    out = {}
+    for name, dtype in (("mfma", torch.bfloat16), ("exact", torch.float32)):
+        sc, tie = _score_forward(qb.to(dtype).to(device).contiguous(), kb.to(dtype).to(device).contiguous(), cu, meta,
+                                 max(lengths), block, 1.0, True)
+        out[name] = (sc.cpu().numpy(), tie.cpu().numpy())
+    np.testing.assert_array_equal(out["mfma"][0], out["exact"][0])
+    np.testing.assert_array_equal(out["mfma"][1], out["exact"][1])
+    sc, tie = out["mfma"]
+    assert np.isneginf(sc[64:300, :, 2]).all() and (tie[64:300, :, 2] == 0).all()  # block 2: all dots NaN
+    assert (sc[32:300, :, 0] == 0.0).all() and (tie[32:300, :, 0] == -31).all()  # 31 zero keys tie
+    # every other (row, block) pair of the pack against the oracle (NaN keys excluded there)
+    kk = kb.double().numpy()
+    assert not np.isnan(sc).any()
+    _, exp32, exp_tie = O.index_score(qb.double().numpy(), np.nan_to_num(kk, nan=0.0), bounds, max(lengths),
+                                      block_size=block)
+    clean = np.ones(sc.shape, dtype=bool)
+    for a, blk in ((0, 0), (0, 2), (0, 4), (300, 1)):
+        s_idx = 0 if a == 0 else 1
+        lo = a + blk * block
+        clean[lo:bounds[s_idx + 1], :, blk] = False  # rows that see a NaN key's block
+    np.testing.assert_array_equal(sc[clean], exp32[clean])
+    np.testing.assert_array_equal(tie[clean], exp_tie[clean])
+
+
 @pytest.mark.parametrize("dim,dtype", [(640, torch.bfloat16), (1100, torch.float32)])
 def test_score_index_dims_beyond_512(dim, dtype, device):
     """Index dims above 512 (no cap upstream): the exact forward, and the backward in
