@@ -379,7 +379,7 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
     double* __restrict__ part, int dc0) {
   __shared__ uint16_t lrow[kDkSeg];   // bucketed row offsets (within the segment)
   __shared__ float lds_w[kDkSeg];     // their ds
-  __shared__ int32_t cnt[128], bstart[128], running[128];
+  __shared__ int32_t cnt[128], bstart[128];
   __shared__ int32_t wcnt[4][128];
   __shared__ int32_t tie_row[kDkTieCap];
   __shared__ double tie_best[kDkTieCap];
@@ -411,34 +411,39 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
   const int nseg_rows = static_cast<int>(r_stop - r_begin);
   const int32_t* tcol = tie_t + static_cast<int64_t>(b) * rows + r_begin;
   const float* dcol = ds_t + static_cast<int64_t>(b) * rows + r_begin;
-  if (tid < 128) {
-    cnt[tid] = 0;
-    running[tid] = 0;
-    wcnt[0][tid] = wcnt[1][tid] = wcnt[2][tid] = wcnt[3][tid] = 0;
-  }
+  // Stable counting sort by winner, one quarter of the segment per wave: wave w takes rows
+  // kWaveRows w .. kWaveRows (w + 1) - 1 (row kWaveRows w + 64 r + lane in round r) and owns
+  // the slice of every key's bucket after the slices of waves 0 .. w - 1. Each wave ranks its
+  // rounds with ballots and advances its own counters, so the rounds need no workgroup
+  // barrier, and every bucket still lists its rows in row order.
+  constexpr int kWaveRows = kDkSeg / 4;
+  constexpr int kRounds = kWaveRows / 64;
+  if (tid < 128) wcnt[0][tid] = wcnt[1][tid] = wcnt[2][tid] = wcnt[3][tid] = 0;
   if (tid == 0) ntie_s = 0;
-  // the segment's tie codes and ds, row tid + 256 j in register j: all loads in flight at once
-  constexpr int kPer = kDkSeg / 256;
-  int32_t tcs[kPer];
-  float dvs[kPer];
+  // the wave's tie codes and ds, round r in register r: all loads in flight at once
+  int32_t tcs[kRounds];
+  float dvs[kRounds];
+  const int wrow0 = kWaveRows * wid;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int i = tid + 256 * j;
-    tcs[j] = i < nseg_rows ? tcol[i] : 0;
-    dvs[j] = i < nseg_rows ? dcol[i] : 0.f;
+  for (int r = 0; r < kRounds; ++r) {
+    const int i = wrow0 + 64 * r + lane;
+    tcs[r] = i < nseg_rows ? tcol[i] : 0;
+    dvs[r] = i < nseg_rows ? dcol[i] : 0.f;
   }
   __syncthreads();
-  // ---- histogram of winners in this key chunk; list the exact ties
+  // ---- per-wave histograms of winners in this key chunk; list the exact ties
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int32_t tc = tcs[j];
+  for (int r = 0; r < kRounds; ++r) {
+    const int32_t tc = tcs[r];
     const int o = tc - 1 - o_lo;
-    if (tc > 0 && o >= 0 && o < 128) atomicAdd(&cnt[o], 1);
+    if (tc > 0 && o >= 0 && o < 128) atomicAdd(&wcnt[wid][o], 1);
     if (tc < 0) {
       const int slot = atomicAdd(&ntie_s, 1);
-      if (slot < kDkTieCap) tie_row[slot] = tid + 256 * j;
+      if (slot < kDkTieCap) tie_row[slot] = wrow0 + 64 * r + lane;
     }
   }
+  __syncthreads();
+  if (tid < 128) cnt[tid] = wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
   __syncthreads();
   if (tid < 64) {  // exclusive scan of the 128 bucket counts (two per lane)
     const int a0 = cnt[2 * tid], a1 = cnt[2 * tid + 1];
@@ -452,15 +457,23 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
     bstart[2 * tid + 1] = x - a1;
   }
   __syncthreads();
-  // ---- stable scatter, 256 rows per step
+  if (tid < 128) {  // each wave's next free position in each bucket
+    int p = bstart[tid];
+#pragma unroll
+    for (int w2 = 0; w2 < 4; ++w2) {
+      const int n = wcnt[w2][tid];
+      wcnt[w2][tid] = p;
+      p += n;
+    }
+  }
+  __syncthreads();
+  // ---- stable scatter, 64 rows per round and wave (the wave's own counters only)
   const uint64_t lt = (uint64_t(1) << lane) - 1;
 #pragma unroll
-  for (int j = 0; j < kPer; ++j) {
-    const int base = 256 * j;
-    if (base >= nseg_rows) break;  // workgroup-uniform
-    const int i = base + tid;
-    const int32_t tc = tcs[j];  // 0 past the segment end
-    const float dv = dvs[j];
+  for (int r = 0; r < kRounds; ++r) {
+    if (wrow0 + 64 * r >= nseg_rows) break;  // wave-uniform
+    const int i = wrow0 + 64 * r + lane;
+    const int32_t tc = tcs[r];  // 0 past the segment end
     const int o = tc - 1 - o_lo;
     const bool on = tc > 0 && o >= 0 && o < 128;
     uint64_t match = __ballot(on);
@@ -471,22 +484,17 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
     }
     const int rank = __popcll(match & lt);
     const int total = __popcll(match);
-    if (on && rank == total - 1) wcnt[wid][o] = total;  // last lane of its group
-    __syncthreads();
     if (on) {
-      int before = running[o] + rank;
-      for (int w2 = 0; w2 < wid; ++w2) before += wcnt[w2][o];
-      const int p = bstart[o] + before;
+      const int p = wcnt[wid][o] + rank;
       lrow[p] = static_cast<uint16_t>(i);
-      lds_w[p] = dv;
+      lds_w[p] = dvs[r];
     }
-    __syncthreads();
-    if (tid < 128) {
-      running[tid] += wcnt[0][tid] + wcnt[1][tid] + wcnt[2][tid] + wcnt[3][tid];
-      wcnt[0][tid] = wcnt[1][tid] = wcnt[2][tid] = wcnt[3][tid] = 0;
-    }
-    __syncthreads();
+    // all of the round's counter reads precede the advance (LDS operations of a wave run in order)
+    __builtin_amdgcn_wave_barrier();
+    if (on && rank == total - 1) wcnt[wid][o] += total;  // last lane of its group
+    __builtin_amdgcn_wave_barrier();
   }
+  __syncthreads();
   // ---- exact ties of the segment (rare): sort the listed rows, block maximum per row
   const int ntie = ntie_s < kDkTieCap ? ntie_s : kDkTieCap;
   const bool tie_overflow = ntie_s > kDkTieCap;
