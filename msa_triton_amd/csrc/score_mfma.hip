@@ -325,15 +325,15 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
     const int row = p / CPK, pc = p % CPK;
     return static_cast<uint32_t>(row * DP + 8 * (pc ^ ((row >> SH) & (CPK - 1))) + (i < NP ? 0 : 16 * DP));
   };
-  auto fetch = [&](const BlockCursor& bc, int into) {
+  auto fetch = [&](const BlockCursor& bc, const uint16_t* gsrc, uint16_t* into) {
     if (bc.s >= nseq) return;
     const int64_t kb = cu[bc.s] + static_cast<int64_t>(bc.b) * B;
     const int64_t end = cu[bc.s + 1];
     const int nk = static_cast<int>(end - kb < B ? end - kb : B);
     if constexpr (FULLD) {
-      char* dst = reinterpret_cast<char*>(sm.k[into]) + wid * KCH * 1024;
+      char* dst = reinterpret_cast<char*>(into) + wid * KCH * 1024;
       if (nk == 128) {  // a complete block: scalar base plus the precomputed offsets
-        const uint16_t* src = ik + kb * DP;
+        const uint16_t* src = gsrc + kb * DP;
 #pragma unroll
         for (int i = 0; i < KCH; ++i)
           __builtin_amdgcn_global_load_lds(src + static_cast<int>(chunk_off(i)),
@@ -345,7 +345,7 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
           const int row = p / CPK, pc = p % CPK;
           const int lc = pc ^ ((row >> SH) & (CPK - 1));
           const int rowc = row < nk ? row : nk - 1;
-          __builtin_amdgcn_global_load_lds(ik + (kb + rowc) * Di + 8 * lc,
+          __builtin_amdgcn_global_load_lds(gsrc + (kb + rowc) * Di + 8 * lc,
                                            (__attribute__((address_space(3))) void*)(dst + i * 1024), 16, 0, 0);
         }
       }
@@ -354,7 +354,7 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
       for (int i = 0; i < KCH; ++i) {
         const int e = tid + kThreads * i;
         const int kl = e / CPK, d0 = 8 * (e % CPK);
-        kreg[i] = (kl < nk && d0 < Di) ? *reinterpret_cast<const uint4*>(ik + (kb + kl) * Di + d0)
+        kreg[i] = (kl < nk && d0 < Di) ? *reinterpret_cast<const uint4*>(gsrc + (kb + kl) * Di + d0)
                                        : make_uint4(0u, 0u, 0u, 0u);
       }
     }
@@ -382,7 +382,7 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
     cur = BlockCursor{s0, 0, last_block_of(cu, s0, r0, nr, G, B)};
   }
   const float cn = block_norm(cur);
-  fetch(cur, 0);
+  fetch(cur, ik, sm.k[0]);
   commit(0);
   __builtin_amdgcn_s_waitcnt(0);  // this thread's direct-to-LDS loads have landed
   __syncthreads();
@@ -392,7 +392,12 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
   while (cur.s < nseq) {
     const BlockCursor nxt = next_block(cu, nseq, cur, r0, nr, G, B);
     const float nn = block_norm(nxt);
-    fetch(nxt, buf ^ 1);  // in flight while this block is evaluated (that buffer's readers passed the last barrier)
+    // The next block's fetch and this block's LDS reads go through the restrict-qualified
+    // pointers of one inlined call, so the compiler's wait insertion can tell the fetch's
+    // LDS writes (buffer buf ^ 1) from the reads (buffer buf): without that it waits for
+    // the whole fetch before the first read, and the fetch would not overlap the block.
+    [&](const uint16_t* __restrict__ ksrc, const uint16_t* __restrict__ kt_base, uint16_t* __restrict__ knext) {
+    fetch(nxt, ksrc, knext);  // in flight while this block is evaluated (that buffer's readers passed the last barrier)
 
     const int64_t start = cu[cur.s], end = cu[cur.s + 1];
     const int64_t kb = start + static_cast<int64_t>(cur.b) * B;
@@ -406,7 +411,6 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
       lim[rt] = v <= 0 ? 0 : (v < nk ? static_cast<int>(v) : nk);
     }
     const bool wave_on = __ballot(lim[0] > 0 || lim[1] > 0) != 0;  // wave-uniform
-    const uint16_t* kt_base = sm.k[buf];
     // approximate logits, 16 keys at a time, key position packed into their low bits,
     // folded into a per-row running top 2: m1 the maximum, m2 the largest other value
     // (med3(m1, v, m2) is the new second largest)
@@ -528,6 +532,7 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
         atomicOr(amb + (bit >> 5), 1u << (bit & 31));
       }
     }
+    }(ik, sm.k[buf], sm.k[buf ^ 1]);
     if (nxt.s < nseq) commit(buf ^ 1);  // that buffer's readers finished before the last barrier
     __builtin_amdgcn_s_waitcnt(0);       // the next block's direct-to-LDS loads have landed
     __syncthreads();  // this block's readers are done; the next block is visible
