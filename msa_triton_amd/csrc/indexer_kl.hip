@@ -343,10 +343,20 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
     ikt[kc] = diq_wave ? frag_tr(sm.ikb, KSI, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 16 * wid, c) : zero_frag();
 
   // ---- row staging (16 edges per tile): q rows (edge * R + head) and index_q rows,
-  // per-row normalisers, visible keys and records
-  uint4 pf[QI], pfi = make_uint4(0u, 0u, 0u, 0u);
-  float4 pst = make_float4(0.f, 0.f, 0.f, 0.f);
-  int pvis = 0, prec = -1;
+  // per-row normalisers, visible keys and records. Two register stages: tile j is
+  // loaded into stage j % 2 two tiles ahead of its use and committed to LDS one tile
+  // ahead (measured: with the rows of every tile cache-hot the KL runs 14 % faster,
+  // so its row gathers are worth hiding).
+  struct Stage {
+    uint4 pf[QI], pfi;
+    float4 pst;
+    int pvis, prec;
+  };
+  Stage st0, st1;
+  st0.pfi = st1.pfi = make_uint4(0u, 0u, 0u, 0u);
+  st0.pst = st1.pst = make_float4(0.f, 0.f, 0.f, 0.f);
+  st0.pvis = st1.pvis = 0;
+  st0.prec = st1.prec = -1;
   // the thread -> (tile edge, head, dims) split of the q rows is the same for every tile
   int qel[QI], qsrc[QI], qdst[QI];
 #pragma unroll
@@ -359,7 +369,11 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
     qdst[i] = (h * 16 + el) * KS + d0;
   }
   const int64_t qrow = static_cast<int64_t>(Hq) * D;
-  auto issue = [&](int e0) {
+  auto issue = [&](int e0, Stage& S) {
+    uint4(&pf)[QI] = S.pf;
+    uint4& pfi = S.pfi;
+    float4& pst = S.pst;
+    int &pvis = S.pvis, &prec = S.prec;
 #pragma unroll
     for (int i = 0; i < QI; ++i) {
       if (qel[i] >= 0) {
@@ -392,7 +406,11 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
       }
     }
   };
-  auto commit = [&](int e0, int buf) {
+  auto commit = [&](int e0, int buf, const Stage& S) {
+    const uint4(&pf)[QI] = S.pf;
+    const uint4& pfi = S.pfi;
+    const float4& pst = S.pst;
+    const int pvis = S.pvis, prec = S.prec;
 #pragma unroll
     for (int i = 0; i < QI; ++i) {
       // head-major rows: the A-operand reads of one head (lane c -> edge c) hit
@@ -417,9 +435,10 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
 #pragma unroll
   for (int dt = 0; dt < NDTI; ++dt) dik[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  issue(0);
-  commit(0, 0);
-  if (ntiles > 1) issue(16);
+  issue(0, st0);
+  commit(0, 0, st0);
+  if (ntiles > 1) issue(16, st1);
+  if (ntiles > 2) issue(32, st0);
   __syncthreads();
 
   for (int t = 0; t < ntiles; ++t) {
@@ -513,10 +532,15 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
     // records read before the barrier: buffer b is refilled (tile t + 2) before the next one
     const int myrec = sm.rec[b][c];
     const int krec = tid < 16 ? sm.rec[b][tid] : -1;
-    // ---- stage the next tile, start loading the one after
+    // ---- stage the next tile (from register stage (t + 1) % 2), then load tile t + 3 into that stage
     if (t + 1 < ntiles) {
-      commit(16 * (t + 1), b ^ 1);
-      if (t + 2 < ntiles) issue(16 * (t + 2));
+      if ((t + 1) & 1) {
+        commit(16 * (t + 1), b ^ 1, st1);
+        if (t + 3 < ntiles) issue(16 * (t + 3), st1);
+      } else {
+        commit(16 * (t + 1), b ^ 1, st0);
+        if (t + 3 < ntiles) issue(16 * (t + 3), st0);
+      }
     }
     __syncthreads();  // planes, KL sums of this tile and rows of the next one complete
     if (krec >= 0) {  // threads 0-15: edge tid of the tile
