@@ -38,6 +38,52 @@ __device__ __forceinline__ RowCtx row_ctx(const int32_t* __restrict__ cu, int ns
   return c;
 }
 
+// Elements [i, i + 8) of a row as fp32, from one 16-byte load (2-byte dtypes) or two
+// (fp32); i a multiple of 8 (16-byte aligned). A lane walking its own key row this way
+// issues one load instruction per 8 elements instead of one per element: with 64 lanes
+// on 64 different rows, the address unit, not the FP64 arithmetic, limits these kernels.
+template <int DT>
+__device__ __forceinline__ void load8_as_f32(const void* __restrict__ base, int64_t i, float (&x)[8]) {
+  if constexpr (DT == kF32) {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i + 4);
+    x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+  } else {
+    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if constexpr (DT == kBF16) {
+        x[2 * u] = __uint_as_float(ws[u] << 16);
+        x[2 * u + 1] = __uint_as_float(ws[u] & 0xffff0000u);
+      } else {
+        x[2 * u] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(ws[u] & 0xffffu)));
+        x[2 * u + 1] = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(ws[u] >> 16)));
+      }
+    }
+  }
+}
+
+// sum_d a[d] * row[off + d] in FP64, d = 0 .. D - 1 in order (a in LDS as fp32, 16-byte
+// aligned when D % 8 == 0).
+template <int DT>
+__device__ __forceinline__ double row_dot(const float* a, const void* __restrict__ row, int64_t off, int D) {
+  double acc = 0.0;
+  if (D % 8 == 0 && (reinterpret_cast<uintptr_t>(row) & 15) == 0) {  // 16-byte aligned rows
+    for (int d = 0; d < D; d += 8) {
+      float x[8];
+      load8_as_f32<DT>(row, off + d, x);
+      const float4 a0 = *reinterpret_cast<const float4*>(a + d), a1 = *reinterpret_cast<const float4*>(a + d + 4);
+      const float av[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+      for (int u = 0; u < 8; ++u) acc = fma(static_cast<double>(av[u]), static_cast<double>(x[u]), acc);
+    }
+  } else {
+    for (int d = 0; d < D; ++d) acc = fma(static_cast<double>(a[d]), static_cast<double>(load_as_f32<DT>(row, off + d)), acc);
+  }
+  return acc;
+}
+
 // Forward: one wavefront per (t, h). Keys are processed 64 at a time: each lane
 // evaluates one key's logit, lanes then own head dims for the P.V update.
 template <int DT, int DPL>
@@ -76,10 +122,7 @@ __global__ __launch_bounds__(256) void attn_fwd_valu(const void* __restrict__ q,
       const int64_t key = base + lane;
       double sv = -__builtin_inf();
       if (key < kend) {
-        const int64_t off = (key * G + g) * D;
-        double acc = 0.0;
-        for (int d = 0; d < D; ++d) acc = fma(static_cast<double>(qs[d]), static_cast<double>(load_as_f32<DT>(k, off + d)), acc);
-        sv = acc * scale;
+        sv = row_dot<DT>(qs, k, (key * G + g) * D, D) * scale;
       }
       const double mt = wave_max_f64(sv);
       const double mn = fmax(m, mt);
@@ -166,11 +209,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_valu(
         double p = 0.0, u = 0.0;
         if (key < kend) {
           const int64_t off = (key * G + g) * D;
-          double sacc = 0.0, dacc = 0.0;
-          for (int d = 0; d < D; ++d) {
-            sacc = fma(static_cast<double>(qs[d]), static_cast<double>(load_as_f32<DT>(k, off + d)), sacc);
-            dacc = fma(static_cast<double>(gs[d]), static_cast<double>(load_as_f32<DT>(v, off + d)), dacc);
-          }
+          const double sacc = row_dot<DT>(qs, k, off, D), dacc = row_dot<DT>(gs, v, off, D);
           p = exp(sacc * scale - row_lse);
           u = p * (dacc - c);
           mass += p;
