@@ -42,15 +42,33 @@ __device__ __forceinline__ RowCtx row_ctx(const int32_t* __restrict__ cu, int ns
 // (fp32); i a multiple of 8 (16-byte aligned). A lane walking its own key row this way
 // issues one load instruction per 8 elements instead of one per element: with 64 lanes
 // on 64 different rows, the address unit, not the FP64 arithmetic, limits these kernels.
+// Eight consecutive elements kept as loaded (16 bytes for 2-byte types, 32 for fp32),
+// and their fp32 values.
 template <int DT>
-__device__ __forceinline__ void load8_as_f32(const void* __restrict__ base, int64_t i, float (&x)[8]) {
+struct Raw8 {
+  uint4 w[DT == kF32 ? 2 : 1];
+};
+
+template <int DT>
+__device__ __forceinline__ Raw8<DT> load8_raw(const void* __restrict__ base, int64_t i) {
+  Raw8<DT> r;
   if constexpr (DT == kF32) {
-    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i);
-    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + i + 4);
-    x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+    r.w[0] = *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + i);
+    r.w[1] = *reinterpret_cast<const uint4*>(static_cast<const float*>(base) + i + 4);
   } else {
-    const uint4 w = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+    r.w[0] = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(base) + i);
+  }
+  return r;
+}
+
+template <int DT>
+__device__ __forceinline__ void unpack8(const Raw8<DT>& r, float (&x)[8]) {
+  if constexpr (DT == kF32) {
+    const uint32_t ws[8] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w, r.w[1].x, r.w[1].y, r.w[1].z, r.w[1].w};
+#pragma unroll
+    for (int u = 0; u < 8; ++u) x[u] = __uint_as_float(ws[u]);
+  } else {
+    const uint32_t ws[4] = {r.w[0].x, r.w[0].y, r.w[0].z, r.w[0].w};
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       if constexpr (DT == kBF16) {
@@ -62,6 +80,12 @@ __device__ __forceinline__ void load8_as_f32(const void* __restrict__ base, int6
       }
     }
   }
+}
+
+// Eight consecutive elements base[i .. i + 7] as fp32 (i 16-byte aligned).
+template <int DT>
+__device__ __forceinline__ void load8_as_f32(const void* __restrict__ base, int64_t i, float (&x)[8]) {
+  unpack8<DT>(load8_raw<DT>(base, i), x);
 }
 
 // sum_d a[d] * row[off + d] in FP64, d = 0 .. D - 1 in order (a in LDS as fp32, 16-byte
@@ -331,6 +355,125 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_valu(
   }
 }
 
+// KV-pass backward for head dims D = 8 LPR with LPR in {1, 2, 4, 8, 16}: one wavefront
+// per (key token, group) as above, but LPR lanes per query row (8 dims each, 16-byte
+// loads), so RPW = 64 / LPR rows of the key's CSR row go at once: row i = (e - e0) R + r
+// (edge e, head r, in order) goes to slot i % RPW. A row's two dot products reduce over
+// its LPR lanes only, and one exponential serves RPW rows. Each slot sums its rows in
+// order; the slot sums are then added pairwise (a fixed butterfly over the slot index).
+template <int DT, int LPR>
+__global__ __launch_bounds__(256, DT == kF32 ? 2 : 3) void attn_bwd_dkdv_rows(
+    const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
+    const void* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
+    const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ qidx,
+    int nseq, int64_t T, int Hq, int G, int D, int B, double scale, void* __restrict__ dk, void* __restrict__ dv) {
+  constexpr int RPW = kWave / LPR;
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t jg = static_cast<int64_t>(blockIdx.x) * 4 + wid;
+  if (jg >= T * G) return;
+  const int slot = lane / LPR, dch = lane % LPR;
+  const int64_t j = jg / G;
+  const int g = static_cast<int>(jg % G);
+  const int s = find_seq(cu, nseq, j);
+  const int64_t blk = (j - cu[s]) / B;
+  const int64_t row = (static_cast<int64_t>(cu_blocks[s]) + blk) * G + g;
+  const int64_t e0 = row_ptr[row], e1 = row_ptr[row + 1];
+  const int R = Hq / G;
+  float kr[8], vr[8];
+  load8_as_f32<DT>(k, jg * D + 8 * dch, kr);
+  load8_as_f32<DT>(v, jg * D + 8 * dch, vr);
+  double gk[8], gv[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) gk[u] = gv[u] = 0.0;
+  // Row i = (e - e0) R + r is walked as the pair (e, r), RPW rows a step. Software
+  // pipeline: the query index two steps ahead, the rows one step ahead (positions past the
+  // end read the row's first edge, so every load stays in bounds).
+  struct Cursor { int64_t e; int r; };
+  const int64_t estep = RPW / R;
+  const int rstep = RPW % R;
+  auto advance = [&](Cursor& c) {
+    c.e += estep;
+    c.r += rstep;
+    if (c.r >= R) c.r -= R, ++c.e;
+  };
+  auto edge_of = [&](const Cursor& c) -> int64_t { return c.e < e1 ? c.e : e0; };
+  struct Rows { Raw8<DT> qw, gw; double2 rs01, rs23; };
+  auto fetch = [&](const Cursor& c, int64_t t, Rows& x) {
+    const int64_t th = t * Hq + static_cast<int64_t>(g) * R + (c.e < e1 ? c.r : 0);
+    x.qw = load8_raw<DT>(q, th * D + 8 * dch);
+    x.gw = load8_raw<DT>(dout, th * D + 8 * dch);
+    x.rs01 = reinterpret_cast<const double2*>(row_state)[th * 2];
+    x.rs23 = reinterpret_cast<const double2*>(row_state)[th * 2 + 1];
+  };
+  if (e1 > e0) {
+    Cursor cc{e0 + slot / R, slot % R};
+    Cursor cn = cc;
+    advance(cn);
+    Cursor cnn = cn;
+    advance(cnn);
+    int64_t tc = qidx[edge_of(cc)];
+    int64_t tn = qidx[edge_of(cn)];
+    Rows cur;
+    fetch(cc, tc, cur);
+    // lane 0 holds a step's first row: the step is live while that row is
+    while (__builtin_amdgcn_readfirstlane(static_cast<int>(cc.e < e1))) {
+      Rows nxt;
+      fetch(cn, tn, nxt);
+      const int64_t tnn = qidx[edge_of(cnn)];
+      const bool ok = cc.e < e1 && tc >= j;
+      float qv[8], gdv[8];
+      unpack8<DT>(cur.qw, qv);
+      unpack8<DT>(cur.gw, gdv);
+      double sp = 0.0, dp = 0.0;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if constexpr (DT == kF32) {
+          sp = fma(static_cast<double>(qv[u]), static_cast<double>(kr[u]), sp);
+          dp = fma(static_cast<double>(gdv[u]), static_cast<double>(vr[u]), dp);
+        } else {  // a product of two 2-byte floats is exact in fp32: the same FP64 sum
+          sp += static_cast<double>(qv[u] * kr[u]);
+          dp += static_cast<double>(gdv[u] * vr[u]);
+        }
+      }
+#pragma unroll
+      for (int o = 1; o < LPR; o <<= 1) {
+        sp += __shfl_xor(sp, o, kWave);
+        dp += __shfl_xor(dp, o, kWave);
+      }
+      if (ok) {
+        const double p = exp(sp * scale - cur.rs01.x) / cur.rs01.y;
+        const double dsv = p * ((dp - cur.rs23.x) - cur.rs23.y) * scale;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          gk[u] = fma(dsv, static_cast<double>(qv[u]), gk[u]);
+          gv[u] = fma(p, static_cast<double>(gdv[u]), gv[u]);
+        }
+      }
+      cur = nxt;
+      tc = tn;
+      tn = tnn;
+      cc = cn;
+      cn = cnn;
+      advance(cnn);
+    }
+  }
+#pragma unroll
+  for (int o = LPR; o < kWave; o <<= 1) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      gk[u] += __shfl_xor(gk[u], o, kWave);
+      gv[u] += __shfl_xor(gv[u], o, kWave);
+    }
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (dk) store_from_f64<DT>(dk, jg * D + 8 * dch + u, gk[u]);
+      if (dv) store_from_f64<DT>(dv, jg * D + 8 * dch + u, gv[u]);
+    }
+  }
+}
+
 template <int DT, int DPL>
 int attn_valu_launch_fwd(const void* q, const void* k, const void* v, const int32_t* idx, const int32_t* cu,
                          int nseq, int64_t T, int Hq, int G, int D, int K, int B, double scale, void* out,
@@ -356,6 +499,20 @@ int attn_valu_launch_dkdv(const void* q, const void* k, const void* v, const voi
                           const int32_t* cu, const int32_t* cu_blocks, const int32_t* row_ptr, const int32_t* qidx,
                           int nseq, int64_t T, int Hq, int G, int D, int B, double scale, void* dk, void* dv,
                           hipStream_t st) {
+  const bool aligned = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
+                         reinterpret_cast<uintptr_t>(dout) | reinterpret_cast<uintptr_t>(rs)) & 15) == 0;
+  if (aligned && (D == 8 || D == 16 || D == 32 || D == 64 || D == 128)) {
+#define MSA_DKDV_ROWS(LPRV) hipLaunchKernelGGL((attn_bwd_dkdv_rows<DT, LPRV>), dim3(grid_1d(T * G, 4)), dim3(256), 0, st, q, k, v, dout, rs, cu, cu_blocks, row_ptr, qidx, nseq, T, Hq, G, D, B, scale, dk, dv)
+    switch (D / 8) {
+      case 1: MSA_DKDV_ROWS(1); break;
+      case 2: MSA_DKDV_ROWS(2); break;
+      case 4: MSA_DKDV_ROWS(4); break;
+      case 8: MSA_DKDV_ROWS(8); break;
+      default: MSA_DKDV_ROWS(16); break;
+    }
+#undef MSA_DKDV_ROWS
+    return status_from(hipGetLastError());
+  }
   for (int dc0 = 0; dc0 < D; dc0 += DPL * kWave)
     hipLaunchKernelGGL((attn_bwd_dkdv_valu<DT, DPL>), dim3(grid_1d(T * G, 4)), dim3(256), 0, st, q, k, v, dout, rs,
                        cu, cu_blocks, row_ptr, qidx, nseq, T, Hq, G, D, B, scale, dk, dv, dc0);
