@@ -716,26 +716,21 @@ def main():
 
         # fp16 inputs take the FP64 VALU kernels (an fp16 output has three more significant bits
         # than bf16, and fp32-accumulated MFMA sums would move too many of them across a rounding
-        # midpoint for the reference's gate): timed on c2's workload (T = 8192), one step at a time
-        c2 = CONFIGS["c2"]
-        c2_t = [x.to(device) for x in make_inputs(c2)]
-        c2_cu = torch.tensor([0, c2["lengths"][0]], dtype=torch.int32, device=device)
-        with torch.no_grad():
-            c2_ids = msa.m3_topk(msa.m3_index_score(c2_t[0], c2_t[1], c2_cu, c2["lengths"][0], block_size=c2["block"]),
-                                 c2_cu, block_size=c2["block"], topk_blocks=c2["topk"], local_blocks=c2["local"])
-        h16 = [x.half().requires_grad_() for x in c2_t[2:5]]
-        dout16 = c2_t[5].half()
+        # midpoint for the reference's gate): the same step on this config's inputs and
+        # selection, converted to fp16, one step at a time
+        h16 = [x.detach().half().requires_grad_() for x in (q, k, v)]
+        dout16 = dout.half()
 
         def step_fp16():
             for x in h16:
                 x.grad = None
-            msa.m3_sparse_attention(*h16, c2_ids, c2_cu, c2["lengths"][0], block_size=c2["block"]).backward(dout16)
+            msa.m3_sparse_attention(*h16, ids, cu, max_len, block_size=block).backward(dout16)
 
-        stages["attention_fwd_bwd_fp16_c2_ms"] = round(time_events(step_fp16, 3)["median"], 4)
-        c2_flops = 3.5 * 4.0 * c2["d"] * (c2["hq"] // c2["g"]) * visible_keys(c2)
-        log(f"attention_fwd_bwd_fp16_c2_ms: {stages['attention_fwd_bwd_fp16_c2_ms']:.3f} "
-            f"({c2_flops / stages['attention_fwd_bwd_fp16_c2_ms'] / 1e9:.1f} TFLOP/s)")
-        del h16, dout16, c2_t
+        stages["attention_fwd_bwd_fp16_ms"] = round(time_events(step_fp16, 3)["median"], 4)
+        peak_mem["attention_fwd_bwd_fp16"] = round(peak_bytes(step_fp16) / 2**20, 1)
+        log(f"attention_fwd_bwd_fp16_ms: {stages['attention_fwd_bwd_fp16_ms']:.3f} "
+            f"({step_flops / stages['attention_fwd_bwd_fp16_ms'] / 1e9:.1f} TFLOP/s)")
+        del h16, dout16
         # the same autograd step with prepared sequence metadata (no host reads of
         # cu_seqlens), eager and replayed from a HIP graph capture
         seqs = msa.prepare_sequences(cu, block_size=block)
@@ -808,11 +803,9 @@ def main():
             "indexer_kl": {"bound": "mfma", "unit": "TFLOP/s",
                            **frac(keys * (2.0 * cfg["d"] * (cfg["hq"] // cfg["g"]) + 6.0 * cfg["di"]),
                                   stages["indexer_kl_fwd_bwd_ms"], MFMA_BF16_PEAK_TFLOPS, 1e12)},
-            # fp16 at c2 on the FP64 VALU kernels, against the dense fp64 vector peak (78.6 TFLOP/s)
-            "attention_fwd_bwd_fp16_c2": {"bound": "valu_f64", "unit": "TFLOP/s",
-                                          **frac(3.5 * 4.0 * CONFIGS["c2"]["d"] * (CONFIGS["c2"]["hq"] // CONFIGS["c2"]["g"])
-                                                 * visible_keys(CONFIGS["c2"]),
-                                                 stages["attention_fwd_bwd_fp16_c2_ms"], 78.6, 1e12)},
+            # fp16 on the FP64 VALU kernels, against the dense fp64 vector peak (78.6 TFLOP/s)
+            "attention_fwd_bwd_fp16": {"bound": "valu_f64", "unit": "TFLOP/s",
+                                       **frac(step_flops, stages["attention_fwd_bwd_fp16_ms"], 78.6, 1e12)},
         }
 
     baseline = None

@@ -38,10 +38,6 @@ __device__ __forceinline__ RowCtx row_ctx(const int32_t* __restrict__ cu, int ns
   return c;
 }
 
-// Elements [i, i + 8) of a row as fp32, from one 16-byte load (2-byte dtypes) or two
-// (fp32); i a multiple of 8 (16-byte aligned). A lane walking its own key row this way
-// issues one load instruction per 8 elements instead of one per element: with 64 lanes
-// on 64 different rows, the address unit, not the FP64 arithmetic, limits these kernels.
 // Eight consecutive elements kept as loaded (16 bytes for 2-byte types, 32 for fp32),
 // and their fp32 values.
 template <int DT>
@@ -82,7 +78,10 @@ __device__ __forceinline__ void unpack8(const Raw8<DT>& r, float (&x)[8]) {
   }
 }
 
-// Eight consecutive elements base[i .. i + 7] as fp32 (i 16-byte aligned).
+// Elements [i, i + 8) of a row as fp32, from one 16-byte load (2-byte dtypes) or two
+// (fp32); i a multiple of 8 (16-byte aligned). A lane walking its own key row this way
+// issues one load instruction per 8 elements instead of one per element: with 64 lanes
+// on 64 different rows, the address unit, not the FP64 arithmetic, limits these kernels.
 template <int DT>
 __device__ __forceinline__ void load8_as_f32(const void* __restrict__ base, int64_t i, float (&x)[8]) {
   unpack8<DT>(load8_raw<DT>(base, i), x);
@@ -278,6 +277,195 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_valu(
   }
 }
 
+// Row-parallel form of the two query-pass kernels above for D = 8 LPR, LPR in
+// {1, 2, 4, 8, 16}, 16-byte aligned rows: the logits stay one lane per key, but the
+// key-weighted row sums (P.V in the forward, the two K sums of dQ) take LPR lanes per
+// key row (8 dims each, one 16-byte load), RPW = 64 / LPR keys a step instead of one
+// key per step with 2-byte loads. Each key slot (lane / LPR) keeps its own FP64 partial
+// sums, added pairwise over the slots at the end (a fixed butterfly).
+template <int DT, int LPR>
+__global__ __launch_bounds__(256) void attn_fwd_rows(const void* __restrict__ q, const void* __restrict__ k,
+                                                     const void* __restrict__ v,
+                                                     const int32_t* __restrict__ indices,
+                                                     const int32_t* __restrict__ cu, int nseq, int64_t T,
+                                                     int Hq, int G, int D, int K, int B, double scale,
+                                                     void* __restrict__ out, float* __restrict__ lse,
+                                                     double* __restrict__ row_state, float* __restrict__ o32) {
+  constexpr int RPW = kWave / LPR;
+  extern __shared__ float smem[];
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t th = static_cast<int64_t>(blockIdx.x) * 4 + wid;
+  const bool active = th < T * Hq;
+  float* qs = smem + wid * D;
+  if (active)
+    for (int d = lane; d < D; d += kWave) qs[d] = load_as_f32<DT>(q, th * D + d);
+  __syncthreads();
+  if (!active) return;
+  const int slot = lane / LPR, dch = lane % LPR;
+  const int64_t t = th / Hq;
+  const int h = static_cast<int>(th % Hq);
+  const int g = h / (Hq / G);
+  const RowCtx rc = row_ctx(cu, nseq, t, B);
+  double m = -__builtin_inf(), l = 0.0;
+  double o[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) o[u] = 0.0;
+  const int32_t* sel = indices + (t * G + g) * K;
+  for (int sk = 0; sk < K; ++sk) {
+    const int blk = sel[sk];
+    if (blk < 0 || blk > rc.qb) continue;
+    const int64_t kb0 = rc.start + static_cast<int64_t>(blk) * B;
+    const int64_t kend = (kb0 + B < t + 1) ? kb0 + B : t + 1;
+    for (int64_t base = kb0; base < kend; base += kWave) {
+      const int64_t key = base + lane;
+      double sv = -__builtin_inf();
+      if (key < kend) sv = row_dot<DT>(qs, k, (key * G + g) * D, D) * scale;
+      const double mt = wave_max_f64(sv);
+      const double mn = fmax(m, mt);
+      const double alpha = (m == -__builtin_inf()) ? 0.0 : exp(m - mn);
+      const double p = (key < kend) ? exp(sv - mn) : 0.0;
+      l = l * alpha + wave_sum_f64(p);
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o[u] *= alpha;
+      const int n = kend - base < kWave ? static_cast<int>(kend - base) : kWave;
+      for (int i0 = 0; i0 < n; i0 += RPW) {
+        const int i = i0 + slot;  // <= 63: i0 < n <= 64 and RPW divides 64
+        const double pi = __shfl(p, i, kWave);
+        const Raw8<DT> w = load8_raw<DT>(v, ((base + (i < n ? i : 0)) * G + g) * D + 8 * dch);
+        if (i < n) {
+          float x[8];
+          unpack8<DT>(w, x);
+#pragma unroll
+          for (int u = 0; u < 8; ++u) o[u] = fma(pi, static_cast<double>(x[u]), o[u]);
+        }
+      }
+      m = mn;
+    }
+  }
+#pragma unroll
+  for (int off = LPR; off < kWave; off <<= 1) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) o[u] += __shfl_xor(o[u], off, kWave);
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t d = th * D + 8 * dch + u;
+      const double r = l > 0.0 ? o[u] / l : 0.0;
+      store_from_f64<DT>(out, d, r);
+      if (o32) o32[d] = static_cast<float>(r);
+    }
+  }
+  if (lane == 0) {
+    const double full = l > 0.0 ? m + log(l) : -__builtin_inf();
+    lse[th] = static_cast<float>(full);
+    if (row_state) {
+      row_state[th * 4] = full;
+      row_state[th * 4 + 1] = 1.0;  // FP64 lse: p = exp(x - lse) needs no mass correction
+    }
+  }
+}
+
+template <int DT, int LPR>
+__global__ __launch_bounds__(256) void attn_bwd_dq_rows(
+    const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
+    const void* __restrict__ out, const void* __restrict__ dout, double* __restrict__ row_state,
+    const int32_t* __restrict__ indices, const int32_t* __restrict__ cu, int nseq, int64_t T, int Hq, int G,
+    int D, int K, int B, double scale, void* __restrict__ dq) {
+  constexpr int RPW = kWave / LPR;
+  extern __shared__ float smem[];
+  const int wid = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t th = static_cast<int64_t>(blockIdx.x) * 4 + wid;
+  const bool active = th < T * Hq;
+  float* qs = smem + wid * 2 * D;
+  float* gs = qs + D;
+  double cpart = 0.0;
+  if (active) {
+    for (int d = lane; d < D; d += kWave) {
+      qs[d] = load_as_f32<DT>(q, th * D + d);
+      const float gd = load_as_f32<DT>(dout, th * D + d);
+      gs[d] = gd;
+      cpart = fma(static_cast<double>(load_as_f32<DT>(out, th * D + d)), static_cast<double>(gd), cpart);
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  const int slot = lane / LPR, dch = lane % LPR;
+  const int64_t t = th / Hq;
+  const int h = static_cast<int>(th % Hq);
+  const int g = h / (Hq / G);
+  const RowCtx rc = row_ctx(cu, nseq, t, B);
+  const double c = wave_sum_f64(cpart);
+  const double row_lse = row_state[th * 4];
+  double mass = 0.0, delta = 0.0;
+  double a[8], bsum[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) a[u] = bsum[u] = 0.0;
+  const int32_t* sel = indices + (t * G + g) * K;
+  if (row_lse != -__builtin_inf()) {
+    for (int sk = 0; sk < K; ++sk) {
+      const int blk = sel[sk];
+      if (blk < 0 || blk > rc.qb) continue;
+      const int64_t kb0 = rc.start + static_cast<int64_t>(blk) * B;
+      const int64_t kend = (kb0 + B < t + 1) ? kb0 + B : t + 1;
+      for (int64_t base = kb0; base < kend; base += kWave) {
+        const int64_t key = base + lane;
+        double p = 0.0, uu = 0.0;
+        if (key < kend) {
+          const int64_t off = (key * G + g) * D;
+          const double sacc = row_dot<DT>(qs, k, off, D), dacc = row_dot<DT>(gs, v, off, D);
+          p = exp(sacc * scale - row_lse);
+          uu = p * (dacc - c);
+          mass += p;
+          delta += uu;
+        }
+        const int n = kend - base < kWave ? static_cast<int>(kend - base) : kWave;
+        for (int i0 = 0; i0 < n; i0 += RPW) {
+          const int i = i0 + slot;  // <= 63: i0 < n <= 64 and RPW divides 64
+          const double pi = __shfl(p, i, kWave);
+          const double ui = __shfl(uu, i, kWave);
+          const Raw8<DT> w = load8_raw<DT>(k, ((base + (i < n ? i : 0)) * G + g) * D + 8 * dch);
+          if (i < n) {
+            float x[8];
+            unpack8<DT>(w, x);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              a[u] = fma(ui, static_cast<double>(x[u]), a[u]);
+              bsum[u] = fma(pi, static_cast<double>(x[u]), bsum[u]);
+            }
+          }
+        }
+      }
+    }
+  }
+  const double msum = wave_sum_f64(mass);
+  const double dsum = wave_sum_f64(delta);
+  const bool has = msum > 0.0;
+  const double dhat = has ? dsum / msum : 0.0;
+  if (dq) {
+#pragma unroll
+    for (int off = LPR; off < kWave; off <<= 1) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        a[u] += __shfl_xor(a[u], off, kWave);
+        bsum[u] += __shfl_xor(bsum[u], off, kWave);
+      }
+    }
+    if (slot == 0) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const double val = has ? static_cast<double>(scale) * (a[u] - dhat * bsum[u]) / msum : 0.0;
+        store_from_f64<DT>(dq, th * D + 8 * dch + u, val);
+      }
+    }
+  }
+  if (lane == 0) {
+    row_state[th * 4 + 1] = has ? msum : 1.0;
+    row_state[th * 4 + 2] = c;
+    row_state[th * 4 + 3] = dhat;
+  }
+}
+
 // KV-pass backward: one wavefront per (key token, group); walks the key's
 // (block, group) CSR row in order, all R heads of each edge.
 template <int DT, int DPL>
@@ -361,8 +549,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_valu(
 // (edge e, head r, in order) goes to slot i % RPW. A row's two dot products reduce over
 // its LPR lanes only, and one exponential serves RPW rows. Each slot sums its rows in
 // order; the slot sums are then added pairwise (a fixed butterfly over the slot index).
-template <int DT, int LPR>
-__global__ __launch_bounds__(256, DT == kF32 ? 2 : 3) void attn_bwd_dkdv_rows(
+template <int DT, int LPR, int NC>
+__global__ __launch_bounds__(256, DT == kF32 || NC == 2 ? 2 : 3) void attn_bwd_dkdv_rows(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
     const void* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ row_ptr, const int32_t* __restrict__ qidx,
@@ -379,12 +567,16 @@ __global__ __launch_bounds__(256, DT == kF32 ? 2 : 3) void attn_bwd_dkdv_rows(
   const int64_t row = (static_cast<int64_t>(cu_blocks[s]) + blk) * G + g;
   const int64_t e0 = row_ptr[row], e1 = row_ptr[row + 1];
   const int R = Hq / G;
-  float kr[8], vr[8];
-  load8_as_f32<DT>(k, jg * D + 8 * dch, kr);
-  load8_as_f32<DT>(v, jg * D + 8 * dch, vr);
-  double gk[8], gv[8];
+  constexpr int E = 8 * NC;  // dims per lane: [E dch, E dch + E)
+  float kr[E], vr[E];
 #pragma unroll
-  for (int u = 0; u < 8; ++u) gk[u] = gv[u] = 0.0;
+  for (int c = 0; c < NC; ++c) {
+    load8_as_f32<DT>(k, jg * D + E * dch + 8 * c, *reinterpret_cast<float(*)[8]>(kr + 8 * c));
+    load8_as_f32<DT>(v, jg * D + E * dch + 8 * c, *reinterpret_cast<float(*)[8]>(vr + 8 * c));
+  }
+  double gk[E], gv[E];
+#pragma unroll
+  for (int u = 0; u < E; ++u) gk[u] = gv[u] = 0.0;
   // Row i = (e - e0) R + r is walked as the pair (e, r), RPW rows a step. Software
   // pipeline: the query index two steps ahead, the rows one step ahead (positions past the
   // end read the row's first edge, so every load stays in bounds).
@@ -397,11 +589,14 @@ __global__ __launch_bounds__(256, DT == kF32 ? 2 : 3) void attn_bwd_dkdv_rows(
     if (c.r >= R) c.r -= R, ++c.e;
   };
   auto edge_of = [&](const Cursor& c) -> int64_t { return c.e < e1 ? c.e : e0; };
-  struct Rows { Raw8<DT> qw, gw; double2 rs01, rs23; };
+  struct Rows { Raw8<DT> qw[NC], gw[NC]; double2 rs01, rs23; };
   auto fetch = [&](const Cursor& c, int64_t t, Rows& x) {
     const int64_t th = t * Hq + static_cast<int64_t>(g) * R + (c.e < e1 ? c.r : 0);
-    x.qw = load8_raw<DT>(q, th * D + 8 * dch);
-    x.gw = load8_raw<DT>(dout, th * D + 8 * dch);
+#pragma unroll
+    for (int z = 0; z < NC; ++z) {
+      x.qw[z] = load8_raw<DT>(q, th * D + E * dch + 8 * z);
+      x.gw[z] = load8_raw<DT>(dout, th * D + E * dch + 8 * z);
+    }
     x.rs01 = reinterpret_cast<const double2*>(row_state)[th * 2];
     x.rs23 = reinterpret_cast<const double2*>(row_state)[th * 2 + 1];
   };
@@ -421,12 +616,15 @@ __global__ __launch_bounds__(256, DT == kF32 ? 2 : 3) void attn_bwd_dkdv_rows(
       fetch(cn, tn, nxt);
       const int64_t tnn = qidx[edge_of(cnn)];
       const bool ok = cc.e < e1 && tc >= j;
-      float qv[8], gdv[8];
-      unpack8<DT>(cur.qw, qv);
-      unpack8<DT>(cur.gw, gdv);
+      float qv[E], gdv[E];
+#pragma unroll
+      for (int z = 0; z < NC; ++z) {
+        unpack8<DT>(cur.qw[z], *reinterpret_cast<float(*)[8]>(qv + 8 * z));
+        unpack8<DT>(cur.gw[z], *reinterpret_cast<float(*)[8]>(gdv + 8 * z));
+      }
       double sp = 0.0, dp = 0.0;
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < E; ++u) {
         if constexpr (DT == kF32) {
           sp = fma(static_cast<double>(qv[u]), static_cast<double>(kr[u]), sp);
           dp = fma(static_cast<double>(gdv[u]), static_cast<double>(vr[u]), dp);
@@ -444,7 +642,7 @@ __global__ __launch_bounds__(256, DT == kF32 ? 2 : 3) void attn_bwd_dkdv_rows(
         const double p = exp(sp * scale - cur.rs01.x) / cur.rs01.y;
         const double dsv = p * ((dp - cur.rs23.x) - cur.rs23.y) * scale;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < E; ++u) {
           gk[u] = fma(dsv, static_cast<double>(qv[u]), gk[u]);
           gv[u] = fma(p, static_cast<double>(gdv[u]), gv[u]);
         }
@@ -460,24 +658,47 @@ __global__ __launch_bounds__(256, DT == kF32 ? 2 : 3) void attn_bwd_dkdv_rows(
 #pragma unroll
   for (int o = LPR; o < kWave; o <<= 1) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
+    for (int u = 0; u < E; ++u) {
       gk[u] += __shfl_xor(gk[u], o, kWave);
       gv[u] += __shfl_xor(gv[u], o, kWave);
     }
   }
   if (slot == 0) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      if (dk) store_from_f64<DT>(dk, jg * D + 8 * dch + u, gk[u]);
-      if (dv) store_from_f64<DT>(dv, jg * D + 8 * dch + u, gv[u]);
+    for (int u = 0; u < E; ++u) {
+      if (dk) store_from_f64<DT>(dk, jg * D + E * dch + u, gk[u]);
+      if (dv) store_from_f64<DT>(dv, jg * D + E * dch + u, gv[u]);
     }
   }
 }
+
+// The row-parallel kernels take D = 8 LPR (LPR a power of two up to 16) and rows that
+// start on 16-byte boundaries.
+template <typename... P>
+bool rows_fit(int D, const P*... ptrs) {
+  const uintptr_t bits = (reinterpret_cast<uintptr_t>(ptrs) | ...);
+  return (D == 8 || D == 16 || D == 32 || D == 64 || D == 128) && (bits & 15) == 0;
+}
+
+#define MSA_ROWS_SWITCH(D, LAUNCH) \
+  switch ((D) / 8) {               \
+    case 1: LAUNCH(1); break;      \
+    case 2: LAUNCH(2); break;      \
+    case 4: LAUNCH(4); break;      \
+    case 8: LAUNCH(8); break;      \
+    default: LAUNCH(16); break;    \
+  }
 
 template <int DT, int DPL>
 int attn_valu_launch_fwd(const void* q, const void* k, const void* v, const int32_t* idx, const int32_t* cu,
                          int nseq, int64_t T, int Hq, int G, int D, int K, int B, double scale, void* out,
                          float* lse, double* rs, float* o32, hipStream_t st) {
+  if (rows_fit(D, q, k, v)) {
+#define MSA_FWD_ROWS(LPRV) hipLaunchKernelGGL((attn_fwd_rows<DT, LPRV>), dim3(grid_1d(T * Hq, 4)), dim3(256), 4 * D * sizeof(float), st, q, k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse, rs, o32)
+    MSA_ROWS_SWITCH(D, MSA_FWD_ROWS);
+#undef MSA_FWD_ROWS
+    return status_from(hipGetLastError());
+  }
   for (int dc0 = 0; dc0 < D; dc0 += DPL * kWave)
     hipLaunchKernelGGL((attn_fwd_valu<DT, DPL>), dim3(grid_1d(T * Hq, 4)), dim3(256), 4 * D * sizeof(float), st, q,
                        k, v, idx, cu, nseq, T, Hq, G, D, K, B, scale, out, lse, rs, o32, dc0);
@@ -488,6 +709,12 @@ template <int DT, int DPL>
 int attn_valu_launch_dq(const void* q, const void* k, const void* v, const void* out, const void* dout, double* rs,
                         const int32_t* idx, const int32_t* cu, int nseq, int64_t T, int Hq, int G, int D, int K,
                         int B, double scale, void* dq, hipStream_t st) {
+  if (rows_fit(D, q, k, v, dout)) {
+#define MSA_DQ_ROWS(LPRV) hipLaunchKernelGGL((attn_bwd_dq_rows<DT, LPRV>), dim3(grid_1d(T * Hq, 4)), dim3(256), 8 * D * sizeof(float), st, q, k, v, out, dout, rs, idx, cu, nseq, T, Hq, G, D, K, B, scale, dq)
+    MSA_ROWS_SWITCH(D, MSA_DQ_ROWS);
+#undef MSA_DQ_ROWS
+    return status_from(hipGetLastError());
+  }
   for (int dc0 = 0; dc0 < D; dc0 += DPL * kWave)
     hipLaunchKernelGGL((attn_bwd_dq_valu<DT, DPL>), dim3(grid_1d(T * Hq, 4)), dim3(256), 8 * D * sizeof(float),
                        st, q, k, v, out, dout, rs, idx, cu, nseq, T, Hq, G, D, K, B, scale, dq, dc0);
@@ -499,16 +726,17 @@ int attn_valu_launch_dkdv(const void* q, const void* k, const void* v, const voi
                           const int32_t* cu, const int32_t* cu_blocks, const int32_t* row_ptr, const int32_t* qidx,
                           int nseq, int64_t T, int Hq, int G, int D, int B, double scale, void* dk, void* dv,
                           hipStream_t st) {
-  const bool aligned = ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v) |
-                         reinterpret_cast<uintptr_t>(dout) | reinterpret_cast<uintptr_t>(rs)) & 15) == 0;
-  if (aligned && (D == 8 || D == 16 || D == 32 || D == 64 || D == 128)) {
-#define MSA_DKDV_ROWS(LPRV) hipLaunchKernelGGL((attn_bwd_dkdv_rows<DT, LPRV>), dim3(grid_1d(T * G, 4)), dim3(256), 0, st, q, k, v, dout, rs, cu, cu_blocks, row_ptr, qidx, nseq, T, Hq, G, D, B, scale, dk, dv)
-    switch (D / 8) {
-      case 1: MSA_DKDV_ROWS(1); break;
-      case 2: MSA_DKDV_ROWS(2); break;
-      case 4: MSA_DKDV_ROWS(4); break;
-      case 8: MSA_DKDV_ROWS(8); break;
-      default: MSA_DKDV_ROWS(16); break;
+  if (rows_fit(D, q, k, v, dout, rs)) {
+#define MSA_DKDV_ROWS(LPRV, NCV) hipLaunchKernelGGL((attn_bwd_dkdv_rows<DT, LPRV, NCV>), dim3(grid_1d(T * G, 4)), dim3(256), 0, st, q, k, v, dout, rs, cu, cu_blocks, row_ptr, qidx, nseq, T, Hq, G, D, B, scale, dk, dv)
+    switch (D) {  // 2-byte types at D = 128: 16 dims a lane; otherwise 8
+      case 8: MSA_DKDV_ROWS(1, 1); break;
+      case 16: MSA_DKDV_ROWS(2, 1); break;
+      case 32: MSA_DKDV_ROWS(4, 1); break;
+      case 64: MSA_DKDV_ROWS(8, 1); break;
+      default:
+        if constexpr (DT == kF32) MSA_DKDV_ROWS(16, 1);
+        else MSA_DKDV_ROWS(8, 2);
+        break;
     }
 #undef MSA_DKDV_ROWS
     return status_from(hipGetLastError());
