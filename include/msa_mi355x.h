@@ -47,6 +47,19 @@ int msa_k2q_build(const int32_t* indices, const int32_t* cu_seqlens, const int32
                   int64_t counter_elems, int32_t* row_ptr, int32_t* query_indices,
                   int32_t* slot_indices, int32_t* workspace, void* stream);
 
+/* Sub-block form of a selection, for blocks larger than the MFMA kernels' 128-key
+ * tiles. With f dividing B, sub-block f b + i (size B / f) holds keys
+ * [b B + i B / f, b B + (i + 1) B / f): the f sub-blocks of id b hold exactly the keys
+ * the reference's kernels visit for block b (triton/sparse_attention.py:35-84 forward,
+ * :87-198 and :223-295 backward), and a sub-block that starts after the query is
+ * skipped by the same id <= query-block rule. out [rows, slots * factor]:
+ * out[r, s f + i] = f in[r, s] + i, or -1 where in[r, s] < 0 or f in[r, s] + i would
+ * pass INT32_MAX. The sub-block selection with its CSR (msa_k2q_build at
+ * block_size / factor) and block_size / factor gives the attention of the original
+ * selection. No counterpart in the reference (its kernels take any block size). */
+int msa_split_block_indices(const int32_t* indices, int64_t rows, int64_t slots, int32_t factor, int32_t* out,
+                            void* stream);
+
 /* msa_k2q_build without the workspace argument; allocates nothing. No counterpart in
  * the reference: for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc). Its workspace is a

@@ -34,6 +34,7 @@ SIGNATURES = {
                              _vp, _vp, _vp, _vp, _vp]),
     "msa_k2q_build_noalloc": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                                      _vp, _vp, _vp, _vp]),
+    "msa_split_block_indices": (_i32, [_vp, _i64, _i64, _i32, _vp, _vp]),
     "msa_score_fwd_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "msa_score_fwd": (_i32, [_vp, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _f64,
                              _vp, _vp, _vp, _vp]),

@@ -20,6 +20,7 @@
 //                    edges on their block id places each edge at row_ptr[row] +
 //                    tile offset + its rank among the tile's edges of that row.
 //   5. k2q_tail    : entries at or beyond row_ptr[rows] become -1.
+#include <algorithm>
 #include <mutex>
 
 #include "common.hpp"
@@ -410,4 +411,37 @@ extern "C" int msa_k2q_build_noalloc(const int32_t* indices, const int32_t* cu_s
   return k2q_build_launch(indices, cu_seqlens, cu_block_lens, tri_prefix, num_seqs, total_tokens, groups,
                           topk_slots, block_size, total_blocks, counter_elems, row_ptr, query_indices, slot_indices,
                           ws, static_cast<hipStream_t>(stream));
+}
+
+namespace msa {
+namespace {
+
+// out[r, s f + i] = f indices[r, s] + i (i < f), or -1 where indices[r, s] is negative or
+// f indices[r, s] + i would pass INT32_MAX (no sequence has that many sub-blocks, so such
+// an id selects nothing either way). Grid-stride over the n f outputs.
+__global__ __launch_bounds__(256) void split_blocks_kernel(const int32_t* __restrict__ indices, int64_t n, int f,
+                                                           int32_t* __restrict__ out) {
+  const int32_t limit = (INT32_MAX - (f - 1)) / f;
+  const int64_t total = n * f;
+  for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total;
+       o += static_cast<int64_t>(gridDim.x) * 256) {
+    const int32_t b = indices[o / f];
+    out[o] = (b >= 0 && b <= limit) ? b * f + static_cast<int32_t>(o % f) : -1;
+  }
+}
+
+}  // namespace
+}  // namespace msa
+
+extern "C" int msa_split_block_indices(const int32_t* indices, int64_t rows, int64_t slots, int32_t factor,
+                                       int32_t* out, void* stream) {
+  if (rows < 0 || slots < 0 || factor <= 0 || (rows > 0 && slots > 0 && (!indices || !out)))
+    return kErrInvalidArgument;
+  if (slots > (int64_t(1) << 31) / factor) return kErrUnsupported;  // sub-block slots per row in int32
+  const int64_t n = rows * slots;
+  if (n == 0) return kOk;
+  const int64_t blocks = std::min<int64_t>((n * factor + 255) / 256, 65536);
+  hipLaunchKernelGGL(split_blocks_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), indices, n, static_cast<int>(factor), out);
+  return status_from(hipGetLastError());
 }

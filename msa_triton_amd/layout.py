@@ -17,6 +17,7 @@ do not reach it (the stale-cache hazard of keying a cache on the caller's tensor
 
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 
 import torch
@@ -132,6 +133,28 @@ def prepare_sequences(cu_seqlens: torch.Tensor, *, block_size: int = 128) -> Pac
         tile_prefix=torch.tensor(meta.tri_prefix, dtype=torch.int64, device=device),
         meta=meta,
     )
+
+
+# PackedSequences re-described for other block sizes, kept with the original.
+_OTHER_BLOCK_SIZES: "weakref.WeakKeyDictionary[PackedSequences, dict[int, PackedSequences]]" = weakref.WeakKeyDictionary()
+
+
+def with_block_size(seqs: PackedSequences, block_size: int) -> PackedSequences:
+    """``seqs`` for another block size: the same ``cu_seqlens`` tensor, block metadata
+    recomputed on the host from ``seqs.meta`` (no device read) and copied to the device
+    on the first request only; later requests return the cached object."""
+    if block_size == seqs.block_size:
+        return seqs
+    cache = _OTHER_BLOCK_SIZES.setdefault(seqs, {})
+    if block_size not in cache:
+        meta = sequence_meta(list(seqs.meta.bounds), block_size)
+        cache[block_size] = PackedSequences(
+            cu_seqlens=seqs.cu_seqlens,
+            cu_block_lens=torch.tensor(meta.cu_block_lens, dtype=torch.int32, device=seqs.device),
+            tile_prefix=torch.tensor(meta.tri_prefix, dtype=torch.int64, device=seqs.device),
+            meta=meta,
+        )
+    return cache[block_size]
 
 
 def prepared_for(seqs: PackedSequences, *, block_size: int, total_tokens: int, device: torch.device) -> SequenceMeta:
