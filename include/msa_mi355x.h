@@ -214,7 +214,7 @@ int msa_indexer_kl(const void* index_q, const void* index_k, const void* q, cons
 
 /* Testing hook; no counterpart in the reference. Overrides the byte budgets that size
  * the query-token chunks of the KV-major bf16 passes: msa_attn_fwd (default 2 GiB of
- * per-(token, head, slot) partial records per chunk), msa_attn_bwd (6 GiB) and
+ * per-(token, head, slot) partial records per chunk), msa_attn_bwd (3 GiB) and
  * msa_indexer_kl (1 GiB); a value <= 0 restores that default. A chunk holds at least
  * 64 tokens. Chunking changes only how sums are split into per-chunk partial sums,
  * not what is computed; tests use it to drive small cases through many chunks.

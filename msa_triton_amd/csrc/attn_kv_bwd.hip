@@ -803,7 +803,7 @@ static BwdLayout bwd_layout(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t
   const int64_t rows = total_blocks * G;
   const int64_t R = Hq / (G > 0 ? G : 1);
   const int64_t DP = 32 * nk_of_dim(static_cast<int>(D));
-  const int64_t tc = kv_chunk_tokens(T, Hq, K, D * 4 + 8, kv_chunk_budget(kPassBwd, int64_t(6) << 30));
+  const int64_t tc = kv_chunk_tokens(T, Hq, K, D * 4 + 8, kv_chunk_budget(kPassBwd, int64_t(3) << 30));
   int64_t sepi = static_cast<int64_t>(kStatItemRows) / (R > 0 ? R : 1);
   if (sepi < 1) sepi = 1;
   b.stat_plan = kv_plan_layout(T, rows, G, K, tc, sepi);

@@ -60,8 +60,8 @@ def _sample_tokens(lengths, block, rng, extra=4):
     return np.array(sorted(out), dtype=np.int64)
 
 
-# Backward chunk budget per config: the default (6 GiB) except c3, which fits in one chunk
-# there; at 2 GiB its third sequence's keys are summed across three chunks.
+# Backward chunk budget per config: the default (3 GiB) except c3, set to 2 GiB so that its
+# third sequence's keys are summed across three chunks.
 BWD_BUDGET = {"c3": 2 << 30}
 
 
@@ -81,7 +81,7 @@ def _sample_keys(lengths, block, name):
     early keys whose blocks are selected by query tokens of several backward chunks, so
     that their dK / dV are sums the backward carries across chunks: c3's third sequence
     (tokens 5120-10239 straddle the chunk boundary at 5462 at its 2 GiB budget), c4 blocks
-    0, 40 and 120 (two chunks), c5 blocks 0 and 3 (eleven chunks)."""
+    0, 40 and 120 (three chunks), c5 blocks 0 and 3 (22 chunks)."""
     bounds = _bounds(lengths)
     s = int(np.argmax(lengths))
     a, n = bounds[s], lengths[s]
@@ -99,7 +99,7 @@ def _sample_keys(lengths, block, name):
 
 def _assert_multi_chunk_keys(cfg, name, ids_np, bounds, keys):
     """Each early key of c3-c5 gets edges from at least two backward chunks."""
-    tc = _bwd_chunk_tokens(cfg, bounds[-1], BWD_BUDGET.get(name, 6 << 30))
+    tc = _bwd_chunk_tokens(cfg, bounds[-1], BWD_BUDGET.get(name, 3 << 30))
     spanning = 0
     for j in keys:
         s = int(np.searchsorted(bounds, j, side="right") - 1)
