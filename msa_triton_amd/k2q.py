@@ -17,7 +17,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .layout import PackedSequences, prepared_for, sequence_meta
+from .layout import PackedSequences, prepared_for, sequence_meta, with_block_size
 
 _INT32_MAX = 2**31 - 1
 
@@ -106,3 +106,39 @@ def _build_device(indices, cu_seqlens, meta, groups, slots, seqs=None) -> K2QCSR
         )
     _lib.check(status, "msa_k2q_build")
     return K2QCSR(row_ptr, query_indices, slot_indices, cu_block_lens)
+
+
+# At most this many sub-blocks per block (partial records, CSR edges and work grow with
+# the sub-block slot count).
+MAX_SUB_BLOCKS = 8
+
+
+def sub_block_selection(indices, meta, block_size, seqs, fits):
+    """The selection with blocks of more than 128 keys (the MFMA kernels' tile) cut into
+    f sub-blocks of ``block_size / f`` keys: (indices, meta, block_size, seqs).
+
+    f is the smallest divisor of ``block_size`` in [ceil(block_size / 128), 8] for which
+    ``fits(f, sub_block_size, sub_meta)`` holds; ``msa_split_block_indices`` maps id b to
+    f b .. f b + f - 1, which hold exactly block b's keys (a sub-block that starts after
+    the query is skipped by the same id <= query-block rule). Returned unchanged when
+    ``block_size <= 128`` or no such f exists."""
+    total, groups, slots = indices.shape
+    if block_size <= 128 or not total:
+        return indices, meta, block_size, seqs
+    for factor in range(-(-block_size // 128), MAX_SUB_BLOCKS + 1):
+        if block_size % factor:
+            continue
+        sub = block_size // factor
+        sub_meta = sequence_meta(list(meta.bounds), sub)
+        if not fits(factor, sub, sub_meta):
+            break
+        split = torch.empty((total, groups, slots * factor), dtype=torch.int32, device=indices.device)
+        with torch.cuda.device(indices.device):
+            status = _lib.lib().msa_split_block_indices(indices.data_ptr(), total * groups, slots, factor,
+                                                        split.data_ptr(), _lib.stream_of(indices.device))
+        _lib.check(status, "msa_split_block_indices")
+        if seqs is None:
+            return split, sub_meta, sub, None
+        sub_seqs = with_block_size(seqs, sub)
+        return split, sub_seqs.meta, sub, sub_seqs
+    return indices, meta, block_size, seqs

@@ -135,6 +135,21 @@ def prepare_sequences(cu_seqlens: torch.Tensor, *, block_size: int = 128) -> Pac
     )
 
 
+def call_sequences(cu_seqlens: torch.Tensor, meta: SequenceMeta) -> PackedSequences:
+    """``PackedSequences`` for one operator call whose ``cu_seqlens`` the host has read and
+    validated already (``meta``): the block metadata reaches the device in one host-to-device
+    copy, and the rest of the call (CSR build, attention passes) reads nothing back. Its
+    ``cu_seqlens`` is the caller's tensor, not a private clone: valid for that call only."""
+    n = meta.num_seqs + 1
+    pad = n + (n & 1)  # int32 entries ahead of the 8-byte aligned int64 tile prefix
+    host = torch.empty(pad + 2 * n, dtype=torch.int32)
+    host[:n] = torch.tensor(meta.cu_block_lens, dtype=torch.int32)
+    host[pad:].view(torch.int64).copy_(torch.tensor(meta.tri_prefix, dtype=torch.int64))
+    dev = host.to(cu_seqlens.device)
+    return PackedSequences(cu_seqlens=cu_seqlens, cu_block_lens=dev[:n], tile_prefix=dev[pad:].view(torch.int64),
+                           meta=meta)
+
+
 # PackedSequences re-described for other block sizes, kept with the original.
 _OTHER_BLOCK_SIZES: "weakref.WeakKeyDictionary[PackedSequences, dict[int, PackedSequences]]" = weakref.WeakKeyDictionary()
 

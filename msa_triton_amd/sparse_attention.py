@@ -27,45 +27,22 @@ import torch
 
 from . import _lib
 from . import k2q as _k2q
-from .layout import PackedSequences, prepared_for, sequence_lengths, sequence_meta, with_block_size
-
-
-# At most this many sub-blocks per block (the forward's partial records and the CSR grow
-# with the sub-block slot count).
-_MAX_SUB_BLOCKS = 8
+from .layout import PackedSequences, call_sequences, prepared_for, sequence_lengths, sequence_meta
 
 
 def _sub_block_view(q, k, indices, meta, block_size, seqs):
-    """The selection as the MFMA kernels take it: (indices, meta, block_size, seqs).
-
-    A bf16 block of more than 128 keys (the kernels' tile) is cut into f sub-blocks of
-    block_size / f keys, f the smallest divisor of block_size in [ceil(block_size / 128), 8]
-    whose sub-block the MFMA kernels take: ``msa_split_block_indices`` maps id b to
-    f b .. f b + f - 1, which hold the same keys. Unchanged for other calls, and where no
-    such f exists (those calls run the FP64 kernels with the original blocks)."""
+    """The selection as the MFMA kernels take it: bf16 blocks above 128 keys as sub-blocks
+    (``k2q.sub_block_selection``); unchanged for other calls."""
     total, heads, dim = q.shape
-    if q.dtype != torch.bfloat16 or block_size <= 128 or not total:
+    if q.dtype != torch.bfloat16:
         return indices, meta, block_size, seqs
-    groups, slots = k.shape[1], indices.shape[2]
     lib = _lib.lib()
-    for factor in range(-(-block_size // 128), _MAX_SUB_BLOCKS + 1):
-        if block_size % factor:
-            continue
-        sub = block_size // factor
-        sub_meta = sequence_meta(list(meta.bounds), sub)
-        if lib.msa_attn_fwd_workspace_bytes(_lib.DTYPE_CODE[q.dtype], total, heads, groups, dim, slots * factor,
-                                            sub_meta.total_blocks, sub) <= 0:
-            break
-        split = torch.empty((total, groups, slots * factor), dtype=torch.int32, device=q.device)
-        with torch.cuda.device(q.device):
-            status = lib.msa_split_block_indices(indices.data_ptr(), total * groups, slots, factor, split.data_ptr(),
-                                                 _lib.stream_of(q.device))
-        _lib.check(status, "msa_split_block_indices")
-        if seqs is None:
-            return split, sub_meta, sub, None
-        sub_seqs = with_block_size(seqs, sub)
-        return split, sub_seqs.meta, sub, sub_seqs
-    return indices, meta, block_size, seqs
+
+    def fits(factor, sub, sub_meta):
+        return lib.msa_attn_fwd_workspace_bytes(_lib.DTYPE_CODE[q.dtype], total, heads, k.shape[1], dim,
+                                                indices.shape[2] * factor, sub_meta.total_blocks, sub) > 0
+
+    return _k2q.sub_block_selection(indices, meta, block_size, seqs, fits)
 
 
 def _attn_forward(q, k, v, indices, cu, meta, block_size, scale, seqs, public_csr=False, save_f32=False):
@@ -245,6 +222,8 @@ def m3_sparse_attention(
         for length in lengths:
             bounds.append(bounds[-1] + length)
         meta = sequence_meta(bounds, block_size)
+        # cu_seqlens was read once above: the rest of the call reads nothing back
+        seqs = call_sequences(cu, meta) if q.shape[0] else None
     else:
         meta = seqs.meta
     output, lse = _SparseAttention.apply(q, k, v, indices, cu, block_size, effective_scale, meta, seqs)

@@ -54,6 +54,9 @@ def _close32(actual, expected, what):
     ([5, 0, 130, 77], 2, 8, 128, 64, 32, 4, 1.0, 0.1),
     ([257, 128], 1, 8, 128, 128, 128, 3, 0.2, None),
     ([64, 200], 4, 2, 64, 128, 64, 2, 1.0, 0.3),
+    # blocks above 128 keys: 2 sub-blocks of 128, 2 of 96
+    ([300, 45], 2, 4, 64, 64, 256, 2, 0.5, None),
+    ([400], 1, 2, 32, 128, 192, 3, 1.0, None),
 ])
 def test_matches_fp64_oracle(lengths, groups, ratio, dim, dim_i, block, topk, index_scale, scale, device):
     iq, ik, q, k, ids, cu = _inputs(lengths, groups, ratio, dim, dim_i, block, topk, 17)
