@@ -66,3 +66,23 @@ def test_operators_check_prepared_metadata_before_launch():
     with pytest.raises(ValueError, match="total_tokens"):
         msa.m3_sparse_attention(q[:5], kv[:5], kv[:5], torch.zeros(5, 1, 1, dtype=torch.int32), seqs, 6,
                                 block_size=4)
+
+
+@pytest.mark.parametrize("bounds,block", [([0, 5, 9], 4), ([0, 3, 3, 10, 20], 4), ([0, 300], 128), ([0, 0], 7)])
+def test_call_and_rescaled_sequences_match_prepared(bounds, block):
+    """The call-scoped metadata (one packed host-to-device copy) and a prepared object
+    re-described for another block size equal a fresh prepare_sequences of the same bounds."""
+    from msa_triton_amd.layout import call_sequences, sequence_meta, with_block_size
+
+    cu = torch.tensor(bounds, dtype=torch.int32)
+    fresh = msa.prepare_sequences(cu, block_size=block)
+    call = call_sequences(cu, sequence_meta(bounds, block))
+    assert call.cu_seqlens is cu and call.meta == fresh.meta
+    assert torch.equal(call.cu_block_lens, fresh.cu_block_lens) and call.cu_block_lens.dtype == torch.int32
+    assert torch.equal(call.tile_prefix, fresh.tile_prefix) and call.tile_prefix.dtype == torch.int64
+    other = with_block_size(msa.prepare_sequences(cu, block_size=2 * block), block)
+    assert other.meta == fresh.meta
+    assert torch.equal(other.cu_block_lens, fresh.cu_block_lens) and torch.equal(other.tile_prefix, fresh.tile_prefix)
+    base = msa.prepare_sequences(cu, block_size=2 * block)
+    assert with_block_size(base, block) is with_block_size(base, block)  # cached with its PackedSequences
+    assert with_block_size(base, 2 * block) is base
