@@ -3,12 +3,14 @@
 // softmax are evaluated in FP64: bf16/fp16/fp32 products are exact in FP64, so
 // the query pass and the KV pass see identical logits/dP values and the
 // softmax-gradient cancellation (dp - delta) is consistent between them. bf16 inputs
-// with head dims up to 128, blocks up to 128 and up to 512 heads per group take the
-// KV-major MFMA kernels (attn_kv_fwd.hip, attn_kv_bwd.hip); this file serves fp16 /
-// fp32 inputs and the shapes outside those templates. fp16 stays here on purpose: an
-// fp16 output has three more significant bits than bf16, and the fp32 sums of the
-// MFMA path would move about eight times as many fp16 outputs across a rounding
-// midpoint, beyond what the reference's gate allows on its small test shapes.
+// with head dims up to 128 and up to 512 heads per group take the KV-major MFMA kernels
+// (attn_kv_fwd.hip, attn_kv_bwd.hip; blocks above 128 keys as sub-blocks); this file
+// serves fp16 / fp32 inputs and the shapes outside those templates. fp16 stays here on
+// purpose: an fp16 output has three more significant bits than bf16, so fp32 sums put
+// about eight times as many fp16 outputs near a rounding midpoint (an fp32-accumulating
+// emulation leaves one outside the reference's gate at one of its small test shapes,
+// which allow none), and the MFMA kernels' exact three-term splits of P and dS have no
+// fp16 counterpart (fp16's five exponent bits: P's residuals underflow, dS can overflow).
 //
 // Semantics (triton/sparse_attention.py):
 //   forward  :35-84  slots with 0 <= id <= qb(t) are visited in slot order,
