@@ -85,7 +85,9 @@ int64_t msa_score_fwd_workspace_bytes(int64_t total_tokens, int64_t groups, int6
 
 /* Stage 1 forward: per-group causal block maxima of scale * (index_q . index_k).
  * Replaces triton/index_score.py:93-136 (_index_score_forward) and the launch at
- * :237-265. scores = fl32(scale * exact winning dot); -inf for blocks with no
+ * :237-265. scores = the reference's FP32 form of the exact winning dot x (:121-127):
+ * fl32(fl32(hi s) + fl32(lo s)) with hi = fl32(x), lo = fl32(x - hi), s = fl32(|scale|)
+ * (fl32(scale x) for |scale| in {0, 1}); -inf for blocks with no
  * causal key. tie_info (nullable, int32 [T,G,NB]): winner offset + 1 for a
  * unique exact maximum, -count for exact ties, 0 for invalid blocks
  * (same encoding as index_score.py:128-136). workspace: at least

@@ -4,11 +4,11 @@
 // tests/reference_fp64.py:16-45): for row (t, g) and sequence-local block b,
 //   score[t,g,b] = max_{j in block b, j <= t} scale * (index_q[t,g] . index_k[j])
 // or -inf when the block holds no causal key. The reference compares winners
-// with a compensated (hi, lo) FP32 dot and publishes fl32(hi*|s| + lo*|s|); for
-// finite bf16/fp16/fp32 inputs that is the correctly rounded exact block max.
-// Here the winning dot is evaluated in FP64 (bf16/fp16/fp32 products are exact
-// in FP64; the accumulation order is fixed, see exact_dot) and rounded once to
-// FP32. Winners are compared on the exact
+// with a compensated (hi, lo) FP32 dot and publishes fl32(fl32(hi*|s|) + fl32(lo*|s|))
+// with |s| in FP32. Here the winning dot is evaluated in FP64 (bf16/fp16/fp32 products
+// are exact in FP64; the accumulation order is fixed, see exact_dot), split into the
+// same FP32 pair (hi = fl32(dot), lo = fl32(dot - hi)) and published by the same
+// FP32 formula (public_score). Winners are compared on the exact
 // (directed) dot, ties are exact equality: tie_info = offset+1 for a unique
 // winner, -count for ties (index_score.py:128-136).
 //
@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256) void score_fwd_exact(const void* __restrict__ 
   const int64_t k1 = (k0 + B < t + 1) ? k0 + B : t + 1;
   const BlockMax bm = block_max_exact<DT>(iq, row * Di, ik, k0, k1, Di, scale, lane);
   if (lane == 0) {
-    scores[out] = static_cast<float>(fabs(scale) * bm.best);
+    scores[out] = public_score(bm.best, static_cast<float>(fabs(scale)));
     if (tie_info) tie_info[out] = bm.count == 1 ? bm.first + 1 : -bm.count;
   }
 }

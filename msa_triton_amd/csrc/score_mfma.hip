@@ -16,8 +16,8 @@
 // pre-pass (score_key_norms), and each key block's largest norm and safety once per
 // block by a second (score_block_norms), instead of per tile.
 //
-// Exactness (the public score must equal fl32(scale * exact winning dot) and
-// the winner set must be the exact one, index_score.py:121-136): with
+// Exactness (the public score is the reference's FP32 form of the exact winning dot,
+// public_score, and the winner set must be the exact one, index_score.py:121-136): with
 //   E = (Di_pad + 8) * 2^-22 * ||q|| * max_k ||k||  >=  |s_mfma - s_exact|,
 // every key whose approximate directed logit is below (max_approx - 2E) is
 // certainly beaten by the approximate winner. The running maximum and runner-up
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
   const int64_t r0 = static_cast<int64_t>(gridDim.x - 1 - blockIdx.x) * kTileRows;  // heaviest tiles first
   const int nr = static_cast<int>(rows - r0 < kTileRows ? rows - r0 : kTileRows);
   const bool neg = scale < 0.0;
-  const double ascale = fabs(scale);
+  const float fscale = static_cast<float>(fabs(scale));  // the reference's FP32 |scale|
   const uint32_t flip = neg ? 0x80008000u : 0u;
   const float cerr = static_cast<float>(DP + 8) * 0x1p-22f;
   // exact_dot's split point (Di % 8 == 0, so h % 4 == 0); compile-time for Di == DP
@@ -523,7 +523,7 @@ __global__ __launch_bounds__(kThreads, NK == 4 && !FULLD ? 1 : 2) void score_fwd
       const double h1 = __longlong_as_double(static_cast<long long>((static_cast<uint64_t>(hhi.b) << 32) | hlo.b));
       if (row_ok && mycnt == 1 && hf == 0) {
         const int64_t out = (r0 + prow) * NB + cur.b;
-        scores[out] = static_cast<float>(ascale * (h0 + h1));
+        scores[out] = public_score(h0 + h1, fscale);
         if (tie) tie[out] = myidx + 1;
       }
       // ambiguous rows: marked for score_fwd_resolve
@@ -675,7 +675,7 @@ __global__ __launch_bounds__(256) void score_fwd_resolve(const uint16_t* __restr
             const int count = __popcll(m0) + __popcll(m1);
             const int first = m0 ? __builtin_ctzll(m0) : 64 + __builtin_ctzll(m1);
             const int64_t out = row * NB + b;
-            scores[out] = static_cast<float>(fabs(scale) * wbest);
+            scores[out] = public_score(wbest, static_cast<float>(fabs(scale)));
             if (tie) tie[out] = count == 1 ? first + 1 : -count;
           }
         }

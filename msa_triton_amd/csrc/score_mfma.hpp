@@ -22,6 +22,20 @@ __device__ __forceinline__ double directed(double dot, double scale) {
   return scale > 0.0 ? dot : (scale < 0.0 ? -dot : 0.0);
 }
 
+// The public score of a block whose directed exact maximum is x, as the reference
+// publishes it (triton/index_score.py:121-127, FP32 arithmetic without fused
+// multiply-add): the FP32 pair hi = fl32(x), lo = fl32(x - hi) of the winning dot, each
+// times s = fl32(|scale|), added in FP32. For |scale| = 1 (and 0) that is fl32(x); for
+// other scales it can differ from fl32(|scale| x) by one ulp (two roundings). x = -inf
+// (no finite visible dot) or an x beyond the FP32 range gives fl32(x) s.
+__device__ __forceinline__ float public_score(double x, float s) {
+#pragma clang fp contract(off)  // two products and a sum, each rounded (HIP contracts by default)
+  const float hi = static_cast<float>(x);
+  if (!__builtin_isfinite(hi)) return __fmul_rn(hi, s);
+  const float lo = static_cast<float>(x - static_cast<double>(hi));  // x - hi is exact in FP64
+  return hi * s + lo * s;
+}
+
 template <int DT>
 __device__ __forceinline__ double exact_half_dot(const void* __restrict__ a, int64_t ia,
                                                  const void* __restrict__ b, int64_t ib, int d0, int d1) {

@@ -5,7 +5,10 @@ validation order, messages and exception types) and its autograd contract
 (:235-295): first-order gradients, with the winner state saved only when grad
 is enabled and an input requires grad.
 
-Numerics: each public score is fl32(scale * exact winning dot). Winners are
+Numerics: each public score is the reference's fp32 form of the exact winning dot x
+(index_score.py:121-127): hi = fl32(x), lo = fl32(x - hi), s = fl32(|scale|), score =
+fl32(fl32(hi s) + fl32(lo s)), i.e. fl32(scale * x) when |scale| is 0, 1 or a power
+of two. Winners are
 decided on exact dot products (FP64 evaluation of bf16/fp16/fp32 products), so
 ties are true mathematical ties and the backward splits ds*scale evenly across
 them like ``torch.amax``. Saved state is one int32 tie/winner code per score

@@ -63,15 +63,30 @@ def _token_positions(bounds):
 # --------------------------------------------------------------------------- stage 1
 
 
+def public_score(best, scale):
+    """The reference's public fp32 score (triton/index_score.py:121-127, fp32 arithmetic
+    with fusion disabled) of directed block maxima ``best`` (float64): the fp32 pair
+    hi = fl32(x), lo = fl32(x - hi), each times s = fl32(|scale|), added in fp32.
+    Non-finite hi gives hi * s."""
+    x = np.asarray(best, dtype=np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        hi = x.astype(np.float32)
+        finite = np.isfinite(hi)
+        lo = np.where(finite, x - np.where(finite, hi, 0).astype(np.float64), 0.0).astype(np.float32)
+        s = np.float32(abs(scale))
+        return np.where(finite, hi * s + lo * s, hi * s).astype(np.float32)
+
+
 def index_score(iq, ik, cu, max_seqlen, *, block_size=128, scale=1.0):
     """Exact block maxima.
 
     Returns (scores_f64, scores_f32, tie) where scores_f64[t,g,b] is
     max over causal keys j of block b of scale * (iq[t,g] . ik[j]) evaluated in
-    float64 (-inf if none), scores_f32 its float32 rounding (the public score),
-    and tie the winner code: offset+1 for a unique maximum, -count for ties,
-    0 for blocks without causal keys. Winners compare the directed dot
-    sign(scale) * dot, as the reference's compensated comparison does.
+    float64 (-inf if none), scores_f32 the public score (``public_score`` of the
+    directed maximum: its fp32 rounding when |scale| is 1 or 0), and tie the
+    winner code: offset+1 for a unique maximum, -count for ties, 0 for blocks
+    without causal keys. Winners compare the directed dot sign(scale) * dot, as
+    the reference's compensated comparison does.
     """
     q = np.asarray(iq, dtype=np.float64)
     k = np.asarray(ik, dtype=np.float64)[:, 0, :]
@@ -80,6 +95,7 @@ def index_score(iq, ik, cu, max_seqlen, *, block_size=128, scale=1.0):
     nb = (max_seqlen + block_size - 1) // block_size
     out = np.full((total, groups, nb), -np.inf)
     tie = np.zeros((total, groups, nb), dtype=np.int32)
+    pub = np.full((total, groups, nb), -np.inf, dtype=np.float32)
     sign = 1.0 if scale > 0 else (-1.0 if scale < 0 else 0.0)
     for a, b in zip(bounds[:-1], bounds[1:]):
         length = b - a
@@ -100,8 +116,9 @@ def index_score(iq, ik, cu, max_seqlen, *, block_size=128, scale=1.0):
             with np.errstate(invalid="ignore"):
                 scores = np.abs(scale) * best
             out[a:b, :, blk] = np.where(valid[:, None], scores, -np.inf)
+            pub[a:b, :, blk] = np.where(valid[:, None], public_score(best, scale), np.float32(-np.inf))
             tie[a:b, :, blk] = np.where(valid[:, None], code, 0)
-    return out, out.astype(np.float32), tie
+    return out, pub, tie
 
 
 def index_score_backward(iq, ik, cu, max_seqlen, ds, *, block_size=128, scale=1.0):
@@ -192,6 +209,7 @@ def index_score_rows(iq, ik, cu, tokens, nb, *, block_size=128, scale=1.0):
     tokens = np.asarray(tokens, dtype=np.int64)
     groups = q.shape[1]
     out = np.full((len(tokens), groups, nb), -np.inf)
+    pub = np.full((len(tokens), groups, nb), -np.inf, dtype=np.float32)
     sign = 1.0 if scale > 0 else (-1.0 if scale < 0 else 0.0)
     for i, t in enumerate(tokens):
         a = int(start[t])
@@ -200,8 +218,10 @@ def index_score_rows(iq, ik, cu, tokens, nb, *, block_size=128, scale=1.0):
         for blk in range(pos // block_size + 1):
             lo, hi = blk * block_size, min((blk + 1) * block_size, pos + 1)
             with np.errstate(invalid="ignore"):
-                out[i, :, blk] = np.abs(scale) * (sign * dots[:, lo:hi]).max(-1)
-    return out, out.astype(np.float32)
+                best = (sign * dots[:, lo:hi]).max(-1)
+                out[i, :, blk] = np.abs(scale) * best
+                pub[i, :, blk] = public_score(best, scale)
+    return out, pub
 
 
 def _amax_weights(directed, allowed, ds_col, scale):

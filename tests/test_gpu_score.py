@@ -1,7 +1,8 @@
 """GPU parity of stage 1 (m3_index_score) against the CPU oracle.
 
-Forward: scores bit-exact to fl32(scale * exact winning dot), -inf pattern
-exact. Backward: within the reference gate (atol=rtol=1e-4 after rounding the
+Forward: scores bit-exact to the reference's public form of the exact winning dot
+(oracle.public_score: fl32(scale * dot) when |scale| is 0, 1 or a power of two, the
+reference's two-term fp32 form otherwise), -inf pattern exact. Backward: within the reference gate (atol=rtol=1e-4 after rounding the
 FP64 oracle to the input dtype, tests/test_triton_score.py:32-77). Cases
 mirror tests/test_triton_score.py, including the low-bit winner known answers.
 """
@@ -41,6 +42,8 @@ def _run(q_cpu, k_cpu, lengths, max_seqlen, block_size, scale, upstream, device)
 @pytest.mark.parametrize("lengths,groups,dim,block_size,scale", [
     ([1], 1, 1, 4, 1.0), ([0, 0], 2, 7, 4, 1.0), ([0, 3, 0, 2, 0], 2, 7, 4, 1.0), ([3, 7], 2, 7, 4, 1.0),
     ([7, 11], 4, 16, 8, 0.5), ([9], 2, 64, 4, 1.0), ([5], 4, 128, 128, 1.0),
+    # scales that are not powers of two: exact path (Di 16) and MFMA path (Di 64, 128)
+    ([7, 11], 4, 16, 8, 0.3), ([90, 41], 2, 64, 16, -1.7), ([300], 2, 128, 64, 0.1),
 ])
 def test_score_forward_backward_fp64(lengths, groups, dim, block_size, scale, device):
     generator = torch.Generator().manual_seed(731)

@@ -51,7 +51,7 @@ def _draw(seed):
     topk = int(rng.integers(1, 7))
     local = int(rng.integers(0, min(topk, 2) + 1))
     scale = None if rng.random() < 0.5 else float(rng.choice([0.05, 0.3, 1.7]))
-    index_scale = float(rng.choice([1.0, 0.5, -0.75]))
+    index_scale = float(rng.choice([1.0, 0.5, -0.75] if seed < 8 else [1.0, 0.5, -0.75, 0.3, -1.7]))
     return dict(lengths=lengths, groups=groups, ratio=ratio, dim=dim, dim_i=dim_i, block=block, topk=topk,
                 local=local, scale=scale, index_scale=index_scale)
 

@@ -84,9 +84,13 @@ def test_groups_remain_independent():
     assert s32[-1, 0].argmax() == 0 and s32[-1, 1].argmax() == 1
 
 
-@pytest.mark.parametrize("scale", [1.0, -1.0, 0.0, 0.3])
-def test_public_score_is_correctly_rounded_exact_max(scale):
-    """Brute force with exact rationals: fl32(max_j scale * dot) for random bf16 data."""
+@pytest.mark.parametrize("scale", [1.0, -1.0, 0.0, 0.3, -1.7, 2.0**-3])
+def test_public_score_is_the_reference_fp32_form_of_the_exact_max(scale):
+    """Brute force with exact rationals: with x the exact directed block maximum
+    (sign(scale) * dot) and s = fl32(|scale|), the reference's public score
+    (triton/index_score.py:121-127, fp32 arithmetic without fusion) is
+    fl32(fl32(hi * s) + fl32(lo * s)) for hi = fl32(x), lo = fl32(x - hi); for |scale| in
+    {0, 1} and powers of two that is fl32(scale * max dot)."""
     gen = torch.Generator().manual_seed(7)
     lengths, groups, dim, block = [5, 7], 2, 9, 3
     q = torch.randn(sum(lengths), groups, dim, generator=gen).bfloat16().double().numpy()
@@ -104,8 +108,16 @@ def test_public_score_is_correctly_rounded_exact_max(scale):
                         continue
                     exact = [sc * sum(Fraction(x) * Fraction(y) for x, y in zip(q[t, g], k[j, 0])) for j in keys]
                     best = max(exact)
-                    expected = _round_f32(best)
+                    sign = 1 if scale > 0 else (-1 if scale < 0 else 0)
+                    directed = max(sign * sum(Fraction(x) * Fraction(y) for x, y in zip(q[t, g], k[j, 0]))
+                                   for j in keys)
+                    s32f = Fraction(float(np.float32(abs(scale))))
+                    hi = Fraction(float(_round_f32(directed)))
+                    lo = Fraction(float(_round_f32(directed - hi)))
+                    expected = _round_f32(Fraction(float(_round_f32(hi * s32f))) + Fraction(float(_round_f32(lo * s32f))))
                     assert s32[t, g, blk] == expected
+                    if abs(scale) in (0.0, 1.0, 2.0**-3):
+                        assert expected == _round_f32(best)  # one rounding of the scaled maximum
                     winners = [i for i, e in enumerate(exact) if e == best]
                     code = winners[0] + 1 if len(winners) == 1 else -len(winners)
                     assert tie[t, g, blk] == code
