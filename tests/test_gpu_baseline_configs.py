@@ -218,3 +218,46 @@ def test_score_backward_against_oracle(name, device):
     keys = np.array(sorted(keys), dtype=np.int64)
     dk_ref = O.index_score_backward_keys(iq64, ik64, cu_np, g_np, keys, block_size=B)
     _check_bf16(b.grad[keys], dk_ref, f"{name}: score dk")
+
+
+@pytest.mark.parametrize("name,dtype", [("c2", torch.float16), ("c4", torch.float16), ("c2", torch.float32)],
+                         ids=["c2-fp16", "c4-fp16", "c2-fp32"])
+def test_fp16_fp32_attention_at_baseline_configs(name, dtype, device):
+    """The FP64 attention kernels at BASELINE sizes: the benchmark's q / k / v / dO in fp16
+    or fp32 with the benchmark's selection (bf16 score and top-k); out / lse / dQ of sampled
+    query tokens and dK / dV of sampled keys against the sparse FP64 oracle, fp32 within
+    the reference's gate, fp16 within its stated analogue (one fp16 ulp, at most 0.1 %
+    outside the gate)."""
+    from tests.test_gpu_sweep import _check_dtype_stated
+
+    cfg = bench.CONFIGS[name]
+    lengths, B, K, L = cfg["lengths"], cfg["block"], cfg["topk"], cfg["local"]
+    bounds = _bounds(lengths)
+    max_len = max(lengths)
+    cu_np = np.array(bounds, dtype=np.int32)
+    iq, ik, q, k, v, dout = bench.make_inputs(cfg)
+    q, k, v, dout = (x.to(dtype) for x in (q, k, v, dout))
+    cu = torch.tensor(bounds, dtype=torch.int32, device=device)
+    print(f"[{name} {dtype}] T={bounds[-1]} Hq={cfg['hq']} G={cfg['g']} K={K}", flush=True)
+    with torch.no_grad():
+        ids = msa.m3_topk(msa.m3_index_score(iq.to(device), ik.to(device), cu, max_len, block_size=B), cu,
+                          block_size=B, topk_blocks=K, local_blocks=L)
+    qd, kd, vd = (x.to(device).requires_grad_() for x in (q, k, v))
+    out, lse = msa.m3_sparse_attention(qd, kd, vd, ids, cu, max_len, block_size=B, return_lse=True)
+    out.backward(dout.to(device))
+    torch.cuda.synchronize()
+    assert out.dtype == dtype and qd.grad.dtype == dtype
+    ids_np = ids.cpu().numpy()
+    tokens = _sample_tokens(lengths, B, np.random.default_rng(2025))
+    keys = _sample_keys(lengths, B, name)
+    q64, k64, v64, do64 = (x.double().numpy() for x in (q, k, v, dout))
+    rows = O.attention_rows(q64, k64, v64, ids_np, cu_np, tokens, block_size=B, dout=do64)
+    dk_ref, dv_ref = O.attention_kv_rows(q64, k64, v64, ids_np, cu_np, do64, keys, block_size=B)
+    _check_dtype_stated(out[tokens], rows["out"], dtype, f"{name}: out")
+    _check_dtype_stated(qd.grad[tokens], rows["dq"], dtype, f"{name}: dq")
+    _check_dtype_stated(kd.grad[keys], dk_ref, dtype, f"{name}: dk")
+    _check_dtype_stated(vd.grad[keys], dv_ref, dtype, f"{name}: dv")
+    lse_np = lse.cpu().numpy()[tokens]
+    assert np.array_equal(np.isneginf(lse_np), np.isneginf(rows["lse"]))
+    fin = np.isfinite(rows["lse"])
+    np.testing.assert_allclose(lse_np[fin], rows["lse"][fin], atol=1e-4, rtol=1e-4, err_msg=f"{name}: lse")
