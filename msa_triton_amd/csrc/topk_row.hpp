@@ -4,16 +4,21 @@
 // Semantics follow triton/topk.py:31-46 (eager twin eager/ops.py:94-129): blocks
 // b > qb(t) are masked to -inf, blocks in (qb-L, qb] are forced to +inf, the
 // min(K, NB) largest are returned in descending order, -inf picks become -1, and
-// the row is right-padded with -1 up to K slots. Ties (equal values, e.g. several
-// +inf local blocks) are emitted in ascending block order.
+// the row is right-padded with -1 up to K slots. NaN scores rank above +inf (as in
+// torch.topk). Ties (equal values, e.g. several +inf local blocks, or NaNs) are
+// emitted in ascending block order.
 #pragma once
 #include "common.hpp"
 
 namespace msa {
 
-// Monotone map of float bits onto uint32 (+0 and -0 collapse to the same key).
+// Monotone map of float bits onto uint32 (+0 and -0 collapse to the same key). NaN of
+// either sign ranks above +inf, as in torch.topk (the reference's selection,
+// triton/topk.py:44-45); 0xfffffffe keeps the 64-bit key of block 0 below the scan's
+// initial bound ~0.
 __device__ __forceinline__ uint32_t ordered_key(float f) {
   uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xfffffffeu;
   if (u == 0x80000000u) u = 0u;
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }

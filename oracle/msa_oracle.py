@@ -155,6 +155,16 @@ def index_score_backward(iq, ik, cu, max_seqlen, ds, *, block_size=128, scale=1.
 # --------------------------------------------------------------------------- stage 2
 
 
+def _rank_order(ranked):
+    """Block order of a descending selection along the last axis, as torch.topk ranks
+    (triton/topk.py:44-45): NaN of either sign above +inf, then larger values first;
+    equal values (and NaNs) in ascending block order."""
+    nan = np.isnan(ranked)
+    value = np.where(nan, 0.0, ranked)
+    blocks = np.broadcast_to(np.arange(ranked.shape[-1]), ranked.shape)
+    return np.lexsort((blocks, -value, ~nan), axis=-1)
+
+
 def topk(scores, cu, *, block_size=128, topk_blocks=16, local_blocks=1):
     """Causal mask, +inf local boost, top-min(K, NB) in canonical order, -1 padding."""
     scores = np.asarray(scores, dtype=np.float32)
@@ -172,7 +182,7 @@ def topk(scores, cu, *, block_size=128, topk_blocks=16, local_blocks=1):
         local = valid & (blocks[None, :] > qb[:, None] - local_blocks)
         ranked = np.where(local[:, None, :], np.inf, ranked)
     count = min(topk_blocks, nb)
-    order = np.argsort(-ranked, axis=-1, kind="stable")[..., :count]
+    order = _rank_order(ranked)[..., :count]
     values = np.take_along_axis(ranked, order, axis=-1)
     result[..., :count] = np.where(values == -np.inf, -1, order).astype(np.int32)
     return result
@@ -194,7 +204,7 @@ def topk_rows(score_rows, positions, *, block_size=128, topk_blocks=16, local_bl
         local = valid & (blocks[None, :] > qb[:, None] - local_blocks)
         ranked = np.where(local[:, None, :], np.inf, ranked)
     count = min(topk_blocks, nb)
-    order = np.argsort(-ranked, axis=-1, kind="stable")[..., :count]
+    order = _rank_order(ranked)[..., :count]
     values = np.take_along_axis(ranked, order, axis=-1)
     result[..., :count] = np.where(values == -np.inf, -1, order).astype(np.int32)
     return result

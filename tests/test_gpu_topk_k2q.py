@@ -59,6 +59,27 @@ def test_topk_adversarial_ties_infinities_and_wide_rows(device):
         np.testing.assert_array_equal(got.cpu().numpy(), ref)
 
 
+@pytest.mark.parametrize("tokens,block", [(200, 4), (4000, 2), (9000, 1)])
+def test_topk_nan_scores_rank_above_inf(tokens, block, device):
+    """NaN scores of either sign rank above +inf, as in torch.topk (the oracle's order is
+    pinned against torch.topk on the CPU), on all three selection paths: 16 lanes per row
+    (50 blocks), a wavefront per row (2000) and the streamed rows (9000); several NaNs per
+    row are emitted in ascending block order, like other equal values."""
+    gen = torch.Generator().manual_seed(tokens)
+    nb = (tokens + block - 1) // block
+    scores = torch.randint(-3, 4, (tokens, 2, nb), generator=gen).float()
+    pick = torch.rand(tokens, 2, nb, generator=gen)
+    scores[pick < 0.02] = float("nan")
+    scores[(pick > 0.02) & (pick < 0.03)] = -float("nan")
+    scores[(pick > 0.5) & (pick < 0.52)] = float("inf")
+    scores[(pick > 0.6) & (pick < 0.7)] = float("-inf")
+    cu = cu_tensor([tokens], device)
+    for k, local in ((8, 0), (24, 2)):
+        got = msa.m3_topk(scores.to(device), cu, block_size=block, topk_blocks=k, local_blocks=local)
+        ref = O.topk(scores.numpy(), [0, tokens], block_size=block, topk_blocks=k, local_blocks=local)
+        np.testing.assert_array_equal(got.cpu().numpy(), ref)
+
+
 @pytest.mark.parametrize("total,groups,nb,k,local", [(8192, 4, 64, 16, 1), (32768, 4, 256, 16, 1), (4096, 8, 512, 32, 2)])
 def test_topk_baseline_sized_rows(total, groups, nb, k, local, device):
     gen = torch.Generator().manual_seed(total)

@@ -184,3 +184,37 @@ def test_eager_baseline_score_and_topk_match_oracle():
     ids = eager_topk(torch.from_numpy(ref32), torch.arange(n), block_size=block, topk_blocks=4, local_blocks=1)
     ref_ids = O.topk(ref32, [0, n], block_size=block, topk_blocks=4, local_blocks=1)
     assert np.array_equal(np.sort(ids.numpy(), -1), np.sort(ref_ids, -1))
+
+
+@pytest.mark.parametrize("local", [0, 1])
+def test_topk_nan_ranks_like_torch_topk(local):
+    """Scores with NaN (either sign) and -inf, at most one NaN per row and distinct values
+    otherwise (so that torch.topk's order is fully determined): the oracle equals the
+    reference's own steps (triton/topk.py:31-46: causal -inf mask, +inf local boost,
+    torch.topk sorted, -inf picks -> -1, -1 padding), in which NaN ranks above +inf."""
+    gen = torch.Generator().manual_seed(11 + local)
+    lengths, block, groups, k = [37, 20], 2, 2, 6
+    cu = cu_list(lengths)
+    nb = (max(lengths) + block - 1) // block
+    total = sum(lengths)
+    scores = torch.randn(total, groups, nb, generator=gen)
+    scores[::5, 0, ::4] = float("-inf")
+    rows = torch.randint(0, nb, (total, groups), generator=gen)
+    sign = torch.where(torch.rand(total, groups, generator=gen) < 0.5, -1.0, 1.0)
+    has_nan = torch.rand(total, groups, generator=gen) < 0.6
+    scores.scatter_(2, rows[..., None], torch.where(has_nan, sign * float("nan"), scores.gather(2, rows[..., None])[..., 0])[..., None])
+    got = O.topk(scores.numpy(), cu, block_size=block, topk_blocks=k, local_blocks=local)
+    start = 0
+    for length in lengths:
+        for pos in range(length):
+            t, qb = start + pos, pos // block
+            for g in range(groups):
+                row = scores[t, g].clone()
+                row[qb + 1:] = float("-inf")
+                if local:
+                    row[max(0, qb - local + 1): qb + 1] = float("inf")
+                count = min(k, nb)
+                val, idx = torch.topk(row, count, sorted=True)
+                want = torch.where(val == float("-inf"), -1, idx).tolist() + [-1] * (k - count)
+                assert got[t, g].tolist() == want, (t, g, row.tolist())
+        start += length
