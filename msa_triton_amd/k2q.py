@@ -17,7 +17,7 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .layout import PackedSequences, prepared_for, sequence_meta, with_block_size
+from .layout import PackedSequences, prepared_for, sequence_meta, tile_prefix_times, with_block_size
 
 _INT32_MAX = 2**31 - 1
 
@@ -89,9 +89,9 @@ def _build_device(indices, cu_seqlens, meta, groups, slots, seqs=None) -> K2QCSR
     if seqs is None:
         cu_block_lens = torch.tensor(meta.cu_block_lens, dtype=torch.int32, device=device)
         tri = torch.tensor([groups * x for x in meta.tri_prefix], dtype=torch.int64, device=device)
-    else:  # prepared device copies (no host-to-device copy: capturable)
+    else:  # prepared device copies (no host-to-device copy: capturable after the first call per G)
         cu_block_lens = seqs.cu_block_lens
-        tri = seqs.tile_prefix * groups
+        tri = tile_prefix_times(seqs, groups)
     counter_elems = groups * meta.tri_prefix[-1]
     row_ptr = torch.empty(num_rows + 1, dtype=torch.int32, device=device)
     query_indices = torch.empty(capacity, dtype=torch.int32, device=device)

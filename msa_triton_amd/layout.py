@@ -135,19 +135,43 @@ def prepare_sequences(cu_seqlens: torch.Tensor, *, block_size: int = 128) -> Pac
     )
 
 
-def call_sequences(cu_seqlens: torch.Tensor, meta: SequenceMeta) -> PackedSequences:
+def call_sequences(cu_seqlens: torch.Tensor, meta: SequenceMeta, groups: int) -> PackedSequences:
     """``PackedSequences`` for one operator call whose ``cu_seqlens`` the host has read and
-    validated already (``meta``): the block metadata reaches the device in one host-to-device
-    copy, and the rest of the call (CSR build, attention passes) reads nothing back. Its
-    ``cu_seqlens`` is the caller's tensor, not a private clone: valid for that call only."""
+    validated already (``meta``): the block metadata, with the k2q tile prefix already
+    multiplied by ``groups`` (``tile_prefix_times``), reaches the device in one
+    host-to-device copy, and the rest of the call (CSR build, attention passes) reads
+    nothing back. Its ``cu_seqlens`` is the caller's tensor, not a private clone: valid
+    for that call only."""
     n = meta.num_seqs + 1
-    pad = n + (n & 1)  # int32 entries ahead of the 8-byte aligned int64 tile prefix
-    host = torch.empty(pad + 2 * n, dtype=torch.int32)
-    host[:n] = torch.tensor(meta.cu_block_lens, dtype=torch.int32)
-    host[pad:].view(torch.int64).copy_(torch.tensor(meta.tri_prefix, dtype=torch.int64))
-    dev = host.to(cu_seqlens.device)
-    return PackedSequences(cu_seqlens=cu_seqlens, cu_block_lens=dev[:n], tile_prefix=dev[pad:].view(torch.int64),
-                           meta=meta)
+    words = list(meta.cu_block_lens)
+    if n & 1:
+        words.append(0)  # the int64 part starts 8-byte aligned
+    pad = len(words)
+    for x in meta.tri_prefix:
+        words += (x & 0xFFFFFFFF, x >> 32)
+    for x in meta.tri_prefix:
+        x *= groups
+        words += (x & 0xFFFFFFFF, x >> 32)
+    # int32 words of nonnegative values below 2^63 (the high words stay below 2^31)
+    dev = torch.tensor([w - (1 << 32) if w >= 1 << 31 else w for w in words], dtype=torch.int32).to(cu_seqlens.device)
+    wide = dev[pad:].view(torch.int64)
+    seqs = PackedSequences(cu_seqlens=cu_seqlens, cu_block_lens=dev[:n], tile_prefix=wide[:n], meta=meta)
+    _TILE_PREFIX_TIMES.setdefault(seqs, {})[groups] = wide[n:]
+    return seqs
+
+
+# tile_prefix * groups per PackedSequences, kept with it.
+_TILE_PREFIX_TIMES: "weakref.WeakKeyDictionary[PackedSequences, dict[int, torch.Tensor]]" = weakref.WeakKeyDictionary()
+
+
+def tile_prefix_times(seqs: PackedSequences, groups: int) -> torch.Tensor:
+    """``seqs.tile_prefix * groups`` on the device (the k2q build's per-sequence counter
+    offsets), computed on the first request for a ``groups`` and kept with ``seqs``."""
+    cache = _TILE_PREFIX_TIMES.setdefault(seqs, {})
+    tri = cache.get(groups)
+    if tri is None:
+        tri = cache[groups] = seqs.tile_prefix * groups
+    return tri
 
 
 # PackedSequences re-described for other block sizes, kept with the original.

@@ -223,7 +223,7 @@ def m3_sparse_attention(
             bounds.append(bounds[-1] + length)
         meta = sequence_meta(bounds, block_size)
         # cu_seqlens was read once above: the rest of the call reads nothing back
-        seqs = call_sequences(cu, meta) if q.shape[0] else None
+        seqs = call_sequences(cu, meta, k.shape[1]) if q.shape[0] else None
     else:
         meta = seqs.meta
     output, lse = _SparseAttention.apply(q, k, v, indices, cu, block_size, effective_scale, meta, seqs)

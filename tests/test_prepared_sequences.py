@@ -70,16 +70,20 @@ def test_operators_check_prepared_metadata_before_launch():
 
 @pytest.mark.parametrize("bounds,block", [([0, 5, 9], 4), ([0, 3, 3, 10, 20], 4), ([0, 300], 128), ([0, 0], 7)])
 def test_call_and_rescaled_sequences_match_prepared(bounds, block):
-    """The call-scoped metadata (one packed host-to-device copy) and a prepared object
-    re-described for another block size equal a fresh prepare_sequences of the same bounds."""
-    from msa_triton_amd.layout import call_sequences, sequence_meta, with_block_size
+    """The call-scoped metadata (one packed host-to-device copy, the G-scaled k2q tile prefix
+    included) and a prepared object re-described for another block size equal a fresh
+    prepare_sequences of the same bounds."""
+    from msa_triton_amd.layout import call_sequences, sequence_meta, tile_prefix_times, with_block_size
 
     cu = torch.tensor(bounds, dtype=torch.int32)
     fresh = msa.prepare_sequences(cu, block_size=block)
-    call = call_sequences(cu, sequence_meta(bounds, block))
+    call = call_sequences(cu, sequence_meta(bounds, block), 3)
     assert call.cu_seqlens is cu and call.meta == fresh.meta
     assert torch.equal(call.cu_block_lens, fresh.cu_block_lens) and call.cu_block_lens.dtype == torch.int32
     assert torch.equal(call.tile_prefix, fresh.tile_prefix) and call.tile_prefix.dtype == torch.int64
+    for g in (3, 5):  # the copied G-scaled prefix, and one computed on request
+        assert torch.equal(tile_prefix_times(call, g), fresh.tile_prefix * g)
+        assert tile_prefix_times(fresh, g) is tile_prefix_times(fresh, g)
     other = with_block_size(msa.prepare_sequences(cu, block_size=2 * block), block)
     assert other.meta == fresh.meta
     assert torch.equal(other.cu_block_lens, fresh.cu_block_lens) and torch.equal(other.tile_prefix, fresh.tile_prefix)
