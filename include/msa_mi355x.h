@@ -26,7 +26,8 @@ extern "C" {
 /* Stage 2: causal top-k with forced local blocks.
  * Replaces triton/topk.py:11-47 (m3_topk; eager twin eager/ops.py:94-129).
  * indices [T,G,topk_blocks] int32, left-aligned, -1 padded; ties in
- * descending-value order are emitted by ascending block id. */
+ * descending-value order are emitted by ascending block id; NaN scores (either
+ * sign) rank above +inf, as torch.topk ranks them. */
 int msa_topk(const float* scores, const int32_t* cu_seqlens, int64_t num_seqs,
              int64_t total_tokens, int64_t groups, int64_t num_blocks, int64_t block_size,
              int64_t topk_blocks, int64_t local_blocks, int32_t* indices, void* stream);
