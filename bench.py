@@ -714,10 +714,9 @@ def main():
         stages["attention_fwd_bwd_ms"] = round(ms, 4)
         peak_mem["attention_fwd_bwd"] = round(peak_bytes(step) / 2**20, 1)
 
-        # fp16 inputs take the FP64 VALU kernels (an fp16 output has three more significant bits
-        # than bf16, and fp32-accumulated MFMA sums would move too many of them across a rounding
-        # midpoint for the reference's gate): the same step on this config's inputs and
-        # selection, converted to fp16, one step at a time
+        # fp16 inputs on the MFMA kernels (fp16 products; P and dS split into fp16 terms under
+        # power-of-two scales, dQ's dS planes in bf16 against K as two bf16 terms): the same step
+        # on this config's inputs and selection, converted to fp16, one step at a time
         h16 = [x.detach().half().requires_grad_() for x in (q, k, v)]
         dout16 = dout.half()
 
@@ -803,9 +802,10 @@ def main():
             "indexer_kl": {"bound": "mfma", "unit": "TFLOP/s",
                            **frac(keys * (2.0 * cfg["d"] * (cfg["hq"] // cfg["g"]) + 6.0 * cfg["di"]),
                                   stages["indexer_kl_fwd_bwd_ms"], MFMA_BF16_PEAK_TFLOPS, 1e12)},
-            # fp16 on the FP64 VALU kernels, against the dense fp64 vector peak (78.6 TFLOP/s)
-            "attention_fwd_bwd_fp16": {"bound": "valu_f64", "unit": "TFLOP/s",
-                                       **frac(step_flops, stages["attention_fwd_bwd_fp16_ms"], 78.6, 1e12)},
+            # fp16 on the MFMA kernels, against the dense fp16 MFMA peak (the bf16 figure)
+            "attention_fwd_bwd_fp16": {"bound": "mfma", "unit": "TFLOP/s",
+                                       **frac(step_flops, stages["attention_fwd_bwd_fp16_ms"], MFMA_BF16_PEAK_TFLOPS,
+                                              1e12)},
         }
 
     baseline = None

@@ -1,4 +1,4 @@
-// Stage 3 backward, KV-major (bf16 inputs).
+// Stage 3 backward, KV-major (bf16 and fp16 inputs).
 //
 // Notation per (token t, head h) row with selected keys j: x_j = fl(q.k_j * scale2)
 // (scale2 = scale * log2 e), p_j = 2^(x_j - lse2) with the forward's base-2 lse,
@@ -88,9 +88,6 @@ struct MainSmem {
   int32_t eslot[kMainEdges];
 };
 
-__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-
 }  // namespace
 
 // O . dO per (token, head) in FP64 (exact products); 32 lanes per row, NR rows per
@@ -100,7 +97,7 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 // center that pass refines. Other rows (flat, with o32, the forward's FP32
 // output): delta = O . dO itself, kept as c = float(delta) plus the residual
 // delta - c (slots 2 and 3).
-template <int NR>
+template <int DT, int NR>
 __global__ __launch_bounds__(256) void kv_bwd_center(const uint16_t* __restrict__ out, const float* __restrict__ o32,
                                                      const uint16_t* __restrict__ dout, int64_t rows_th, int D,
                                                      double* __restrict__ row_state) {
@@ -128,15 +125,15 @@ __global__ __launch_bounds__(256) void kv_bwd_center(const uint16_t* __restrict_
         o[r][0] = x.x, o[r][1] = x.y, o[r][2] = x.z, o[r][3] = x.w;
       } else {
         const uint2 x = *reinterpret_cast<const uint2*>(out + th * D + d0);
-        o[r][0] = bf16_lo(x.x), o[r][1] = bf16_hi(x.x), o[r][2] = bf16_lo(x.y), o[r][3] = bf16_hi(x.y);
+        o[r][0] = lo16_f32<DT>(x.x), o[r][1] = hi16_f32<DT>(x.x), o[r][2] = lo16_f32<DT>(x.y), o[r][3] = hi16_f32<DT>(x.y);
       }
     }
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      acc[r] = fma(static_cast<double>(o[r][0]), static_cast<double>(bf16_lo(g[r].x)), acc[r]);
-      acc[r] = fma(static_cast<double>(o[r][1]), static_cast<double>(bf16_hi(g[r].x)), acc[r]);
-      acc[r] = fma(static_cast<double>(o[r][2]), static_cast<double>(bf16_lo(g[r].y)), acc[r]);
-      acc[r] = fma(static_cast<double>(o[r][3]), static_cast<double>(bf16_hi(g[r].y)), acc[r]);
+      acc[r] = fma(static_cast<double>(o[r][0]), static_cast<double>(lo16_f32<DT>(g[r].x)), acc[r]);
+      acc[r] = fma(static_cast<double>(o[r][1]), static_cast<double>(hi16_f32<DT>(g[r].x)), acc[r]);
+      acc[r] = fma(static_cast<double>(o[r][2]), static_cast<double>(lo16_f32<DT>(g[r].y)), acc[r]);
+      acc[r] = fma(static_cast<double>(o[r][3]), static_cast<double>(hi16_f32<DT>(g[r].y)), acc[r]);
     }
   }
 #pragma unroll
@@ -165,7 +162,7 @@ __global__ __launch_bounds__(256) void kv_bwd_center(const uint16_t* __restrict_
 // row (all_rows) or for the rows the forward marked peaked (row_state slot 1 < 0).
 // Structure of the forward partial kernel: K and V blocks row-major in LDS,
 // kStatWaves waves x 16 kStatRT rows per tile; S^T = K Q^T and dP^T = V dO^T (lane: row c, keys 4*q4 + i).
-template <int NK, bool FULLD>
+template <int DT, int NK, bool FULLD>
 __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
@@ -295,8 +292,8 @@ __global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
         f32x4 sa = {0.f, 0.f, 0.f, 0.f}, da = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk) {
-          sa = mfma(kf[kk], qf[rt][kk], sa);
-          da = mfma(vf[kk], gf[rt][kk], da);
+          sa = mfma_t<DT>(kf[kk], qf[rt][kk], sa);
+          da = mfma_t<DT>(vf[kk], gf[rt][kk], da);
         }
         if (full) {
 #pragma unroll
@@ -412,7 +409,7 @@ __global__ __launch_bounds__(256) void kv_bwd_stats_combine(const int32_t* __res
 // Row tiles and dS planes are double-buffered, so one barrier per tile orders all
 // LDS traffic; the next tile's rows are committed before it and the one after is
 // loaded from memory during the current tile.
-template <int NK, bool FULLD>
+template <int DT, int NK, bool FULLD>
 __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
@@ -483,13 +480,29 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
   for (int kk = 0; kk < NK; ++kk) kf[kk] = load_frag(sm.k + (16 * wid + c) * KS + 32 * kk + 8 * q4);
   const int rh = wid >> 2, dq = wid & 3;
   const bool dq_active = 32 * dq < DP;
-  bf16x8 kt[2][4];  // A operand of dQ^T: K^T[dim 32 dq + 16 dt2 + c][keys 32 kc + 8 q4 + j]
+  // A operand of dQ^T (a bf16 product, dS entering as bf16 planes for either input type):
+  // K^T[dim 32 dq + 16 dt2 + c][keys 32 kc + 8 q4 + j]; fp16 K as two exact bf16 terms
+  // (kt the high terms, ktl the low ones).
+  bf16x8 kt[2][4], ktl[2][4];
 #pragma unroll
   for (int dt2 = 0; dt2 < 2; ++dt2)
 #pragma unroll
-    for (int kc = 0; kc < 4; ++kc)
-      kt[dt2][kc] = dq_active ? frag_tr(sm.k, KS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 32 * dq + 16 * dt2, c)
-                              : zero_frag();
+    for (int kc = 0; kc < 4; ++kc) {
+      const bf16x8 x = dq_active ? frag_tr(sm.k, KS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 32 * dq + 16 * dt2, c)
+                                 : zero_frag();
+      if constexpr (DT == kF16) {
+        const uint4 w = __builtin_bit_cast(uint4, x);
+        uint4 h, l;
+        f16_pair_to_bf16_terms(w.x, h.x, l.x);
+        f16_pair_to_bf16_terms(w.y, h.y, l.y);
+        f16_pair_to_bf16_terms(w.z, h.z, l.z);
+        f16_pair_to_bf16_terms(w.w, h.w, l.w);
+        kt[dt2][kc] = __builtin_bit_cast(bf16x8, h);
+        ktl[dt2][kc] = __builtin_bit_cast(bf16x8, l);
+      } else {
+        kt[dt2][kc] = x;
+      }
+    }
 
   // ---- row staging: a tile is 32 rows of Q (threads 0-255) and of dO (threads 256-511);
   // TPR threads per row, each CPT 16-byte chunks TPR apart (per load, the row's threads
@@ -550,6 +563,12 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
   f32x4 dk[NDT], dv[NDT];  // C[key 16 w + 4 q4 + i][dim 16 dt + c]
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) dk[dt] = dv[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // fp16: dS enters dK as fp16 terms of 2^ks dS, ks per key (this lane's key c) from the
+  // running maximum kmax of |dS| over the item's tiles so far: 2^ks kmax < 2^15, so ks
+  // only decreases (the key's accumulators are then rescaled, exactly). dk holds
+  // 2^ks dK and dv 2^15 dV until the item's partial is stored.
+  float kmax = 0.f;
+  int ks = 15;
 
   MSA_MAIN_ISSUE(0)
   MSA_MAIN_COMMIT(0, 0)
@@ -568,8 +587,8 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       for (int kk = 0; kk < NK; ++kk) {
         const bf16x8 qa = load_frag(sm.qs[b] + (16 * rt + c) * KS + 32 * kk + 8 * q4);
         const bf16x8 ga = load_frag(sm.gs[b] + (16 * rt + c) * KS + 32 * kk + 8 * q4);
-        a = mfma(qa, kf[kk], a);
-        g = mfma(ga, vf[kk], g);
+        a = mfma_t<DT>(qa, kf[kk], a);
+        g = mfma_t<DT>(ga, vf[kk], g);
       }
       s[rt] = a;
       dp[rt] = g;
@@ -577,7 +596,10 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     // ---- P and dS, split into three bf16 terms; element j = 4 rt + i is row pi(q4, j)
     const int myrec = sm.rec[b][16 * rh + c];  // read before the barrier: the buffer is refilled after it
     const bool full = 32 * t + 32 <= nrows && sm.vis[b][0] >= 16 * wid + 16;  // rows are in token order
+    // bf16: P and dS as three bf16 terms (ph.., dh..); fp16: dS as bf16 terms for the dQ
+    // planes, P and dS kept (Pv, Dv; element j = 4 rt + i) for their fp16 splits below
     uint32_t ph[8], pm[8], pl[8], dh[8], dm[8], dl[8];
+    float Pv[8], Dv[8];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       float4 stv[4];
@@ -588,8 +610,12 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
         for (int i = 0; i < 4; ++i) {
           const float P = __builtin_amdgcn_exp2f(s[rt][i] * scale2 - stv[i].x) * stv[i].y;
           const float d = P * ((dp[rt][i] - stv[i].z) - stv[i].w);
-          split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
-          split3_bits(d, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
+          if constexpr (DT == kF16) {
+            Pv[4 * rt + i] = P, Dv[4 * rt + i] = d;
+          } else {
+            split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
+            split3_bits(d, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
+          }
         }
       } else {
         const int4 vis = *reinterpret_cast<const int4*>(&sm.vis[b][16 * rt + 4 * q4]);
@@ -599,10 +625,18 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
           const bool ok = key < vv[i];
           const float P = ok ? __builtin_amdgcn_exp2f(s[rt][i] * scale2 - stv[i].x) * stv[i].y : 0.f;
           const float d = ok ? P * ((dp[rt][i] - stv[i].z) - stv[i].w) : 0.f;
-          split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
-          split3_bits(d, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
+          if constexpr (DT == kF16) {
+            Pv[4 * rt + i] = P, Dv[4 * rt + i] = d;
+          } else {
+            split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
+            split3_bits(d, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
+          }
         }
       }
+    }
+    if constexpr (DT == kF16) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) split3_bits(Dv[j], dh[j], dm[j], dl[j]);
     }
     bf16x8 ap[3], ad[3];  // [hi, mid, lo]
     {
@@ -620,12 +654,47 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
         *reinterpret_cast<uint2*>(sm.ds[b][p3] + plane_offset(key, q4)) = make_uint2(w[p3][0], w[p3][1]);
         *reinterpret_cast<uint2*>(sm.ds[b][p3] + plane_offset(key, 4 + q4)) = make_uint2(w[p3][2], w[p3][3]);
       }
-      ap[0] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(ph[0], ph[1]), pack_hi16(ph[2], ph[3]),
-                                                    pack_hi16(ph[4], ph[5]), pack_hi16(ph[6], ph[7])));
-      ap[1] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pm[0], pm[1]), pack_hi16(pm[2], pm[3]),
-                                                    pack_hi16(pm[4], pm[5]), pack_hi16(pm[6], pm[7])));
-      ap[2] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pl[0], pl[1]), pack_hi16(pl[2], pl[3]),
-                                                    pack_hi16(pl[4], pl[5]), pack_hi16(pl[6], pl[7])));
+      if constexpr (DT == kF16) {
+        // P: fp16 terms of 2^15 P
+        uint32_t wp[3][4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          split3_pk_f16(Pv[2 * jj] * kPScaleF16, Pv[2 * jj + 1] * kPScaleF16, wp[0][jj], wp[1][jj], wp[2][jj]);
+        // dS: the key's running maximum over this tile's 32 rows (the four lanes of key c)
+        float mx = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) mx = fmaxf(mx, fabsf(Dv[j]));
+        kmax = fmaxf(kmax, quad_max(mx));
+        const int ks_new = 15 - __builtin_amdgcn_frexp_expf(kmax);  // kmax < 2^(15 - ks_new)
+        const int dlt = ks_new - ks;  // < 0, or any value while the key's accumulators are all zero
+        ks = ks_new;
+        if (__ballot(dlt != 0) != 0) {  // wave-uniform
+          // accumulator entry i of this lane is key 4 q4 + i: lane 4 q4 + i (c = 4 q4 + i) holds its shift
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int di = __shfl(dlt, 4 * q4 + i, kWave);
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) dk[dt][i] = __builtin_amdgcn_ldexpf(dk[dt][i], di);
+          }
+        }
+        uint32_t wd[3][4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          split3_pk_f16(__builtin_amdgcn_ldexpf(Dv[2 * jj], ks), __builtin_amdgcn_ldexpf(Dv[2 * jj + 1], ks), wd[0][jj],
+                        wd[1][jj], wd[2][jj]);
+#pragma unroll
+        for (int p3 = 0; p3 < 3; ++p3) {
+          ap[p3] = __builtin_bit_cast(bf16x8, make_uint4(wp[p3][0], wp[p3][1], wp[p3][2], wp[p3][3]));
+          ad[p3] = __builtin_bit_cast(bf16x8, make_uint4(wd[p3][0], wd[p3][1], wd[p3][2], wd[p3][3]));
+        }
+      } else {
+        ap[0] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(ph[0], ph[1]), pack_hi16(ph[2], ph[3]),
+                                                      pack_hi16(ph[4], ph[5]), pack_hi16(ph[6], ph[7])));
+        ap[1] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pm[0], pm[1]), pack_hi16(pm[2], pm[3]),
+                                                      pack_hi16(pm[4], pm[5]), pack_hi16(pm[6], pm[7])));
+        ap[2] = __builtin_bit_cast(bf16x8, make_uint4(pack_hi16(pl[0], pl[1]), pack_hi16(pl[2], pl[3]),
+                                                      pack_hi16(pl[4], pl[5]), pack_hi16(pl[6], pl[7])));
+      }
     }
     // ---- dV += P^T dO, dK += dS^T Q: B = X[rows pi(q4, j)][dim 16 dt + c], read transposed
 #pragma unroll
@@ -633,13 +702,13 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       const bf16x8 gb = frag_tr(sm.gs[b], KS, 4 * q4, 16 + 4 * q4, 16 * dt, c);
       const bf16x8 qb = frag_tr(sm.qs[b], KS, 4 * q4, 16 + 4 * q4, 16 * dt, c);
       f32x4 x = dv[dt];
-      x = mfma(ap[2], gb, x);
-      x = mfma(ap[1], gb, x);
-      dv[dt] = mfma(ap[0], gb, x);
+      x = mfma_t<DT>(ap[2], gb, x);
+      x = mfma_t<DT>(ap[1], gb, x);
+      dv[dt] = mfma_t<DT>(ap[0], gb, x);
       f32x4 y = dk[dt];
-      y = mfma(ad[2], qb, y);
-      y = mfma(ad[1], qb, y);
-      dk[dt] = mfma(ad[0], qb, y);
+      y = mfma_t<DT>(ad[2], qb, y);
+      y = mfma_t<DT>(ad[1], qb, y);
+      dk[dt] = mfma_t<DT>(ad[0], qb, y);
     }
     // ---- stage the next tile, start loading the one after
     if (t + 1 < ntiles) {
@@ -660,7 +729,14 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
         const bf16x8 bh = frag_tr_at(sm.ds[b][0] + oa, sm.ds[b][0] + ob);
 #pragma unroll
         for (int dt2 = 0; dt2 < 2; ++dt2) {
-          acc[dt2] = mfma(kt[dt2][kc], bl, acc[dt2]);
+          if constexpr (DT == kF16) {  // (Kh + Kl)(Dh + Dm + Dl), the smaller products first
+            acc[dt2] = mfma(ktl[dt2][kc], bl, acc[dt2]);
+            acc[dt2] = mfma(ktl[dt2][kc], bm, acc[dt2]);
+            acc[dt2] = mfma(kt[dt2][kc], bl, acc[dt2]);
+            acc[dt2] = mfma(ktl[dt2][kc], bh, acc[dt2]);
+          } else {
+            acc[dt2] = mfma(kt[dt2][kc], bl, acc[dt2]);
+          }
           acc[dt2] = mfma(kt[dt2][kc], bm, acc[dt2]);
           acc[dt2] = mfma(kt[dt2][kc], bh, acc[dt2]);
         }
@@ -681,6 +757,17 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
   // ---- this item's dK / dV contribution, in accumulator-fragment order:
   // kvpart[item][0 = dK, 1 = dV][wave][dt][lane][i] holds key 16 wave + 4 q4 + i, dim 16 dt + c.
   f32x4* base = reinterpret_cast<f32x4*>(kvpart + static_cast<int64_t>(item) * 2 * 128 * DP) + wid * NDT * 64 + lane;
+  if constexpr (DT == kF16) {  // divide out the scales (powers of two: exact)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int si = __shfl(ks, 4 * q4 + i, kWave);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        dk[dt][i] = __builtin_amdgcn_ldexpf(dk[dt][i], -si);
+        dv[dt][i] *= 1.f / kPScaleF16;
+      }
+    }
+  }
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) {
     __builtin_nontemporal_store(dk[dt], base + dt * 64);
@@ -696,7 +783,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
 // chunk does both and never touches acc. Per key the value is the same FP32 chain
 // acc = ((s_0 + s_1) + ...) as with a cleared accumulator (0 + s_0 == s_0: the item
 // sums start from +0, so s_0 is never -0).
-template <int DP>
+template <int DT, int DP>
 __global__ __launch_bounds__(256) void kv_bwd_accumulate(const int32_t* __restrict__ cu,
                                                          const int32_t* __restrict__ cu_blocks,
                                                          const int32_t* __restrict__ starts, int nseq, int G, int D,
@@ -728,8 +815,8 @@ __global__ __launch_bounds__(256) void kv_bwd_accumulate(const int32_t* __restri
         xv = acc[T * G * D + off] + xv;
       }
       if (last) {
-        if (dk) dk[off] = f32_to_bf16_bits(xk * scale);
-        if (dv) dv[off] = f32_to_bf16_bits(xv);
+        if (dk) store_from_f32<DT>(dk, off, xk * scale);
+        if (dv) store_from_f32<DT>(dv, off, xv);
       } else {
         acc[off] = xk;
         acc[T * G * D + off] = xv;
@@ -745,6 +832,7 @@ __global__ __launch_bounds__(256) void kv_bwd_accumulate(const int32_t* __restri
 // (token, head) rows per dQ-combine workgroup, one 32-lane segment each (measured at c4:
 // 16 rows 1.47 ms, 8 rows 1.49, 4 rows 1.49, 32 rows 1.49).
 constexpr int kDqCombineRows = 16;
+template <int DT>
 __global__ __launch_bounds__(32 * kDqCombineRows) void kv_bwd_dq_combine(const int32_t* __restrict__ indices,
                                                          const int32_t* __restrict__ cu, int nseq, int64_t t0,
                                                          int64_t t1, int Hq, int G, int D, int K, int B, double scale,
@@ -784,11 +872,7 @@ __global__ __launch_bounds__(32 * kDqCombineRows) void kv_bwd_dq_combine(const i
       }
     }
   }
-  const uint32_t w0 = f32_to_bf16_bits(static_cast<float>(a0 * scale)) |
-                      (static_cast<uint32_t>(f32_to_bf16_bits(static_cast<float>(a1 * scale))) << 16);
-  const uint32_t w1 = f32_to_bf16_bits(static_cast<float>(a2 * scale)) |
-                      (static_cast<uint32_t>(f32_to_bf16_bits(static_cast<float>(a3 * scale))) << 16);
-  *reinterpret_cast<uint2*>(dq + th * D + 4 * sub) = make_uint2(w0, w1);
+  *reinterpret_cast<uint2*>(dq + th * D + 4 * sub) = pack4_from_f64<DT>(a0 * scale, a1 * scale, a2 * scale, a3 * scale);
 }
 
 static int nk_of_dim(int D) { return D <= 32 ? 1 : (D <= 64 ? 2 : 4); }
@@ -823,11 +907,13 @@ int64_t attn_bwd_kv_workspace_bytes(int64_t T, int64_t Hq, int64_t G, int64_t D,
   return bwd_layout(T, Hq, G, D, K, total_blocks).total;
 }
 
-int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, const void* dout, double* rs,
+int attn_bwd_kv(int dt, const void* q, const void* k, const void* v, const void* out, const void* dout, double* rs,
                 const int32_t* indices, const int32_t* cu, int nseq, int64_t T, int Hq, int G, int D, int K, int B,
                 float scale, const int32_t* cu_blocks, int64_t total_blocks, const int32_t* row_ptr,
                 const int32_t* qidx, const int32_t* sidx, void* dq, void* dk, void* dv, void* ws, int64_t ws_bytes,
                 const float* o32, hipStream_t st) {
+  if (dt != kBF16 && dt != kF16) return kErrInvalidArgument;
+  const bool f16 = dt == kF16;
   const int64_t rows = total_blocks * G;
   const BwdLayout L = bwd_layout(T, Hq, G, D, K, total_blocks);
   if (ws_bytes < L.total) return kErrInvalidArgument;
@@ -861,7 +947,11 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
   const int rshift = (ratio & (ratio - 1)) == 0 ? __builtin_ctz(ratio) : -1;  // power-of-two ratios shift
   {
     ProfScope ps(kProfBwdCenter, st);
-    hipLaunchKernelGGL(kv_bwd_center<kCenterRows>, dim3(grid_1d(T * Hq, 8 * kCenterRows)), dim3(256), 0, st, ob, o32, gb, T * Hq, D, rs);
+    const dim3 cgrid(grid_1d(T * Hq, 8 * kCenterRows));
+    if (f16)
+      hipLaunchKernelGGL((kv_bwd_center<kF16, kCenterRows>), cgrid, dim3(256), 0, st, ob, o32, gb, T * Hq, D, rs);
+    else
+      hipLaunchKernelGGL((kv_bwd_center<kBF16, kCenterRows>), cgrid, dim3(256), 0, st, ob, o32, gb, T * Hq, D, rs);
   }
   {
     ProfScope ps(kProfBwdPlan, st);
@@ -881,10 +971,13 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       const int32_t* ord = nullptr;
       const int sepi = static_cast<int>(sp.epi);
       const dim3 grid(static_cast<unsigned>(sp.max_items)), block(kStatThreads);
-#define MSA_BWD_STATS(NKV, FD) hipLaunchKernelGGL((kv_bwd_stats_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, sepi, it0, all_rows, spart)
-      if (nk == 1) { if (fd) MSA_BWD_STATS(1, true); else MSA_BWD_STATS(1, false); }
-      else if (nk == 2) { if (fd) MSA_BWD_STATS(2, true); else MSA_BWD_STATS(2, false); }
-      else { if (fd) MSA_BWD_STATS(4, true); else MSA_BWD_STATS(4, false); }
+#define MSA_BWD_STATS(DTV, NKV, FD) hipLaunchKernelGGL((kv_bwd_stats_kernel<DTV, NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, sepi, it0, all_rows, spart)
+#define MSA_BWD_STATS_NK(DTV)                                                                  \
+  if (nk == 1) { if (fd) MSA_BWD_STATS(DTV, 1, true); else MSA_BWD_STATS(DTV, 1, false); }       \
+  else if (nk == 2) { if (fd) MSA_BWD_STATS(DTV, 2, true); else MSA_BWD_STATS(DTV, 2, false); }  \
+  else { if (fd) MSA_BWD_STATS(DTV, 4, true); else MSA_BWD_STATS(DTV, 4, false); }
+      if (f16) { MSA_BWD_STATS_NK(kF16) } else { MSA_BWD_STATS_NK(kBF16) }
+#undef MSA_BWD_STATS_NK
 #undef MSA_BWD_STATS
     }
     {
@@ -902,10 +995,13 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
       const dim3 grid(static_cast<unsigned>(mp.max_items)), block(kMainThreads);
       {
         ProfScope ps(kProfBwdMain, st);
-#define MSA_BWD_MAIN(NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, rshift, rowf, dqpart, kvpart)
-        if (nk == 1) { if (fd) MSA_BWD_MAIN(1, true); else MSA_BWD_MAIN(1, false); }
-        else if (nk == 2) { if (fd) MSA_BWD_MAIN(2, true); else MSA_BWD_MAIN(2, false); }
-        else { if (fd) MSA_BWD_MAIN(4, true); else MSA_BWD_MAIN(4, false); }
+#define MSA_BWD_MAIN(DTV, NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<DTV, NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, rshift, rowf, dqpart, kvpart)
+#define MSA_BWD_MAIN_NK(DTV)                                                                 \
+  if (nk == 1) { if (fd) MSA_BWD_MAIN(DTV, 1, true); else MSA_BWD_MAIN(DTV, 1, false); }       \
+  else if (nk == 2) { if (fd) MSA_BWD_MAIN(DTV, 2, true); else MSA_BWD_MAIN(DTV, 2, false); }  \
+  else { if (fd) MSA_BWD_MAIN(DTV, 4, true); else MSA_BWD_MAIN(DTV, 4, false); }
+        if (f16) { MSA_BWD_MAIN_NK(kF16) } else { MSA_BWD_MAIN_NK(kBF16) }
+#undef MSA_BWD_MAIN_NK
 #undef MSA_BWD_MAIN
       }
       if (need_kv) {
@@ -915,17 +1011,23 @@ int attn_bwd_kv(const void* q, const void* k, const void* v, const void* out, co
         const int first = c == 0, last = c + 1 == sp.nch;
         auto* dkb = static_cast<uint16_t*>(dk);
         auto* dvb = static_cast<uint16_t*>(dv);
-#define MSA_BWD_ACC(DPV) hipLaunchKernelGGL(kv_bwd_accumulate<DPV>, agrid, dim3(256), 0, st, cu, cu_blocks, starts, nseq, G, D, B, T, kvpart, acc, first, last, scale, dkb, dvb)
-        if (nk == 1) MSA_BWD_ACC(32);
-        else if (nk == 2) MSA_BWD_ACC(64);
-        else MSA_BWD_ACC(128);
+#define MSA_BWD_ACC(DTV, DPV) hipLaunchKernelGGL((kv_bwd_accumulate<DTV, DPV>), agrid, dim3(256), 0, st, cu, cu_blocks, starts, nseq, G, D, B, T, kvpart, acc, first, last, scale, dkb, dvb)
+#define MSA_BWD_ACC_NK(DTV) \
+  if (nk == 1) MSA_BWD_ACC(DTV, 32); else if (nk == 2) MSA_BWD_ACC(DTV, 64); else MSA_BWD_ACC(DTV, 128);
+        if (f16) { MSA_BWD_ACC_NK(kF16) } else { MSA_BWD_ACC_NK(kBF16) }
+#undef MSA_BWD_ACC_NK
 #undef MSA_BWD_ACC
       }
     }
     if (dq) {
       ProfScope ps(kProfBwdDqCombine, st);
-      hipLaunchKernelGGL(kv_bwd_dq_combine, dim3(grid_1d((t1 - t0) * Hq, kDqCombineRows)), dim3(32 * kDqCombineRows), 0, st, indices, cu, nseq, t0,
-                         t1, Hq, G, D, K, B, static_cast<double>(scale), dqpart, static_cast<uint16_t*>(dq));
+      const dim3 qgrid(grid_1d((t1 - t0) * Hq, kDqCombineRows)), qblock(32 * kDqCombineRows);
+      if (f16)
+        hipLaunchKernelGGL(kv_bwd_dq_combine<kF16>, qgrid, qblock, 0, st, indices, cu, nseq, t0, t1, Hq, G, D, K, B,
+                           static_cast<double>(scale), dqpart, static_cast<uint16_t*>(dq));
+      else
+        hipLaunchKernelGGL(kv_bwd_dq_combine<kBF16>, qgrid, qblock, 0, st, indices, cu, nseq, t0, t1, Hq, G, D, K, B,
+                           static_cast<double>(scale), dqpart, static_cast<uint16_t*>(dq));
     }
   }
   return status_from(hipGetLastError());

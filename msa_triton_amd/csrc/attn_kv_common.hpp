@@ -1,4 +1,4 @@
-// Shared pieces of the KV-major stage-3 kernels (bf16 MFMA path).
+// Shared pieces of the KV-major stage-3 kernels (bf16 and fp16 MFMA paths).
 //
 // The k2q CSR has one row per (key block, group); its edges are the (query
 // token, slot) pairs that selected the block, ordered by query token. KV-major
@@ -15,6 +15,13 @@ namespace msa {
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr double kLn2 = 0.6931471805599453;
+
+// fp16 kernels split probabilities P <= 1 into fp16 terms after scaling them by 2^15 (the
+// top binade of fp16, so that the split is exact down to P = 2^-16 and within 2^-40 of P
+// below); the products they feed carry the factor, which is divided out exactly later.
+constexpr float kPScaleF16 = 32768.f;
+template <int DT>
+constexpr double p_scale() { return DT == kF16 ? 32768.0 : 1.0; }
 
 // Two 8-byte reads of tile[row][base + pi(q4, j)] where pi(q4, j) = 16*(j/4) + 4*q4 + j%4.
 __device__ __forceinline__ bf16x8 read_keys_pi(const uint16_t* tile, int stride, int row, int base, int q4) {

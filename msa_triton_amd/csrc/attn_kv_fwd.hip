@@ -1,4 +1,4 @@
-// Stage 3 forward, KV-major (bf16 inputs).
+// Stage 3 forward, KV-major (bf16 and fp16 inputs).
 //
 // Query-major attention streams each token's selected K/V blocks (K/V bytes
 // gathered per token = #slots x block x D x 4: ~137 GB at 32K tokens). Here the
@@ -22,7 +22,9 @@
 //
 // The logits use the K row fragment and the Q row fragment over the same dims
 // in the same k order as the backward kernels. P.V is computed exactly in its
-// products: P is split into three bf16 terms (hi + mid + lo == P).
+// products: P is split into three terms of the input type (hi + mid + lo == P); fp16
+// splits 2^15 P (fp16's exponent range ends at 2^-24), and the partial O carries that
+// factor until the combine divides it out.
 #include <atomic>
 #include <type_traits>
 
@@ -204,7 +206,7 @@ __global__ __launch_bounds__(1024) void kv_item_order(const int32_t* __restrict_
   }
 }
 
-template <int NK, bool FULLD>
+template <int DT, int NK, bool FULLD>
 __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx,
@@ -307,7 +309,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
       for (int rt = 0; rt < 2; ++rt) {
         f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) a = mfma(kf[kk], qf[rt][kk], a);
+        for (int kk = 0; kk < NK; ++kk) a = mfma_t<DT>(kf[kk], qf[rt][kk], a);
         s[rt][kt] = a;
       }
     }
@@ -361,7 +363,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
           for (int jj = 0; jj < 4; ++jj) {
             // elements j = 2*jj, 2*jj + 1 -> C tile 2*kc + j/4, entry j%4
             const int j0 = 2 * jj, j1 = 2 * jj + 1;
-            split3_pk(s[rt][2 * kc + j0 / 4][j0 % 4], s[rt][2 * kc + j1 / 4][j1 % 4], wh[jj], wm[jj], wl[jj]);
+            const float x0 = s[rt][2 * kc + j0 / 4][j0 % 4], x1 = s[rt][2 * kc + j1 / 4][j1 % 4];
+            if constexpr (DT == kF16)
+              split3_pk_f16(x0 * kPScaleF16, x1 * kPScaleF16, wh[jj], wm[jj], wl[jj]);
+            else
+              split3_pk(x0, x1, wh[jj], wm[jj], wl[jj]);
           }
           ph[rt] = __builtin_bit_cast(bf16x8, make_uint4(wh[0], wh[1], wh[2], wh[3]));
           pm[rt] = __builtin_bit_cast(bf16x8, make_uint4(wm[0], wm[1], wm[2], wm[3]));
@@ -374,9 +380,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
 #pragma unroll
           for (int rt = 0; rt < 2; ++rt) {
             f32x4 acc = kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : o[rt][dt];
-            acc = mfma(vb, pl[rt], acc);
-            acc = mfma(vb, pm[rt], acc);
-            o[rt][dt] = mfma(vb, ph[rt], acc);
+            acc = mfma_t<DT>(vb, pl[rt], acc);
+            acc = mfma_t<DT>(vb, pm[rt], acc);
+            o[rt][dt] = mfma_t<DT>(vb, ph[rt], acc);
           }
         }
       }
@@ -412,6 +418,7 @@ constexpr int kCombineBatch = 8;
 // FP64 oracle as the statistics pass for every row, at logit scales 0.3x to 16x.
 constexpr double kFlatRowMass = 20.0;
 
+template <int DT>
 __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restrict__ indices,
                                                         const int32_t* __restrict__ cu, int nseq, int64_t t0,
                                                         int64_t t1, int Hq, int G, int D, int K, int B,
@@ -493,13 +500,14 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
   for (int o = 16; o > 0; o >>= 1) L += __shfl_xor(L, o, 32);
   const bool has = L > 0.0;
   if (has_dims) {
-    float r[4];
+    double x[4];  // the partials carry the P scale of the input type (a power of two)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = has ? static_cast<float>(acc[i] / L) : 0.f;
-    const uint32_t w0 = f32_to_bf16_bits(r[0]) | (f32_to_bf16_bits(r[1]) << 16);
-    const uint32_t w1 = f32_to_bf16_bits(r[2]) | (f32_to_bf16_bits(r[3]) << 16);
-    *reinterpret_cast<uint2*>(out + th * D + 4 * sub) = make_uint2(w0, w1);
-    if (o32) *reinterpret_cast<float4*>(o32 + th * D + 4 * sub) = make_float4(r[0], r[1], r[2], r[3]);
+    for (int i = 0; i < 4; ++i) x[i] = has ? acc[i] / L * (1.0 / p_scale<DT>()) : 0.0;
+    *reinterpret_cast<uint2*>(out + th * D + 4 * sub) = pack4_from_f64<DT>(x[0], x[1], x[2], x[3]);
+    if (o32)
+      *reinterpret_cast<float4*>(o32 + th * D + 4 * sub) =
+          make_float4(static_cast<float>(x[0]), static_cast<float>(x[1]), static_cast<float>(x[2]),
+                      static_cast<float>(x[3]));
   }
   if (sub == 0) {
     // row_state keeps the base-2 lse (the backward's p = 2^(x - lse2) is then exactly
@@ -606,10 +614,11 @@ int64_t attn_fwd_kv_workspace_bytes(int64_t T, int64_t Hq, int64_t G, int64_t D,
   return fwd_layout(T, Hq, G, D, K, total_blocks).total;
 }
 
-int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indices, const int32_t* cu, int nseq,
-                int64_t T, int Hq, int G, int D, int K, int B, float scale, const int32_t* cu_blocks,
+int attn_fwd_kv(int dt, const void* q, const void* k, const void* v, const int32_t* indices, const int32_t* cu,
+                int nseq, int64_t T, int Hq, int G, int D, int K, int B, float scale, const int32_t* cu_blocks,
                 int64_t total_blocks, const int32_t* row_ptr, const int32_t* qidx, const int32_t* sidx, void* ws,
                 int64_t ws_bytes, void* out, float* lse, double* rs, float* o32, hipStream_t st) {
+  if (dt != kBF16 && dt != kF16) return kErrInvalidArgument;
   const int64_t rows = total_blocks * G;
   const FwdLayout f = fwd_layout(T, Hq, G, D, K, total_blocks);
   if (ws_bytes < f.total) return kErrInvalidArgument;
@@ -639,17 +648,25 @@ int attn_fwd_kv(const void* q, const void* k, const void* v, const int32_t* indi
       const int2* its = kv_plan_items(pl, base, c);
       const int32_t* ord = kv_plan_order(pl, base, c);
       const int it0 = static_cast<int>(t0);
-#define MSA_FWD_PARTIAL(NKV, FD) hipLaunchKernelGGL((attn_fwd_partial_kernel<NKV, FD>), grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, epi, it0, opart, ml)
+#define MSA_FWD_PARTIAL(DTV, NKV, FD) hipLaunchKernelGGL((attn_fwd_partial_kernel<DTV, NKV, FD>), grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, epi, it0, opart, ml)
+#define MSA_FWD_PARTIAL_NK(DTV)                                                                   \
+  if (nk == 1) { if (fd) MSA_FWD_PARTIAL(DTV, 1, true); else MSA_FWD_PARTIAL(DTV, 1, false); }       \
+  else if (nk == 2) { if (fd) MSA_FWD_PARTIAL(DTV, 2, true); else MSA_FWD_PARTIAL(DTV, 2, false); }  \
+  else { if (fd) MSA_FWD_PARTIAL(DTV, 4, true); else MSA_FWD_PARTIAL(DTV, 4, false); }
       const int nk = nk_of_dim(D);
       const bool fd = D == 32 * nk;
-      if (nk == 1) { if (fd) MSA_FWD_PARTIAL(1, true); else MSA_FWD_PARTIAL(1, false); }
-      else if (nk == 2) { if (fd) MSA_FWD_PARTIAL(2, true); else MSA_FWD_PARTIAL(2, false); }
-      else { if (fd) MSA_FWD_PARTIAL(4, true); else MSA_FWD_PARTIAL(4, false); }
+      if (dt == kF16) { MSA_FWD_PARTIAL_NK(kF16) } else { MSA_FWD_PARTIAL_NK(kBF16) }
+#undef MSA_FWD_PARTIAL_NK
 #undef MSA_FWD_PARTIAL
     }
     ProfScope ps(kProfFwdCombine, st);
-    hipLaunchKernelGGL(attn_fwd_combine, dim3(grid_1d((t1 - t0) * Hq, 8)), dim3(256), 0, st, indices, cu, nseq, t0, t1,
-                       Hq, G, D, K, B, opart, ml, ob, lse, rs, o32);
+    const dim3 cgrid(grid_1d((t1 - t0) * Hq, 8));
+    if (dt == kF16)
+      hipLaunchKernelGGL(attn_fwd_combine<kF16>, cgrid, dim3(256), 0, st, indices, cu, nseq, t0, t1, Hq, G, D, K, B,
+                         opart, ml, ob, lse, rs, o32);
+    else
+      hipLaunchKernelGGL(attn_fwd_combine<kBF16>, cgrid, dim3(256), 0, st, indices, cu, nseq, t0, t1, Hq, G, D, K, B,
+                         opart, ml, ob, lse, rs, o32);
   }
   return status_from(hipGetLastError());
 }

@@ -1,4 +1,5 @@
-// MFMA fragment helpers shared by the gfx950 kernels (v_mfma_f32_16x16x32_bf16).
+// MFMA fragment helpers shared by the gfx950 kernels (v_mfma_f32_16x16x32_bf16 and its
+// fp16 form v_mfma_f32_16x16x32_f16).
 //
 // Lane l (c = l % 16, q4 = l / 16) holds A[c][8*q4 + j], B[8*q4 + j][c] (j = 0..7)
 // and C[4*q4 + i][c] (i = 0..3). Fragments are assembled in 32-bit words: the
@@ -63,6 +64,90 @@ __device__ __forceinline__ void split3_pk(float x0, float x1, uint32_t& hi, uint
   const float r0 = sub_lo_half(hi, x0), r1 = sub_hi_half(hi, x1);
   mid = cvt_pk_bf16(r0, r1);
   lo = cvt_pk_bf16(sub_lo_half(mid, r0), sub_hi_half(mid, r1));
+}
+
+// ---- fp16 operands (v_mfma_f32_16x16x32_f16: the fragment layout of the bf16 form; the
+// bf16x8 container carries the 16-bit words unchanged)
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_pk __attribute__((ext_vector_type(2)));
+
+// The MFMA of the input type DT (kBF16 or kF16): products exact in fp32 for both.
+template <int DT>
+__device__ __forceinline__ f32x4 mfma_t(bf16x8 a, bf16x8 b, f32x4 c) {
+  if constexpr (DT == kF16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  else
+    return mfma(a, b, c);
+}
+
+// Two fp32 values rounded to nearest fp16, packed (x0 in the low half): v_cvt_pk_f16_f32.
+__device__ __forceinline__ uint32_t cvt_pk_f16(float x0, float x1) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_pk){x0, x1}, f16x2_pk));
+}
+
+// x - (fp16 half of w) as one v_dot2_f32_f16 against (-1, -0): exact as in sub_lo_half.
+__device__ __forceinline__ float sub_lo_half_f16(uint32_t w, float x) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_pk, w), __builtin_bit_cast(f16x2_pk, 0x8000bc00u), x, false);
+}
+__device__ __forceinline__ float sub_hi_half_f16(uint32_t w, float x) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_pk, w), __builtin_bit_cast(f16x2_pk, 0xbc008000u), x, false);
+}
+
+// Split of two fp32 values into three packed fp16 words by round-to-nearest: hi = rn(x),
+// mid = rn(x - hi), lo = rn(x - hi - mid) (x0 in the low halves). x - hi and x - hi - mid
+// are exact in fp32 (multiples of ulp(x) below half an ulp of the term before), and
+// x == hi + mid + lo exactly when 2^-1 <= |x| <= 2^15: the last residual has <= 2
+// significant bits on the grid of ulp(x) >= 2^-24, fp16's smallest subnormal. Below
+// 2^-1 the error is at most 2^-25 (half that subnormal). Callers scale their values
+// into that range by a power of two first (fp16's exponent range is 2^-24 .. 2^15).
+__device__ __forceinline__ void split3_pk_f16(float x0, float x1, uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+  hi = cvt_pk_f16(x0, x1);
+  const float r0 = sub_lo_half_f16(hi, x0), r1 = sub_hi_half_f16(hi, x1);
+  mid = cvt_pk_f16(r0, r1);
+  lo = cvt_pk_f16(sub_lo_half_f16(mid, r0), sub_hi_half_f16(mid, r1));
+}
+
+// The fp32 value of the low / high 16-bit element of w, read as the input type DT
+// (scalar bit casts: no element extraction from 16-bit vector types).
+template <int DT>
+__device__ __forceinline__ float lo16_f32(uint32_t w) {
+  if constexpr (DT == kF16)
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w)));
+  else
+    return __uint_as_float(w << 16);
+}
+template <int DT>
+__device__ __forceinline__ float hi16_f32(uint32_t w) {
+  if constexpr (DT == kF16)
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+  else
+    return __uint_as_float(w & 0xffff0000u);
+}
+
+// fp16 -> two bf16 terms, exactly: an fp16 value has 11 significant bits and its
+// exponent range lies inside bf16's, so hi = rn_bf16(x) and lo = x - hi (<= 3 bits) are
+// both exact. One 32-bit word of two fp16 values gives a word of his and one of los.
+__device__ __forceinline__ void f16_pair_to_bf16_terms(uint32_t w, uint32_t& hi, uint32_t& lo) {
+  const float x0 = lo16_f32<kF16>(w), x1 = hi16_f32<kF16>(w);
+  hi = cvt_pk_bf16(x0, x1);
+  lo = cvt_pk_bf16(sub_lo_half(hi, x0), sub_hi_half(hi, x1));
+}
+
+// Four FP64 results as four elements of DT (x0 lowest), each rounded as store_from_f64
+// rounds it: bf16 through fp32, fp16 once (round-to-odd through fp32).
+template <int DT>
+__device__ __forceinline__ uint2 pack4_from_f64(double x0, double x1, double x2, double x3) {
+  if constexpr (DT == kF16) {
+    auto h = [](double x) {
+      return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f64_to_f32_odd(x))));
+    };
+    return make_uint2(h(x0) | (h(x1) << 16), h(x2) | (h(x3) << 16));
+  } else {
+    auto b = [](double x) { return static_cast<uint32_t>(f32_to_bf16_bits(static_cast<float>(x))); };
+    return make_uint2(b(x0) | (b(x1) << 16), b(x2) | (b(x3) << 16));
+  }
 }
 
 // One 32-bit word holding the bf16 truncations (upper halves) of a (low half) and b (high half).

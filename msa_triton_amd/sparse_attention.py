@@ -6,7 +6,7 @@ defaults, validation order, messages and exception types) and the
 ``needs_input_grad``; the public ``build_k2q_csr`` is invoked by the backward
 exactly when dK or dV is needed; lse is non-differentiable.
 
-Execution: ``msa_attn_fwd`` and ``msa_attn_bwd``. For bf16 both are KV-major
+Execution: ``msa_attn_fwd`` and ``msa_attn_bwd``. For bf16 and fp16 both are KV-major
 over the selection's k2q CSR (per-block partials merged in slot order, dK/dV
 owned per key block, no floating-point atomics); the forward builds the CSR
 itself and keeps it for a backward that needs only dQ. ``cu_seqlens`` may be a
@@ -31,10 +31,10 @@ from .layout import PackedSequences, call_sequences, prepared_for, sequence_leng
 
 
 def _sub_block_view(q, k, indices, meta, block_size, seqs):
-    """The selection as the MFMA kernels take it: bf16 blocks above 128 keys as sub-blocks
-    (``k2q.sub_block_selection``); unchanged for other calls."""
+    """The selection as the MFMA kernels take it: bf16 / fp16 blocks above 128 keys as
+    sub-blocks (``k2q.sub_block_selection``); unchanged for other calls."""
     total, heads, dim = q.shape
-    if q.dtype != torch.bfloat16:
+    if q.dtype not in (torch.bfloat16, torch.float16):
         return indices, meta, block_size, seqs
     lib = _lib.lib()
 

@@ -51,12 +51,18 @@ def test_host_only_helpers():
     assert handle.msa_k2q_counter_elems(2, cb.ctypes.data, 4) == 4 * (3 + 1)
     # block-major (tie, ds) copies plus FP64 dk partials: 3 blocks x 1 key group x 1 segment x 8 keys x 128 dims
     assert handle.msa_score_bwd_workspace_bytes(10, 2, 3, 8, 4, 3) >= 10 * 2 * 3 * 8 + 3 * 8 * 128 * 8
-    assert handle.msa_attn_fwd_workspace_bytes(2, 256, 8, 2, 64, 4, 2, 128) > 0
-    assert handle.msa_attn_bwd_workspace_bytes(2, 256, 8, 2, 64, 4, 2, 128) > 0
-    # fp32 / fp16 and unsupported bf16 shapes run the VALU kernels: no workspace
+    # bf16 and fp16 run the KV-major MFMA kernels (same workspace layout for both)
+    for code in (1, 2):
+        assert handle.msa_attn_fwd_workspace_bytes(code, 256, 8, 2, 64, 4, 2, 128) > 0
+        assert handle.msa_attn_bwd_workspace_bytes(code, 256, 8, 2, 64, 4, 2, 128) > 0
+    assert (handle.msa_attn_bwd_workspace_bytes(1, 256, 8, 2, 64, 4, 2, 128)
+            == handle.msa_attn_bwd_workspace_bytes(2, 256, 8, 2, 64, 4, 2, 128))
+    # fp32 and unsupported shapes (D % 8 != 0, blocks above 128) run the VALU kernels: no workspace
     assert handle.msa_attn_fwd_workspace_bytes(0, 256, 8, 2, 64, 4, 2, 128) == 0
-    assert handle.msa_attn_bwd_workspace_bytes(1, 256, 8, 2, 64, 4, 2, 128) == 0
-    assert handle.msa_attn_bwd_workspace_bytes(2, 256, 8, 2, 60, 4, 2, 128) == 0
+    assert handle.msa_attn_bwd_workspace_bytes(0, 256, 8, 2, 64, 4, 2, 128) == 0
+    for code in (1, 2):
+        assert handle.msa_attn_bwd_workspace_bytes(code, 256, 8, 2, 60, 4, 2, 128) == 0
+        assert handle.msa_attn_fwd_workspace_bytes(code, 256, 8, 2, 64, 4, 2, 131) == 0
 
 
 def _cu(values):

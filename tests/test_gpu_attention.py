@@ -45,7 +45,8 @@ def _assert_lse(actual, expected):
     torch.testing.assert_close(actual[finite], expected[finite], atol=1e-4, rtol=1e-4)
 
 
-@pytest.mark.parametrize("lengths,groups,ratio,dimension,block_size,topk,scale", [
+# The reference's attention test shapes (tests/test_triton_attention.py:58-93).
+REFERENCE_SHAPES = [
     ([1], 1, 1, 5, 128, 1, None),
     ([7, 3], 2, 2, 8, 3, 3, None),
     ([17, 5], 3, 1, 16, 8, 2, 0.2),
@@ -54,7 +55,10 @@ def _assert_lse(actual, expected):
     ([5, 1, 9], 2, 4, 32, 4, 4, None),
     ([5, 3], 2, 2, 128, 4, 2, None),
     ([0, 3, 0, 2, 0], 2, 2, 8, 2, 2, None),
-])
+]
+
+
+@pytest.mark.parametrize("lengths,groups,ratio,dimension,block_size,topk,scale", REFERENCE_SHAPES)
 def test_forward_backward_against_fp64(lengths, groups, ratio, dimension, block_size, topk, scale, device):
     cpu, indices, cu = attention_inputs(lengths, groups, ratio, dimension, block_size, topk)
     tensors, indices_d, cu_d = _to(device, cpu, indices, cu)
@@ -68,6 +72,37 @@ def test_forward_backward_against_fp64(lengths, groups, ratio, dimension, block_
     actual.backward(grad.to(device))
     for tensor, ref in zip(tensors, (dq, dk, dv)):
         _close(tensor.grad, ref)
+
+
+@pytest.mark.parametrize("lengths,groups,ratio,dimension,block_size,topk,scale", REFERENCE_SHAPES)
+def test_fp16_forward_backward_against_fp64(lengths, groups, ratio, dimension, block_size, topk, scale, device):
+    """The reference's test shapes with fp16 inputs (the reference's q / k / v values, cast
+    to fp16): the MFMA kernels wherever the shape fits them (all but head dim 5), against
+    the FP64 oracle within the stated fp16 tolerance -- every element within
+    1e-4 + 2^-10 |x| of the FP64 value, at most 0.1 % (at least one) outside the gate.
+    fp16 has 3 more significant bits than bf16, so a value is about 8 times likelier to
+    fall within fp32 arithmetic's reach of an fp16 rounding midpoint."""
+    from msa_triton_amd import _lib
+    from tests.test_gpu_sweep import _check_dtype_stated
+
+    cpu, indices, cu = attention_inputs(lengths, groups, ratio, dimension, block_size, topk)
+    cpu = tuple(x.to(torch.float16) for x in cpu)
+    total, heads = sum(lengths), groups * ratio
+    blocks = sum((n + block_size - 1) // block_size for n in lengths)
+    on_mfma = _lib.lib().msa_attn_fwd_workspace_bytes(1, total, heads, groups, dimension, topk, blocks,
+                                                      block_size) > 0
+    assert on_mfma == (dimension % 8 == 0)
+    tensors, indices_d, cu_d = _to(device, cpu, indices, cu)
+    grad = torch.randn(cpu[0].shape, generator=torch.Generator().manual_seed(5678)).to(torch.float16)
+    out, lse, dq, dk, dv = _oracle(cpu, indices, cu, block_size, scale, grad)
+    actual, actual_lse = msa.m3_sparse_attention(*tensors, indices_d, cu_d, max(lengths), block_size=block_size,
+                                                 scale=scale, return_lse=True)
+    assert actual.dtype == torch.float16
+    _check_dtype_stated(actual, out, torch.float16, "out")
+    _assert_lse(actual_lse, lse)
+    actual.backward(grad.to(device))
+    for tensor, ref, name in zip(tensors, (dq, dk, dv), ("dq", "dk", "dv")):
+        _check_dtype_stated(tensor.grad, ref, torch.float16, name)
 
 
 @pytest.mark.parametrize("topk", [0, 3])

@@ -4,7 +4,9 @@ fp32 inputs, forward and backward against the FP64 oracle: fp32 within the refer
 gate, fp16 within its stated analogue (every element within one fp16 ulp of the FP64
 value, at most 0.1 % outside the gate). Head ratio 3 makes a KV-pass step span edges
 (3 heads per edge against 4 to 16 rows per step); ragged lengths and blocks of 16 leave
-partly visible blocks, and the blocks of 128 keys fill the forward's 64-key steps."""
+partly visible blocks, and the blocks of 128 keys fill the forward's 64-key steps.
+fp16 takes these kernels only for shapes outside the MFMA kernels: its cases use blocks
+of 131 and 257 keys (primes above 128, so no sub-block split applies)."""
 
 from __future__ import annotations
 
@@ -20,12 +22,18 @@ from tests.test_gpu_sweep import _check_dtype_stated
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("block", [16, 128])
+@pytest.mark.parametrize("block_index", [0, 1], ids=["short", "long"])
 @pytest.mark.parametrize("dim", [8, 16, 32, 64, 128])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32], ids=["fp16", "fp32"])
-def test_row_parallel_fp64_kernels_against_oracle(dtype, dim, block, device):
+def test_row_parallel_fp64_kernels_against_oracle(dtype, dim, block_index, device):
+    from msa_triton_amd import _lib
+
+    block = ([131, 257] if dtype == torch.float16 else [16, 128])[block_index]
     lengths, groups, ratio, topk = [150, 61], 2, 3, 4
     total = sum(lengths)
+    nblocks = sum((n + block - 1) // block for n in lengths)
+    assert _lib.lib().msa_attn_fwd_workspace_bytes(_lib.DTYPE_CODE[dtype], total, groups * ratio, groups, dim, topk,
+                                                   nblocks, block) == 0  # the FP64 kernels
     g = torch.Generator().manual_seed(dim + block)
     ids = random_selection(total, groups, topk, lengths, block, 1, g)
     q, k, v, dout = (torch.randn(total, h, dim, generator=g).to(dtype) for h in (groups * ratio, groups, groups,
