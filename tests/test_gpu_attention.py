@@ -105,6 +105,46 @@ def test_fp16_forward_backward_against_fp64(lengths, groups, ratio, dimension, b
         _check_dtype_stated(tensor.grad, ref, torch.float16, name)
 
 
+def test_fp16_gradients_follow_power_of_two_output_gradients(device):
+    """fp16 on the MFMA kernels carries dS into dK under a per-key power-of-two scale (from
+    the running maximum of |dS|) and P under a fixed 2^15. Scaling dO by 2^s (exact: every
+    |dO| in [2^-2, 2^2), s = -10 .. 5) scales every fp32 / fp64 quantity of the backward
+    exactly, so dQ, dK and dV must come out as 2^s times the s = 0 gradients bit for bit
+    (where those stay in fp16's normal range; within a subnormal step, scaled, below it). A
+    peaked softmax (scale 0.5) spreads dS over many binades within each tile. The s = 0
+    run is checked against the FP64 oracle within the stated fp16 tolerance."""
+    from tests.test_gpu_sweep import _check_dtype_stated
+
+    lengths, groups, ratio, dim, block, topk, scale = [300, 45], 2, 4, 64, 16, 5, 0.5
+    cpu, indices, cu = attention_inputs(lengths, groups, ratio, dim, block, topk)
+    cpu = tuple(x.to(torch.float16) for x in cpu)
+    g = torch.Generator().manual_seed(77)
+    mag = 2.0 ** (torch.rand(cpu[0].shape, generator=g) * 4 - 2)  # [2^-2, 2^2)
+    sign = torch.where(torch.rand(cpu[0].shape, generator=g) < 0.5, -1.0, 1.0)
+    dout = (sign * mag).to(torch.float16)
+    out_ref, _, dq_ref, dk_ref, dv_ref = _oracle(cpu, indices, cu, block, scale, dout)
+    results = {}
+    for shift in (0, -10, 5):
+        tensors, indices_d, cu_d = _to(device, cpu, indices, cu)
+        out = msa.m3_sparse_attention(*tensors, indices_d, cu_d, max(lengths), block_size=block, scale=scale)
+        out.backward((dout.double() * 2.0 ** shift).to(torch.float16).to(device))
+        results[shift] = [t.grad.detach().cpu().double() for t in tensors]
+        if shift == 0:
+            _check_dtype_stated(out, out_ref, torch.float16, "out")
+            for grad, ref, name in zip(results[0], (dq_ref, dk_ref, dv_ref), ("dq", "dk", "dv")):
+                _check_dtype_stated(grad, ref, torch.float16, name)
+    for shift in (-10, 5):
+        for base, got, name in zip(results[0], results[shift], ("dq", "dk", "dv")):
+            want = base * 2.0 ** shift
+            normal = (want.abs() >= 2.0 ** -14) & (base.abs() >= 2.0 ** -14)
+            assert torch.equal(got[normal], want[normal]), f"{name} at 2^{shift}: not an exact power-of-two image"
+            # below the normal range one of the two roundings lands on the subnormal grid (step 2^-24)
+            limit = 2.0 ** -24 * max(1.0, 2.0 ** shift)
+            assert float((got - want).abs().max()) <= limit, f"{name} at 2^{shift}: subnormal outputs"
+            print(f"{name} at 2^{shift}: {int(normal.sum())} of {base.numel()} compared bit for bit", flush=True)
+            assert int(normal.sum()) > 0.5 * base.numel()
+
+
 @pytest.mark.parametrize("topk", [0, 3])
 def test_empty_selection_has_zero_output_and_gradients(topk, device):
     cpu, indices, cu = attention_inputs([3, 2], 2, 2, 7, 2, topk)
