@@ -129,7 +129,9 @@ int msa_score_bwd(const void* index_q, const void* index_k, int32_t dtype,
                   double scale, void* grad_q, void* grad_k, void* workspace, void* stream);
 
 /* Stage 3 forward workspace in bytes; 0 means this configuration runs the VALU
- * kernels, which need neither the CSR nor a workspace. */
+ * kernels, which need neither the CSR nor a workspace. Non-zero (the KV-major MFMA
+ * kernels) for bf16 and fp16 inputs with head ratio <= 512, head dim 8..128 a
+ * multiple of 8 and blocks of at most 128 keys. */
 int64_t msa_attn_fwd_workspace_bytes(int32_t dtype, int64_t total_tokens, int64_t q_heads,
                                      int64_t kv_groups, int64_t head_dim, int64_t topk_slots,
                                      int64_t total_blocks, int64_t block_size);
