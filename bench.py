@@ -301,6 +301,7 @@ class Harness:
         self.cfg = cfg
         iq, ik, q, k, v, dout = tensors
         self.q, self.k, self.v, self.dout = q, k, v, dout
+        self.dtype_code = _lib.DTYPE_CODE[q.dtype]
         self.ids, self.cu = ids, cu
         bounds = [0]
         for n in cfg["lengths"]:
@@ -318,19 +319,19 @@ class Harness:
         self.dk = torch.empty_like(k)
         self.dv = torch.empty_like(v)
         self.csr = build_k2q_csr(ids, cu, block_size=cfg["block"])
-        self.fws_bytes = self.lib.msa_attn_fwd_workspace_bytes(2, self.T, cfg["hq"], cfg["g"], cfg["d"], cfg["topk"],
-                                                               self.meta.total_blocks, cfg["block"])
+        self.fws_bytes = self.lib.msa_attn_fwd_workspace_bytes(self.dtype_code, self.T, cfg["hq"], cfg["g"], cfg["d"],
+                                                               cfg["topk"], self.meta.total_blocks, cfg["block"])
         self.fws = torch.empty(max(1, self.fws_bytes), dtype=torch.uint8, device=device)
-        self.ws_bytes = self.lib.msa_attn_bwd_workspace_bytes(2, self.T, cfg["hq"], cfg["g"], cfg["d"], cfg["topk"],
-                                                              self.meta.total_blocks, cfg["block"])
+        self.ws_bytes = self.lib.msa_attn_bwd_workspace_bytes(self.dtype_code, self.T, cfg["hq"], cfg["g"], cfg["d"],
+                                                              cfg["topk"], self.meta.total_blocks, cfg["block"])
         self.ws = torch.empty(max(1, self.ws_bytes), dtype=torch.uint8, device=device)
         self.stream = torch.cuda.current_stream(device).cuda_stream
 
     def fwd(self):
         c = self.cfg
         csr = self.csr
-        st = self.lib.msa_attn_fwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), 2, self.ids.data_ptr(),
-                                   self.cu.data_ptr(), self.meta.num_seqs, self.T, c["hq"], c["g"], c["d"], c["topk"],
+        st = self.lib.msa_attn_fwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.dtype_code,
+                                   self.ids.data_ptr(), self.cu.data_ptr(), self.meta.num_seqs, self.T, c["hq"], c["g"], c["d"], c["topk"],
                                    c["block"], self.scale, csr.cu_block_lens.data_ptr(), self.meta.total_blocks,
                                    csr.row_ptr.data_ptr(), csr.query_indices.data_ptr(), csr.slot_indices.data_ptr(),
                                    self.fws.data_ptr(), self.fws_bytes, self.out.data_ptr(), self.lse.data_ptr(),
@@ -340,8 +341,8 @@ class Harness:
     def bwd(self):
         c = self.cfg
         csr = self.csr
-        st = self.lib.msa_attn_bwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), 2, self.out.data_ptr(),
-                                   self.dout.data_ptr(), self.rs.data_ptr(),
+        st = self.lib.msa_attn_bwd(self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.dtype_code,
+                                   self.out.data_ptr(), self.dout.data_ptr(), self.rs.data_ptr(),
                                    self.o32.data_ptr() if self.use_f32 else None, self.ids.data_ptr(), self.cu.data_ptr(),
                                    self.meta.num_seqs, self.T, c["hq"], c["g"], c["d"], c["topk"], c["block"],
                                    self.scale, csr.cu_block_lens.data_ptr(), self.meta.total_blocks,
