@@ -88,6 +88,29 @@ struct MainSmem {
   int32_t eslot[kMainEdges];
 };
 
+// 256 dims: the K block is read only while the item's register fragments are built, so
+// it shares its LDS with the row tiles (exactly their size: 128 rows = 2 x 2 x 32 rows),
+// 122 KiB in all instead of 190 (a barrier separates the last fragment read from the
+// first tile's rows).
+template <>
+struct MainSmem<8> {
+  static constexpr int DP = 256;
+  static constexpr int KS = lds_row_stride<DP>();
+  union {
+    alignas(16) uint16_t k[128 * KS];
+    struct {
+      alignas(16) uint16_t qs[2][32 * KS];
+      alignas(16) uint16_t gs[2][32 * KS];
+    };
+  };
+  alignas(16) uint16_t ds[2][3][128 * 32];
+  alignas(16) float4 st[2][32];
+  alignas(16) int32_t vis[2][32];
+  alignas(16) int32_t rec[2][32];
+  int32_t etok[kMainEdges];
+  int32_t eslot[kMainEdges];
+};
+
 }  // namespace
 
 // O . dO per (token, head) in FP64 (exact products); 32 lanes per row, NR rows per
@@ -163,7 +186,7 @@ __global__ __launch_bounds__(256) void kv_bwd_center(const uint16_t* __restrict_
 // Structure of the forward partial kernel: K and V blocks row-major in LDS,
 // kStatWaves waves x 16 kStatRT rows per tile; S^T = K Q^T and dP^T = V dO^T (lane: row c, keys 4*q4 + i).
 template <int DT, int NK, bool FULLD>
-__global__ __launch_bounds__(kStatThreads, 2) void kv_bwd_stats_kernel(
+__global__ __launch_bounds__(kStatThreads, NK == 8 ? 1 : 2) void kv_bwd_stats_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx, const int32_t* __restrict__ sidx,
@@ -417,8 +440,11 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items, const int2* __restrict__ items,
     const int32_t* __restrict__ order, int nseq, int Hq, int G, int D, int K, int B, float scale2, int epi, int t0,
     uint32_t rmagic, int rshift, const float4* __restrict__ rowf, float* __restrict__ dqpart,
-    float* __restrict__ kvpart) {
-  constexpr int DP = 32 * NK, NDT = DP / 16, KS = MainSmem<NK>::KS;
+    float* __restrict__ kvpart, int dhalf) {
+  // DP dims enter S and dP; the dK, dV and dQ outputs of one launch cover DPO dims from
+  // dhalf (256 dims: two launches, dhalf = 0 and 128, each recomputing S and dP)
+  constexpr int DP = 32 * NK, DPO = NK == 8 ? 128 : DP, NDT = DPO / 16, KS = MainSmem<NK>::KS;
+  if constexpr (NK != 8) dhalf = 0;  // (compile-time zero below 256 dims)
   constexpr int RV = DP / 8;             // 16-byte chunks per row
   constexpr int CPT = RV >= 8 ? RV / 8 : 1;  // chunks per staging thread (threads 0-255: Q, 256-511: dO)
   constexpr int TPR = RV / CPT;          // staging threads per row
@@ -461,25 +487,33 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       }
     }
   }
-  bf16x8 vf[NK];
-  {
-    const int kl = 16 * wid + c;
-    const int klc = kl < rg.nk ? kl : rg.nk - 1;
+  // B operands of dP and S: V / K[key 16 w + c][dims 32 kk + 8 q4 + j]. At 256 dims both
+  // come from memory (the item's K / V rows stay in L2), and again after each tile's dV / dK
+  // products, so that they are not live through the tile's splits (64 VGPRs).
+  bf16x8 vf[NK], kf[NK];
+  const int kl_own = 16 * wid + c;
+  const int64_t own_off = ((rg.kb + (kl_own < rg.nk ? kl_own : rg.nk - 1)) * G + rg.g) * D;
+  auto load_own = [&](const uint16_t* base, bf16x8* f) __attribute__((always_inline)) {
+    const uint16_t* p = base + own_off;
+    if constexpr (NK == 8) asm volatile("" : "+v"(p));  // a fresh load each time (kept inside the tile loop)
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
       const int d0 = 32 * kk + 8 * q4;
       const int d0c = (FULLD || d0 < D) ? d0 : D - 8;
-      const bf16x8 x = load_frag(v + ((rg.kb + klc) * G + rg.g) * D + d0c);
-      vf[kk] = kl < rg.nk && (FULLD || d0 < D) ? x : zero_frag();
+      const bf16x8 x = load_frag(p + d0c);
+      f[kk] = kl_own < rg.nk && (FULLD || d0 < D) ? x : zero_frag();
     }
-  }
+  };
+  load_own(v, vf);
+  if constexpr (NK == 8) load_own(k, kf);
   __syncthreads();  // K block and edges visible
 
-  bf16x8 kf[NK];  // B operand of S: K[key 16 w + c][dims 32 kk + 8 q4 + j]
+  if constexpr (NK != 8) {
 #pragma unroll
-  for (int kk = 0; kk < NK; ++kk) kf[kk] = load_frag(sm.k + (16 * wid + c) * KS + 32 * kk + 8 * q4);
+    for (int kk = 0; kk < NK; ++kk) kf[kk] = load_frag(sm.k + (16 * wid + c) * KS + 32 * kk + 8 * q4);
+  }
   const int rh = wid >> 2, dq = wid & 3;
-  const bool dq_active = 32 * dq < DP;
+  const bool dq_active = 32 * dq < DPO;
   // A operand of dQ^T (a bf16 product, dS entering as bf16 planes for either input type):
   // K^T[dim 32 dq + 16 dt2 + c][keys 32 kc + 8 q4 + j]; fp16 K as two exact bf16 terms
   // (kt the high terms, ktl the low ones).
@@ -488,8 +522,9 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
   for (int dt2 = 0; dt2 < 2; ++dt2)
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
-      const bf16x8 x = dq_active ? frag_tr(sm.k, KS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, 32 * dq + 16 * dt2, c)
-                                 : zero_frag();
+      const bf16x8 x =
+          dq_active ? frag_tr(sm.k, KS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, dhalf + 32 * dq + 16 * dt2, c)
+                    : zero_frag();
       if constexpr (DT == kF16) {
         const uint4 w = __builtin_bit_cast(uint4, x);
         uint4 h, l;
@@ -571,6 +606,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
   int ks = 15;
 
   MSA_MAIN_ISSUE(0)
+  if constexpr (NK == 8) __syncthreads();  // the K block's LDS becomes the row tiles
   MSA_MAIN_COMMIT(0, 0)
   if (ntiles > 1) MSA_MAIN_ISSUE(32)
   __syncthreads();
@@ -589,6 +625,9 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
         const bf16x8 ga = load_frag(sm.gs[b] + (16 * rt + c) * KS + 32 * kk + 8 * q4);
         a = mfma_t<DT>(qa, kf[kk], a);
         g = mfma_t<DT>(ga, vf[kk], g);
+        if constexpr (NK == 8) {
+          if (kk % 2 == 1) __builtin_amdgcn_sched_barrier(0);  // bounds the fragment reads in flight
+        }
       }
       s[rt] = a;
       dp[rt] = g;
@@ -699,8 +738,8 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     // ---- dV += P^T dO, dK += dS^T Q: B = X[rows pi(q4, j)][dim 16 dt + c], read transposed
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      const bf16x8 gb = frag_tr(sm.gs[b], KS, 4 * q4, 16 + 4 * q4, 16 * dt, c);
-      const bf16x8 qb = frag_tr(sm.qs[b], KS, 4 * q4, 16 + 4 * q4, 16 * dt, c);
+      const bf16x8 gb = frag_tr(sm.gs[b], KS, 4 * q4, 16 + 4 * q4, dhalf + 16 * dt, c);
+      const bf16x8 qb = frag_tr(sm.qs[b], KS, 4 * q4, 16 + 4 * q4, dhalf + 16 * dt, c);
       f32x4 x = dv[dt];
       x = mfma_t<DT>(ap[2], gb, x);
       x = mfma_t<DT>(ap[1], gb, x);
@@ -709,6 +748,12 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       y = mfma_t<DT>(ad[2], qb, y);
       y = mfma_t<DT>(ad[1], qb, y);
       dk[dt] = mfma_t<DT>(ad[0], qb, y);
+    }
+    if constexpr (NK == 8) {
+      if (t + 1 < ntiles) {
+        load_own(k, kf);
+        load_own(v, vf);
+      }
     }
     // ---- stage the next tile, start loading the one after
     if (t + 1 < ntiles) {
@@ -746,7 +791,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       if (myrec >= 0) {
 #pragma unroll
         for (int dt2 = 0; dt2 < 2; ++dt2) {
-          const int d0 = 32 * dq + 16 * dt2 + 4 * q4;
+          const int d0 = dhalf + 32 * dq + 16 * dt2 + 4 * q4;
           if (FULLD || d0 < D)
             __builtin_nontemporal_store(acc[dt2], reinterpret_cast<f32x4*>(dqpart + static_cast<uint32_t>(myrec * D + d0)));
         }
@@ -758,7 +803,8 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
 
   // ---- this item's dK / dV contribution, in accumulator-fragment order:
   // kvpart[item][0 = dK, 1 = dV][wave][dt][lane][i] holds key 16 wave + 4 q4 + i, dim 16 dt + c.
-  f32x4* base = reinterpret_cast<f32x4*>(kvpart + static_cast<int64_t>(item) * 2 * 128 * DP) + wid * NDT * 64 + lane;
+  f32x4* base = reinterpret_cast<f32x4*>(kvpart + static_cast<int64_t>(item) * 2 * 128 * DP) + wid * (DP / 16) * 64 +
+                (dhalf / 16) * 64 + lane;
   if constexpr (DT == kF16) {  // divide out the scales (powers of two: exact)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -834,7 +880,7 @@ __global__ __launch_bounds__(256) void kv_bwd_accumulate(const int32_t* __restri
 // (token, head) rows per dQ-combine workgroup, one 32-lane segment each (measured at c4:
 // 16 rows 1.47 ms, 8 rows 1.49, 4 rows 1.49, 32 rows 1.49).
 constexpr int kDqCombineRows = 16;
-template <int DT>
+template <int DT, int DC>
 __global__ __launch_bounds__(32 * kDqCombineRows) void kv_bwd_dq_combine(const int32_t* __restrict__ indices,
                                                          const int32_t* __restrict__ cu, int nseq, int64_t t0,
                                                          int64_t t1, int Hq, int G, int D, int K, int B, double scale,
@@ -851,7 +897,10 @@ __global__ __launch_bounds__(32 * kDqCombineRows) void kv_bwd_dq_combine(const i
   const int64_t qb = (t - cu[s]) / B;
   const int32_t* sel = indices + (t * G + g) * K;
   const int64_t rec0 = ((t - t0) * Hq + h) * static_cast<int64_t>(K);
-  if (4 * sub >= D) return;
+#pragma unroll
+  for (int hc = 0; hc < DC; ++hc) {  // 128-dim halves of the row (4 dims per lane in each)
+  const int dc = 128 * hc + 4 * sub;
+  if (dc >= D) return;
   double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
   for (int s0 = 0; s0 < K; s0 += kBatch) {
     float4 x[kBatch];
@@ -861,7 +910,7 @@ __global__ __launch_bounds__(32 * kDqCombineRows) void kv_bwd_dq_combine(const i
       const int slot = s0 + u < K ? s0 + u : K - 1;
       const int id = sel[slot];
       ok[u] = s0 + u < K && id >= 0 && id <= qb;
-      const f32x4 y = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dqpart + (rec0 + slot) * D + 4 * sub));
+      const f32x4 y = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(dqpart + (rec0 + slot) * D + dc));
       x[u] = make_float4(y[0], y[1], y[2], y[3]);
     }
 #pragma unroll
@@ -874,10 +923,11 @@ __global__ __launch_bounds__(32 * kDqCombineRows) void kv_bwd_dq_combine(const i
       }
     }
   }
-  *reinterpret_cast<uint2*>(dq + th * D + 4 * sub) = pack4_from_f64<DT>(a0 * scale, a1 * scale, a2 * scale, a3 * scale);
+  *reinterpret_cast<uint2*>(dq + th * D + dc) = pack4_from_f64<DT>(a0 * scale, a1 * scale, a2 * scale, a3 * scale);
+  }
 }
 
-static int nk_of_dim(int D) { return D <= 32 ? 1 : (D <= 64 ? 2 : 4); }
+static int nk_of_dim(int D) { return D <= 32 ? 1 : (D <= 64 ? 2 : (D <= 128 ? 4 : 8)); }
 
 struct BwdLayout {
   KvPlan stat_plan, main_plan;
@@ -977,7 +1027,8 @@ int attn_bwd_kv(int dt, const void* q, const void* k, const void* v, const void*
 #define MSA_BWD_STATS_NK(DTV)                                                                  \
   if (nk == 1) { if (fd) MSA_BWD_STATS(DTV, 1, true); else MSA_BWD_STATS(DTV, 1, false); }       \
   else if (nk == 2) { if (fd) MSA_BWD_STATS(DTV, 2, true); else MSA_BWD_STATS(DTV, 2, false); }  \
-  else { if (fd) MSA_BWD_STATS(DTV, 4, true); else MSA_BWD_STATS(DTV, 4, false); }
+  else if (nk == 4) { if (fd) MSA_BWD_STATS(DTV, 4, true); else MSA_BWD_STATS(DTV, 4, false); }  \
+  else { if (fd) MSA_BWD_STATS(DTV, 8, true); else MSA_BWD_STATS(DTV, 8, false); }
       if (f16) { MSA_BWD_STATS_NK(kF16) } else { MSA_BWD_STATS_NK(kBF16) }
 #undef MSA_BWD_STATS_NK
 #undef MSA_BWD_STATS
@@ -997,11 +1048,14 @@ int attn_bwd_kv(int dt, const void* q, const void* k, const void* v, const void*
       const dim3 grid(static_cast<unsigned>(mp.max_items)), block(kMainThreads);
       {
         ProfScope ps(kProfBwdMain, st);
-#define MSA_BWD_MAIN(DTV, NKV, FD) hipLaunchKernelGGL((kv_bwd_main_kernel<DTV, NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, rshift, rowf, dqpart, kvpart)
-#define MSA_BWD_MAIN_NK(DTV)                                                                 \
-  if (nk == 1) { if (fd) MSA_BWD_MAIN(DTV, 1, true); else MSA_BWD_MAIN(DTV, 1, false); }       \
-  else if (nk == 2) { if (fd) MSA_BWD_MAIN(DTV, 2, true); else MSA_BWD_MAIN(DTV, 2, false); }  \
-  else { if (fd) MSA_BWD_MAIN(DTV, 4, true); else MSA_BWD_MAIN(DTV, 4, false); }
+#define MSA_BWD_MAIN(DTV, NKV, FD, DH) hipLaunchKernelGGL((kv_bwd_main_kernel<DTV, NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, rshift, rowf, dqpart, kvpart, DH)
+#define MSA_BWD_MAIN_NK(DTV)                                                                       \
+  if (nk == 1) { if (fd) MSA_BWD_MAIN(DTV, 1, true, 0); else MSA_BWD_MAIN(DTV, 1, false, 0); }       \
+  else if (nk == 2) { if (fd) MSA_BWD_MAIN(DTV, 2, true, 0); else MSA_BWD_MAIN(DTV, 2, false, 0); }  \
+  else if (nk == 4) { if (fd) MSA_BWD_MAIN(DTV, 4, true, 0); else MSA_BWD_MAIN(DTV, 4, false, 0); }  \
+  else for (int dh = 0; dh < 256; dh += 128) {                                                     \
+    if (fd) MSA_BWD_MAIN(DTV, 8, true, dh); else MSA_BWD_MAIN(DTV, 8, false, dh);                  \
+  }
         if (f16) { MSA_BWD_MAIN_NK(kF16) } else { MSA_BWD_MAIN_NK(kBF16) }
 #undef MSA_BWD_MAIN_NK
 #undef MSA_BWD_MAIN
@@ -1014,8 +1068,9 @@ int attn_bwd_kv(int dt, const void* q, const void* k, const void* v, const void*
         auto* dkb = static_cast<uint16_t*>(dk);
         auto* dvb = static_cast<uint16_t*>(dv);
 #define MSA_BWD_ACC(DTV, DPV) hipLaunchKernelGGL((kv_bwd_accumulate<DTV, DPV>), agrid, dim3(256), 0, st, cu, cu_blocks, starts, nseq, G, D, B, T, kvpart, acc, first, last, scale, dkb, dvb)
-#define MSA_BWD_ACC_NK(DTV) \
-  if (nk == 1) MSA_BWD_ACC(DTV, 32); else if (nk == 2) MSA_BWD_ACC(DTV, 64); else MSA_BWD_ACC(DTV, 128);
+#define MSA_BWD_ACC_NK(DTV)                                                                           \
+  if (nk == 1) MSA_BWD_ACC(DTV, 32); else if (nk == 2) MSA_BWD_ACC(DTV, 64); else if (nk == 4) MSA_BWD_ACC(DTV, 128); \
+  else MSA_BWD_ACC(DTV, 256);
         if (f16) { MSA_BWD_ACC_NK(kF16) } else { MSA_BWD_ACC_NK(kBF16) }
 #undef MSA_BWD_ACC_NK
 #undef MSA_BWD_ACC
@@ -1024,12 +1079,12 @@ int attn_bwd_kv(int dt, const void* q, const void* k, const void* v, const void*
     if (dq) {
       ProfScope ps(kProfBwdDqCombine, st);
       const dim3 qgrid(grid_1d((t1 - t0) * Hq, kDqCombineRows)), qblock(32 * kDqCombineRows);
-      if (f16)
-        hipLaunchKernelGGL(kv_bwd_dq_combine<kF16>, qgrid, qblock, 0, st, indices, cu, nseq, t0, t1, Hq, G, D, K, B,
-                           static_cast<double>(scale), dqpart, static_cast<uint16_t*>(dq));
-      else
-        hipLaunchKernelGGL(kv_bwd_dq_combine<kBF16>, qgrid, qblock, 0, st, indices, cu, nseq, t0, t1, Hq, G, D, K, B,
-                           static_cast<double>(scale), dqpart, static_cast<uint16_t*>(dq));
+#define MSA_DQ_COMBINE(DTV, DCV)                                                                              \
+  hipLaunchKernelGGL((kv_bwd_dq_combine<DTV, DCV>), qgrid, qblock, 0, st, indices, cu, nseq, t0, t1, Hq, G, D, K, B, \
+                     static_cast<double>(scale), dqpart, static_cast<uint16_t*>(dq))
+      if (f16) { if (D > 128) MSA_DQ_COMBINE(kF16, 2); else MSA_DQ_COMBINE(kF16, 1); }
+      else { if (D > 128) MSA_DQ_COMBINE(kBF16, 2); else MSA_DQ_COMBINE(kBF16, 1); }
+#undef MSA_DQ_COMBINE
     }
   }
   return status_from(hipGetLastError());

@@ -39,9 +39,20 @@ namespace msa {
 
 namespace {
 
-constexpr int kRowsPerTile = 128;  // (edge, head) rows per tile: 4 waves x 32
+constexpr int kRowsPerTile = 128;  // (edge, head) rows per tile
 constexpr int kTilesPerItem = 4;   // tiles per work item
 constexpr int kItemRows = kRowsPerTile * kTilesPerItem;
+
+// Workgroup shape of the partial pass: 4 waves x 32 rows (two 16-row operands per wave)
+// up to 128 dims; 8 waves x 16 rows at 256 dims, whose query fragments, logits and
+// output accumulators of 16 rows fill what 32 rows take at 128 dims (the K and V blocks,
+// 136 KiB of LDS there, leave one workgroup per CU: two waves per SIMD).
+template <int NK>
+struct FwdShape {
+  static constexpr int kWaves = NK == 8 ? 8 : 4;
+  static constexpr int kThreads = 64 * kWaves;
+  static constexpr int kRT = kRowsPerTile / (16 * kWaves);  // 16-row operands per wave
+};
 
 template <int NK>
 struct FwdSmem {
@@ -207,13 +218,14 @@ __global__ __launch_bounds__(1024) void kv_item_order(const int32_t* __restrict_
 }
 
 template <int DT, int NK, bool FULLD>
-__global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
+__global__ __launch_bounds__(FwdShape<NK>::kThreads, NK == 8 ? 1 : 2) void attn_fwd_partial_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks, const int32_t* __restrict__ qidx,
     const int32_t* __restrict__ sidx, const int32_t* __restrict__ e_hi, const int32_t* __restrict__ n_items,
     const int2* __restrict__ items, const int32_t* __restrict__ order, int nseq, int Hq, int G, int D, int K, int B, float scale2, int epi, int t0,
     float* __restrict__ opart, float2* __restrict__ mlpart) {
   constexpr int DP = 32 * NK, NDT = DP / 16, KS = FwdSmem<NK>::KS;
+  constexpr int NT = FwdShape<NK>::kThreads, RT = FwdShape<NK>::kRT;
   __shared__ FwdSmem<NK> sm;
   if (static_cast<int>(blockIdx.x) >= *n_items) return;
   const int item = order[blockIdx.x];  // largest items first
@@ -227,11 +239,11 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
 
   // ---- stage the K and V blocks (row-major) and the item's row metadata in LDS.
   // All global loads are issued before any LDS store.
-  constexpr int KVI = 128 * (DP / 8) / 256;  // 16-byte K (and V) loads per thread
+  constexpr int KVI = 128 * (DP / 8) / NT;  // 16-byte K (and V) loads per thread
   uint4 kw[KVI], vw[KVI];
 #pragma unroll
   for (int it = 0; it < KVI; ++it) {
-    const int e = tid + 256 * it;
+    const int e = tid + NT * it;
     const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));  // lanes along dims
     // unconditional loads from clamped (in-bounds) addresses; out-of-range lanes are zeroed at the store
     const int klc = kl < rg.nk ? kl : rg.nk - 1, d0c = (FULLD || d0 < D) ? d0 : D - 8;
@@ -239,18 +251,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     kw[it] = *reinterpret_cast<const uint4*>(k + off);
     vw[it] = *reinterpret_cast<const uint4*>(v + off);
   }
-  constexpr int MI = kItemRows / 256;
+  constexpr int MI = kItemRows / NT;
   int32_t mtok[MI], mslot[MI];
 #pragma unroll
   for (int j = 0; j < MI; ++j) {
-    const int rho = tid + 256 * j;
+    const int rho = tid + NT * j;
     const int eo = (rho < nrows ? rho : nrows - 1) / R;  // nrows >= 1
     mtok[j] = qidx[e_begin + eo];
     mslot[j] = sidx[e_begin + eo];
   }
 #pragma unroll
   for (int it = 0; it < KVI; ++it) {
-    const int e = tid + 256 * it;
+    const int e = tid + NT * it;
     const int kl = e / (DP / 8), d0 = 8 * (e % (DP / 8));
     const bool ok = kl < rg.nk && (FULLD || d0 < D);
     *reinterpret_cast<uint4*>(sm.k + kl * KS + d0) = ok ? kw[it] : make_uint4(0u, 0u, 0u, 0u);
@@ -258,7 +270,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
   }
 #pragma unroll
   for (int j = 0; j < MI; ++j) {
-    const int rho = tid + 256 * j;
+    const int rho = tid + NT * j;
     if (rho < nrows) {
       const int eo = rho / R;
       const int h = rg.g * R + (rho - eo * R);
@@ -269,13 +281,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
   }
   __syncthreads();
 
-  // Waves are independent from here on. Wave wid owns rows r0 + 32*wid + 16*rt + c of each tile.
+  // Waves are independent from here on. Wave wid owns rows r0 + 16*RT*wid + 16*rt + c of each tile.
   const int ntiles = (nrows + kRowsPerTile - 1) / kRowsPerTile;
-  bf16x8 qf[2][NK];
+  bf16x8 qf[RT][NK];
   auto load_q = [&](int r0) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int rho = r0 + 32 * wid + 16 * rt + c;
+    for (int rt = 0; rt < RT; ++rt) {
+      const int rho = r0 + 16 * RT * wid + 16 * rt + c;
       const bool ok = rho < nrows;
       const int64_t th = ok ? static_cast<int64_t>(t0) * Hq + sm.th[rho] : 0;
 #pragma unroll
@@ -288,17 +300,17 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
   load_q(0);
   for (int tile = 0; tile < ntiles; ++tile) {
     const int r0 = tile * kRowsPerTile;
-    const int rbase = r0 + 32 * wid;
+    const int rbase = r0 + 16 * RT * wid;
     if (rbase >= nrows) break;  // wave-uniform: no rows of this wave are left
-    int lim[2];  // visible keys of the lane's rows
+    int lim[RT];  // visible keys of the lane's rows
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const int rho = rbase + 16 * rt + c;
       const int64_t vis = rho < nrows ? static_cast<int64_t>(sm.tok[rho]) - rg.kb + 1 : 0;
       lim[rt] = vis < rg.nk ? static_cast<int>(vis) : rg.nk;
     }
     // ---- logits S^T = K Q^T: lane holds S[row 16*rt + c][key 16*kt + 4*q4 + i]
-    f32x4 s[2][8];
+    f32x4 s[RT][8];
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
       bf16x8 kf[NK];
@@ -306,7 +318,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
       for (int kk = 0; kk < NK; ++kk)
         kf[kk] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(sm.k + (16 * kt + c) * KS + 32 * kk + 8 * q4));
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
+      for (int rt = 0; rt < RT; ++rt) {
         f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < NK; ++kk) a = mfma_t<DT>(kf[kk], qf[rt][kk], a);
@@ -319,13 +331,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
     // x = fl(acc * scale2), m = max x, p = 2^(x - m) (exactly 1 at the maximum).
     // Wave-uniform: every row of the wave sees all 128 keys (no masks), or not. The two
     // cases are separate code paths so the unmasked one carries no per-logit selects.
-    const bool full = __ballot(lim[0] < 128 || lim[1] < 128) == 0;
-    float mrow[2], lrow[2];
-    f32x4 o[2][NDT];
+    bool part = false;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) part = part || lim[rt] < 128;
+    const bool full = __ballot(part) == 0;
+    float mrow[RT], lrow[RT];
+    f32x4 o[RT][NDT];
     auto softmax_pv = [&](auto full_tag) __attribute__((always_inline)) {
       constexpr bool FULL = decltype(full_tag)::value;
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
+      for (int rt = 0; rt < RT; ++rt) {
         float m = -__builtin_inff();
 #pragma unroll
         for (int kt = 0; kt < 8; ++kt)
@@ -355,9 +370,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
       // ---- O^T = V^T P^T over 4 chunks of 32 keys: A = V^T[dim c][keys pi], B = P^T[keys pi][row c]
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
-        bf16x8 ph[2], pm[2], pl[2];
+        bf16x8 ph[RT], pm[RT], pl[RT];
 #pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
+        for (int rt = 0; rt < RT; ++rt) {
           uint32_t wh[4], wm[4], wl[4];
 #pragma unroll
           for (int jj = 0; jj < 4; ++jj) {
@@ -378,7 +393,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
           // V^T[dim 16*dt + c][keys pi(q4, j)] read transposed from the row-major V block
           const bf16x8 vb = frag_tr(sm.v, KS, 32 * kc + 4 * q4, 32 * kc + 16 + 4 * q4, 16 * dt, c);
 #pragma unroll
-          for (int rt = 0; rt < 2; ++rt) {
+          for (int rt = 0; rt < RT; ++rt) {
             f32x4 acc = kc == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : o[rt][dt];
             acc = mfma_t<DT>(vb, pl[rt], acc);
             acc = mfma_t<DT>(vb, pm[rt], acc);
@@ -393,7 +408,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
       softmax_pv(std::false_type{});
     // ---- store partials: o lane holds O[row 16*rt + c][dims 16*dt + 4*q4 + 0..3]
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const int rho = rbase + 16 * rt + c;
       if (rho < nrows) {
         float* dst = opart + static_cast<int64_t>(sm.rec[rho]) * D + 4 * q4;
@@ -406,7 +421,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_partial_kernel(
   }
 }
 
-// 32 lanes per (token, head) of the chunk, 4 dims each (D <= 128): merge the
+// 32 lanes per (token, head) of the chunk, 4 dims in each of DC 128-dim halves (D <= 128 DC): merge the
 // valid slots' partials in slot order in FP64. Slots are taken 8 at a time with
 // all of their partial loads issued before any arithmetic (records are in bounds
 // for every slot, valid or not; invalid slots are masked, never multiplied).
@@ -418,7 +433,7 @@ constexpr int kCombineBatch = 8;
 // FP64 oracle as the statistics pass for every row, at logit scales 0.3x to 16x.
 constexpr double kFlatRowMass = 20.0;
 
-template <int DT>
+template <int DT, int DC>
 __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restrict__ indices,
                                                         const int32_t* __restrict__ cu, int nseq, int64_t t0,
                                                         int64_t t1, int Hq, int G, int D, int K, int B,
@@ -450,9 +465,15 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
   for (int o = 16; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o, 32));
 
   double L = 0.0;
-  double acc[4] = {0.0, 0.0, 0.0, 0.0};
-  const bool has_dims = 4 * sub < D;
-  const int dcol = has_dims ? 4 * sub : 0;  // lanes without dims read (and ignore) dims 0..3
+  double acc[DC][4];
+  bool has_dims[DC];
+  int dcol[DC];
+#pragma unroll
+  for (int hc = 0; hc < DC; ++hc) {
+    acc[hc][0] = acc[hc][1] = acc[hc][2] = acc[hc][3] = 0.0;
+    has_dims[hc] = 128 * hc + 4 * sub < D;
+    dcol[hc] = has_dims[hc] ? 128 * hc + 4 * sub : 0;  // lanes without dims read (and ignore) dims 0..3
+  }
   if (M != -__builtin_inff()) {
     for (int s0 = 0; s0 < K; s0 += 32) {
       const int slot = s0 + sub;
@@ -472,12 +493,15 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
       const uint64_t wbits = __double_as_longlong(w);
       const uint32_t wlo = static_cast<uint32_t>(wbits), whi = static_cast<uint32_t>(wbits >> 32);
       for (int j0 = 0; j0 < n; j0 += kCombineBatch) {
-        float4 op[kCombineBatch];
+        float4 op[kCombineBatch][DC];
 #pragma unroll
         for (int u = 0; u < kCombineBatch; ++u) {
           const int j = j0 + u < n ? j0 + u : n - 1;
-          const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(opart + (rec0 + static_cast<int64_t>(s0 + j) * Hq) * D + dcol));
-          op[u] = make_float4(x[0], x[1], x[2], x[3]);
+#pragma unroll
+          for (int hc = 0; hc < DC; ++hc) {
+            const f32x4 x = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(opart + (rec0 + static_cast<int64_t>(s0 + j) * Hq) * D + dcol[hc]));
+            op[u][hc] = make_float4(x[0], x[1], x[2], x[3]);
+          }
         }
 #pragma unroll
         for (int u = 0; u < kCombineBatch; ++u) {
@@ -487,10 +511,13 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
           const double wj = __longlong_as_double(static_cast<long long>(
               (static_cast<uint64_t>(upper ? bhi : ahi) << 32) | (upper ? blo : alo)));
           if (j0 + u < n && wj != 0.0) {  // invalid slot (or a weight that underflowed to zero)
-            acc[0] = fma(wj, static_cast<double>(op[u].x), acc[0]);
-            acc[1] = fma(wj, static_cast<double>(op[u].y), acc[1]);
-            acc[2] = fma(wj, static_cast<double>(op[u].z), acc[2]);
-            acc[3] = fma(wj, static_cast<double>(op[u].w), acc[3]);
+#pragma unroll
+            for (int hc = 0; hc < DC; ++hc) {
+              acc[hc][0] = fma(wj, static_cast<double>(op[u][hc].x), acc[hc][0]);
+              acc[hc][1] = fma(wj, static_cast<double>(op[u][hc].y), acc[hc][1]);
+              acc[hc][2] = fma(wj, static_cast<double>(op[u][hc].z), acc[hc][2]);
+              acc[hc][3] = fma(wj, static_cast<double>(op[u][hc].w), acc[hc][3]);
+            }
           }
         }
       }
@@ -499,15 +526,18 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
 #pragma unroll
   for (int o = 16; o > 0; o >>= 1) L += __shfl_xor(L, o, 32);
   const bool has = L > 0.0;
-  if (has_dims) {
-    double x[4];  // the partials carry the P scale of the input type (a power of two)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = has ? acc[i] / L * (1.0 / p_scale<DT>()) : 0.0;
-    *reinterpret_cast<uint2*>(out + th * D + 4 * sub) = pack4_from_f64<DT>(x[0], x[1], x[2], x[3]);
-    if (o32)
-      *reinterpret_cast<float4*>(o32 + th * D + 4 * sub) =
-          make_float4(static_cast<float>(x[0]), static_cast<float>(x[1]), static_cast<float>(x[2]),
-                      static_cast<float>(x[3]));
+  for (int hc = 0; hc < DC; ++hc) {
+    if (has_dims[hc]) {
+      double x[4];  // the partials carry the P scale of the input type (a power of two)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = has ? acc[hc][i] / L * (1.0 / p_scale<DT>()) : 0.0;
+      *reinterpret_cast<uint2*>(out + th * D + dcol[hc]) = pack4_from_f64<DT>(x[0], x[1], x[2], x[3]);
+      if (o32)
+        *reinterpret_cast<float4*>(o32 + th * D + dcol[hc]) =
+            make_float4(static_cast<float>(x[0]), static_cast<float>(x[1]), static_cast<float>(x[2]),
+                        static_cast<float>(x[3]));
+    }
   }
   if (sub == 0) {
     // row_state keeps the base-2 lse (the backward's p = 2^(x - lse2) is then exactly
@@ -532,11 +562,11 @@ __global__ __launch_bounds__(256) void attn_fwd_combine(const int32_t* __restric
 // ---------------------------------------------------------------------------- host side
 
 bool attn_mfma_supported(int64_t ratio, int64_t head_dim, int64_t block_size) {
-  return ratio >= 1 && ratio <= kItemRows && head_dim >= 8 && head_dim <= 128 && head_dim % 8 == 0 &&
+  return ratio >= 1 && ratio <= kItemRows && head_dim >= 8 && head_dim <= 256 && head_dim % 8 == 0 &&
          block_size >= 1 && block_size <= 128;
 }
 
-static int nk_of_dim(int D) { return D <= 32 ? 1 : (D <= 64 ? 2 : 4); }
+static int nk_of_dim(int D) { return D <= 32 ? 1 : (D <= 64 ? 2 : (D <= 128 ? 4 : 8)); }
 
 static int64_t fwd_epi(int64_t R) {
   const int64_t e = static_cast<int64_t>(kRowsPerTile) * kTilesPerItem / R;
@@ -642,17 +672,18 @@ int attn_fwd_kv(int dt, const void* q, const void* k, const void* v, const int32
     const int64_t t0 = c * pl.tc, t1 = t0 + pl.tc < T ? t0 + pl.tc : T;
     if (rows > 0) {
       ProfScope ps(kProfFwdPartial, st);
-      const dim3 grid(static_cast<unsigned>(pl.max_items)), block(256);
+      const dim3 grid(static_cast<unsigned>(pl.max_items));
       const int32_t* hi = kv_plan_hi(pl, base, c);
       const int32_t* nit = kv_plan_count(pl, base, c);
       const int2* its = kv_plan_items(pl, base, c);
       const int32_t* ord = kv_plan_order(pl, base, c);
       const int it0 = static_cast<int>(t0);
-#define MSA_FWD_PARTIAL(DTV, NKV, FD) hipLaunchKernelGGL((attn_fwd_partial_kernel<DTV, NKV, FD>), grid, block, 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, epi, it0, opart, ml)
+#define MSA_FWD_PARTIAL(DTV, NKV, FD) hipLaunchKernelGGL((attn_fwd_partial_kernel<DTV, NKV, FD>), grid, dim3(FwdShape<NKV>::kThreads), 0, st, qb, kb, vb, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, epi, it0, opart, ml)
 #define MSA_FWD_PARTIAL_NK(DTV)                                                                   \
   if (nk == 1) { if (fd) MSA_FWD_PARTIAL(DTV, 1, true); else MSA_FWD_PARTIAL(DTV, 1, false); }       \
   else if (nk == 2) { if (fd) MSA_FWD_PARTIAL(DTV, 2, true); else MSA_FWD_PARTIAL(DTV, 2, false); }  \
-  else { if (fd) MSA_FWD_PARTIAL(DTV, 4, true); else MSA_FWD_PARTIAL(DTV, 4, false); }
+  else if (nk == 4) { if (fd) MSA_FWD_PARTIAL(DTV, 4, true); else MSA_FWD_PARTIAL(DTV, 4, false); }  \
+  else { if (fd) MSA_FWD_PARTIAL(DTV, 8, true); else MSA_FWD_PARTIAL(DTV, 8, false); }
       const int nk = nk_of_dim(D);
       const bool fd = D == 32 * nk;
       if (dt == kF16) { MSA_FWD_PARTIAL_NK(kF16) } else { MSA_FWD_PARTIAL_NK(kBF16) }
@@ -661,12 +692,12 @@ int attn_fwd_kv(int dt, const void* q, const void* k, const void* v, const int32
     }
     ProfScope ps(kProfFwdCombine, st);
     const dim3 cgrid(grid_1d((t1 - t0) * Hq, 8));
-    if (dt == kF16)
-      hipLaunchKernelGGL(attn_fwd_combine<kF16>, cgrid, dim3(256), 0, st, indices, cu, nseq, t0, t1, Hq, G, D, K, B,
-                         opart, ml, ob, lse, rs, o32);
-    else
-      hipLaunchKernelGGL(attn_fwd_combine<kBF16>, cgrid, dim3(256), 0, st, indices, cu, nseq, t0, t1, Hq, G, D, K, B,
-                         opart, ml, ob, lse, rs, o32);
+#define MSA_FWD_COMBINE(DTV, DCV)                                                                               \
+  hipLaunchKernelGGL((attn_fwd_combine<DTV, DCV>), cgrid, dim3(256), 0, st, indices, cu, nseq, t0, t1, Hq, G, D, K, B, \
+                     opart, ml, ob, lse, rs, o32)
+    if (dt == kF16) { if (D > 128) MSA_FWD_COMBINE(kF16, 2); else MSA_FWD_COMBINE(kF16, 1); }
+    else { if (D > 128) MSA_FWD_COMBINE(kBF16, 2); else MSA_FWD_COMBINE(kBF16, 1); }
+#undef MSA_FWD_COMBINE
   }
   return status_from(hipGetLastError());
 }

@@ -145,6 +145,44 @@ def test_fp16_gradients_follow_power_of_two_output_gradients(device):
             assert int(normal.sum()) > 0.5 * base.numel()
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("lengths,groups,ratio,dimension,block_size,topk,scale", [
+    ([300, 45], 2, 4, 256, 16, 5, None),
+    ([127, 128, 257], 1, 3, 200, 128, 3, 0.1),
+    ([5, 1, 9], 2, 2, 136, 4, 4, None),
+])
+def test_head_dims_to_256_on_mfma_against_fp64(lengths, groups, ratio, dimension, block_size, topk, scale, dtype,
+                                               device):
+    """Head dims above 128 (up to 256) on the MFMA kernels: the forward with 8 waves of 16
+    rows, the backward's main pass as two launches over the two 128-dim halves of dK, dV and
+    dQ (each recomputing S and dP over every dim). Against the FP64 oracle within the
+    stated tolerance of the dtype (bf16: 1e-4 + 2^-8 |x|, fp16: 1e-4 + 2^-10 |x|; at most
+    0.1 %, at least one, outside the gate)."""
+    from msa_triton_amd import _lib
+    from tests.test_gpu_sweep import _check_dtype_stated
+
+    cpu, indices, cu = attention_inputs(lengths, groups, ratio, dimension, block_size, topk)
+    cpu = tuple(x.to(dtype) for x in cpu)
+    total, heads = sum(lengths), groups * ratio
+    blocks = sum((n + block_size - 1) // block_size for n in lengths)
+    lib = _lib.lib()
+    code = _lib.DTYPE_CODE[dtype]
+    assert lib.msa_attn_fwd_workspace_bytes(code, total, heads, groups, dimension, topk, blocks, block_size) > 0
+    assert lib.msa_attn_bwd_workspace_bytes(code, total, heads, groups, dimension, topk, blocks, block_size) > 0
+    tensors, indices_d, cu_d = _to(device, cpu, indices, cu)
+    grad = torch.randn(cpu[0].shape, generator=torch.Generator().manual_seed(256)).to(dtype)
+    out, lse, dq, dk, dv = _oracle(cpu, indices, cu, block_size, scale, grad)
+    actual, actual_lse = msa.m3_sparse_attention(*tensors, indices_d, cu_d, max(lengths), block_size=block_size,
+                                                 scale=scale, return_lse=True)
+    check = (lambda a, r, n: check_bf16_stated(a, r, n)) if dtype == torch.bfloat16 else (
+        lambda a, r, n: _check_dtype_stated(a, r, torch.float16, n))
+    check(actual, out, "out")
+    _assert_lse(actual_lse, lse)
+    actual.backward(grad.to(device))
+    for tensor, ref, name in zip(tensors, (dq, dk, dv), ("dq", "dk", "dv")):
+        check(tensor.grad, ref, name)
+
+
 @pytest.mark.parametrize("topk", [0, 3])
 def test_empty_selection_has_zero_output_and_gradients(topk, device):
     cpu, indices, cu = attention_inputs([3, 2], 2, 2, 7, 2, topk)
