@@ -432,7 +432,11 @@ __global__ __launch_bounds__(256) void kv_bwd_stats_combine(const int32_t* __res
 // Row tiles and dS planes are double-buffered, so one barrier per tile orders all
 // LDS traffic; the next tile's rows are committed before it and the one after is
 // loaded from memory during the current tile.
-template <int DT, int NK, bool FULLD>
+// PARTS selects the outputs: kPartAll (dK, dV and dQ) up to 128 dims; at 256 dims each
+// 128-dim half takes a kPartKV launch and a kPartQ launch (the two together exceed the
+// registers of a wave there), each recomputing S and dP over every dim.
+enum MainParts : int { kPartKV = 1, kPartQ = 2, kPartAll = 3 };
+template <int DT, int NK, bool FULLD, int PARTS>
 __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
     const uint16_t* __restrict__ dout, const double* __restrict__ row_state, const int32_t* __restrict__ cu,
@@ -442,7 +446,8 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     uint32_t rmagic, int rshift, const float4* __restrict__ rowf, float* __restrict__ dqpart,
     float* __restrict__ kvpart, int dhalf) {
   // DP dims enter S and dP; the dK, dV and dQ outputs of one launch cover DPO dims from
-  // dhalf (256 dims: two launches, dhalf = 0 and 128, each recomputing S and dP)
+  // dhalf (256 dims: launches for dhalf = 0 and 128)
+  constexpr bool DO_KV = (PARTS & kPartKV) != 0, DO_Q = (PARTS & kPartQ) != 0;
   constexpr int DP = 32 * NK, DPO = NK == 8 ? 128 : DP, NDT = DPO / 16, KS = MainSmem<NK>::KS;
   if constexpr (NK != 8) dhalf = 0;  // (compile-time zero below 256 dims)
   constexpr int RV = DP / 8;             // 16-byte chunks per row
@@ -487,15 +492,13 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       }
     }
   }
-  // B operands of dP and S: V / K[key 16 w + c][dims 32 kk + 8 q4 + j]. At 256 dims both
-  // come from memory (the item's K / V rows stay in L2), and again after each tile's dV / dK
-  // products, so that they are not live through the tile's splits (64 VGPRs).
+  // B operands of dP and S: V / K[key 16 w + c][dims 32 kk + 8 q4 + j], from memory (K at
+  // 256 dims too: its LDS block is shared with the row tiles)
   bf16x8 vf[NK], kf[NK];
   const int kl_own = 16 * wid + c;
   const int64_t own_off = ((rg.kb + (kl_own < rg.nk ? kl_own : rg.nk - 1)) * G + rg.g) * D;
   auto load_own = [&](const uint16_t* base, bf16x8* f) __attribute__((always_inline)) {
     const uint16_t* p = base + own_off;
-    if constexpr (NK == 8) asm volatile("" : "+v"(p));  // a fresh load each time (kept inside the tile loop)
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
       const int d0 = 32 * kk + 8 * q4;
@@ -519,7 +522,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
   // (kt the high terms, ktl the low ones).
   bf16x8 kt[2][4], ktl[2][4];
 #pragma unroll
-  for (int dt2 = 0; dt2 < 2; ++dt2)
+  for (int dt2 = 0; dt2 < (DO_Q ? 2 : 0); ++dt2)
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       const bf16x8 x =
@@ -625,9 +628,6 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
         const bf16x8 ga = load_frag(sm.gs[b] + (16 * rt + c) * KS + 32 * kk + 8 * q4);
         a = mfma_t<DT>(qa, kf[kk], a);
         g = mfma_t<DT>(ga, vf[kk], g);
-        if constexpr (NK == 8) {
-          if (kk % 2 == 1) __builtin_amdgcn_sched_barrier(0);  // bounds the fragment reads in flight
-        }
       }
       s[rt] = a;
       dp[rt] = g;
@@ -652,7 +652,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
           if constexpr (DT == kF16) {
             Pv[4 * rt + i] = P, Dv[4 * rt + i] = d;
           } else {
-            split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
+            if constexpr (DO_KV) split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
             split3_bits(d, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
           }
         }
@@ -667,7 +667,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
           if constexpr (DT == kF16) {
             Pv[4 * rt + i] = P, Dv[4 * rt + i] = d;
           } else {
-            split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
+            if constexpr (DO_KV) split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
             split3_bits(d, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
           }
         }
@@ -690,10 +690,13 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       for (int p3 = 0; p3 < 3; ++p3) {
         ad[p3] = __builtin_bit_cast(bf16x8, make_uint4(w[p3][0], w[p3][1], w[p3][2], w[p3][3]));
         // plane rows: key 16 w + c, columns (tile rows) 4 q4 .. +3 and 16 + 4 q4 .. +3
-        *reinterpret_cast<uint2*>(sm.ds[b][p3] + plane_offset(key, q4)) = make_uint2(w[p3][0], w[p3][1]);
-        *reinterpret_cast<uint2*>(sm.ds[b][p3] + plane_offset(key, 4 + q4)) = make_uint2(w[p3][2], w[p3][3]);
+        if constexpr (DO_Q) {
+          *reinterpret_cast<uint2*>(sm.ds[b][p3] + plane_offset(key, q4)) = make_uint2(w[p3][0], w[p3][1]);
+          *reinterpret_cast<uint2*>(sm.ds[b][p3] + plane_offset(key, 4 + q4)) = make_uint2(w[p3][2], w[p3][3]);
+        }
       }
-      if constexpr (DT == kF16) {
+      if constexpr (!DO_KV) {
+      } else if constexpr (DT == kF16) {
         // P: fp16 terms of 2^15 P
         uint32_t wp[3][4];
 #pragma unroll
@@ -737,7 +740,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     }
     // ---- dV += P^T dO, dK += dS^T Q: B = X[rows pi(q4, j)][dim 16 dt + c], read transposed
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
+    for (int dt = 0; dt < (DO_KV ? NDT : 0); ++dt) {
       const bf16x8 gb = frag_tr(sm.gs[b], KS, 4 * q4, 16 + 4 * q4, dhalf + 16 * dt, c);
       const bf16x8 qb = frag_tr(sm.qs[b], KS, 4 * q4, 16 + 4 * q4, dhalf + 16 * dt, c);
       f32x4 x = dv[dt];
@@ -749,12 +752,6 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       y = mfma_t<DT>(ad[1], qb, y);
       dk[dt] = mfma_t<DT>(ad[0], qb, y);
     }
-    if constexpr (NK == 8) {
-      if (t + 1 < ntiles) {
-        load_own(k, kf);
-        load_own(v, vf);
-      }
-    }
     // ---- stage the next tile, start loading the one after
     if (t + 1 < ntiles) {
       MSA_MAIN_COMMIT(32 * (t + 1), b ^ 1)
@@ -762,7 +759,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     }
     __syncthreads();  // dS planes of this tile and rows of the next one complete
     // ---- dQ^T = K^T dS^T: C[dim 32 dq + 16 dt2 + 4 q4 + i][row 16 rh + c]
-    if (dq_active) {
+    if (DO_Q && dq_active) {
       f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
@@ -803,6 +800,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
 
   // ---- this item's dK / dV contribution, in accumulator-fragment order:
   // kvpart[item][0 = dK, 1 = dV][wave][dt][lane][i] holds key 16 wave + 4 q4 + i, dim 16 dt + c.
+  if constexpr (!DO_KV) return;
   f32x4* base = reinterpret_cast<f32x4*>(kvpart + static_cast<int64_t>(item) * 2 * 128 * DP) + wid * (DP / 16) * 64 +
                 (dhalf / 16) * 64 + lane;
   if constexpr (DT == kF16) {  // divide out the scales (powers of two: exact)
@@ -1048,13 +1046,14 @@ int attn_bwd_kv(int dt, const void* q, const void* k, const void* v, const void*
       const dim3 grid(static_cast<unsigned>(mp.max_items)), block(kMainThreads);
       {
         ProfScope ps(kProfBwdMain, st);
-#define MSA_BWD_MAIN(DTV, NKV, FD, DH) hipLaunchKernelGGL((kv_bwd_main_kernel<DTV, NKV, FD>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, rshift, rowf, dqpart, kvpart, DH)
-#define MSA_BWD_MAIN_NK(DTV)                                                                       \
-  if (nk == 1) { if (fd) MSA_BWD_MAIN(DTV, 1, true, 0); else MSA_BWD_MAIN(DTV, 1, false, 0); }       \
-  else if (nk == 2) { if (fd) MSA_BWD_MAIN(DTV, 2, true, 0); else MSA_BWD_MAIN(DTV, 2, false, 0); }  \
-  else if (nk == 4) { if (fd) MSA_BWD_MAIN(DTV, 4, true, 0); else MSA_BWD_MAIN(DTV, 4, false, 0); }  \
-  else for (int dh = 0; dh < 256; dh += 128) {                                                     \
-    if (fd) MSA_BWD_MAIN(DTV, 8, true, dh); else MSA_BWD_MAIN(DTV, 8, false, dh);                  \
+#define MSA_BWD_MAIN(DTV, NKV, FD, PT, DH) hipLaunchKernelGGL((kv_bwd_main_kernel<DTV, NKV, FD, PT>), grid, block, 0, st, qb, kb, vb, gb, rs, cu, cu_blocks, qidx, sidx, hi, nit, its, ord, nseq, Hq, G, D, K, B, scale2, mepi, it0, rmagic, rshift, rowf, dqpart, kvpart, DH)
+#define MSA_BWD_MAIN_NK(DTV)                                                                                     \
+  if (nk == 1) { if (fd) MSA_BWD_MAIN(DTV, 1, true, kPartAll, 0); else MSA_BWD_MAIN(DTV, 1, false, kPartAll, 0); }       \
+  else if (nk == 2) { if (fd) MSA_BWD_MAIN(DTV, 2, true, kPartAll, 0); else MSA_BWD_MAIN(DTV, 2, false, kPartAll, 0); }  \
+  else if (nk == 4) { if (fd) MSA_BWD_MAIN(DTV, 4, true, kPartAll, 0); else MSA_BWD_MAIN(DTV, 4, false, kPartAll, 0); }  \
+  else for (int dh = 0; dh < 256; dh += 128) {                                                                   \
+    if (need_kv) { if (fd) MSA_BWD_MAIN(DTV, 8, true, kPartKV, dh); else MSA_BWD_MAIN(DTV, 8, false, kPartKV, dh); }   \
+    if (dq) { if (fd) MSA_BWD_MAIN(DTV, 8, true, kPartQ, dh); else MSA_BWD_MAIN(DTV, 8, false, kPartQ, dh); }          \
   }
         if (f16) { MSA_BWD_MAIN_NK(kF16) } else { MSA_BWD_MAIN_NK(kBF16) }
 #undef MSA_BWD_MAIN_NK
