@@ -731,6 +731,25 @@ def main():
         log(f"attention_fwd_bwd_fp16_ms: {stages['attention_fwd_bwd_fp16_ms']:.3f} "
             f"({step_flops / stages['attention_fwd_bwd_fp16_ms'] / 1e9:.1f} TFLOP/s)")
         del h16, dout16
+        # head dim 256 on the MFMA kernels: this config's tokens, heads and selection with
+        # bf16 q / k / v / dO of 256 dims (seeded N(0, 1)); twice the FLOPs of D = 128
+        g256 = torch.Generator().manual_seed(256)
+        d256 = [torch.randn(x.shape[0], x.shape[1], 256, generator=g256).to(torch.bfloat16).to(device)
+                for x in (q, k, v, dout)]
+        for x in d256[:3]:
+            x.requires_grad_()
+
+        def step_d256():
+            for x in d256[:3]:
+                x.grad = None
+            msa.m3_sparse_attention(*d256[:3], ids, cu, max_len, block_size=block).backward(d256[3])
+
+        stages["attention_fwd_bwd_d256_ms"] = round(time_events(step_d256, 3)["median"], 4)
+        peak_mem["attention_fwd_bwd_d256"] = round(peak_bytes(step_d256) / 2**20, 1)
+        d256_flops = step_flops * 256 / cfg["d"]
+        log(f"attention_fwd_bwd_d256_ms: {stages['attention_fwd_bwd_d256_ms']:.3f} "
+            f"({d256_flops / stages['attention_fwd_bwd_d256_ms'] / 1e9:.1f} TFLOP/s)")
+        del d256
         # the same autograd step with prepared sequence metadata (no host reads of
         # cu_seqlens), eager and replayed from a HIP graph capture
         seqs = msa.prepare_sequences(cu, block_size=block)
@@ -807,6 +826,10 @@ def main():
             "attention_fwd_bwd_fp16": {"bound": "mfma", "unit": "TFLOP/s",
                                        **frac(step_flops, stages["attention_fwd_bwd_fp16_ms"], MFMA_BF16_PEAK_TFLOPS,
                                               1e12)},
+            # head dim 256 (bf16): the step's FLOPs scaled by 256 / D
+            "attention_fwd_bwd_d256": {"bound": "mfma", "unit": "TFLOP/s",
+                                       **frac(step_flops * 256 / cfg["d"], stages["attention_fwd_bwd_d256_ms"],
+                                              MFMA_BF16_PEAK_TFLOPS, 1e12)},
         }
 
     baseline = None
