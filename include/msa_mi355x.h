@@ -130,7 +130,7 @@ int msa_score_bwd(const void* index_q, const void* index_k, int32_t dtype,
 
 /* Stage 3 forward workspace in bytes; 0 means this configuration runs the VALU
  * kernels, which need neither the CSR nor a workspace. Non-zero (the KV-major MFMA
- * kernels) for bf16 and fp16 inputs with head ratio <= 512, head dim 8..128 a
+ * kernels) for bf16 and fp16 inputs with head ratio <= 512, head dim 8..256 a
  * multiple of 8 and blocks of at most 128 keys. */
 int64_t msa_attn_fwd_workspace_bytes(int32_t dtype, int64_t total_tokens, int64_t q_heads,
                                      int64_t kv_groups, int64_t head_dim, int64_t topk_slots,

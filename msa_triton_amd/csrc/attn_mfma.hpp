@@ -6,7 +6,7 @@
 namespace msa {
 
 // Shapes the MFMA kernels cover: head ratio <= 512 (a work item holds whole edges of
-// at most 512 rows), 8 <= D <= 128 with D % 8 == 0, block <= 128.
+// at most 512 rows), 8 <= D <= 256 with D % 8 == 0, block <= 128.
 bool attn_mfma_supported(int64_t ratio, int64_t head_dim, int64_t block_size);
 
 int64_t attn_fwd_kv_workspace_bytes(int64_t T, int64_t Hq, int64_t G, int64_t D, int64_t K, int64_t total_blocks);
