@@ -433,8 +433,9 @@ __global__ __launch_bounds__(256) void kv_bwd_stats_combine(const int32_t* __res
 // LDS traffic; the next tile's rows are committed before it and the one after is
 // loaded from memory during the current tile.
 // PARTS selects the outputs: kPartAll (dK, dV and dQ) up to 128 dims; at 256 dims each
-// 128-dim half takes a kPartKV launch and a kPartQ launch (the two together exceed the
-// registers of a wave there), each recomputing S and dP over every dim.
+// 128-dim half takes a kPartKV launch, and dQ a kPartQ launch per half for fp16, one for
+// both halves for bf16 (all three outputs in one launch exceed the registers of a wave
+// there), each recomputing S and dP over every dim.
 enum MainParts : int { kPartKV = 1, kPartQ = 2, kPartAll = 3 };
 template <int DT, int NK, bool FULLD, int PARTS>
 __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
@@ -517,17 +518,20 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
   }
   const int rh = wid >> 2, dq = wid & 3;
   const bool dq_active = 32 * dq < DPO;
+  // dQ dims of this wave: NQ 16-dim tiles, qdim(dt2) + c. A bf16 dQ-only launch at 256 dims
+  // covers both 128-dim halves (dims 32 dq .. + 31 of each), the others 32 dims of one.
+  constexpr int NQ = (NK == 8 && PARTS == kPartQ && DT == kBF16) ? 4 : 2;
+  auto qdim = [&](int dt2) { return dhalf + 128 * (dt2 >> 1) + 32 * dq + 16 * (dt2 & 1); };
   // A operand of dQ^T (a bf16 product, dS entering as bf16 planes for either input type):
-  // K^T[dim 32 dq + 16 dt2 + c][keys 32 kc + 8 q4 + j]; fp16 K as two exact bf16 terms
-  // (kt the high terms, ktl the low ones).
-  bf16x8 kt[2][4], ktl[2][4];
+  // K^T[dim qdim(dt2) + c][keys 32 kc + 8 q4 + j]; fp16 K as two exact bf16 terms (kt the
+  // high terms, ktl the low ones).
+  bf16x8 kt[NQ][4], ktl[NQ][4];
 #pragma unroll
-  for (int dt2 = 0; dt2 < (DO_Q ? 2 : 0); ++dt2)
+  for (int dt2 = 0; dt2 < (DO_Q ? NQ : 0); ++dt2)
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc) {
       const bf16x8 x =
-          dq_active ? frag_tr(sm.k, KS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, dhalf + 32 * dq + 16 * dt2, c)
-                    : zero_frag();
+          dq_active ? frag_tr(sm.k, KS, 32 * kc + 8 * q4, 32 * kc + 8 * q4 + 4, qdim(dt2), c) : zero_frag();
       if constexpr (DT == kF16) {
         const uint4 w = __builtin_bit_cast(uint4, x);
         uint4 h, l;
@@ -760,7 +764,9 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     __syncthreads();  // dS planes of this tile and rows of the next one complete
     // ---- dQ^T = K^T dS^T: C[dim 32 dq + 16 dt2 + 4 q4 + i][row 16 rh + c]
     if (DO_Q && dq_active) {
-      f32x4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+      f32x4 acc[NQ];
+#pragma unroll
+      for (int dt2 = 0; dt2 < NQ; ++dt2) acc[dt2] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
         // B[keys 32 kc + 8 q4 + j][tile rows 16 rh + c]: lane c reads key (.. + c / 4), piece 4 rh + c % 4
@@ -770,7 +776,7 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
         const bf16x8 bm = frag_tr_at(sm.ds[b][1] + oa, sm.ds[b][1] + ob);
         const bf16x8 bh = frag_tr_at(sm.ds[b][0] + oa, sm.ds[b][0] + ob);
 #pragma unroll
-        for (int dt2 = 0; dt2 < 2; ++dt2) {
+        for (int dt2 = 0; dt2 < NQ; ++dt2) {
           if constexpr (DT == kF16) {
             // (Kh + Kl)(Dh + Dm + Dl), the smaller products first; Kl Dl (|Kl| <= 2^-8 |K|,
             // |Dl| < 2^-14 |dS|) lies below 2^-22 of K dS, the order of the fp32 sums' own
@@ -787,8 +793,8 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       }
       if (myrec >= 0) {
 #pragma unroll
-        for (int dt2 = 0; dt2 < 2; ++dt2) {
-          const int d0 = dhalf + 32 * dq + 16 * dt2 + 4 * q4;
+        for (int dt2 = 0; dt2 < NQ; ++dt2) {
+          const int d0 = qdim(dt2) + 4 * q4;
           if (FULLD || d0 < D)
             __builtin_nontemporal_store(acc[dt2], reinterpret_cast<f32x4*>(dqpart + static_cast<uint32_t>(myrec * D + d0)));
         }
@@ -1053,7 +1059,10 @@ int attn_bwd_kv(int dt, const void* q, const void* k, const void* v, const void*
   else if (nk == 4) { if (fd) MSA_BWD_MAIN(DTV, 4, true, kPartAll, 0); else MSA_BWD_MAIN(DTV, 4, false, kPartAll, 0); }  \
   else for (int dh = 0; dh < 256; dh += 128) {                                                                   \
     if (need_kv) { if (fd) MSA_BWD_MAIN(DTV, 8, true, kPartKV, dh); else MSA_BWD_MAIN(DTV, 8, false, kPartKV, dh); }   \
-    if (dq) { if (fd) MSA_BWD_MAIN(DTV, 8, true, kPartQ, dh); else MSA_BWD_MAIN(DTV, 8, false, kPartQ, dh); }          \
+    /* bf16: one dQ launch covers both halves */                                                               \
+    if (dq && (DTV == kF16 || dh == 0)) {                                                                      \
+      if (fd) MSA_BWD_MAIN(DTV, 8, true, kPartQ, dh); else MSA_BWD_MAIN(DTV, 8, false, kPartQ, dh);             \
+    }                                                                                                          \
   }
         if (f16) { MSA_BWD_MAIN_NK(kF16) } else { MSA_BWD_MAIN_NK(kBF16) }
 #undef MSA_BWD_MAIN_NK
