@@ -21,6 +21,8 @@
 //   dq combine    dQ = scale * sum of the row's block partials (FP64, slot order)
 // No floating-point atomics; every sum has a fixed order. Partial records are
 // written and read once each, with non-temporal (streaming) stores and loads.
+#include <type_traits>
+
 #include "attn_kv_common.hpp"
 #include "profile.hpp"
 
@@ -618,6 +620,48 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
   if (ntiles > 1) MSA_MAIN_ISSUE(32)
   __syncthreads();
 
+  // dQ^T = K^T dS^T of the tile whose planes sit in buffer PB, into ACC[NQ]:
+  // C[dim qdim(dt2) + 4 q4 + i][row 16 rh + c]
+#define MSA_DQ_PRODUCTS(PB, ACC)                                                                          \
+  _Pragma("unroll") for (int dt2 = 0; dt2 < NQ; ++dt2) ACC[dt2] = f32x4{0.f, 0.f, 0.f, 0.f};                \
+  _Pragma("unroll") for (int kc = 0; kc < 4; ++kc) {                                                      \
+    /* B[keys 32 kc + 8 q4 + j][tile rows 16 rh + c]: lane c reads key (.. + c / 4), piece 4 rh + c % 4 */  \
+    const int ka = 32 * kc + 8 * q4 + (c >> 2), kb = ka + 4;                                              \
+    const int oa = plane_offset(ka, 4 * rh + (c & 3)), ob = plane_offset(kb, 4 * rh + (c & 3));           \
+    const bf16x8 bl = frag_tr_at(sm.ds[PB][2] + oa, sm.ds[PB][2] + ob);                                   \
+    const bf16x8 bm = frag_tr_at(sm.ds[PB][1] + oa, sm.ds[PB][1] + ob);                                   \
+    const bf16x8 bh = frag_tr_at(sm.ds[PB][0] + oa, sm.ds[PB][0] + ob);                                   \
+    _Pragma("unroll") for (int dt2 = 0; dt2 < NQ; ++dt2) {                                                \
+      if constexpr (DT == kF16) {                                                                         \
+        /* (Kh + Kl)(Dh + Dm + Dl), the smaller products first; Kl Dl (|Kl| <= 2^-8 |K|, |Dl| <       \
+           2^-14 |dS|) lies below 2^-22 of K dS, the order of the fp32 sums' own rounding, and is left \
+           out (bit-identical dQ at the benchmark's c4 shape) */                                          \
+        ACC[dt2] = mfma(ktl[dt2][kc], bm, ACC[dt2]);                                                      \
+        ACC[dt2] = mfma(kt[dt2][kc], bl, ACC[dt2]);                                                       \
+        ACC[dt2] = mfma(ktl[dt2][kc], bh, ACC[dt2]);                                                      \
+      } else {                                                                                            \
+        ACC[dt2] = mfma(kt[dt2][kc], bl, ACC[dt2]);                                                       \
+      }                                                                                                   \
+      ACC[dt2] = mfma(kt[dt2][kc], bm, ACC[dt2]);                                                         \
+      ACC[dt2] = mfma(kt[dt2][kc], bh, ACC[dt2]);                                                         \
+    }                                                                                                     \
+  }
+  auto dq_store = [&](int rec, const f32x4 (&acc)[NQ]) __attribute__((always_inline)) {
+    if (rec >= 0) {
+#pragma unroll
+      for (int dt2 = 0; dt2 < NQ; ++dt2) {
+        const int d0 = qdim(dt2) + 4 * q4;
+        if (FULLD || d0 < D)
+          __builtin_nontemporal_store(acc[dt2], reinterpret_cast<f32x4*>(dqpart + static_cast<uint32_t>(rec * D + d0)));
+      }
+    }
+  };
+  // LAG (bf16, 128 dims, all outputs): tile t - 1's dQ products are issued among tile t's
+  // P / dS arithmetic (its planes stay in the other buffer until the barrier that ends tile
+  // t), so that a wave's MFMA and VALU work overlap (main pass 6.02 -> 5.84 ms at c4); the
+  // last tile's dQ follows the loop.
+  constexpr bool LAG = DT == kBF16 && NK == 4 && PARTS == kPartAll;
+  int myrec_prev = -1;
   const int key = 16 * wid + c;
   for (int t = 0; t < ntiles; ++t) {
     const int b = t & 1;
@@ -643,22 +687,25 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
     // planes, P and dS kept (Pv, Dv; element j = 4 rt + i) for their fp16 splits below
     uint32_t ph[8], pm[8], pl[8], dh[8], dm[8], dl[8];
     float Pv[8], Dv[8];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    // rows 16 rt + 4 q4 + i of this lane; FULL: every row sees the wave's 16 keys (no masks)
+    auto pds_rows = [&](int rt, auto full_tag) __attribute__((always_inline)) {
+      constexpr bool FULL = decltype(full_tag)::value;
       float4 stv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) stv[i] = sm.st[b][16 * rt + 4 * q4 + i];
-      if (full) {
+      auto keep = [&](int i, float P, float d) __attribute__((always_inline)) {
+        if constexpr (DT == kF16) {
+          Pv[4 * rt + i] = P, Dv[4 * rt + i] = d;
+        } else {
+          if constexpr (DO_KV) split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
+          split3_bits(d, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
+        }
+      };
+      if constexpr (FULL) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float P = __builtin_amdgcn_exp2f(s[rt][i] * scale2 - stv[i].x) * stv[i].y;
-          const float d = P * ((dp[rt][i] - stv[i].z) - stv[i].w);
-          if constexpr (DT == kF16) {
-            Pv[4 * rt + i] = P, Dv[4 * rt + i] = d;
-          } else {
-            if constexpr (DO_KV) split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
-            split3_bits(d, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
-          }
+          keep(i, P, P * ((dp[rt][i] - stv[i].z) - stv[i].w));
         }
       } else {
         const int4 vis = *reinterpret_cast<const int4*>(&sm.vis[b][16 * rt + 4 * q4]);
@@ -667,14 +714,31 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
         for (int i = 0; i < 4; ++i) {
           const bool ok = key < vv[i];
           const float P = ok ? __builtin_amdgcn_exp2f(s[rt][i] * scale2 - stv[i].x) * stv[i].y : 0.f;
-          const float d = ok ? P * ((dp[rt][i] - stv[i].z) - stv[i].w) : 0.f;
-          if constexpr (DT == kF16) {
-            Pv[4 * rt + i] = P, Dv[4 * rt + i] = d;
-          } else {
-            if constexpr (DO_KV) split3_bits(P, ph[4 * rt + i], pm[4 * rt + i], pl[4 * rt + i]);
-            split3_bits(d, dh[4 * rt + i], dm[4 * rt + i], dl[4 * rt + i]);
-          }
+          keep(i, P, ok ? P * ((dp[rt][i] - stv[i].z) - stv[i].w) : 0.f);
         }
+      }
+    };
+    if constexpr (LAG) {
+      // the previous tile's dQ products and this tile's P / dS arithmetic in one block
+      f32x4 lacc[NQ];
+      auto lagged = [&](auto full_tag) __attribute__((always_inline)) {
+        MSA_DQ_PRODUCTS(b ^ 1, lacc)
+        pds_rows(0, full_tag);
+        pds_rows(1, full_tag);
+      };
+      if (full)
+        lagged(std::true_type{});
+      else
+        lagged(std::false_type{});
+      if (t > 0) dq_store(myrec_prev, lacc);
+      myrec_prev = myrec;
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        if (full)
+          pds_rows(rt, std::true_type{});
+        else
+          pds_rows(rt, std::false_type{});
       }
     }
     if constexpr (DT == kF16) {
@@ -762,47 +826,21 @@ __global__ __launch_bounds__(kMainThreads, 1) void kv_bwd_main_kernel(
       if (t + 2 < ntiles) MSA_MAIN_ISSUE(32 * (t + 2))
     }
     __syncthreads();  // dS planes of this tile and rows of the next one complete
-    // ---- dQ^T = K^T dS^T: C[dim 32 dq + 16 dt2 + 4 q4 + i][row 16 rh + c]
-    if (DO_Q && dq_active) {
+    // ---- dQ^T = K^T dS^T: C[dim qdim(dt2) + 4 q4 + i][row 16 rh + c]
+    if (!LAG && DO_Q && dq_active) {
       f32x4 acc[NQ];
-#pragma unroll
-      for (int dt2 = 0; dt2 < NQ; ++dt2) acc[dt2] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        // B[keys 32 kc + 8 q4 + j][tile rows 16 rh + c]: lane c reads key (.. + c / 4), piece 4 rh + c % 4
-        const int ka = 32 * kc + 8 * q4 + (c >> 2), kb = ka + 4;
-        const int oa = plane_offset(ka, 4 * rh + (c & 3)), ob = plane_offset(kb, 4 * rh + (c & 3));
-        const bf16x8 bl = frag_tr_at(sm.ds[b][2] + oa, sm.ds[b][2] + ob);
-        const bf16x8 bm = frag_tr_at(sm.ds[b][1] + oa, sm.ds[b][1] + ob);
-        const bf16x8 bh = frag_tr_at(sm.ds[b][0] + oa, sm.ds[b][0] + ob);
-#pragma unroll
-        for (int dt2 = 0; dt2 < NQ; ++dt2) {
-          if constexpr (DT == kF16) {
-            // (Kh + Kl)(Dh + Dm + Dl), the smaller products first; Kl Dl (|Kl| <= 2^-8 |K|,
-            // |Dl| < 2^-14 |dS|) lies below 2^-22 of K dS, the order of the fp32 sums' own
-            // rounding, and is left out (bit-identical dQ at the benchmark's c4 shape)
-            acc[dt2] = mfma(ktl[dt2][kc], bm, acc[dt2]);
-            acc[dt2] = mfma(kt[dt2][kc], bl, acc[dt2]);
-            acc[dt2] = mfma(ktl[dt2][kc], bh, acc[dt2]);
-          } else {
-            acc[dt2] = mfma(kt[dt2][kc], bl, acc[dt2]);
-          }
-          acc[dt2] = mfma(kt[dt2][kc], bm, acc[dt2]);
-          acc[dt2] = mfma(kt[dt2][kc], bh, acc[dt2]);
-        }
-      }
-      if (myrec >= 0) {
-#pragma unroll
-        for (int dt2 = 0; dt2 < NQ; ++dt2) {
-          const int d0 = qdim(dt2) + 4 * q4;
-          if (FULLD || d0 < D)
-            __builtin_nontemporal_store(acc[dt2], reinterpret_cast<f32x4*>(dqpart + static_cast<uint32_t>(myrec * D + d0)));
-        }
-      }
+      MSA_DQ_PRODUCTS(b, acc)
+      dq_store(myrec, acc);
     }
+  }
+  if constexpr (LAG) {  // the last tile's dQ (its planes are complete after the loop's last barrier)
+    f32x4 acc[NQ];
+    MSA_DQ_PRODUCTS((ntiles - 1) & 1, acc)
+    dq_store(myrec_prev, acc);
   }
 #undef MSA_MAIN_ISSUE
 #undef MSA_MAIN_COMMIT
+#undef MSA_DQ_PRODUCTS
 
   // ---- this item's dK / dV contribution, in accumulator-fragment order:
   // kvpart[item][0 = dK, 1 = dV][wave][dt][lane][i] holds key 16 wave + 4 q4 + i, dim 16 dt + c.
