@@ -261,3 +261,47 @@ def test_fp16_fp32_attention_at_baseline_configs(name, dtype, device):
     assert np.array_equal(np.isneginf(lse_np), np.isneginf(rows["lse"]))
     fin = np.isfinite(rows["lse"])
     np.testing.assert_allclose(lse_np[fin], rows["lse"][fin], atol=1e-4, rtol=1e-4, err_msg=f"{name}: lse")
+
+
+@pytest.mark.parametrize("name,dtype", [("c2", torch.bfloat16), ("c4", torch.bfloat16), ("c2", torch.float16)],
+                         ids=["c2-bf16", "c4-bf16", "c2-fp16"])
+def test_head_dim_256_attention_at_baseline_configs(name, dtype, device):
+    """Head dim 256 on the MFMA kernels at BASELINE sizes: the config's tokens, heads and
+    selection (bf16 score and top-k from the benchmark's index inputs) with seeded N(0, 1)
+    q / k / v / dO of 256 dims; out / lse / dQ of sampled query tokens and dK / dV of
+    sampled keys against the sparse FP64 oracle within the dtype's stated tolerance."""
+    from tests.test_gpu_sweep import _check_dtype_stated
+
+    cfg = bench.CONFIGS[name]
+    lengths, B, K, L = cfg["lengths"], cfg["block"], cfg["topk"], cfg["local"]
+    bounds = _bounds(lengths)
+    max_len = max(lengths)
+    cu_np = np.array(bounds, dtype=np.int32)
+    iq, ik = bench.make_inputs(cfg)[:2]
+    T = bounds[-1]
+    g = torch.Generator().manual_seed(2560)
+    q, k, v, dout = (torch.randn(T, h, 256, generator=g).to(dtype) for h in (cfg["hq"], cfg["g"], cfg["g"], cfg["hq"]))
+    cu = torch.tensor(bounds, dtype=torch.int32, device=device)
+    print(f"[{name} {dtype} D=256] T={T} Hq={cfg['hq']} G={cfg['g']} K={K}", flush=True)
+    with torch.no_grad():
+        ids = msa.m3_topk(msa.m3_index_score(iq.to(device), ik.to(device), cu, max_len, block_size=B), cu,
+                          block_size=B, topk_blocks=K, local_blocks=L)
+    qd, kd, vd = (x.to(device).requires_grad_() for x in (q, k, v))
+    out, lse = msa.m3_sparse_attention(qd, kd, vd, ids, cu, max_len, block_size=B, return_lse=True)
+    out.backward(dout.to(device))
+    torch.cuda.synchronize()
+    ids_np = ids.cpu().numpy()
+    tokens = _sample_tokens(lengths, B, np.random.default_rng(256))
+    keys = _sample_keys(lengths, B, name)
+    q64, k64, v64, do64 = (x.double().numpy() for x in (q, k, v, dout))
+    rows = O.attention_rows(q64, k64, v64, ids_np, cu_np, tokens, block_size=B, dout=do64)
+    dk_ref, dv_ref = O.attention_kv_rows(q64, k64, v64, ids_np, cu_np, do64, keys, block_size=B)
+    check = _check_bf16 if dtype == torch.bfloat16 else (lambda a, r, n: _check_dtype_stated(a, r, dtype, n))
+    check(out[tokens], rows["out"], f"{name}: out")
+    check(qd.grad[tokens], rows["dq"], f"{name}: dq")
+    check(kd.grad[keys], dk_ref, f"{name}: dk")
+    check(vd.grad[keys], dv_ref, f"{name}: dv")
+    lse_np = lse.cpu().numpy()[tokens]
+    assert np.array_equal(np.isneginf(lse_np), np.isneginf(rows["lse"]))
+    fin = np.isfinite(rows["lse"])
+    np.testing.assert_allclose(lse_np[fin], rows["lse"][fin], atol=1e-4, rtol=1e-4, err_msg=f"{name}: lse")
