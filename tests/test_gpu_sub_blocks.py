@@ -1,11 +1,11 @@
-"""bf16 attention with blocks of more than 128 keys, on the MFMA kernels through
+"""bf16 and fp16 attention with blocks of more than 128 keys, on the MFMA kernels through
 sub-blocks: ``msa_split_block_indices`` maps block id b to sub-blocks f b .. f b + f - 1
 of block_size / f keys, which hold the same keys (triton/sparse_attention.py:35-84: a
 selected block b covers keys [b B, b B + B) of the sequence, clipped at the query).
 
 The split itself is compared with a numpy statement of that map (including -1 padding,
 future blocks and ids near INT32_MAX); the attention forward and backward with the
-FP64 oracle at the original block size, within the stated bf16 tolerance; the prepared
+FP64 oracle at the original block size, within the stated tolerance of the dtype; the prepared
 (PackedSequences) call bit for bit with the plain one.
 """
 
@@ -48,22 +48,28 @@ def test_split_block_indices_match_the_map(factor, device):
 
 
 # (lengths, groups, ratio, dim, block, topk): blocks of 256 (2 x 128), 192 (2 x 96) and
-# 384 (3 x 128), with a ragged packing and a causal tail in each
+# 384 (3 x 128), with a ragged packing and a causal tail in each; one case at head dim 256
 CASES = [
     ([700, 300], 2, 2, 64, 256, 2),
     ([650], 1, 4, 32, 192, 3),
     ([900, 5], 2, 1, 128, 384, 2),
+    ([420, 33], 1, 2, 256, 256, 2),
 ]
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("lengths,groups,ratio,dim,block,topk", CASES)
-def test_large_blocks_run_sub_blocks_on_mfma(lengths, groups, ratio, dim, block, topk, device, monkeypatch):
+def test_large_blocks_run_sub_blocks_on_mfma(lengths, groups, ratio, dim, block, topk, dtype, device, monkeypatch):
+    from tests.test_gpu_sweep import _check_dtype_stated
+
+    check = check_bf16_stated if dtype == torch.bfloat16 else (
+        lambda a, r, n: _check_dtype_stated(a, r, torch.float16, n))
     total = sum(lengths)
     gen = torch.Generator().manual_seed(block + dim)
-    q = torch.randn(total, groups * ratio, dim, generator=gen).bfloat16()
-    k = torch.randn(total, groups, dim, generator=gen).bfloat16()
-    v = torch.randn(total, groups, dim, generator=gen).bfloat16()
-    grad = torch.randn(total, groups * ratio, dim, generator=gen).bfloat16()
+    q = torch.randn(total, groups * ratio, dim, generator=gen).to(dtype)
+    k = torch.randn(total, groups, dim, generator=gen).to(dtype)
+    v = torch.randn(total, groups, dim, generator=gen).to(dtype)
+    grad = torch.randn(total, groups * ratio, dim, generator=gen).to(dtype)
     ids = random_selection(total, groups, topk, lengths, block, 1, gen)
     cu = cu_tensor(lengths)
 
@@ -85,12 +91,12 @@ def test_large_blocks_run_sub_blocks_on_mfma(lengths, groups, ratio, dim, block,
 
     ref_out, ref_lse, dq, dk, dv = O.sparse_attention(np64(q), np64(k), np64(v), ids.numpy(), cu.numpy(),
                                                       block_size=block, dout=np64(grad))
-    check_bf16_stated(out, ref_out, "out")
+    check(out, ref_out, "out")
     finite = np.isfinite(ref_lse)
     np.testing.assert_array_equal(np.isneginf(lse.detach().cpu().numpy()), np.isneginf(ref_lse))
     np.testing.assert_allclose(lse.detach().cpu().numpy()[finite], ref_lse[finite], atol=1e-4, rtol=1e-4)
     for name, t, ref in zip(("dq", "dk", "dv"), tensors, (dq, dk, dv)):
-        check_bf16_stated(t.grad, ref, name)
+        check(t.grad, ref, name)
 
     # the prepared form takes the same sub-blocks: identical results
     seqs = msa.prepare_sequences(cu.to(device), block_size=block)
