@@ -14,8 +14,9 @@ public API, then checks every stage at its stated bar:
     most 0.1 % outside the reference's gate, tests/test_triton_attention.py:58-97 --
     fp32 arithmetic leaves values within ~2^-22 of a bf16 rounding midpoint undecided,
     a few elements in 10^5 on these shapes); lse within 1e-4.
-Two smaller sweeps cover the VALU attention kernels (fp16 / fp32 inputs, head dims off
-the MFMA templates) and the indexer KL (eager/ops.py:153-180 restated in the oracle).
+Smaller sweeps cover fp16 / fp32 inputs (fp16 on the MFMA kernels where the head dim
+fits them, the FP64 kernels otherwise), head dims 136-256 on the MFMA kernels, and the
+indexer KL (eager/ops.py:153-180 restated in the oracle).
 The shapes are small enough for the oracle to finish in about a second each.
 """
 
@@ -133,7 +134,8 @@ def _check_dtype_stated(actual, expected, dtype, what):
 
 @pytest.mark.parametrize("seed", range(max(8, CASES // 3)))
 def test_random_shape_fp16_fp32_attention_against_oracle(seed, device):
-    """The VALU kernels (fp16 / fp32 inputs, any head dim) on random shapes and selections."""
+    """fp16 / fp32 inputs, any head dim, on random shapes and selections (fp32 and head dims
+    off the MFMA kernels' shapes on the FP64 kernels, fp16 otherwise on the MFMA ones)."""
     from tests.helpers import random_selection
 
     rng = np.random.default_rng(2000 + seed)
@@ -164,6 +166,44 @@ def test_random_shape_fp16_fp32_attention_against_oracle(seed, device):
     out.backward(dout.to(device))
     for name, tensor, ref in (("dq", qd, r_dq), ("dk", kd, r_dk), ("dv", vd, r_dv)):
         _check_dtype_stated(tensor.grad, ref, dtype, f"case {seed} {name}")
+
+
+@pytest.mark.parametrize("seed", range(max(6, CASES // 4)))
+def test_random_shape_wide_head_attention_against_oracle(seed, device):
+    """Head dims 136-256 on the MFMA kernels (bf16 for even seeds, fp16 for odd ones; the
+    backward's main pass in its per-half launches) on random shapes and selections,
+    within the stated tolerance of the dtype."""
+    from tests.helpers import random_selection
+
+    rng = np.random.default_rng(3000 + seed)
+    dtype = torch.float16 if seed % 2 else torch.bfloat16
+    lengths = [int(rng.integers(1, 300)) for _ in range(int(rng.integers(1, 3)))]
+    groups, ratio = int(rng.integers(1, 3)), int(rng.choice([1, 2, 3, 8]))
+    dim = int(rng.choice([136, 168, 200, 224, 256]))
+    block = int(rng.choice([4, 16, 64, 128]))
+    topk, local = int(rng.integers(1, 5)), int(rng.integers(0, 2))
+    scale = None if seed % 3 else 0.2
+    print(f"case {seed}: {lengths} G={groups} R={ratio} D={dim} B={block} K={topk} L={local} {dtype}", flush=True)
+    total = sum(lengths)
+    g = torch.Generator().manual_seed(seed)
+    ids = random_selection(total, groups, topk, lengths, block, local, g)
+    q, k, v, dout = (torch.randn(total, h, dim, generator=g).to(dtype) for h in (groups * ratio, groups, groups,
+                                                                                groups * ratio))
+    cu_h = cu_list(lengths)
+    qd, kd, vd = (x.to(device).requires_grad_() for x in (q, k, v))
+    out, lse = msa.m3_sparse_attention(qd, kd, vd, ids.to(device), cu_tensor(lengths, device), max(lengths),
+                                       block_size=block, scale=scale, return_lse=True)
+    r_out, r_lse, r_dq, r_dk, r_dv = O.sparse_attention(np64(q), np64(k), np64(v), ids.numpy(), np.asarray(cu_h),
+                                                        block_size=block, scale=scale, dout=np64(dout))
+    check = (lambda a, r, n: check_bf16_stated(a, r, n)) if dtype == torch.bfloat16 else (
+        lambda a, r, n: _check_dtype_stated(a, r, dtype, n))
+    check(out, r_out, f"case {seed} out")
+    finite = np.isfinite(r_lse)
+    assert np.array_equal(np.isfinite(lse.cpu().numpy()), finite)
+    np.testing.assert_allclose(lse.cpu().numpy()[finite], r_lse[finite], rtol=1e-4, atol=1e-4)
+    out.backward(dout.to(device))
+    for name, tensor, ref in (("dq", qd, r_dq), ("dk", kd, r_dk), ("dv", vd, r_dv)):
+        check(tensor.grad, ref, f"case {seed} {name}")
 
 
 @pytest.mark.parametrize("seed", range(max(8, CASES // 3)))
