@@ -188,9 +188,9 @@ int msa_attn_bwd(const void* q, const void* k, const void* v, int32_t dtype, con
                  const int32_t* slot_indices, void* grad_q, void* grad_k, void* grad_v,
                  void* workspace, int64_t workspace_bytes, void* stream);
 
-/* Indexer KL (bf16): workspace bytes; 0 means the configuration is not supported
- * (other dtypes, head or index dim not 32 / 64 / 128, more than 8 query heads per
- * group, block above 128). */
+/* Indexer KL (bf16 or fp16; index_q, index_k, q and k all of `dtype`): workspace
+ * bytes; 0 means the configuration is not supported (other dtypes, head or index dim
+ * not 32 / 64 / 128, more than 8 query heads per group, block above 128). */
 int64_t msa_indexer_kl_workspace_bytes(int32_t dtype, int64_t total_tokens, int64_t q_heads,
                                        int64_t kv_groups, int64_t head_dim, int64_t index_dim,
                                        int64_t topk_slots, int64_t total_blocks, int64_t block_size);

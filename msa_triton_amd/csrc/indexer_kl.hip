@@ -40,8 +40,16 @@ constexpr int kl_stride() { return DP + 16; }
 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 
+typedef _Float16 v4f16 __attribute__((ext_vector_type(4)));
+
+// 16x16x16 MFMA of the input type (bf16 or fp16 operand words in v4i16 containers).
+template <int DT>
 __device__ __forceinline__ f32x4 mfma16(v4i16 a, v4i16 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  if constexpr (DT == kF16)
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(v4f16, a), __builtin_bit_cast(v4f16, b), c, 0,
+                                                 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
 
 template <int NK, int NKI>
@@ -78,7 +86,7 @@ __device__ __forceinline__ float2 lane_max_sum(float (&x)[8][4]) {
 // Pass 1: waves own 16 edges each per tile (lane c = edge), all 128 keys of the
 // block. Logits^T = K_block . rows^T (A = block rows from LDS, B = the edge's query
 // row from memory): lane (c, q4) holds keys 16 kt + 4 q4 + i of edge c.
-template <int NK, int NKI>
+template <int DT, int NK, int NKI>
 __global__ __launch_bounds__(kKlThreads, 2) void kl_stats_kernel(
     const uint16_t* __restrict__ iq, const uint16_t* __restrict__ ik, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ k, const int32_t* __restrict__ cu, const int32_t* __restrict__ cu_blocks,
@@ -142,7 +150,7 @@ __global__ __launch_bounds__(kKlThreads, 2) void kl_stats_kernel(
       for (int kt = 0; kt < 8; ++kt) {
         f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < NKI; ++kk) a = mfma(load_frag(sm.ik + (16 * kt + c) * KSI + 32 * kk + 8 * q4), bq[kk], a);
+        for (int kk = 0; kk < NKI; ++kk) a = mfma_t<DT>(load_frag(sm.ik + (16 * kt + c) * KSI + 32 * kk + 8 * q4), bq[kk], a);
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[kt][i] = FULL || 16 * kt + 4 * q4 + i < lim ? a[i] * zs2 : -__builtin_inff();
       }
@@ -161,7 +169,7 @@ __global__ __launch_bounds__(kKlThreads, 2) void kl_stats_kernel(
       for (int kt = 0; kt < 8; ++kt) {
         f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) a = mfma(load_frag(sm.k + (16 * kt + c) * KS + 32 * kk + 8 * q4), bq[kk], a);
+        for (int kk = 0; kk < NK; ++kk) a = mfma_t<DT>(load_frag(sm.k + (16 * kt + c) * KS + 32 * kk + 8 * q4), bq[kk], a);
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[kt][i] = FULL || 16 * kt + 4 * q4 + i < lim ? a[i] * as2 : -__builtin_inff();
       }
@@ -282,7 +290,7 @@ struct KlMainSmem {
 //     dz planes -> LDS [key][edge]; barrier
 //     d_iq^T = ik^T dz^T  wave w: dims 16 w .. 16 w + 15, all 16 edges, all 128 keys
 // Row tiles, planes and the KL scratch are double-buffered: one barrier per tile.
-template <int NK, int NKI>
+template <int DT, int NK, int NKI>
 __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
     const uint16_t* __restrict__ iq, const uint16_t* __restrict__ ik, const uint16_t* __restrict__ q,
     const uint16_t* __restrict__ k, const float4* __restrict__ tstate, const float4* __restrict__ sstate,
@@ -460,7 +468,7 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
       if (h < R) {  // wave-uniform; unrolled so that heads interleave
         f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) a = mfma(load_frag(sm.qs[b] + (h * 16 + c) * KS + 32 * kk + 8 * q4), kf[kk], a);
+        for (int kk = 0; kk < NK; ++kk) a = mfma_t<DT>(load_frag(sm.qs[b] + (h * 16 + c) * KS + 32 * kk + 8 * q4), kf[kk], a);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float2 st = sm.tst[b][(4 * q4 + i) * R + h];
@@ -472,7 +480,7 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
     // ---- student, KL terms and dz
     f32x4 z = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kk = 0; kk < NKI; ++kk) z = mfma(load_frag(sm.iqs[b] + c * KSI + 32 * kk + 8 * q4), ikf[kk], z);
+    for (int kk = 0; kk < NKI; ++kk) z = mfma_t<DT>(load_frag(sm.iqs[b] + c * KSI + 32 * kk + 8 * q4), ikf[kk], z);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float4 st = sm.sst[b][4 * q4 + i];
@@ -504,9 +512,15 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
       for (int i = 0; i < 4; ++i) sm.red[b][wid][4 * q4 + i] = klv[i];
     }
     // ---- dz split: words of edges (4 q4, 4 q4 + 1) and (4 q4 + 2, 4 q4 + 3) per term
+    // (fp16: terms of 2^15 dz, |dz| <= 1; the d_ik and d_iq partials carry the factor until stored)
     uint32_t w[3][2];
-    split3_pk(dz[0], dz[1], w[0][0], w[1][0], w[2][0]);
-    split3_pk(dz[2], dz[3], w[0][1], w[1][1], w[2][1]);
+    if constexpr (DT == kF16) {
+      split3_pk_f16(dz[0] * kPScaleF16, dz[1] * kPScaleF16, w[0][0], w[1][0], w[2][0]);
+      split3_pk_f16(dz[2] * kPScaleF16, dz[3] * kPScaleF16, w[0][1], w[1][1], w[2][1]);
+    } else {
+      split3_pk(dz[0], dz[1], w[0][0], w[1][0], w[2][0]);
+      split3_pk(dz[2], dz[3], w[0][1], w[1][1], w[2][1]);
+    }
     if (need_dik) {
       // d_ik[key][dim 16 dt + c'] += dz^T[key][edges] iq[edges][dim]: A = dz (lane c = key,
       // edges 4 q4 + j), B[edges 4 q4 + j][dim 16 dt + c] read transposed from the iq rows
@@ -518,9 +532,9 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
         const uint2 raw = lds_read_tr16(sm.iqs[b] + (4 * q4 + (c >> 2)) * KSI + 16 * dt + 4 * (c & 3));
         const v4i16 bq = __builtin_bit_cast(v4i16, raw);
         f32x4 x = dik[dt];
-        x = mfma16(al, bq, x);
-        x = mfma16(am, bq, x);
-        dik[dt] = mfma16(ah, bq, x);
+        x = mfma16<DT>(al, bq, x);
+        x = mfma16<DT>(am, bq, x);
+        dik[dt] = mfma16<DT>(ah, bq, x);
       }
     }
     if (need_diq) {
@@ -560,10 +574,11 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
         const bf16x8 bl = frag_tr_at(sm.dz[b][2] + oa, sm.dz[b][2] + ob);
         const bf16x8 bm = frag_tr_at(sm.dz[b][1] + oa, sm.dz[b][1] + ob);
         const bf16x8 bh = frag_tr_at(sm.dz[b][0] + oa, sm.dz[b][0] + ob);
-        acc = mfma(ikt[kc], bl, acc);
-        acc = mfma(ikt[kc], bm, acc);
-        acc = mfma(ikt[kc], bh, acc);
+        acc = mfma_t<DT>(ikt[kc], bl, acc);
+        acc = mfma_t<DT>(ikt[kc], bm, acc);
+        acc = mfma_t<DT>(ikt[kc], bh, acc);
       }
+      if constexpr (DT == kF16) acc *= 1.f / kPScaleF16;
       if (myrec >= 0)
         __builtin_nontemporal_store(acc, reinterpret_cast<f32x4*>(diqpart + static_cast<int64_t>(myrec) * Di + 16 * wid + 4 * q4));
     }
@@ -574,7 +589,10 @@ __global__ __launch_bounds__(kKlThreads, 1) void kl_main_kernel(
   if (need_dik) {
     f32x4* base = reinterpret_cast<f32x4*>(ikpart + static_cast<int64_t>(item) * 128 * Di) + wid * NDTI * 64 + lane;
 #pragma unroll
-    for (int dt = 0; dt < NDTI; ++dt) __builtin_nontemporal_store(dik[dt], base + dt * 64);
+    for (int dt = 0; dt < NDTI; ++dt) {
+      if constexpr (DT == kF16) dik[dt] *= 1.f / kPScaleF16;
+      __builtin_nontemporal_store(dik[dt], base + dt * 64);
+    }
   }
 }
 
@@ -743,7 +761,7 @@ using namespace msa;
 extern "C" int64_t msa_indexer_kl_workspace_bytes(int32_t dtype, int64_t total_tokens, int64_t q_heads,
                                                   int64_t kv_groups, int64_t head_dim, int64_t index_dim,
                                                   int64_t topk_slots, int64_t total_blocks, int64_t block_size) {
-  if (dtype != kBF16 || total_tokens <= 0 || topk_slots < 0 || total_blocks < 0) return 0;
+  if ((dtype != kBF16 && dtype != kF16) || total_tokens <= 0 || topk_slots < 0 || total_blocks < 0) return 0;
   if (!kl_supported(q_heads, kv_groups, head_dim, index_dim, block_size)) return 0;
   return kl_layout(total_tokens, q_heads, kv_groups, index_dim, topk_slots, total_blocks).total;
 }
@@ -759,7 +777,8 @@ extern "C" int msa_indexer_kl(const void* index_q, const void* index_k, const vo
   if (num_seqs <= 0 || total_tokens < 0 || topk_slots < 0 || total_blocks < 0 || !loss || q_heads <= 0 ||
       kv_groups <= 0 || q_heads % kv_groups)
     return kErrInvalidArgument;
-  if (dtype != kBF16 || !kl_supported(q_heads, kv_groups, head_dim, index_dim, block_size)) return kErrUnsupported;
+  if ((dtype != kBF16 && dtype != kF16) || !kl_supported(q_heads, kv_groups, head_dim, index_dim, block_size))
+    return kErrUnsupported;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t T = total_tokens, Hq = q_heads, G = kv_groups, D = head_dim, Di = index_dim, K = topk_slots;
   if (T == 0) {
@@ -808,21 +827,24 @@ extern "C" int msa_indexer_kl(const void* index_q, const void* index_k, const vo
     const int epi = static_cast<int>(pl.epi);
     const dim3 grid(static_cast<unsigned>(pl.max_items > 0 ? pl.max_items : 1)), block(kKlThreads);
     if (rows > 0 && pl.max_items > 0) {
-#define MSA_KL_STATS(A, C) hipLaunchKernelGGL((kl_stats_kernel<A, C>), grid, block, 0, st, iqb, ikb, qb, kb, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, ord, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, teacher_lse ? 0 : 1, tpart, spart)
-#define MSA_KL_DISPATCH(M)                                   \
-  if (nk == 1) { if (nki == 1) M(1, 1); else if (nki == 2) M(1, 2); else M(1, 4); } \
-  else if (nk == 2) { if (nki == 1) M(2, 1); else if (nki == 2) M(2, 2); else M(2, 4); } \
-  else { if (nki == 1) M(4, 1); else if (nki == 2) M(4, 2); else M(4, 4); }
+#define MSA_KL_STATS(DTV, A, C) hipLaunchKernelGGL((kl_stats_kernel<DTV, A, C>), grid, block, 0, st, iqb, ikb, qb, kb, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, ord, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, teacher_lse ? 0 : 1, tpart, spart)
+#define MSA_KL_DISPATCH_DT(M, DTV)                                                         \
+  if (nk == 1) { if (nki == 1) M(DTV, 1, 1); else if (nki == 2) M(DTV, 1, 2); else M(DTV, 1, 4); }       \
+  else if (nk == 2) { if (nki == 1) M(DTV, 2, 1); else if (nki == 2) M(DTV, 2, 2); else M(DTV, 2, 4); }  \
+  else { if (nki == 1) M(DTV, 4, 1); else if (nki == 2) M(DTV, 4, 2); else M(DTV, 4, 4); }
+#define MSA_KL_DISPATCH(M) \
+  if (dtype == kF16) { MSA_KL_DISPATCH_DT(M, kF16) } else { MSA_KL_DISPATCH_DT(M, kBF16) }
       MSA_KL_DISPATCH(MSA_KL_STATS)
 #undef MSA_KL_STATS
     }
     hipLaunchKernelGGL(kl_stats_combine, dim3(grid_1d((t1 - t0) * (Hq + G), 16)), dim3(256), 0, st, indices,
                        cu_seqlens, nseq, t0, t1, iHq, iG, iK, iB, tpart, spart, teacher_lse, tstate, sstate);
     if (rows > 0 && pl.max_items > 0) {
-#define MSA_KL_MAIN(A, C) hipLaunchKernelGGL((kl_main_kernel<A, C>), grid, block, 0, st, iqb, ikb, qb, kb, tstate, sstate, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, ord, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, need_diq, need_dik, klpart, diqpart, ikpart)
+#define MSA_KL_MAIN(DTV, A, C) hipLaunchKernelGGL((kl_main_kernel<DTV, A, C>), grid, block, 0, st, iqb, ikb, qb, kb, tstate, sstate, cu_seqlens, cu_block_lens, query_indices, slot_indices, hi, nit, its, ord, nseq, iHq, iG, iK, iB, zs2, as2, epi, it0, need_diq, need_dik, klpart, diqpart, ikpart)
       MSA_KL_DISPATCH(MSA_KL_MAIN)
 #undef MSA_KL_MAIN
 #undef MSA_KL_DISPATCH
+#undef MSA_KL_DISPATCH_DT
     }
     hipLaunchKernelGGL(kl_row_combine, dim3(grid_1d((t1 - t0) * G, 8)), dim3(256), 0, st, indices, cu_seqlens, nseq,
                        t0, t1, iG, iK, iB, iDi, gscale, klpart, diqpart, rowkl, row_kl, grad_index_q);

@@ -19,10 +19,10 @@ Over the causal tokens of each (token, group)'s selected blocks:
 Execution: ``msa_indexer_kl`` (two KV-major MFMA passes over the selection's k2q
 CSR, deterministic). The forward also produces the fp32 gradients of the loss when
 ``index_q`` or ``index_k`` requires grad; the backward scales them by the incoming
-gradient. bf16 only, head and index dims of 32, 64 or 128, at most 8 query heads per
-group, block size up to 128 (larger blocks run as f <= 8 sub-blocks of at most 128 keys
-when f divides the block size: the same keys, so the same loss); other configurations
-raise ``NotImplementedError``.
+gradient. bf16 or fp16 (all four inputs of one dtype), head and index dims of 32, 64 or
+128, at most 8 query heads per group, block size up to 128 (larger blocks run as f <= 8
+sub-blocks of at most 128 keys when f divides the block size: the same keys, so the same
+loss); other configurations raise ``NotImplementedError``.
 """
 
 from __future__ import annotations
@@ -41,6 +41,8 @@ def _launch(iq, ik, q, k, indices, cu, meta, seqs, block_size, index_scale, scal
     total, groups, dim_i = iq.shape
     heads, dim = q.shape[1], q.shape[2]
     lib = _lib.lib()
+    if q.dtype != iq.dtype:  # the kernels take one input type for all four tensors
+        raise NotImplementedError("m3_indexer_kl takes index_q / index_k and q / k of one dtype")
 
     def fits(factor, sub, sub_meta):
         return lib.msa_indexer_kl_workspace_bytes(_lib.DTYPE_CODE[iq.dtype], total, heads, groups, dim, dim_i,
@@ -53,8 +55,8 @@ def _launch(iq, ik, q, k, indices, cu, meta, seqs, block_size, index_scale, scal
                                                   slots, meta.total_blocks, block_size)
     if total and ws_bytes == 0:
         raise NotImplementedError(
-            "m3_indexer_kl supports bf16 inputs with head and index dims of 32, 64 or 128, at most 8 query "
-            "heads per group and block_size <= 128 (or a multiple of at most 8 sub-blocks of <= 128)")
+            "m3_indexer_kl supports bf16 or fp16 inputs with head and index dims of 32, 64 or 128, at most 8 "
+            "query heads per group and block_size <= 128 (or a multiple of at most 8 sub-blocks of <= 128)")
     device = iq.device
     loss = torch.zeros(1, dtype=torch.float32, device=device)
     row_kl = torch.zeros((total, groups), dtype=torch.float32, device=device) if want_rows else None

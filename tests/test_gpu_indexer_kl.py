@@ -23,13 +23,13 @@ from tests.helpers import cu_list, random_selection
 pytestmark = pytest.mark.gpu
 
 
-def _inputs(lengths, groups, ratio, dim, dim_i, block, topk, seed, q_scale=1.0):
+def _inputs(lengths, groups, ratio, dim, dim_i, block, topk, seed, q_scale=1.0, dtype=torch.bfloat16):
     g = torch.Generator().manual_seed(seed)
     total = sum(lengths)
-    iq = torch.randn(total, groups, dim_i, generator=g).bfloat16()
-    ik = torch.randn(total, 1, dim_i, generator=g).bfloat16()
-    q = (q_scale * torch.randn(total, groups * ratio, dim, generator=g)).bfloat16()
-    k = torch.randn(total, groups, dim, generator=g).bfloat16()
+    iq = torch.randn(total, groups, dim_i, generator=g).to(dtype)
+    ik = torch.randn(total, 1, dim_i, generator=g).to(dtype)
+    q = (q_scale * torch.randn(total, groups * ratio, dim, generator=g)).to(dtype)
+    k = torch.randn(total, groups, dim, generator=g).to(dtype)
     ids = random_selection(total, groups, topk, lengths, block, 1, g)
     cu = torch.tensor(cu_list(lengths), dtype=torch.int32)
     return iq, ik, q, k, ids, cu
@@ -48,6 +48,7 @@ def _close32(actual, expected, what):
     assert np.all(err <= bound), f"{what}: max err/bound {float((err / bound).max()):.3f}"
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("lengths,groups,ratio,dim,dim_i,block,topk,index_scale,scale", [
     ([37], 1, 1, 32, 32, 8, 3, 1.0, None),
     ([300, 45], 2, 4, 64, 64, 16, 5, 0.5, None),
@@ -58,8 +59,9 @@ def _close32(actual, expected, what):
     ([300, 45], 2, 4, 64, 64, 256, 2, 0.5, None),
     ([400], 1, 2, 32, 128, 192, 3, 1.0, None),
 ])
-def test_matches_fp64_oracle(lengths, groups, ratio, dim, dim_i, block, topk, index_scale, scale, device):
-    iq, ik, q, k, ids, cu = _inputs(lengths, groups, ratio, dim, dim_i, block, topk, 17)
+def test_matches_fp64_oracle(lengths, groups, ratio, dim, dim_i, block, topk, index_scale, scale, dtype, device):
+    """bf16 and fp16 (fp16: dz = S - T enters the gradient products as fp16 terms of 2^15 dz)."""
+    iq, ik, q, k, ids, cu = _inputs(lengths, groups, ratio, dim, dim_i, block, topk, 17, dtype=dtype)
     sc = dim ** -0.5 if scale is None else scale
     ref = _oracle(iq, ik, q, k, ids, cu, block, index_scale, sc)
     meta = sequence_meta(cu.tolist(), block)
@@ -69,16 +71,17 @@ def test_matches_fp64_oracle(lengths, groups, ratio, dim, dim_i, block, topk, in
     np.testing.assert_allclose(rows.cpu().double().numpy(), ref["row_kl"], rtol=1e-5, atol=1e-6)
     _close32(d_iq, ref["d_iq"], "d_iq")
     _close32(d_ik, ref["d_ik"], "d_ik")
-    # the autograd path: same loss, bf16 gradients of the loss
+    # the autograd path: same loss, gradients of the loss in the input dtype (one ulp)
     a, b = d[0].clone().requires_grad_(), d[1].clone().requires_grad_()
     out = msa.m3_indexer_kl(a, b, d[2], d[3], d[4], d[5], max(lengths), block_size=block, index_scale=index_scale,
                             scale=scale)
     assert float(out.detach()) == float(loss)
     out.backward()
+    ulp = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
     for grad, exp in ((a.grad, ref["d_iq"]), (b.grad, ref["d_ik"])):
-        assert grad.dtype == torch.bfloat16
+        assert grad.dtype == dtype
         act = grad.float().cpu().double().numpy()
-        assert np.all(np.abs(act - exp) <= 1e-6 + 2.0 ** -8 * np.abs(exp))
+        assert np.all(np.abs(act - exp) <= 1e-6 + ulp * np.abs(exp))
 
 
 def test_zero_when_student_equals_teacher(device):
@@ -139,6 +142,8 @@ def test_unsupported_configurations_raise(device):
     with pytest.raises(NotImplementedError):
         q16 = torch.randn(20, 16, 32, device=device).bfloat16()
         msa.m3_indexer_kl(d[0], d[1], q16, d[3], d[4], d[5], 20, block_size=8)
+    with pytest.raises(NotImplementedError):  # index inputs and attention inputs of different dtypes
+        msa.m3_indexer_kl(d[0], d[1], d[2].half(), d[3].half(), d[4], d[5], 20, block_size=8)
 
 
 def test_teacher_lse_from_the_attention(device):
