@@ -750,6 +750,24 @@ def main():
         log(f"attention_fwd_bwd_d256_ms: {stages['attention_fwd_bwd_d256_ms']:.3f} "
             f"({d256_flops / stages['attention_fwd_bwd_d256_ms'] / 1e9:.1f} TFLOP/s)")
         del d256
+        # one rank's share under group (head) parallelism over the config's G groups: group
+        # 0's query heads, K / V and selection (G = 1, Hq / G heads), i.e. the kernels a rank
+        # runs when the G groups are spread over G GPUs (no exchange inside the operators)
+        rheads = cfg["hq"] // cfg["g"]
+        share = [x.detach()[:, :rheads if x.shape[1] == cfg["hq"] else 1].contiguous() for x in (q, k, v, dout)]
+        for x in share[:3]:
+            x.requires_grad_()
+        ids_share = ids[:, :1].contiguous()
+
+        def step_share():
+            for x in share[:3]:
+                x.grad = None
+            msa.m3_sparse_attention(*share[:3], ids_share, cu, max_len, block_size=block).backward(share[3])
+
+        stages["attention_fwd_bwd_rank_share_ms"] = round(time_events(step_share, 5)["median"], 4)
+        log(f"attention_fwd_bwd_rank_share_ms (G = 1, Hq = {rheads}): {stages['attention_fwd_bwd_rank_share_ms']:.3f} "
+            f"({step_flops / cfg['g'] / stages['attention_fwd_bwd_rank_share_ms'] / 1e9:.1f} TFLOP/s)")
+        del share, ids_share
         # the same autograd step with prepared sequence metadata (no host reads of
         # cu_seqlens), eager and replayed from a HIP graph capture
         seqs = msa.prepare_sequences(cu, block_size=block)
@@ -826,6 +844,10 @@ def main():
             "attention_fwd_bwd_fp16": {"bound": "mfma", "unit": "TFLOP/s",
                                        **frac(step_flops, stages["attention_fwd_bwd_fp16_ms"], MFMA_BF16_PEAK_TFLOPS,
                                               1e12)},
+            # one rank's share under G-way group parallelism: 1 / G of the step's FLOPs
+            "attention_fwd_bwd_rank_share": {"bound": "mfma", "unit": "TFLOP/s",
+                                             **frac(step_flops / cfg["g"], stages["attention_fwd_bwd_rank_share_ms"],
+                                                    MFMA_BF16_PEAK_TFLOPS, 1e12)},
             # head dim 256 (bf16): the step's FLOPs scaled by 256 / D
             "attention_fwd_bwd_d256": {"bound": "mfma", "unit": "TFLOP/s",
                                        **frac(step_flops * 256 / cfg["d"], stages["attention_fwd_bwd_d256_ms"],
