@@ -386,14 +386,13 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
   __shared__ int32_t tie_count[kDkTieCap];
   __shared__ int32_t ntie_s;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  // Workgroups are dispatched to the 8 XCDs round-robin (workgroup i on XCD i % 8), each
-  // with its own L2. Logical work L = (i % 8) * ceil(n / 8) + i / 8, segment-major, gives
-  // every XCD a contiguous run of (segment, block) pairs, so the query rows it gathers
-  // (one 2 MiB segment at a time) stay in its L2.
-  // The grid is padded to 8 x ceil(n / 8) workgroups so that this covers every L < n.
+  // Work L = workgroup index, segment-major over (segment, key block). Workgroups go to the
+  // 8 XCDs round-robin, so consecutive pairs run on different XCDs. The nonempty pairs are
+  // concentrated in the low segments (a late key block has few rows), so contiguous runs
+  // of L per XCD would leave the XCDs unevenly loaded (at one 32K sequence with G = 4: 496
+  // nonempty pairs on the first XCD, 48 on the last).
   const int64_t nwork = nblk * nseg;
-  const int64_t per_xcd = gridDim.x / 8;
-  const int64_t lw = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  const int64_t lw = blockIdx.x;
   if (lw >= nwork) return;  // whole workgroup (padding)
   const int sg = static_cast<int>(lw / nblk);
   const int64_t gb = lw % nblk;
@@ -760,7 +759,7 @@ int score_bwd_launch(const void* iq, const void* ik, const int32_t* cu, const in
     hipLaunchKernelGGL(score_bwd_transpose, tgrid, dim3(256), 0, st, tie, ds, rows, NB, tie_t, ds_t);
     const int nseg = static_cast<int>(dk_nseg(rows));
     const int kchunks = (B + 127) / 128;
-    const dim3 grid(static_cast<unsigned>(8 * ((total_blocks * nseg + 7) / 8)), static_cast<unsigned>(kchunks));
+    const dim3 grid(static_cast<unsigned>(total_blocks * nseg), static_cast<unsigned>(kchunks));
 #define MSA_DK_PART(DPLV, DC0) hipLaunchKernelGGL((score_bwd_dk_part<DT, DPLV>), grid, dim3(256), 0, st, iq, ik, cu, cu_blocks, nseq, tie_t, ds_t, rows, G, Di, B, total_blocks, nseg, scale, part, DC0)
     if (Di <= 64) MSA_DK_PART(1, 0);
     else if (Di <= 128) MSA_DK_PART(2, 0);
