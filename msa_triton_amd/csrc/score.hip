@@ -62,15 +62,24 @@ __global__ __launch_bounds__(256) void score_fwd_exact(const void* __restrict__ 
 // ---- backward -----------------------------------------------------------------
 
 // Transpose (tie, ds) from [rows, NB] to block-major [NB, rows] so the key-block
-// pass reads them contiguously. 64x64 tiles through LDS.
+// pass reads them contiguously. 64x64 tiles through LDS. The key-block pass reads block
+// b's column only from the rows that see it (position >= b B), so a tile whose rows lie in
+// one sequence and see none of its blocks is skipped (about half the tiles of a long
+// sequence).
 __global__ __launch_bounds__(256) void score_bwd_transpose(const int32_t* __restrict__ tie,
                                                            const float* __restrict__ ds, int64_t rows,
-                                                           int NB, int32_t* __restrict__ tie_t,
+                                                           int NB, const int32_t* __restrict__ cu, int nseq,
+                                                           int G, int B, int32_t* __restrict__ tie_t,
                                                            float* __restrict__ ds_t) {
   __shared__ int32_t tt[64][65];
   __shared__ float dt[64][65];
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * 64;
   const int b0 = blockIdx.y * 64;
+  {
+    const int64_t t0 = r0 / G, t1 = (r0 + 63 < rows ? r0 + 63 : rows - 1) / G;
+    const int s1 = find_seq(cu, nseq, t1);
+    if (find_seq(cu, nseq, t0) == s1 && static_cast<int64_t>(b0) * B > t1 - cu[s1]) return;  // whole workgroup
+  }
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
   for (int i = ty; i < 64; i += 4) {
     const int64_t r = r0 + i;
@@ -756,7 +765,7 @@ int score_bwd_launch(const void* iq, const void* ik, const int32_t* cu, const in
     float* ds_t = reinterpret_cast<float*>(tie_t + rows * NB);
     double* part = reinterpret_cast<double*>(ds_t + rows * NB);  // 8 * rows * NB bytes in: 8-byte aligned
     const dim3 tgrid(grid_1d(rows, 64), static_cast<unsigned>((NB + 63) / 64));
-    hipLaunchKernelGGL(score_bwd_transpose, tgrid, dim3(256), 0, st, tie, ds, rows, NB, tie_t, ds_t);
+    hipLaunchKernelGGL(score_bwd_transpose, tgrid, dim3(256), 0, st, tie, ds, rows, NB, cu, nseq, G, B, tie_t, ds_t);
     const int nseg = static_cast<int>(dk_nseg(rows));
     const int kchunks = (B + 127) / 128;
     const dim3 grid(static_cast<unsigned>(total_blocks * nseg), static_cast<unsigned>(kchunks));
