@@ -395,25 +395,29 @@ __global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
   __shared__ int32_t tie_count[kDkTieCap];
   __shared__ int32_t ntie_s;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
-  // Work L = workgroup index, segment-major over (segment, key block). Workgroups go to the
-  // 8 XCDs round-robin, so consecutive pairs run on different XCDs. The nonempty pairs are
-  // concentrated in the low segments (a late key block has few rows), so contiguous runs
-  // of L per XCD would leave the XCDs unevenly loaded (at one 32K sequence with G = 4: 496
-  // nonempty pairs on the first XCD, 48 on the last).
+  // Segments are aligned to multiples of kDkSeg in the row space: key block gb takes segment
+  // S0 + sg, S0 = (its first row) / kDkSeg, clipped to its rows. Work L = workgroup index,
+  // S-major over (S, key block): the workgroups running together gather from the same one or
+  // two 2 MiB segments of index_q. Workgroups go to the 8 XCDs round-robin, so consecutive
+  // pairs run on different XCDs (contiguous runs of L per XCD would load them unevenly: the
+  // nonempty pairs are concentrated in the low segments at one long sequence).
   const int64_t nwork = nblk * nseg;
   const int64_t lw = blockIdx.x;
   if (lw >= nwork) return;  // whole workgroup (padding)
-  const int sg = static_cast<int>(lw / nblk);
+  const int64_t S = lw / nblk;
   const int64_t gb = lw % nblk;
-  const int64_t w = gb * nseg + sg;  // (gb, sg): index of this pair's partial sums
   const int kc = blockIdx.y, kchunks = gridDim.y;
   int s = upper_index(cu_blocks, nseq + 1, gb);
   while (s < nseq && cu_blocks[s + 1] <= gb) ++s;
   const int b = static_cast<int>(gb - cu_blocks[s]);
   const int64_t start = cu[s], end = cu[s + 1];
   const int64_t k0 = start + static_cast<int64_t>(b) * B;
-  const int64_t r_begin = k0 * G + static_cast<int64_t>(sg) * kDkSeg;
-  const int64_t r_stop = r_begin + kDkSeg < end * G ? r_begin + kDkSeg : end * G;
+  const int64_t S0 = k0 * G / kDkSeg;
+  if (S < S0) return;  // whole workgroup: the block starts after this segment
+  const int sg = static_cast<int>(S - S0);
+  const int64_t w = gb * nseg + sg;  // (gb, sg): index of this pair's partial sums
+  const int64_t r_begin = S == S0 ? k0 * G : S * kDkSeg;
+  const int64_t r_stop = (S + 1) * kDkSeg < end * G ? (S + 1) * kDkSeg : end * G;
   if (r_begin >= r_stop) return;  // whole workgroup: empty segment (the reduce skips it)
   const int o_lo = 128 * kc;      // this chunk's first key offset in the block
   const int nseg_rows = static_cast<int>(r_stop - r_begin);
@@ -708,9 +712,10 @@ __global__ __launch_bounds__(256) void score_bwd_dk_reduce(const int32_t* __rest
   const int64_t gb = cu_blocks[s] + b;
   const int64_t k0 = start + static_cast<int64_t>(b) * B;
   const int kc = o / 128, kchunks = (B + 127) / 128;
+  const int64_t S0 = k0 * G / kDkSeg;  // the block's first segment (aligned to kDkSeg rows)
   double sum = 0.0;
   for (int sg = 0; sg < nseg; ++sg) {
-    if (k0 * G + static_cast<int64_t>(sg) * kDkSeg >= end * G) break;  // empty segment (nothing written)
+    if ((S0 + sg) * kDkSeg >= end * G) break;  // empty segment (nothing written)
     const int64_t w = gb * nseg + sg;
     sum += part[((w * kchunks + kc) * 128 + o % 128) * static_cast<int64_t>(Di) + d];
   }
