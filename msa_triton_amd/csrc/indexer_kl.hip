@@ -254,11 +254,19 @@ __global__ __launch_bounds__(256) void kl_stats_combine(const int32_t* __restric
 
 namespace {
 
-// dz planes [key][edge] are unpadded (32 bytes per key); the 8-byte piece p (edges
-// 4p .. 4p + 3) of key k sits at piece p ^ ((k >> 2) & 3). Measured with
-// SQ_LDS_BANK_CONFLICT over kl_main_kernel: 0.82 conflict cycles per LDS instruction,
-// against 1.08 unswizzled and 0.90 with p ^ ((k >> 1) & 3).
-__device__ __forceinline__ int dz_offset(int key, int piece) { return key * 16 + 4 * (piece ^ ((key >> 2) & 3)); }
+// dz planes [key][edge] are unpadded (32 bytes per key, so a row's 8 banks are set by its
+// row index mod 8). Key k sits in row k ^ (4 ((k >> 3) & 1)) and its 8-byte piece p (edges
+// 4p .. 4p + 3) at piece p ^ ((k >> 2) & 3). The transposed reads of 32 lanes take keys
+// k0 .. k0 + 3 and k0 + 8 .. k0 + 11 (k0 a multiple of 8, or those plus 4), all four pieces:
+// the row permutation puts the two key groups on different halves of the 64 banks, so the
+// 32 reads of 8 bytes hit 64 distinct banks; the plane writes of 32 lanes (keys k0 .. k0 +
+// 15, pieces 0 and 1) pair rows r and r ^ 12, whose piece swizzles differ in bit 1, so they
+// are conflict-free too. SQ_LDS_BANK_CONFLICT over kl_main_kernel at c4: 0.47 conflict
+// cycles per LDS instruction (the piece swizzle alone 0.82, unswizzled 1.08; the rest come
+// from its other LDS accesses); the kernel's time is unchanged within run-to-run noise.
+__device__ __forceinline__ int dz_offset(int key, int piece) {
+  return (key ^ (((key >> 3) & 1) << 2)) * 16 + 4 * (piece ^ ((key >> 2) & 3));
+}
 
 template <int NK, int NKI>
 struct KlMainSmem {
