@@ -233,7 +233,7 @@ __global__ __launch_bounds__(256) void score_bwd_dq(const void* __restrict__ iq,
 // slot + RPI, ... of the list into FP64 sums of its 8 dims, and the RPI slot sums
 // are added in slot order at the end (a fixed order). Exact ties (rare) are added
 // by every slot-0 lane after the chunk's unique winners, in block order.
-constexpr int kDqWideUnroll = 8;  // key-row gather instructions in flight per wave
+constexpr int kDqWideUnroll = 4;  // key-row gather instructions in flight per wave (80 VGPRs: 6 waves per SIMD)
 
 template <int DT, int LPR>
 __global__ __launch_bounds__(256) void score_bwd_dq_wide(const void* __restrict__ iq,
