@@ -377,11 +377,14 @@ __device__ __forceinline__ void dk_add_row(double (&acc)[8], double wgt, const v
 
 constexpr int kDkSeg = 8192;
 constexpr int kDkBatch = 16;
-constexpr int kDkWideUnroll = 8;  // row-gather instructions per batch (4 rows each; two batches in flight)
-constexpr int kDkTieCap = 256;
+constexpr int kDkWideUnroll = 4;  // row-gather instructions per batch (4 rows each; two batches in flight)
+// Listed exact ties per segment (a segment with more rescans its rows per key). With 4-instruction
+// batches (131 VGPRs) and this list the pass fits three workgroups per CU (53 KB of LDS each):
+// at c4 1.13-1.17 vs 1.21-1.24 ms for the score backward with two (8-instruction batches).
+constexpr int kDkTieCap = 64;
 
 template <int DT, int DPL>
-__global__ __launch_bounds__(256, 2) void score_bwd_dk_part(
+__global__ __launch_bounds__(256, DPL >= 8 ? 2 : 3) void score_bwd_dk_part(
     const void* __restrict__ iq, const void* __restrict__ ik, const int32_t* __restrict__ cu,
     const int32_t* __restrict__ cu_blocks, int nseq, const int32_t* __restrict__ tie_t,
     const float* __restrict__ ds_t, int64_t rows, int G, int Di, int B, int64_t nblk, int nseg, double scale,

@@ -55,6 +55,44 @@ def test_score_forward_backward_fp64(lengths, groups, dim, block_size, scale, de
     _run(q_cpu, k_cpu, lengths, max_seqlen, block_size, scale, upstream, device)
 
 
+@pytest.mark.parametrize("dim,dtype", [(128, torch.bfloat16), (128, torch.float16), (64, torch.bfloat16)],
+                         ids=["bf16-128", "fp16-128", "bf16-64"])
+def test_score_backward_many_exact_ties_in_one_segment(dim, dtype, device):
+    """One index_k vector for every token makes every visible key of every block an exact
+    tie: 380 tied (row, block) pairs per key block, all in one 8192-row segment of the
+    key-block (dk) pass, more than its list of tied rows holds, so that pass takes its
+    rescan path; each ds is split evenly over the tied keys. Scores bit-exact; gradients
+    within the stated tolerance against the FP64 oracle (the products of one repeated key
+    vector land exactly on rounding midpoints of the output type far more often than
+    random data does, where the last bit of the FP64 sum of the split weights decides)."""
+    from tests.helpers import check_bf16_stated
+    from tests.test_gpu_sweep import _check_dtype_stated
+
+    lengths, groups, block, scale = [150, 40], 2, 128, 1.0
+    gen = torch.Generator().manual_seed(11)
+    q_cpu = torch.randn(sum(lengths), groups, dim, generator=gen).to(dtype)
+    k_cpu = torch.randn(1, 1, dim, generator=gen).to(dtype).expand(sum(lengths), 1, dim).contiguous()
+    max_seqlen = max(lengths)
+    nb = (max_seqlen + block - 1) // block
+    upstream = torch.randn((sum(lengths), groups, nb), generator=gen).to(torch.bfloat16).float()
+    q = q_cpu.to(device).clone().requires_grad_()
+    k = k_cpu.to(device).clone().requires_grad_()
+    cu = cu_tensor(lengths, device)
+    scores = msa.m3_index_score(q, k, cu, max_seqlen, block_size=block, scale=scale)
+    _, exp32, tie = O.index_score(q_cpu.double().numpy(), k_cpu.double().numpy(), cu_list(lengths), max_seqlen,
+                                  block_size=block, scale=scale)
+    np.testing.assert_array_equal(scores.detach().cpu().numpy(), exp32)
+    assert int((tie[:lengths[0], :, 0] < 0).sum()) > 64  # block 0 of the first sequence: 298 tied rows
+    scores.backward(upstream.to(device))
+    dq, dk = O.index_score_backward(q_cpu.double().numpy(), k_cpu.double().numpy(), cu_list(lengths), max_seqlen,
+                                    upstream.double().numpy(), block_size=block, scale=scale)
+    for got, ref, what in ((q.grad, dq, "tied dq"), (k.grad, dk, "tied dk")):
+        if dtype == torch.bfloat16:
+            check_bf16_stated(got, ref, what)
+        else:
+            _check_dtype_stated(got, ref, dtype, what)
+
+
 @pytest.mark.parametrize("lengths", [[127], [128], [129], [1, 129, 257]])
 def test_score_causal_block_and_packing_boundaries(lengths, device):
     generator = torch.Generator().manual_seed(97)
